@@ -1,0 +1,249 @@
+"""chatterbox.cpp_amd -- MI355X (gfx950) T3 logits->token sampler.
+
+Python view of the C ABI in include/cbx_sampler.h (libcbx_sampler.so, built
+in-tree by ``make -C chatterbox.cpp_amd``).  The product is the shared library;
+this module only loads it with ctypes and passes device pointers (taken from
+torch tensors) and the current HIP stream.  There is no Python or CPU fallback:
+if the library is missing, importing or calling raises.
+
+The per-row semantics are those of the reference's
+``tts_cpp::chatterbox::detail::sample_next_token_ex`` (src/main.cpp:726-801).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libcbx_sampler.so")
+
+CBX_OK = 0
+CBX_ERR_INVALID = -1
+CBX_ERR_HIP = -2
+CBX_ERR_UNSUPPORTED = -3
+CBX_ERR_NOMEM = -4
+
+CBX_INFO_DREW = 0x01
+CBX_INFO_GREEDY = 0x02
+CBX_INFO_EMPTY = 0x04
+CBX_INFO_TOPP_TIE = 0x08
+CBX_INFO_NONFINITE = 0x10
+CBX_INFO_OVERFLOW = 0x20
+
+CBX_DRAW_UNIFORM = 0
+CBX_DRAW_PHILOX = 1
+
+
+class Params(ctypes.Structure):
+    """cbx_params (include/cbx_sampler.h); the first four fields are
+    chatterbox_sampling_params (src/chatterbox_t3_internal.h:113-118)."""
+
+    _fields_ = [
+        ("top_k", ctypes.c_int32),
+        ("top_p", ctypes.c_float),
+        ("temp", ctypes.c_float),
+        ("repeat_penalty", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("cfg_weight", ctypes.c_float),
+    ]
+
+
+PARAMS_DTYPE_FIELDS = ("top_k", "top_p", "temp", "repeat_penalty", "min_p", "cfg_weight")
+
+
+class Batch(ctypes.Structure):
+    """cbx_batch (include/cbx_sampler.h)."""
+
+    _fields_ = [
+        ("n_rows", ctypes.c_int32),
+        ("n_vocab", ctypes.c_int32),
+        ("n_steps", ctypes.c_int32),
+        ("stop_token", ctypes.c_int32),
+        ("logits", ctypes.c_void_p),
+        ("ld_logits", ctypes.c_int64),
+        ("logits_uncond", ctypes.c_void_p),
+        ("params", ctypes.c_void_p),
+        ("history", ctypes.c_void_p),
+        ("history_len", ctypes.c_void_p),
+        ("ld_history", ctypes.c_int64),
+        ("allowed", ctypes.c_void_p),
+        ("ld_allowed", ctypes.c_int64),
+        ("force_stop", ctypes.c_void_p),
+        ("draw_mode", ctypes.c_int32),
+        ("max_survivors", ctypes.c_int32),
+        ("uniforms", ctypes.c_void_p),
+        ("seed", ctypes.c_uint64),
+        ("stream_ids", ctypes.c_void_p),
+        ("step0", ctypes.c_uint64),
+        ("tokens", ctypes.c_void_p),
+        ("info", ctypes.c_void_p),
+        ("probs", ctypes.c_void_p),
+        ("ld_probs", ctypes.c_int64),
+    ]
+
+
+class CbxError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"cbx error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libcbx_sampler.so and declare its prototypes.  Raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is not built; run `make -C chatterbox.cpp_amd` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    vp, i32, i64, u64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
+    lib.cbx_max_vocab.restype = i32
+    lib.cbx_max_vocab.argtypes = []
+    lib.cbx_sampler_create.restype = ctypes.c_int
+    lib.cbx_sampler_create.argtypes = [ctypes.POINTER(vp), i32, i32, i32]
+    lib.cbx_sampler_destroy.restype = ctypes.c_int
+    lib.cbx_sampler_destroy.argtypes = [vp]
+    lib.cbx_sample_row.restype = ctypes.c_int
+    lib.cbx_sample_row.argtypes = [vp, vp, i32, vp, i32, ctypes.POINTER(Params), ctypes.c_double,
+                                   ctypes.POINTER(i32), ctypes.POINTER(ctypes.c_uint32)]
+    lib.cbx_sample_row_ex.restype = ctypes.c_int
+    lib.cbx_sample_row_ex.argtypes = [vp, vp, vp, i32, vp, i32, ctypes.POINTER(Params), vp, i32,
+                                      i32, ctypes.c_double, ctypes.POINTER(i32),
+                                      ctypes.POINTER(ctypes.c_uint32), vp]
+    lib.cbx_sample_batch.restype = ctypes.c_int
+    lib.cbx_sample_batch.argtypes = [vp, ctypes.POINTER(Batch), vp]
+    lib.cbx_debug_expf.restype = ctypes.c_int
+    lib.cbx_debug_expf.argtypes = [vp, vp, vp, i64, vp]
+    lib.cbx_debug_philox.restype = ctypes.c_int
+    lib.cbx_debug_philox.argtypes = [vp, u64, vp, u64, i32, vp, vp]
+    lib.cbx_last_error.restype = ctypes.c_char_p
+    lib.cbx_last_error.argtypes = []
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != CBX_OK:
+        raise CbxError(rc, _lib.cbx_last_error().decode(errors="replace"))
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream_ptr():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def params_tensor(rows, device="cuda"):
+    """Pack per-row knobs into a device tensor laid out as cbx_params[n]:
+    rows is a sequence of dicts or Params."""
+    import numpy as np
+    import torch
+    n = len(rows)
+    arr = (Params * n)()
+    for i, r in enumerate(rows):
+        if isinstance(r, Params):
+            arr[i] = r
+        else:
+            arr[i] = Params(**r)
+    raw = np.frombuffer(bytes(arr), dtype=np.uint8).copy()
+    return torch.from_numpy(raw).to(device)
+
+
+class Sampler:
+    """Owns one cbx_sampler handle (include/cbx_sampler.h)."""
+
+    def __init__(self, device: int = 0, max_vocab: int = 32768, max_history: int = 4096):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self.lib.cbx_sampler_create(ctypes.byref(h), device, max_vocab, max_history))
+        self.handle = h
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.cbx_sampler_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- single row, host memory (the reference call shape) -------------------
+    def sample_row(self, logits, history, params, u, logits_uncond=None, allowed=None,
+                   force_stop=False, stop_token=0, want_probs=False):
+        import numpy as np
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        hist = np.ascontiguousarray(history if history is not None else [], dtype=np.int32)
+        unc = None if logits_uncond is None else np.ascontiguousarray(logits_uncond, dtype=np.float32)
+        al = None if allowed is None else np.ascontiguousarray(allowed, dtype=np.uint32)
+        probs = np.zeros(lg.size, dtype=np.float32) if want_probs else None
+        p = params if isinstance(params, Params) else Params(**params)
+        tok = ctypes.c_int32()
+        info = ctypes.c_uint32()
+        _check(self.lib.cbx_sample_row_ex(
+            self.handle, lg.ctypes.data, None if unc is None else unc.ctypes.data, lg.size,
+            hist.ctypes.data if hist.size else None, hist.size, ctypes.byref(p),
+            None if al is None else al.ctypes.data, 1 if force_stop else 0, stop_token,
+            float(u), ctypes.byref(tok), ctypes.byref(info),
+            None if probs is None else probs.ctypes.data))
+        return (tok.value, info.value, probs) if want_probs else (tok.value, info.value)
+
+    # -- batched, device memory ------------------------------------------------
+    def sample_batch(self, logits, params, tokens, *, n_steps=1, uniforms=None,
+                     logits_uncond=None, history=None, history_len=None, allowed=None,
+                     force_stop=None, stop_token=0, info=None, probs=None,
+                     draw_mode=None, seed=0, stream_ids=None, step0=0, max_survivors=0,
+                     n_vocab=None, stream=None):
+        """logits: device float32 [n_steps*n_rows, ld] (or [n_steps, n_rows, ld]);
+        params: device uint8 tensor from params_tensor(); tokens: device int32.
+        n_vocab defaults to ld (the row stride)."""
+        ld = logits.shape[-1]
+        total_rows = logits.numel() // ld
+        n_rows = total_rows // n_steps
+        n_vocab = ld if n_vocab is None else n_vocab
+        b = Batch()
+        b.n_rows = n_rows
+        b.n_vocab = n_vocab
+        b.n_steps = n_steps
+        b.stop_token = stop_token
+        b.logits = logits.data_ptr()
+        b.ld_logits = ld
+        b.logits_uncond = None if logits_uncond is None else logits_uncond.data_ptr()
+        b.params = params.data_ptr()
+        b.history = None if history is None else history.data_ptr()
+        b.history_len = None if history_len is None else history_len.data_ptr()
+        b.ld_history = 0 if history is None else history.shape[-1]
+        b.allowed = None if allowed is None else allowed.data_ptr()
+        b.ld_allowed = 0 if allowed is None else allowed.shape[-1]
+        b.force_stop = None if force_stop is None else force_stop.data_ptr()
+        if draw_mode is None:
+            draw_mode = CBX_DRAW_UNIFORM if uniforms is not None else CBX_DRAW_PHILOX
+        b.draw_mode = draw_mode
+        b.max_survivors = max_survivors
+        b.uniforms = None if uniforms is None else uniforms.data_ptr()
+        b.seed = seed
+        b.stream_ids = None if stream_ids is None else stream_ids.data_ptr()
+        b.step0 = step0
+        b.tokens = tokens.data_ptr()
+        b.info = None if info is None else info.data_ptr()
+        b.probs = None if probs is None else probs.data_ptr()
+        b.ld_probs = 0 if probs is None else probs.shape[-1]
+        st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
+        _check(self.lib.cbx_sample_batch(self.handle, ctypes.byref(b), st))
+
+    def debug_expf(self, x, out):
+        _check(self.lib.cbx_debug_expf(self.handle, x.data_ptr(), out.data_ptr(), x.numel(),
+                                       _stream_ptr()))
+
+    def debug_philox(self, seed, stream_ids, step, n, out):
+        _check(self.lib.cbx_debug_philox(self.handle, seed,
+                                         None if stream_ids is None else stream_ids.data_ptr(),
+                                         step, n, out.data_ptr(), _stream_ptr()))

@@ -1,0 +1,338 @@
+// cbx_capi.cpp -- the extern "C" boundary of libcbx_sampler.so.
+//
+// Validates arguments, owns the per-handle stream and staging buffers for the
+// single-row calls, and forwards to the kernels.  No exception crosses the
+// boundary: every entry point returns CBX_OK or a negative CBX_ERR_* and
+// leaves a message for cbx_last_error() on the calling thread.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+#include "cbx_internal.h"
+
+struct cbx_sampler {
+    int32_t device = 0;
+    int32_t max_vocab = 0;
+    int32_t max_history = 0;
+    size_t lds_limit = 0;
+    hipStream_t stream = nullptr;
+    // device buffers for single-row calls
+    float* d_logits = nullptr;
+    float* d_uncond = nullptr;
+    int32_t* d_hist = nullptr;
+    int32_t* d_hist_len = nullptr;
+    cbx_params* d_params = nullptr;
+    uint32_t* d_allowed = nullptr;
+    uint8_t* d_force = nullptr;
+    double* d_u = nullptr;
+    int32_t* d_token = nullptr;
+    uint32_t* d_info = nullptr;
+    float* d_probs = nullptr;
+    // pinned host staging for the small per-call inputs/outputs
+    struct Small {
+        cbx_params params;
+        double u;
+        int32_t hist_len;
+        int32_t token;
+        uint32_t info;
+        uint8_t force;
+    }* h_small = nullptr;
+};
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define CBX_HIP(call)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(CBX_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));       \
+    } while (0)
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+void release(cbx_sampler* s) {
+    DeviceGuard g(s->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    (void)hipFree(s->d_logits);
+    (void)hipFree(s->d_uncond);
+    (void)hipFree(s->d_hist);
+    (void)hipFree(s->d_hist_len);
+    (void)hipFree(s->d_params);
+    (void)hipFree(s->d_allowed);
+    (void)hipFree(s->d_force);
+    (void)hipFree(s->d_u);
+    (void)hipFree(s->d_token);
+    (void)hipFree(s->d_info);
+    (void)hipFree(s->d_probs);
+    if (s->h_small) (void)hipHostFree(s->h_small);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+}
+
+// Survivor capacity for a launch: the smaller of n_vocab and the caller's
+// hint, rounded up to a power of two, limited by the device's LDS.
+int32_t pick_cap(const cbx_sampler* s, int32_t n_vocab, int32_t hint) {
+    int32_t want = (hint > 0 && hint < n_vocab) ? hint : n_vocab;
+    int32_t cap = 64;
+    while (cap < want) cap <<= 1;
+    const int32_t lim = cbx::max_cap_for_lds(n_vocab, s->lds_limit);
+    return cap < lim ? cap : lim;
+}
+
+bool params_ok(const cbx_params* p) {
+    // NaN knobs would make the reference's activation tests meaningless.
+    return p->top_p == p->top_p && p->temp == p->temp && p->repeat_penalty == p->repeat_penalty &&
+           p->min_p == p->min_p && p->cfg_weight == p->cfg_weight;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cbx_last_error(void) { return g_err; }
+
+int32_t cbx_max_vocab(void) { return cbx::kMaxVocab; }
+
+int cbx_sampler_create(cbx_sampler** out, int32_t device, int32_t max_vocab, int32_t max_history) {
+    if (!out) return fail(CBX_ERR_INVALID, "cbx_sampler_create: out is NULL");
+    *out = nullptr;
+    if (max_vocab < 1 || max_vocab > cbx::kMaxVocab)
+        return fail(CBX_ERR_INVALID, "cbx_sampler_create: max_vocab %d outside [1, %d]", max_vocab,
+                    cbx::kMaxVocab);
+    if (max_history < 0) return fail(CBX_ERR_INVALID, "cbx_sampler_create: max_history < 0");
+    int n_dev = 0;
+    CBX_HIP(hipGetDeviceCount(&n_dev));
+    if (device < 0 || device >= n_dev)
+        return fail(CBX_ERR_INVALID, "cbx_sampler_create: device %d of %d", device, n_dev);
+
+    cbx_sampler* s = new (std::nothrow) cbx_sampler();
+    if (!s) return fail(CBX_ERR_NOMEM, "cbx_sampler_create: out of host memory");
+    s->device = device;
+    s->max_vocab = max_vocab;
+    s->max_history = max_history;
+    DeviceGuard g(device);
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        release(s);
+        return fail(CBX_ERR_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    }
+    s->lds_limit = prop.sharedMemPerBlock > prop.sharedMemPerBlockOptin ? prop.sharedMemPerBlock
+                                                                         : prop.sharedMemPerBlockOptin;
+    const size_t W = (size_t)(max_vocab + 31) / 32;
+    const size_t h = (size_t)(max_history > 0 ? max_history : 1);
+    e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc(&s->d_logits, sizeof(float) * max_vocab);
+    if (e == hipSuccess) e = hipMalloc(&s->d_uncond, sizeof(float) * max_vocab);
+    if (e == hipSuccess) e = hipMalloc(&s->d_hist, sizeof(int32_t) * h);
+    if (e == hipSuccess) e = hipMalloc(&s->d_hist_len, sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&s->d_params, sizeof(cbx_params));
+    if (e == hipSuccess) e = hipMalloc(&s->d_allowed, sizeof(uint32_t) * W);
+    if (e == hipSuccess) e = hipMalloc(&s->d_force, 1);
+    if (e == hipSuccess) e = hipMalloc(&s->d_u, sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&s->d_token, sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&s->d_info, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&s->d_probs, sizeof(float) * max_vocab);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_small, sizeof(cbx_sampler::Small));
+    if (e != hipSuccess) {
+        release(s);
+        return fail(e == hipErrorOutOfMemory ? CBX_ERR_NOMEM : CBX_ERR_HIP,
+                    "cbx_sampler_create: %s", hipGetErrorString(e));
+    }
+    *out = s;
+    return CBX_OK;
+}
+
+int cbx_sampler_destroy(cbx_sampler* s) {
+    if (!s) return CBX_OK;
+    release(s);
+    return CBX_OK;
+}
+
+int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_uncond,
+                      int32_t n_vocab, const int32_t* history, int32_t n_history,
+                      const cbx_params* params, const uint32_t* allowed, int32_t force_stop,
+                      int32_t stop_token, double u, int32_t* token_out, uint32_t* info_out,
+                      float* probs_out) {
+    if (!s || !logits || !params || !token_out)
+        return fail(CBX_ERR_INVALID, "cbx_sample_row: NULL handle, logits, params or token_out");
+    if (n_vocab < 1 || n_vocab > s->max_vocab)
+        return fail(CBX_ERR_INVALID, "cbx_sample_row: n_vocab %d outside [1, %d]", n_vocab,
+                    s->max_vocab);
+    if (n_history < 0 || n_history > s->max_history || (n_history > 0 && !history))
+        return fail(CBX_ERR_INVALID, "cbx_sample_row: history of %d ids (handle holds %d)",
+                    n_history, s->max_history);
+    if (!params_ok(params)) return fail(CBX_ERR_INVALID, "cbx_sample_row: NaN parameter");
+    if (!(u >= 0.0 && u < 1.0)) return fail(CBX_ERR_INVALID, "cbx_sample_row: u outside [0, 1)");
+    DeviceGuard g(s->device);
+    hipStream_t st = s->stream;
+    cbx_sampler::Small* hs = s->h_small;
+    hs->params = *params;
+    hs->u = u;
+    hs->hist_len = n_history;
+    hs->force = force_stop ? 1 : 0;
+    const size_t W = (size_t)(n_vocab + 31) / 32;
+    CBX_HIP(hipMemcpyAsync(s->d_logits, logits, sizeof(float) * n_vocab, hipMemcpyHostToDevice, st));
+    if (logits_uncond)
+        CBX_HIP(hipMemcpyAsync(s->d_uncond, logits_uncond, sizeof(float) * n_vocab,
+                               hipMemcpyHostToDevice, st));
+    if (n_history > 0)
+        CBX_HIP(hipMemcpyAsync(s->d_hist, history, sizeof(int32_t) * n_history,
+                               hipMemcpyHostToDevice, st));
+    if (allowed)
+        CBX_HIP(hipMemcpyAsync(s->d_allowed, allowed, sizeof(uint32_t) * W, hipMemcpyHostToDevice, st));
+    CBX_HIP(hipMemcpyAsync(s->d_params, &hs->params, sizeof(cbx_params), hipMemcpyHostToDevice, st));
+    CBX_HIP(hipMemcpyAsync(s->d_u, &hs->u, sizeof(double), hipMemcpyHostToDevice, st));
+    CBX_HIP(hipMemcpyAsync(s->d_hist_len, &hs->hist_len, sizeof(int32_t), hipMemcpyHostToDevice, st));
+    CBX_HIP(hipMemcpyAsync(s->d_force, &hs->force, 1, hipMemcpyHostToDevice, st));
+
+    cbx::KernelArgs a{};
+    a.n_rows = 1;
+    a.n_vocab = n_vocab;
+    a.n_steps = 1;
+    a.stop_token = stop_token;
+    a.logits = s->d_logits;
+    a.ld_logits = n_vocab;
+    a.uncond = logits_uncond ? s->d_uncond : nullptr;
+    a.params = s->d_params;
+    a.history = s->d_hist;
+    a.history_len = s->d_hist_len;
+    a.ld_history = n_history;
+    a.allowed = allowed ? s->d_allowed : nullptr;
+    a.ld_allowed = (int64_t)W;
+    a.force_stop = s->d_force;
+    a.draw_mode = CBX_DRAW_UNIFORM;
+    a.cap = pick_cap(s, n_vocab, (params->top_k > 0 && params->top_k < n_vocab) ? params->top_k : 0);
+    a.uniforms = s->d_u;
+    a.tokens = s->d_token;
+    a.info = s->d_info;
+    a.probs = probs_out ? s->d_probs : nullptr;
+    a.ld_probs = n_vocab;
+    CBX_HIP(cbx::launch_sample(a, st));
+    CBX_HIP(hipMemcpyAsync(&hs->info, s->d_info, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    CBX_HIP(hipStreamSynchronize(st));
+    if ((hs->info & CBX_INFO_OVERFLOW) && a.cap < pick_cap(s, n_vocab, 0)) {
+        // ties at the top-k threshold left more survivors than k: redo the
+        // row with the largest capacity the device allows
+        a.cap = pick_cap(s, n_vocab, 0);
+        CBX_HIP(cbx::launch_sample(a, st));
+    }
+    CBX_HIP(hipMemcpyAsync(&hs->token, s->d_token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    CBX_HIP(hipMemcpyAsync(&hs->info, s->d_info, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    if (probs_out)
+        CBX_HIP(hipMemcpyAsync(probs_out, s->d_probs, sizeof(float) * n_vocab, hipMemcpyDeviceToHost, st));
+    CBX_HIP(hipStreamSynchronize(st));
+    *token_out = hs->token;
+    if (info_out) *info_out = hs->info;
+    if (hs->info & CBX_INFO_OVERFLOW)
+        return fail(CBX_ERR_UNSUPPORTED,
+                    "cbx_sample_row: more survivors after top-k than the on-chip capacity %d", a.cap);
+    return CBX_OK;
+}
+
+int cbx_sample_row(cbx_sampler* s, const float* logits, int32_t n_vocab, const int32_t* history,
+                   int32_t n_history, const cbx_params* params, double u, int32_t* token_out,
+                   uint32_t* info_out) {
+    return cbx_sample_row_ex(s, logits, nullptr, n_vocab, history, n_history, params, nullptr, 0,
+                             0, u, token_out, info_out, nullptr);
+}
+
+int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
+    if (!s || !b) return fail(CBX_ERR_INVALID, "cbx_sample_batch: NULL handle or batch");
+    if (b->n_rows < 1 || b->n_steps < 1)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: n_rows %d, n_steps %d", b->n_rows, b->n_steps);
+    if ((int64_t)b->n_rows * b->n_steps > 0x7fffffffLL)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: n_rows * n_steps exceeds 2^31-1");
+    if (b->n_vocab < 1 || b->n_vocab > cbx::kMaxVocab)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: n_vocab %d outside [1, %d]", b->n_vocab,
+                    cbx::kMaxVocab);
+    if (!b->logits || !b->params || !b->tokens)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: NULL logits, params or tokens");
+    if (b->ld_logits < b->n_vocab)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: ld_logits %lld < n_vocab %d",
+                    (long long)b->ld_logits, b->n_vocab);
+    if (b->history && (!b->history_len || b->ld_history < 0))
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: history without history_len/ld_history");
+    if (b->allowed && b->ld_allowed < (b->n_vocab + 31) / 32)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: ld_allowed %lld < ceil(n_vocab/32)",
+                    (long long)b->ld_allowed);
+    if (b->probs && b->ld_probs < b->n_vocab)
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: ld_probs %lld < n_vocab",
+                    (long long)b->ld_probs);
+    if (b->draw_mode == CBX_DRAW_UNIFORM) {
+        if (!b->uniforms) return fail(CBX_ERR_INVALID, "cbx_sample_batch: uniforms is NULL");
+    } else if (b->draw_mode != CBX_DRAW_PHILOX) {
+        return fail(CBX_ERR_INVALID, "cbx_sample_batch: unknown draw_mode %d", b->draw_mode);
+    }
+    if (b->max_survivors < 0) return fail(CBX_ERR_INVALID, "cbx_sample_batch: max_survivors < 0");
+    DeviceGuard g(s->device);
+    cbx::KernelArgs a{};
+    a.n_rows = b->n_rows;
+    a.n_vocab = b->n_vocab;
+    a.n_steps = b->n_steps;
+    a.stop_token = b->stop_token;
+    a.logits = b->logits;
+    a.ld_logits = b->ld_logits;
+    a.uncond = b->logits_uncond;
+    a.params = b->params;
+    a.history = b->history;
+    a.history_len = b->history_len;
+    a.ld_history = b->ld_history;
+    a.allowed = b->allowed;
+    a.ld_allowed = b->ld_allowed;
+    a.force_stop = b->force_stop;
+    a.draw_mode = b->draw_mode;
+    a.cap = pick_cap(s, b->n_vocab, b->max_survivors);
+    a.uniforms = b->uniforms;
+    a.seed = b->seed;
+    a.stream_ids = b->stream_ids;
+    a.step0 = b->step0;
+    a.tokens = b->tokens;
+    a.info = b->info;
+    a.probs = b->probs;
+    a.ld_probs = b->ld_probs;
+    CBX_HIP(cbx::launch_sample(a, (hipStream_t)stream));
+    return CBX_OK;
+}
+
+int cbx_debug_expf(cbx_sampler* s, const float* in, float* out, int64_t n, void* stream) {
+    if (!s || !in || !out || n < 0) return fail(CBX_ERR_INVALID, "cbx_debug_expf: bad argument");
+    if (n == 0) return CBX_OK;
+    DeviceGuard g(s->device);
+    CBX_HIP(cbx::launch_debug_expf(in, out, n, (hipStream_t)stream));
+    return CBX_OK;
+}
+
+int cbx_debug_philox(cbx_sampler* s, uint64_t seed, const uint64_t* stream_ids, uint64_t step,
+                     int32_t n, double* out, void* stream) {
+    if (!s || !out || n < 0) return fail(CBX_ERR_INVALID, "cbx_debug_philox: bad argument");
+    if (n == 0) return CBX_OK;
+    DeviceGuard g(s->device);
+    CBX_HIP(cbx::launch_debug_philox(seed, stream_ids, step, n, out, (hipStream_t)stream));
+    return CBX_OK;
+}
+
+}  // extern "C"

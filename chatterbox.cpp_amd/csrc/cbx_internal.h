@@ -1,0 +1,50 @@
+// cbx_internal.h -- shared between the C ABI layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/cbx_sampler.h"
+
+namespace cbx {
+
+// Device-side view of one cbx_batch launch (all pointers device addresses).
+struct KernelArgs {
+    int32_t n_rows, n_vocab, n_steps, stop_token;
+    const float* logits;
+    int64_t ld_logits;
+    const float* uncond;
+    const cbx_params* params;
+    const int32_t* history;
+    const int32_t* history_len;
+    int64_t ld_history;
+    const uint32_t* allowed;
+    int64_t ld_allowed;
+    const uint8_t* force_stop;
+    int32_t draw_mode;
+    int32_t cap;  // survivor capacity of the on-chip lists (power of two)
+    const double* uniforms;
+    uint64_t seed;
+    const uint64_t* stream_ids;
+    uint64_t step0;
+    int32_t* tokens;
+    uint32_t* info;
+    float* probs;
+    int64_t ld_probs;
+};
+
+constexpr int32_t kMaxVocab = 32768;
+
+// Largest survivor capacity whose lists fit `lds_bytes` of LDS for n_vocab.
+int32_t max_cap_for_lds(int32_t n_vocab, size_t lds_bytes);
+// LDS bytes one workgroup needs for (cap, n_vocab).
+size_t lds_bytes_for(int32_t cap, int32_t n_vocab);
+
+// Launch the sampler over n_steps * n_rows rows.  Returns a hipError_t.
+hipError_t launch_sample(const KernelArgs& a, hipStream_t stream);
+
+hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream);
+hipError_t launch_debug_philox(uint64_t seed, const uint64_t* stream_ids, uint64_t step,
+                               int32_t n, double* out, hipStream_t stream);
+
+}  // namespace cbx

@@ -1,0 +1,152 @@
+/*
+ * cbx_sampler.h -- C ABI of the MI355X (gfx950) T3 logits->token sampler.
+ *
+ * Drop-in for the per-step sampler of chatterbox.cpp,
+ *   int32_t tts_cpp::chatterbox::detail::sample_next_token_ex(
+ *       const std::vector<float>& logits, const std::vector<int32_t>& generated,
+ *       const chatterbox_sampling_params& params, std::mt19937& rng)
+ * (src/main.cpp:726-801, declared at src/chatterbox_t3_internal.h:144-148),
+ * called from src/chatterbox_engine.cpp:338,351 and, through the wrapper at
+ * src/chatterbox_cli.cpp:394-405, from chatterbox_cli.cpp:1270,1283,1633,1643.
+ *
+ * Semantics are the reference's, bit for bit: given the same logits, history,
+ * parameters and the same uniform u in [0,1) for the draw, the token id is the
+ * one the reference returns.  The draw's uniform is supplied by the caller
+ * (CBX_DRAW_UNIFORM; include/cbx_sampler.hpp derives it from the caller's
+ * std::mt19937 exactly as std::discrete_distribution does) or generated on the
+ * device by Philox4x32-10 keyed (seed, stream, step) (CBX_DRAW_PHILOX).
+ *
+ * Plain C: every pointer is a plain address, every size an integer; device
+ * pointers are HIP device addresses, `stream` is a hipStream_t (NULL = the
+ * null stream).  No C++ exception crosses this boundary.
+ *
+ * Return codes: CBX_OK (0) or a negative CBX_ERR_*; cbx_last_error() gives a
+ * thread-local message for the last failing call on the calling thread.
+ */
+#ifndef CBX_SAMPLER_H
+#define CBX_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CBX_OK               0
+#define CBX_ERR_INVALID     (-1)  /* bad argument (null pointer, size out of range) */
+#define CBX_ERR_HIP         (-2)  /* a HIP runtime call failed                      */
+#define CBX_ERR_UNSUPPORTED (-3)  /* valid request this build does not implement    */
+#define CBX_ERR_NOMEM       (-4)  /* device or host allocation failed               */
+
+/* Per-row sampling knobs.  The first four are chatterbox_sampling_params
+ * (src/chatterbox_t3_internal.h:113-118; defaults 1000, 0.95, 0.8, 1.2) and
+ * keep the reference's activation rules (main.cpp:735, 740, 750, 774). */
+typedef struct cbx_params {
+    int32_t top_k;          /* active when 0 < top_k < n_vocab                      */
+    float   top_p;          /* active when top_p < 1                                */
+    float   temp;           /* scale by 1/temp when temp > 0 && temp != 1;
+                               temp <= 0 selects the first argmax (no draw)        */
+    float   repeat_penalty; /* active when != 1 and the history is non-empty      */
+    float   min_p;          /* extension, active when > 0: after top-p, drop ids
+                               with expf(s - s_max) < min_p                         */
+    float   cfg_weight;     /* extension, used when uncond logits are given:
+                               l = c + w * (c - u), each operation rounded once     */
+} cbx_params;
+
+/* Per-row result flags. */
+#define CBX_INFO_DREW      0x01u /* the uniform was consumed (reference drew from rng) */
+#define CBX_INFO_GREEDY    0x02u /* temp <= 0: first argmax of the probabilities       */
+#define CBX_INFO_EMPTY     0x04u /* every score was -inf: token 0 (main.cpp:792)       */
+#define CBX_INFO_TOPP_TIE  0x08u /* equal scores straddle the top-p cutoff: which of
+                                    them is kept depends on std::sort's tie order     */
+#define CBX_INFO_NONFINITE 0x10u /* NaN or +inf scores: outside the contract           */
+#define CBX_INFO_OVERFLOW  0x20u /* more survivors than the on-chip capacity:
+                                    token -1, row not sampled                         */
+
+#define CBX_DRAW_UNIFORM 0 /* uniforms[step][row] supplied by the caller            */
+#define CBX_DRAW_PHILOX  1 /* Philox4x32-10: counter {step lo, step hi, stream lo,
+                              stream hi}, key {seed lo, seed hi}; u = ((x0>>5)*2^26 +
+                              (x1>>6)) * 2^-53                                        */
+
+typedef struct cbx_sampler cbx_sampler; /* opaque; one per decode thread */
+
+/* Batched request: n_steps independent batches of n_rows streams, step-major.
+ * All pointers are device pointers.  Optional ones may be NULL. */
+typedef struct cbx_batch {
+    int32_t n_rows;             /* streams per step (>= 1)                          */
+    int32_t n_vocab;            /* 2 .. cbx_max_vocab()                             */
+    int32_t n_steps;            /* >= 1                                             */
+    int32_t stop_token;         /* id kept by force_stop rows                       */
+    const float*    logits;     /* [n_steps][n_rows][ld_logits]                     */
+    int64_t         ld_logits;  /* >= n_vocab                                       */
+    const float*    logits_uncond; /* optional CFG uncond rows, same layout         */
+    const cbx_params* params;   /* [n_rows]                                         */
+    const int32_t*  history;    /* optional [n_rows][ld_history] generated ids      */
+    const int32_t*  history_len;/* [n_rows], required with history                  */
+    int64_t         ld_history;
+    const uint32_t* allowed;    /* optional [n_rows][ld_allowed] bitmask, bit (i&31)
+                                   of word i>>5 set = id i allowed                  */
+    int64_t         ld_allowed; /* >= ceil(n_vocab/32)                              */
+    const uint8_t*  force_stop; /* optional [n_steps][n_rows]: nonzero = every id
+                                   but stop_token is masked                        */
+    int32_t         draw_mode;  /* CBX_DRAW_UNIFORM or CBX_DRAW_PHILOX              */
+    int32_t         max_survivors; /* host hint: bound on ids left by top-k (e.g. the
+                                   largest active top_k); 0 = n_vocab.  Rows that
+                                   exceed it report CBX_INFO_OVERFLOW              */
+    const double*   uniforms;   /* CBX_DRAW_UNIFORM: [n_steps][n_rows] in [0,1)      */
+    uint64_t        seed;       /* CBX_DRAW_PHILOX key                              */
+    const uint64_t* stream_ids; /* CBX_DRAW_PHILOX: [n_rows]; NULL = row index      */
+    uint64_t        step0;      /* CBX_DRAW_PHILOX: counter of step 0               */
+    int32_t*        tokens;     /* out [n_steps][n_rows]                            */
+    uint32_t*       info;       /* optional out [n_steps][n_rows] CBX_INFO_* bits   */
+    float*          probs;      /* optional out [n_steps][n_rows][ld_probs]:
+                                   post-filter probabilities (main.cpp:793)        */
+    int64_t         ld_probs;
+} cbx_batch;
+
+/* Largest n_vocab this build accepts. */
+int32_t cbx_max_vocab(void);
+
+/* Create a handle on HIP device `device` sized for single-row calls of up to
+ * max_vocab logits and max_history history ids (its pinned staging and device
+ * buffers).  Batched calls use caller memory and need no sizing. */
+int cbx_sampler_create(cbx_sampler** out, int32_t device, int32_t max_vocab,
+                       int32_t max_history);
+int cbx_sampler_destroy(cbx_sampler* s);
+
+/* Single row, host memory in and out, synchronous: the reference call shape
+ * (logits, history, params in; token out).  Replaces the body of
+ * sample_next_token_ex (main.cpp:726-801); `u` is the draw's uniform. */
+int cbx_sample_row(cbx_sampler* s, const float* logits, int32_t n_vocab,
+                   const int32_t* history, int32_t n_history,
+                   const cbx_params* params, double u,
+                   int32_t* token_out, uint32_t* info_out);
+
+/* Single row with the extensions: optional CFG uncond logits, allowed bitmask
+ * (ceil(n_vocab/32) words), forced stop, and the post-filter probabilities
+ * (n_vocab floats) out.  Host memory, synchronous. */
+int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_uncond,
+                      int32_t n_vocab, const int32_t* history, int32_t n_history,
+                      const cbx_params* params, const uint32_t* allowed,
+                      int32_t force_stop, int32_t stop_token, double u,
+                      int32_t* token_out, uint32_t* info_out, float* probs_out);
+
+/* Batched, device memory, asynchronous on `stream`.  The handle only supplies
+ * the device; no handle state is written, so one handle may serve several
+ * streams.  Replaces n_steps x n_rows calls of sample_next_token_ex. */
+int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream);
+
+/* Diagnostics: the device exponential used by the sampler (the glibc expf
+ * algorithm restated for the GPU) applied elementwise, and the device Philox
+ * uniforms for (seed, stream_ids[i] or i, step).  Device memory, async. */
+int cbx_debug_expf(cbx_sampler* s, const float* in, float* out, int64_t n, void* stream);
+int cbx_debug_philox(cbx_sampler* s, uint64_t seed, const uint64_t* stream_ids,
+                     uint64_t step, int32_t n, double* out, void* stream);
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* cbx_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

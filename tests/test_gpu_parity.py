@@ -1,0 +1,344 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs and the same uniforms.
+
+Every case prints its name before touching the GPU.  Sizes are those of the
+measured configurations where the oracle finishes in seconds.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import parity
+import pkg
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def cbx(torch_cuda):
+    mod = pkg.load()
+    s = mod.Sampler(device=0, max_vocab=32768, max_history=4096)
+    yield mod, s
+    s.close()
+
+
+def oparams(d):
+    return O.OParams(d["top_k"], d["top_p"], d["temp"], d["repeat_penalty"], d["min_p"],
+                     d["cfg_weight"])
+
+
+def oracle_rows(logits, plist, u, history=None, hist_len=None, uncond=None, allowed=None,
+                force_stop=None, stop=0, want_probs=True):
+    n = logits.shape[0]
+    toks = np.zeros(n, np.int32)
+    infos = np.zeros(n, np.uint32)
+    probs = np.zeros(logits.shape, np.float32) if want_probs else None
+    for r in range(n):
+        pr = r % len(plist)
+        h = [] if history is None else history[pr][: hist_len[pr]]
+        res = O.sample_row(logits[r], h, oparams(plist[pr]), u[r],
+                           uncond=None if uncond is None else uncond[r],
+                           allowed=None if allowed is None else allowed[pr],
+                           force_stop=bool(force_stop[r]) if force_stop is not None else False,
+                           stop_token=stop, want_probs=want_probs)
+        toks[r], infos[r] = res[0], res[1]
+        if want_probs:
+            probs[r] = res[2]
+    return toks, infos, probs
+
+
+def gpu_batch(cbx, torch, logits, plist, u=None, history=None, hist_len=None, uncond=None,
+              allowed=None, force_stop=None, stop=0, n_steps=1, want_probs=True, **kw):
+    mod, s = cbx
+    dev = "cuda"
+    lg = torch.from_numpy(np.ascontiguousarray(logits)).to(dev)
+    n = logits.shape[0]
+    w = pkg.workloads()
+    prm = torch.from_numpy(w.pack_params(plist)).to(dev)
+    tok = torch.full((n,), -7, dtype=torch.int32, device=dev)
+    info = torch.zeros(n, dtype=torch.int32, device=dev)
+    probs = torch.full(logits.shape, -1.0, dtype=torch.float32, device=dev) if want_probs else None
+    args = dict(n_steps=n_steps, info=info, probs=probs, stop_token=stop)
+    if u is not None:
+        args["uniforms"] = torch.from_numpy(np.ascontiguousarray(u, np.float64)).to(dev)
+    if history is not None:
+        args["history"] = torch.from_numpy(np.ascontiguousarray(history, np.int32)).to(dev)
+        args["history_len"] = torch.from_numpy(np.ascontiguousarray(hist_len, np.int32)).to(dev)
+    if uncond is not None:
+        args["logits_uncond"] = torch.from_numpy(np.ascontiguousarray(uncond)).to(dev)
+    if allowed is not None:
+        args["allowed"] = torch.from_numpy(np.ascontiguousarray(allowed, np.uint32).view(np.int32)).to(dev)
+    if force_stop is not None:
+        args["force_stop"] = torch.from_numpy(np.ascontiguousarray(force_stop, np.uint8)).to(dev)
+    args.update(kw)
+    s.sample_batch(lg, prm, tok, **args)
+    torch.cuda.synchronize()
+    return (tok.cpu().numpy(), info.cpu().numpy().view(np.uint32),
+            None if probs is None else probs.cpu().numpy())
+
+
+# --------------------------------------------------------------------------
+
+
+def test_device_expf_exhaustive(cbx, torch_cuda):
+    """The device exponential equals host libm expf for every binary32 input
+    the sampler can produce (all x <= 0 down to -104), checked in chunks."""
+    torch = torch_cuda
+    mod, s = cbx
+    lo, hi = 0x80000000, 0xC2D00001
+    chunk = 1 << 27
+    bad = 0
+    start = lo
+    while start < hi:
+        n = min(chunk, hi - start)
+        say(f"expf chunk 0x{start:08x} +{n}")
+        bits = torch.arange(n, dtype=torch.int64, device="cuda") + start
+        x = (bits - (1 << 32) * (bits >= 2**31).long()).to(torch.int32).view(torch.float32)
+        out = torch.empty_like(x)
+        s.debug_expf(x, out)
+        host = out.cpu().numpy()
+        bad += O.lib().cbx_oracle_expf_mismatch(start, n, host.ctypes.data, 16)
+        start += n
+    assert bad == 0
+
+
+def test_device_philox_matches_oracle(cbx, torch_cuda):
+    torch = torch_cuda
+    mod, s = cbx
+    say("philox uniforms")
+    n = 4096
+    sids = np.arange(n, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15)
+    for seed, step in ((0, 0), (42, 17), (0xDEADBEEFCAFEF00D, 2**40 + 3)):
+        out = torch.empty(n, dtype=torch.float64, device="cuda")
+        s.debug_philox(seed, torch.from_numpy(sids.view(np.int64)).cuda(), step, n, out)
+        got = out.cpu().numpy()
+        want = np.array([O.philox_uniform(seed, int(sids[i]), step) for i in range(n)])
+        assert np.array_equal(got, want)
+
+
+def test_single_stream_as_is(cbx, torch_cuda):
+    """500 steps, V=6563, k=1000 p=0.95 T=0.8 pen=1.2, min_p=0 (the reference's
+    own knobs): uniforms from the reference's mt19937 front end."""
+    w = pkg.workloads()
+    d = w.single_stream(steps=500, min_p=0.0)
+    say("single_stream min_p=0 batch of 500 steps")
+    u = O.mt_canonical(42, 500)
+    hist = np.tile(d["history"], (1, 1))
+    hl = np.array([d["history"].size], np.int32)
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], [d["params"]], u, hist, hl, n_steps=500,
+                           max_survivors=1000)
+    tr, ir, pr = oracle_rows(d["logits"], [d["params"]], u, hist, hl)
+    parity.compare("single_stream_as_is", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_single_stream_min_p(cbx, torch_cuda):
+    w = pkg.workloads()
+    d = w.single_stream(steps=500, min_p=0.05, seed=0x5EED11)
+    say("single_stream min_p=0.05")
+    u = O.mt_canonical(7, 500)
+    hist = d["history"][None, :]
+    hl = np.array([d["history"].size], np.int32)
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], [d["params"]], u, hist, hl, n_steps=500)
+    tr, ir, pr = oracle_rows(d["logits"], [d["params"]], u, hist, hl)
+    parity.compare("single_stream_min_p", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_engine_loop_mt19937_row_api(cbx, torch_cuda):
+    """The engine's loop (chatterbox_engine.cpp:338-353): one mt19937(seed),
+    history growing by each token; the GPU row API fed the uniforms the
+    reference's std::discrete_distribution consumed."""
+    mod, s = cbx
+    w = pkg.workloads()
+    d = w.single_stream(steps=200, min_p=0.0, seed=0x5EED12)
+    p = d["params"]
+    say("engine loop, row API, 200 steps")
+    toks, us = O.run_mt19937(d["logits"], np.array([], np.int32), oparams(p), seed=42)
+    hist = []
+    for t in range(200):
+        tok, info = s.sample_row(d["logits"][t], hist, p, us[t])
+        assert tok == toks[t], t
+        hist.append(tok)
+
+
+def test_cfg_pair_growing_history(cbx, torch_cuda):
+    """CFG pair, V=8194, 1000 steps with the history growing by each sampled
+    id: the oracle's id sequence defines every step's history, and one launch
+    checks all 1000 steps."""
+    w = pkg.workloads()
+    d = w.cfg_pair(steps=1000)
+    steps = d["cond"].shape[0]
+    u = O.mt_canonical(1234, steps)
+    say("cfg_pair oracle sequence")
+    seq = []
+    ref_t, ref_i = np.zeros(steps, np.int32), np.zeros(steps, np.uint32)
+    ref_p = np.zeros(d["cond"].shape, np.float32)
+    for t in range(steps):
+        tok, info, probs, _ = O.sample_row(d["cond"][t], seq, oparams(d["params"]), u[t],
+                                           uncond=d["uncond"][t], want_probs=True)
+        ref_t[t], ref_i[t], ref_p[t] = tok, info, probs
+        seq.append(tok)
+    hist = np.zeros((steps, steps), np.int32)
+    for t in range(steps):
+        hist[t, :t] = seq[:t]
+    hl = np.arange(steps, dtype=np.int32)
+    say("cfg_pair gpu (1000 rows, one per step)")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["cond"], [d["params"]] * steps, u, hist, hl,
+                           uncond=d["uncond"])
+    parity.compare("cfg_pair", tg, ig, ref_t, ref_i, u, pg, ref_p)
+
+
+def test_batched_streams(cbx, torch_cuda):
+    """B=256, V=6563, per-row temperature and top-k, 4 independent steps."""
+    w = pkg.workloads()
+    d = w.batched_streams(B=256, steps=4)
+    n = d["logits"].shape[0]
+    u = O.mt_canonical(99, n)
+    say("batched_streams B=256 x 4 steps")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], n_steps=4, max_survivors=1000)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
+    parity.compare("batched_streams", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_batched_streams_philox(cbx, torch_cuda):
+    """Device Philox draws keyed (seed, stream, step) equal the oracle fed the
+    oracle's Philox uniforms."""
+    w = pkg.workloads()
+    d = w.batched_streams(B=256, steps=2, seed=0x5EED33)
+    n = d["logits"].shape[0]
+    seed, step0 = 0xC0FFEE, 1000
+    u = np.array([O.philox_uniform(seed, r % 256, step0 + r // 256) for r in range(n)])
+    say("batched_streams philox")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], None, d["history"],
+                           d["hist_len"], n_steps=2, draw_mode=1, seed=seed, step0=step0)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
+    parity.compare("batched_streams_philox", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_masked_stress(cbx, torch_cuda):
+    """B=1024, V=32768, 20% allowed bitmask, forced stop rows, k=50, p=0.9,
+    min_p=0.02, pen=1.3, history 512."""
+    w = pkg.workloads()
+    d = w.masked_stress()
+    u = O.mt_canonical(5, d["B"])
+    say("masked_stress B=1024 V=32768")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], allowed=d["allowed"], force_stop=d["force_stop"],
+                           stop=d["stop"], max_survivors=50)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"],
+                             allowed=d["allowed"], force_stop=d["force_stop"], stop=d["stop"])
+    parity.compare("masked_stress", tg, ig, tr, ir, u, pg, pr)
+    assert np.all(tg[d["force_stop"] == 1] == d["stop"])
+
+
+EDGE_CASES = [
+    # name, V, params, logits builder, u
+    ("all_masked", 64, dict(top_k=10, top_p=0.9, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: np.full(V, -np.inf, F32), 0.5),
+    ("greedy", 300, dict(top_k=0, top_p=1.0, temp=0.0, repeat_penalty=1.0),
+     lambda V, r: np.where(np.arange(V) % 7 == 3, F32(5), F32(1)).astype(F32), 0.5),
+    ("greedy_filters", 300, dict(top_k=20, top_p=0.5, temp=-1.0, repeat_penalty=1.5),
+     lambda V, r: (r.standard_normal(V) * 3).astype(F32), 0.9),
+    ("u_zero", 500, dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: (r.standard_normal(V) * 3).astype(F32), 0.0),
+    ("u_top", 500, dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: (r.standard_normal(V) * 3).astype(F32), math.nextafter(1.0, 0.0)),
+    ("last_id_forced", 4, dict(top_k=0, top_p=1.0, temp=1.0, repeat_penalty=1.0),
+     lambda V, r: np.array([0, 0, 0, -np.inf], F32), math.nextafter(1.0, 0.0)),
+    ("v1", 1, dict(top_k=0, top_p=0.5, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: np.array([3.0], F32), 0.5),
+    ("v2", 2, dict(top_k=1, top_p=0.9, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: np.array([1.0, 2.0], F32), 0.5),
+    ("topk_ties_large", 200, dict(top_k=3, top_p=1.0, temp=1.0, repeat_penalty=1.0),
+     lambda V, r: np.concatenate([[9, 5, 5, 5, 5], np.zeros(V - 5)]).astype(F32), 0.7),
+    ("topk_ties_small", 200, dict(top_k=3, top_p=1.0, temp=1.0, repeat_penalty=1.0),
+     lambda V, r: np.concatenate([[0.5, 1e-4, 1e-4, 1e-4, 1e-4], np.full(V - 5, -1)]).astype(F32),
+     0.7),
+    ("topp_zero", 300, dict(top_k=0, top_p=0.0, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: (r.standard_normal(V) * 3).astype(F32), 0.3),
+    ("topp_equal_scores", 64, dict(top_k=0, top_p=0.5, temp=1.0, repeat_penalty=1.0),
+     lambda V, r: np.full(V, 2.5, F32), 0.3),
+    ("topk_off_full_sort", 6563, dict(top_k=0, top_p=0.95, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: (r.standard_normal(V) * 3).astype(F32), 0.61),
+    ("topk_eq_V_minus_1", 777, dict(top_k=776, top_p=0.99, temp=1.3, repeat_penalty=0.8),
+     lambda V, r: (r.standard_normal(V) * 2).astype(F32), 0.42),
+    ("neg_scores_penalty", 900, dict(top_k=100, top_p=0.95, temp=0.8, repeat_penalty=1.7),
+     lambda V, r: (r.standard_normal(V) - 20).astype(F32), 0.77),
+    ("subnormal_probs", 400, dict(top_k=0, top_p=1.0, temp=1.0, repeat_penalty=1.0),
+     lambda V, r: np.concatenate([[0.0], np.full(V - 1, -95.0)]).astype(F32), 0.999),
+    ("huge_spread", 2048, dict(top_k=0, top_p=0.999, temp=0.5, repeat_penalty=1.0),
+     lambda V, r: (r.standard_normal(V) * 40).astype(F32), 0.5),
+]
+
+
+@pytest.mark.parametrize("case", EDGE_CASES, ids=[c[0] for c in EDGE_CASES])
+def test_edge_cases(cbx, torch_cuda, case):
+    name, V, p, build, u = case
+    rng = np.random.default_rng(abs(hash(name)) % 2**32)
+    pd = dict(min_p=0.0, cfg_weight=0.0)
+    pd.update(p)
+    x = build(V, rng)[None, :]
+    hist = rng.integers(-5, V + 5, size=(1, 64)).astype(np.int32)
+    hl = np.array([64], np.int32)
+    uu = np.array([u])
+    say(f"edge {name} V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, [pd], uu, hist, hl)
+    tr, ir, pr = oracle_rows(x, [pd], uu, hist, hl)
+    parity.compare(f"edge_{name}", tg, ig, tr, ir, uu, pg, pr)
+    # the single-row host API gives the same answer
+    mod, s = cbx
+    tok, info = s.sample_row(x[0], hist[0], pd, u)
+    assert tok == tr[0]
+
+
+def test_row_api_extensions(cbx, torch_cuda):
+    """cbx_sample_row_ex with CFG, mask, forced stop and probabilities out."""
+    mod, s = cbx
+    w = pkg.workloads()
+    rng = np.random.default_rng(3)
+    V = 8194
+    say("row api extensions")
+    for t in range(30):
+        c = (rng.standard_normal(V) * 3).astype(F32)
+        un = (c + rng.standard_normal(V)).astype(F32)
+        bits = rng.random((1, V)) < 0.5
+        al = w.pack_bitmask(bits)[0]
+        p = dict(top_k=int(rng.integers(0, 2000)), top_p=float(rng.uniform(0.5, 1.0)),
+                 temp=float(rng.uniform(0.3, 1.5)), repeat_penalty=1.2,
+                 min_p=float(rng.choice([0.0, 0.05])), cfg_weight=0.5)
+        h = rng.integers(0, V, size=100)
+        u = float(rng.random())
+        fs = bool(t % 10 == 9)
+        tok, info, probs = s.sample_row(c, h, p, u, logits_uncond=un, allowed=al, force_stop=fs,
+                                        stop_token=V - 2, want_probs=True)
+        tr, ir, pr, _ = O.sample_row(c, h, oparams(p), u, uncond=un, allowed=al, force_stop=fs,
+                                     stop_token=V - 2, want_probs=True)
+        parity.compare(f"row_ext_{t}", [tok], [info], [tr], [ir], [u], probs[None], pr[None])
+
+
+def test_golden_fixtures(cbx, torch_cuda):
+    path = os.path.join(os.path.dirname(__file__), "golden", "sampler_cases.npz")
+    g = np.load(path)
+    n = g["logits"].shape[0]
+    say(f"golden fixtures ({n} rows)")
+    plist = [dict(zip(("top_k", "top_p", "temp", "repeat_penalty", "min_p", "cfg_weight"),
+                      (int(r[0]),) + tuple(float(v) for v in r[1:]))) for r in g["params"]]
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, g["logits"], plist, g["u"], g["history"],
+                           g["hist_len"], allowed=g["allowed"])
+    parity.compare("golden", tg, ig, g["tokens"], g["info"], g["u"], pg, g["probs"])
