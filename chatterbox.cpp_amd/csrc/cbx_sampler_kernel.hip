@@ -394,7 +394,8 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
     }
 
     // ---- repetition penalty (main.cpp:774-781) from a bitmap of the history ----
-    const int hlen = a.history ? a.history_len[row] : 0;
+    // a history longer than its row stride is read only up to the stride
+    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
     const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
     if (use_pen) {
         const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
