@@ -122,6 +122,9 @@ def main():
                     help="also time this many steps issued one launch per step (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after timing, run a plain device copy of this many MiB (3 times) so "
+                         "a counter run can scale FETCH_SIZE / WRITE_SIZE by known bytes")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -202,6 +205,15 @@ def main():
         torch.cuda.synchronize()
         ms = a.elapsed_time(b) / args.single_launch_steps
         single = {"ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1)}
+
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     parity = None
