@@ -99,6 +99,13 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise FileNotFoundError(
             f"{path} is not built; run `make -C chatterbox.cpp_amd` (or __graft_entry__.build())")
+    # Load torch's HIP runtime first when torch is present, so the library
+    # binds to the same runtime instance (same devices, streams and memory)
+    # instead of loading a second copy of libamdhip64 into the process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     vp, i32, i64, u64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
     lib.cbx_max_vocab.restype = i32

@@ -40,7 +40,7 @@ struct Exp2Table {
 };
 
 #if defined(__HIPCC__)
-__device__ __constant__ const Exp2Table kExp2TabDev = {{
+static __device__ __constant__ const Exp2Table kExp2TabDev = {{
 #else
 static const Exp2Table kExp2TabHost = {{
 #endif
@@ -122,5 +122,44 @@ CBX_HD float expf_libm(float x) {
     y = y * s;
     return (float)y;
 }
+
+// The same function without branches: the main path runs on an argument
+// replaced by 0 where a special case applies, and the special value is
+// selected afterwards.  `tab` points at the 32 table words (on the device an
+// LDS copy, so the lookup is a local read).  Bit-identical to expf_libm for
+// every input (checked exhaustively on the host).
+CBX_HD float expf_libm_branchless(float x, const uint64_t* tab) {
+    using namespace expf_detail;
+    const uint32_t ux = f2u(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    const bool minus_inf = ux == 0xff800000u;
+    const bool inf_nan = abstop >= (0x7f800000u >> 20);
+    const bool over = x > 0x1.62e42ep6f;
+    const bool under = x < -0x1.9fe368p6f;
+    const bool special = minus_inf || inf_nan || over || under;
+    const double xd = (double)(special ? 0.0f : x);
+    double kd = fma64(kInvLn2N, xd, kShift);
+    const uint64_t ki = d2u(kd);
+    kd -= kShift;
+    const double r = fma64(kInvLn2N, xd, -kd);
+    uint64_t t = tab[ki % 32];
+    t += ki << (52 - 5);
+    const double s = u2d(t);
+    const double z = fma64(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = fma64(kC2, r, 1.0);
+    y = fma64(z, r2, y);
+    y = y * s;
+    const float main = (float)y;
+    const float sp = minus_inf ? 0.0f
+                   : inf_nan   ? x + x
+                   : over      ? __builtin_huge_valf()
+                               : 0.0f;
+    return special ? sp : main;
+}
+
+#if !defined(__HIPCC__)
+inline float expf_libm_branchless(float x) { return expf_libm_branchless(x, kExp2TabHost.t); }
+#endif
 
 }  // namespace cbx

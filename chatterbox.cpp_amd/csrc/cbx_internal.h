@@ -42,6 +42,12 @@ size_t lds_bytes_for(int32_t cap, int32_t n_vocab);
 
 // Launch the sampler over n_steps * n_rows rows.  Returns a hipError_t.
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream);
+// One vocabulary class each (lanes x scores per lane), used by launch_sample.
+hipError_t launch_v256x16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v256x26(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v256x32(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v1024x16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v1024x32(const KernelArgs& a, hipStream_t stream);
 
 hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream);
 hipError_t launch_debug_philox(uint64_t seed, const uint64_t* stream_ids, uint64_t step,

@@ -1,0 +1,1180 @@
+// cbx_sampler_impl.h -- gfx950 kernels for the T3 logits->token sampler
+// (templates; each cbx_sampler_v*.hip instantiates one vocabulary class so
+// the variants compile in parallel).
+//
+// One workgroup samples one (step, stream) row; a launch covers
+// n_steps x n_rows rows.  The row's scores arrive in registers (EPT per lane,
+// element i = j*BLOCK + tid, so every global load and store is coalesced).
+// Stage order and arithmetic follow sample_next_token_ex (src/main.cpp:726-801):
+//
+//   load + CFG combine + masks + temperature   (main.cpp:733-738)
+//   top-k (main.cpp:740-748): the (k+1)-th largest score is found by one
+//          histogram over value bins spanning [min, max] -- a monotone map, so
+//          the bin holding rank k is exact -- and an exact selection among
+//          the few scores in that bin; rows with non-finite scores use a
+//          12+12+8-bit radix select instead.  Then the -1e-10f nudge.
+//   fast path (<= 2048 survivors): the survivors move to a register list;
+//          top-p sorts it with a bitonic network (lane shuffles in a wave,
+//          LDS across waves), min-p and the penalty work on the list
+//   general path (more survivors): scores stay per element, top-p sorts
+//          (score, id) pairs in LDS
+//   top-p (main.cpp:750-772), min-p [extension], repetition penalty from an
+//          LDS bitmap of the history (main.cpp:774-781), softmax with the
+//          binary32 running sum in id order (main.cpp:783-793), greedy argmax
+//          or the libstdc++ discrete_distribution CDF (main.cpp:795-800;
+//          random.tcc:2657-2712)
+//
+// Exactness.  The binary32 running sums are evaluated in the reference's order
+// by one wave: 64 terms per load, then a chain of dependent IEEE adds reading
+// each lane's term (v_readlane), so every partial sum is the reference's.
+// The binary64 CDF is located in parallel with a certified margin: the
+// parallel cumulative values differ from the reference's sequential ones by
+// < 1.5e-11, so when the uniform lies more than 1e-9 from both neighbouring
+// boundaries the token is the reference's; otherwise (about 4e-9 of draws)
+// one lane replays the reference's sequential CDF exactly.
+// Arithmetic uses explicitly rounded intrinsics (__fadd_rn, ...), and the
+// library is built with -ffp-contract=off as well.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "cbx_expf.h"
+#include "cbx_internal.h"
+#include "cbx_philox.h"
+
+namespace cbx {
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+constexpr int kFastMax = 2048;    // survivors handled on the register-list path
+constexpr int kValueBins = 2048;  // value histogram of the top-k select
+constexpr int kCandMax = 512;     // scores in the selected bin
+constexpr int kRadixBins = 4096;  // 12-bit digits of the fallback radix select
+constexpr double kCdfMargin = 1e-9;
+// Word 3 of a raw buffer resource on gfx9-family parts (data format 32-bit,
+// no swizzle): loads past num_records return 0.
+constexpr int kBufferWord3 = 0x00020000;
+
+// ---------------------------------------------------------------- helpers
+
+// Monotone map float -> uint32 (ascending float order = ascending key).
+__device__ __forceinline__ uint32_t okey(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f);
+    return b ^ ((b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
+}
+__device__ __forceinline__ float okey_inv(uint32_t k) {
+    const uint32_t b = k ^ ((k & 0x80000000u) ? 0x80000000u : 0xFFFFFFFFu);
+    return __builtin_bit_cast(float, b);
+}
+// Composite sort key: ascending order = descending score, then ascending id.
+__device__ __forceinline__ uint64_t desc_key(float s, uint32_t idx) {
+    return ((uint64_t)(~okey(s)) << 32) | idx;
+}
+__device__ __forceinline__ float desc_key_value(uint64_t k) { return okey_inv(~(uint32_t)(k >> 32)); }
+
+// Values that are the same in every lane, kept in scalar registers so that
+// the branches they control are scalar branches.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float unif(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(x, o, 64);
+        if (lane >= o) x += t;
+    }
+    return x;
+}
+__device__ __forceinline__ double wave_incl_scan_f64(double x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(x, o, 64);
+        if (lane >= o) x = __dadd_rn(x, t);
+    }
+    return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ float wave_min(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_min_i(int x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ int wave_or_i(int x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x |= __shfl_xor(x, o, 64);
+    return x;
+}
+
+struct Shared {
+    int red_i[16];
+    float red_f[16];
+    float red_f2[16];
+    double red_d[16];
+    uint32_t sel_digit, sel_above;
+    int bin, above_bins, n_cand, above;
+    float thr;
+    float psum;        // broadcast of a running sum
+    float mx;          // broadcast of the top survivor score
+    int n_kept;        // survivors after top-p
+    int token;
+    double cdf_lo, cdf_hi;
+    float tie[2];      // scores at the top-p cutoff and just after it
+    uint32_t flags;
+};
+
+// Exclusive block scan of one int per lane; `total` receives the block sum.
+template <int BLOCK>
+__device__ __forceinline__ int block_excl_scan(int v, Shared& sh, int& total) {
+    constexpr int NW = BLOCK / 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int incl = wave_incl_scan(v, lane);
+    if (lane == 63) sh.red_i[wid] = incl;
+    __syncthreads();
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const int t = sh.red_i[w];
+        before += (w < wid) ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    total = uni(tot);
+    return before + incl - v;
+}
+
+template <int BLOCK>
+__device__ __forceinline__ int block_sum(int v, Shared& sh) {
+    int total;
+    (void)block_excl_scan<BLOCK>(v, sh, total);
+    return total;
+}
+
+// Exclusive block scan of one double per lane (approximate: any order).
+template <int BLOCK>
+__device__ __forceinline__ double block_excl_scan_f64(double v, Shared& sh, double& total) {
+    constexpr int NW = BLOCK / 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const double incl = wave_incl_scan_f64(v, lane);
+    if (lane == 63) sh.red_d[wid] = incl;
+    __syncthreads();
+    double before = 0.0, tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const double t = sh.red_d[w];
+        if (w < wid) before = __dadd_rn(before, t);
+        tot = __dadd_rn(tot, t);
+    }
+    __syncthreads();
+    total = tot;
+    return __dsub_rn(__dadd_rn(before, incl), v);
+}
+
+template <int BLOCK>
+__device__ __forceinline__ float block_max(float v, Shared& sh) {
+    constexpr int NW = BLOCK / 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_max(v);
+    if (lane == 0) sh.red_f[wid] = v;
+    __syncthreads();
+    float m = sh.red_f[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, sh.red_f[w]);
+    __syncthreads();
+    return unif(m);
+}
+
+template <int BLOCK>
+__device__ __forceinline__ int block_min_i(int v, Shared& sh) {
+    constexpr int NW = BLOCK / 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_min_i(v);
+    if (lane == 0) sh.red_i[wid] = v;
+    __syncthreads();
+    int m = sh.red_i[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = min(m, sh.red_i[w]);
+    __syncthreads();
+    return uni(m);
+}
+
+// min and max of the finite scores and whether any score is NaN / +inf.
+template <int BLOCK>
+__device__ __forceinline__ void block_minmax(float lo, float hi, int bad, Shared& sh, float& blo,
+                                             float& bhi, int& bbad) {
+    constexpr int NW = BLOCK / 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    bad = wave_or_i(bad);
+    if (lane == 0) { sh.red_f[wid] = lo; sh.red_f2[wid] = hi; sh.red_i[wid] = bad; }
+    __syncthreads();
+    float l = sh.red_f[0], h = sh.red_f2[0];
+    int b = sh.red_i[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        l = fminf(l, sh.red_f[w]);
+        h = fmaxf(h, sh.red_f2[w]);
+        b |= sh.red_i[w];
+    }
+    __syncthreads();
+    blo = unif(l);
+    bhi = unif(h);
+    bbad = uni(b);
+}
+
+// --------------------------------------------------------- top-k selection
+
+// One radix-select pass over BITS bits at SHIFT of the keys matching `prefix`
+// under `pmask`; finds the digit holding the element with `rem` larger
+// matching keys (descending) and narrows prefix / pmask / rem.
+template <int BLOCK, int EPT, int SHIFT, int BITS>
+__device__ __forceinline__ void radix_pass(const float (&s)[EPT], int n_valid, uint32_t& prefix,
+                                           uint32_t& pmask, uint32_t& rem, uint32_t* hist,
+                                           Shared& sh) {
+    constexpr int NB = 1 << BITS;
+    constexpr int BPT = NB >= BLOCK ? NB / BLOCK : 1;  // bins per lane
+    constexpr int NT = NB / BPT;                        // lanes holding bins
+    const int tid = threadIdx.x;
+    for (int i = tid; i < NB; i += BLOCK) hist[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = j * BLOCK + tid;
+        const uint32_t k = okey(s[j]);
+        if (i < n_valid && (k & pmask) == prefix) atomicAdd(&hist[(k >> SHIFT) & (NB - 1)], 1u);
+    }
+    __syncthreads();
+    uint32_t c[BPT];
+    int tot = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        c[q] = (tid < NT) ? hist[NB - 1 - (tid * BPT + q)] : 0u;
+        tot += (int)c[q];
+    }
+    int all;
+    uint32_t excl = (uint32_t)block_excl_scan<BLOCK>(tot, sh, all);
+    if (tid < NT && excl <= rem && rem < excl + (uint32_t)tot) {
+#pragma unroll
+        for (int q = 0; q < BPT; ++q) {
+            if (excl + c[q] > rem) {
+                sh.sel_digit = (uint32_t)(NB - 1 - (tid * BPT + q));
+                sh.sel_above = excl;
+                break;
+            }
+            excl += c[q];
+        }
+    }
+    __syncthreads();
+    prefix |= (uint32_t)uni((int)sh.sel_digit) << SHIFT;
+    pmask |= (uint32_t)(NB - 1) << SHIFT;
+    rem -= (uint32_t)uni((int)sh.sel_above);
+    __syncthreads();
+}
+
+// The (rank+1)-th largest key among the first n_valid elements (rank 0-based).
+template <int BLOCK, int EPT>
+__device__ __forceinline__ uint32_t radix_select_desc(const float (&s)[EPT], int n_valid, int rank,
+                                      uint32_t* hist, Shared& sh) {
+    uint32_t prefix = 0, pmask = 0, rem = (uint32_t)rank;
+    radix_pass<BLOCK, EPT, 20, 12>(s, n_valid, prefix, pmask, rem, hist, sh);
+    radix_pass<BLOCK, EPT, 8, 12>(s, n_valid, prefix, pmask, rem, hist, sh);
+    radix_pass<BLOCK, EPT, 0, 8>(s, n_valid, prefix, pmask, rem, hist, sh);
+    return prefix;
+}
+
+// Top-k threshold by value bins.  bin(v) = min(NB-1, int((v - lo) * scale))
+// is non-decreasing in v (each rounded operation is monotone), so every
+// score in a higher bin is strictly larger than every score in a lower one:
+// the bin holding rank k is found from the histogram and the threshold is the
+// exact (rem+1)-th largest among that bin's scores.  Returns false (the
+// caller falls back to the radix select) when the bin width is not a finite
+// positive number or the bin holds more than kCandMax scores.  On success thr
+// is the (k+1)-th largest score (-inf when at most k scores are finite) and
+// `above` the number of scores strictly larger.
+template <int BLOCK, int EPT>
+__device__ __forceinline__ bool topk_value_bins(const float (&s)[EPT], int k, float lo, float hi, uint32_t* hist,
+                                float* cand, Shared& sh, float& thr, int& above) {
+    constexpr int NB = kValueBins;
+    constexpr int BPT = NB / BLOCK >= 1 ? NB / BLOCK : 1;
+    constexpr int NT = NB / BPT;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const float scale = __fdiv_rn((float)NB, __fsub_rn(hi, lo));
+    if (!(scale < kPosInf) || !(scale > 0.0f)) return false;
+    for (int i = tid; i < NB; i += BLOCK) hist[i] = 0u;
+    if (tid == 0) sh.n_cand = 0;
+    __syncthreads();
+    // bin of a score (recomputed where needed rather than held per element)
+    auto bin_of = [&](float v) { return min(NB - 1, (int)__fmul_rn(__fsub_rn(v, lo), scale)); };
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (s[j] != kNegInf) atomicAdd(&hist[bin_of(s[j])], 1u);
+    __syncthreads();
+    // bins in descending order: lane t owns NB-1-t*BPT .. NB-BPT-t*BPT
+    uint32_t c[BPT];
+    int tot = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        c[q] = (tid < NT) ? hist[NB - 1 - (tid * BPT + q)] : 0u;
+        tot += (int)c[q];
+    }
+    int n_fin;
+    int excl = block_excl_scan<BLOCK>(tot, sh, n_fin);
+    if (n_fin <= k) {  // the (k+1)-th largest is -inf: nothing is removed
+        thr = kNegInf;
+        above = n_fin;
+        return true;
+    }
+    if (tid < NT && excl <= k && k < excl + tot) {
+#pragma unroll
+        for (int q = 0; q < BPT; ++q) {
+            if (excl + (int)c[q] > k) {
+                sh.bin = NB - 1 - (tid * BPT + q);
+                sh.above_bins = excl;
+                break;
+            }
+            excl += (int)c[q];
+        }
+    }
+    __syncthreads();
+    const int bsel = uni(sh.bin);
+    const int above_bins = uni(sh.above_bins);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        if (s[j] != kNegInf && bin_of(s[j]) == bsel) {
+            const int at = atomicAdd(&sh.n_cand, 1);
+            if (at < kCandMax) cand[at] = s[j];
+        }
+    }
+    __syncthreads();
+    const int n_c = uni(sh.n_cand);
+    if (n_c > kCandMax) return false;
+    const int rem = k - above_bins;  // 0 <= rem < n_c
+    if (wid == 0) {
+        for (int c0 = lane; c0 < n_c; c0 += 64) {
+            const float v = cand[c0];
+            int gt = 0, ge = 0;
+            for (int t = 0; t < n_c; ++t) {
+                const float w = cand[t];
+                gt += (w > v) ? 1 : 0;
+                ge += (w >= v) ? 1 : 0;
+            }
+            if (gt <= rem && rem < ge) {  // equal candidates all write the same
+                sh.thr = v;
+                sh.above = above_bins + gt;
+            }
+        }
+    }
+    __syncthreads();
+    thr = unif(sh.thr);
+    above = uni(sh.above);
+    return true;
+}
+
+// ------------------------------------------------------------------ sorting
+
+// Value of lane (lane ^ J) of the wave, J < 64: DPP quad permutes for J = 1, 2,
+// ds_swizzle (xor mode, within 32 lanes) for J = 4..16, ds_bpermute for 32.
+template <int J>
+__device__ __forceinline__ uint32_t xlane(uint32_t v) {
+    if constexpr (J == 1) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (J == 2) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (J < 32) {
+        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (J << 10));
+    } else {
+        return (uint32_t)__builtin_amdgcn_ds_bpermute((int)(((threadIdx.x & 63) ^ 32) << 2), (int)v);
+    }
+}
+template <int J>
+__device__ __forceinline__ uint64_t xlane64(uint64_t v) {
+    return ((uint64_t)xlane<J>((uint32_t)(v >> 32)) << 32) | xlane<J>((uint32_t)v);
+}
+
+// One stage (block size K, partner distance J) of an ascending bitonic
+// network over NR*BLOCK keys held at positions r*BLOCK + tid.
+template <int BLOCK, int NR, int K, int J>
+__device__ __forceinline__ void bitonic_stage(uint64_t (&x)[NR], uint64_t* xbuf) {
+    const int tid = threadIdx.x;
+    if constexpr (J >= BLOCK) {  // partner in the same lane, another row
+        constexpr int JR = J / BLOCK;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if ((r & JR) == 0) {
+                const int i = r * BLOCK + tid;
+                const bool up = (i & K) == 0;
+                const uint64_t p = x[r], q = x[r | JR];
+                const bool sw = (p > q) == up;
+                x[r] = sw ? q : p;
+                x[r | JR] = sw ? p : q;
+            }
+        }
+    } else if constexpr (J >= 64) {  // partner in another wave: through LDS
+#pragma unroll
+        for (int r = 0; r < NR; ++r) xbuf[r * BLOCK + tid] = x[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const uint64_t o = xbuf[r * BLOCK + (tid ^ J)];
+            const int i = r * BLOCK + tid;
+            const bool keep_min = ((i & J) == 0) == ((i & K) == 0);
+            x[r] = keep_min ? (x[r] < o ? x[r] : o) : (x[r] > o ? x[r] : o);
+        }
+        __syncthreads();
+    } else {  // partner in the same wave
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const uint64_t o = xlane64<J>(x[r]);
+            const int i = r * BLOCK + tid;
+            const bool keep_min = ((i & J) == 0) == ((i & K) == 0);
+            x[r] = keep_min ? (x[r] < o ? x[r] : o) : (x[r] > o ? x[r] : o);
+        }
+    }
+}
+
+template <int BLOCK, int NR, int K, int J>
+__device__ __forceinline__ void bitonic_stages_j(uint64_t (&x)[NR], uint64_t* xbuf) {
+    if constexpr (J > 0) {
+        bitonic_stage<BLOCK, NR, K, J>(x, xbuf);
+        bitonic_stages_j<BLOCK, NR, K, J / 2>(x, xbuf);
+    }
+}
+template <int BLOCK, int NR, int K, int N>
+__device__ __forceinline__ void bitonic_stages_k(uint64_t (&x)[NR], uint64_t* xbuf) {
+    if constexpr (K <= N) {
+        bitonic_stages_j<BLOCK, NR, K, K / 2>(x, xbuf);
+        bitonic_stages_k<BLOCK, NR, K * 2, N>(x, xbuf);
+    }
+}
+
+// Ascending bitonic sort of the first N positions (N a power of two, at
+// least 64, at most NR*BLOCK; positions >= N hold the maximum key and stay
+// put), fully unrolled: the network is fixed at compile time.
+template <int BLOCK, int NR, int N>
+__device__ __forceinline__ void sort_static(uint64_t (&x)[NR], uint64_t* xbuf) {
+    bitonic_stages_k<BLOCK, NR, 2, N>(x, xbuf);
+}
+
+// Sort dispatch for a register list of NR rows holding n2 positions
+// (n2 = max(64, pow2ceil(survivors)), the same in every lane).  A 64-key
+// network runs on wave 0 alone.
+template <int BLOCK, int NR>
+__device__ __forceinline__ void sort_list(uint64_t (&x)[NR], int n2, uint64_t* xbuf) {
+    const int wid = threadIdx.x >> 6;
+    if constexpr (NR == 1) {
+        if (n2 == 64) {
+            if (wid == 0) sort_static<BLOCK, 1, 64>(x, xbuf);
+        } else if (n2 == 128) {
+            sort_static<BLOCK, 1, 128>(x, xbuf);
+        } else if (n2 == 256) {
+            sort_static<BLOCK, 1, 256>(x, xbuf);
+        } else if constexpr (BLOCK >= 1024) {
+            if (n2 == 512) sort_static<BLOCK, 1, 512>(x, xbuf);
+            else sort_static<BLOCK, 1, 1024>(x, xbuf);
+        }
+    } else {
+        sort_static<BLOCK, NR, NR * BLOCK>(x, xbuf);
+    }
+}
+
+// Ascending bitonic sort of (key, id) pairs [0, n2) in LDS (large lists).
+template <int BLOCK>
+__device__ __forceinline__ void bitonic_sort_pairs(uint32_t* key, uint16_t* id, int n2) {
+    n2 = uni(n2);
+    for (int k = 2; k <= n2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = threadIdx.x; t < (n2 >> 1); t += BLOCK) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const int p = i + j;
+                const bool up = (i & k) == 0;
+                const uint32_t ka = key[i], kb = key[p];
+                const uint16_t ia = id[i], ib = id[p];
+                const bool a_gt_b = (ka > kb) || (ka == kb && ia > ib);
+                if (a_gt_b == up) { key[i] = kb; key[p] = ka; id[i] = ib; id[p] = ia; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ------------------------------------------------------ reference-order sums
+
+__device__ __forceinline__ float lane_term(int xi, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, l));
+}
+
+// acc + v[0] + ... + v[n-1] in index order, binary32, by one wave: 64 terms
+// per load, then a chain of dependent adds reading each lane's term.
+__device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc) {
+    const int lane = threadIdx.x & 63;
+    n = uni(n);
+    int base = 0;
+    for (; base + 64 <= n; base += 64) {
+        const int xi = __builtin_bit_cast(int, v[base + lane]);
+#pragma unroll
+        for (int l = 0; l < 64; ++l) acc = __fadd_rn(acc, lane_term(xi, l));
+    }
+    if (base < n) {
+        const int xi = __builtin_bit_cast(int, base + lane < n ? v[base + lane] : 0.0f);
+        const int m = n - base;
+        for (int l = 0; l < m; ++l) acc = __fadd_rn(acc, lane_term(xi, l));
+    }
+    return acc;
+}
+
+// First i with (0 + v[0] + ... + v[i]) >= thr (binary32, index order), or
+// n-1 when the running sum never reaches thr.  One wave.  Terms are
+// non-negative, so the running sum never decreases: a 64-term chunk is redone
+// term by term only when its end value reaches thr.
+__device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr) {
+    const int lane = threadIdx.x & 63;
+    n = uni(n);
+    float acc = 0.0f;
+    for (int base = 0; base < n; base += 64) {
+        const int m = min(64, n - base);
+        const int xi = __builtin_bit_cast(int, lane < m ? v[base + lane] : 0.0f);
+        float a = acc;
+#pragma unroll
+        for (int l = 0; l < 64; ++l) a = __fadd_rn(a, lane_term(xi, l));
+        if (a >= thr) {
+            for (int l = 0; l < m; ++l) {
+                acc = __fadd_rn(acc, lane_term(xi, l));
+                if (acc >= thr) return base + l;
+            }
+        }
+        acc = a;
+    }
+    return n - 1;
+}
+
+// --------------------------------------------------------------- bitmaps
+
+__device__ __forceinline__ int pow2ceil(int n) {
+    int p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t* words, int i) {
+    return (words[i >> 5] >> (i & 31)) & 1u;
+}
+
+__device__ __forceinline__ int rank_of(const uint32_t* keptw, const uint32_t* woff, int i) {
+    const uint32_t wb = keptw[i >> 5];
+    return (int)woff[i >> 5] + __popc(wb & ((1u << (i & 31)) - 1u));
+}
+
+// Id of the rank-th set bit of the kept bitmap (ranks from the word offsets).
+__device__ __forceinline__ int id_of_rank(const uint32_t* keptw, const uint32_t* woff, int W, int rank) {
+    int lo = 0, hi = W - 1;  // last word w with woff[w] <= rank
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((int)woff[mid] <= rank) lo = mid; else hi = mid - 1;
+    }
+    uint32_t bits = keptw[lo];
+    for (int k = rank - (int)woff[lo]; k > 0; --k) bits &= bits - 1u;
+    return lo * 32 + __ffs(bits) - 1;
+}
+
+// Exclusive prefix counts of the kept bitmap's words; returns the count.
+template <int BLOCK>
+__device__ __forceinline__ int bitmap_offsets(const uint32_t* keptw, uint32_t* woff, int W, Shared& sh) {
+    constexpr int WPT = (kMaxVocab / 32 + BLOCK - 1) / BLOCK;  // words per lane
+    const int tid = threadIdx.x;
+    int cnt[WPT];
+    int local = 0;
+#pragma unroll
+    for (int q = 0; q < WPT; ++q) {
+        const int w = tid * WPT + q;
+        cnt[q] = (w < W) ? __popc(keptw[w]) : 0;
+        local += cnt[q];
+    }
+    int n;
+    int base = block_excl_scan<BLOCK>(local, sh, n);
+#pragma unroll
+    for (int q = 0; q < WPT; ++q) {
+        const int w = tid * WPT + q;
+        if (w < W) woff[w] = (uint32_t)base;
+        base += cnt[q];
+    }
+    __syncthreads();
+    return n;
+}
+
+// ----------------------------------------------------------------- the draw
+
+// Token for uniform u from the id-ordered probabilities F[0, n) (the kept ids
+// of the bitmap): random.tcc:2665-2676 builds double weights summed from 0.0
+// in id order, divides each by the sum, takes running partial sums and
+// forces the last entry (id V-1) to 1.0; :2708-2712 returns the first id whose
+// cumulative value is >= u.  Ids before the first kept one have cumulative
+// value 0, so u == 0 gives id 0.
+template <int BLOCK>
+__device__ __forceinline__ int draw_token(const float* F, int n, const uint32_t* keptw, const uint32_t* woff,
+                          int W, int V, double u, Shared& sh) {
+    const int tid = threadIdx.x;
+    const bool last_kept = bit_of(keptw, V - 1);
+    // parallel pass over contiguous chunks: unnormalised prefix sums
+    const int C = (n + BLOCK - 1) / BLOCK;
+    const int r0 = min(tid * C, n), r1 = min(r0 + C, n);
+    double part = 0.0;
+    for (int r = r0; r < r1; ++r) part = __dadd_rn(part, (double)F[r]);
+    double total;
+    double cp = block_excl_scan_f64<BLOCK>(part, sh, total);
+    const double target = __dmul_rn(u, total);  // cumulative >= u  <=>  prefix >= u*total
+    int found = 0x7fffffff;
+    double lo = 0.0, hi = 0.0;
+    for (int r = r0; r < r1; ++r) {
+        const double before = cp;
+        cp = __dadd_rn(cp, (double)F[r]);
+        const bool forced = (r == n - 1 && last_kept);
+        if (forced || cp >= target) { found = r; lo = before; hi = forced ? total : cp; break; }
+    }
+    const int rank = block_min_i<BLOCK>(found, sh);
+    if (found == rank && found != 0x7fffffff) { sh.cdf_lo = lo; sh.cdf_hi = hi; }
+    __syncthreads();
+    if (tid == 0) {
+        const double inv = __ddiv_rn(1.0, total);
+        int tok;
+        bool certain;
+        if (!(u > 0.0)) {
+            tok = 0;
+            certain = true;
+        } else if (rank == 0x7fffffff) {
+            tok = V - 1;  // past every computed value: the forced last entry
+            certain = u - __dmul_rn(total, inv) > kCdfMargin;
+        } else {
+            tok = id_of_rank(keptw, woff, W, rank);
+            const bool exact_hi = (rank == n - 1 && last_kept);
+            certain = (rank == 0 || u - __dmul_rn(sh.cdf_lo, inv) > kCdfMargin) &&
+                      (exact_hi || __dmul_rn(sh.cdf_hi, inv) - u >= kCdfMargin);
+        }
+        if (!certain) {
+            // the reference's sequential CDF, exactly (rare)
+            double sum = 0.0;
+            for (int r = 0; r < n; ++r) sum = __dadd_rn(sum, (double)F[r]);
+            double acc = 0.0;
+            int rk = -1;
+            for (int r = 0; r < n; ++r) {
+                acc = __dadd_rn(acc, __ddiv_rn((double)F[r], sum));
+                const double c = (r == n - 1 && last_kept) ? 1.0 : acc;
+                if (c >= u) { rk = r; break; }
+            }
+            tok = rk < 0 ? V - 1 : id_of_rank(keptw, woff, W, rk);
+        }
+        sh.token = tok;
+    }
+    __syncthreads();
+    return uni(sh.token);
+}
+
+// Softmax over the kept entries (val[q], id[q] for bit q of `kept`), then
+// greedy or draw; writes token, info and, if asked, the probability row
+// (element owners read the id-ordered F through the bitmap).  Shared by both
+// paths.
+template <int BLOCK, int EPT, int N>
+__device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], uint64_t kept,
+                           const KernelArgs& a, const cbx_params& P, int64_t rs, int row, int step,
+                           uint32_t flags, uint32_t* keptw, uint32_t* woff, float* F,
+                           const uint64_t* tab, Shared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int V = a.n_vocab;
+    const int W = (V + 31) >> 5;
+    // final kept bitmap and id-order ranks
+    for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < N; ++q)
+        if ((kept >> q) & 1u) atomicOr(&keptw[id[q] >> 5], 1u << (id[q] & 31));
+    __syncthreads();
+    const int n_final = bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+
+    // softmax (main.cpp:783-793)
+    float m = kNegInf;
+#pragma unroll
+    for (int q = 0; q < N; ++q) m = ((kept >> q) & 1u) ? fmaxf(m, val[q]) : m;
+    const float mx2 = block_max<BLOCK>(m, sh);
+#pragma unroll
+    for (int q = 0; q < N; ++q) {
+        if ((kept >> q) & 1u) {
+            val[q] = expf_libm_branchless(__fsub_rn(val[q], mx2), tab);
+            F[rank_of(keptw, woff, id[q])] = val[q];
+        }
+    }
+    __syncthreads();
+    if (wid == 0) {
+        const float ps = wave_chain_sum(F, n_final, 0.0f);
+        if (lane == 0) sh.psum = ps;
+    }
+    __syncthreads();
+    const float psum2 = unif(sh.psum);
+    const bool empty = (psum2 == 0.0f);
+    if (!empty) {
+#pragma unroll
+        for (int q = 0; q < N; ++q) {
+            if ((kept >> q) & 1u) {
+                val[q] = __fdiv_rn(val[q], psum2);
+                F[rank_of(keptw, woff, id[q])] = val[q];
+            }
+        }
+    }
+    __syncthreads();
+
+    // greedy or draw (main.cpp:795-800)
+    int token = 0;
+    if (empty) {
+        flags |= CBX_INFO_EMPTY;
+    } else if (P.temp <= 0.0f) {
+        // first argmax over the full probability vector (zeros elsewhere)
+        float best = -1.0f;
+#pragma unroll
+        for (int q = 0; q < N; ++q) best = ((kept >> q) & 1u) ? fmaxf(best, val[q]) : best;
+        best = block_max<BLOCK>(best, sh);
+        int first = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < N; ++q)
+            first = (((kept >> q) & 1u) && val[q] == best) ? min(first, id[q]) : first;
+        token = block_min_i<BLOCK>(first, sh);
+        if (token == 0x7fffffff) token = 0;  // only NaN probabilities: no maximum
+        flags |= CBX_INFO_GREEDY;
+    } else if (V >= 2) {
+        flags |= CBX_INFO_DREW;
+        double u;
+        if (a.draw_mode == CBX_DRAW_PHILOX) {
+            const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
+            u = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
+        } else {
+            u = a.uniforms[rs];
+        }
+        token = draw_token<BLOCK>(F, n_final, keptw, woff, W, V, u, sh);
+    }
+
+    if (tid == 0) {
+        a.tokens[rs] = token;
+        if (a.info) a.info[rs] = flags | sh.flags;
+    }
+    if (a.probs) {
+        float* prow = a.probs + rs * a.ld_probs;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int i = j * BLOCK + tid;
+            if (i < V) prow[i] = (!empty && bit_of(keptw, i)) ? F[rank_of(keptw, woff, i)] : 0.0f;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ kernel
+
+// The rest of a row whose n_surv <= NR*BLOCK survivors sit in the LDS list
+// xbuf[0, n_surv) as composite keys: each lane holds positions r*BLOCK + tid.
+template <int BLOCK, int EPT, int NR>
+__device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params& P, int64_t rs,
+                                          int row, int step, uint32_t flags, int n_surv,
+                                          bool use_topp, bool use_pen, const uint32_t* seen,
+                                          uint32_t* keptw, uint32_t* woff, uint8_t* region,
+                                          const uint64_t* tab, Shared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    uint64_t* xbuf = reinterpret_cast<uint64_t*>(region);
+    float* E = reinterpret_cast<float*>(region);
+    float* F = reinterpret_cast<float*>(region);
+    const int n2 = uni(max(64, pow2ceil(n_surv)));
+    uint64_t x[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int i = r * BLOCK + tid;
+        x[r] = (i < n_surv) ? xbuf[i] : ~0ull;
+    }
+    __syncthreads();
+    uint64_t kept = 0;  // bit r: list entry r kept
+    float mx_surv = kNegInf;
+    // ---- top-p (main.cpp:750-772) ----
+    if (use_topp) {
+        sort_list<BLOCK, NR>(x, n2, xbuf);
+        if (tid == 0) sh.mx = desc_key_value(x[0]);
+        __syncthreads();
+        mx_surv = unif(sh.mx);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = r * BLOCK + tid;
+            if (i < n_surv)
+                E[i] = expf_libm_branchless(__fsub_rn(desc_key_value(x[r]), mx_surv), tab);
+        }
+        __syncthreads();
+        if (wid == 0) {
+            const float ps = wave_chain_sum(E, n_surv, 0.0f);
+            if (lane == 0) sh.psum = ps;
+        }
+        __syncthreads();
+        const float psum = unif(sh.psum);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = r * BLOCK + tid;
+            if (i < n_surv) E[i] = __fdiv_rn(E[i], psum);
+        }
+        __syncthreads();
+        if (wid == 0) {
+            const int last = wave_chain_cross(E, n_surv, P.top_p);
+            if (lane == 0) sh.n_kept = last + 1;
+        }
+        __syncthreads();
+        const int n_kept = uni(sh.n_kept);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = r * BLOCK + tid;
+            if (i < n_kept) kept |= (uint64_t)1 << r;
+            if (i == n_kept - 1) sh.tie[0] = desc_key_value(x[r]);
+            if (i == n_kept && i < n_surv) sh.tie[1] = desc_key_value(x[r]);
+        }
+        __syncthreads();
+        if (tid == 0 && n_kept < n_surv && sh.tie[0] == sh.tie[1]) sh.flags |= CBX_INFO_TOPP_TIE;
+    } else {
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            if (r * BLOCK + tid < n_surv) kept |= (uint64_t)1 << r;
+    }
+    float val[NR];
+    int id[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        val[r] = desc_key_value(x[r]);
+        id[r] = (int)(uint32_t)x[r];
+    }
+    // ---- min-p [extension]: drop expf(s - s_max) < min_p ----
+    if (P.min_p > 0.0f) {
+        float m = kNegInf;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) m = ((kept >> r) & 1u) ? fmaxf(m, val[r]) : m;
+        const float mx_kept = use_topp ? mx_surv : block_max<BLOCK>(m, sh);
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            if (((kept >> r) & 1u) &&
+                expf_libm_branchless(__fsub_rn(val[r], mx_kept), tab) < P.min_p)
+                kept &= ~((uint64_t)1 << r);
+    }
+    // ---- repetition penalty (main.cpp:774-781), seen bitmap built at load ----
+    if (use_pen) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            if (((kept >> r) & 1u) && bit_of(seen, id[r]))
+                val[r] = val[r] > 0.0f ? __fdiv_rn(val[r], P.repeat_penalty)
+                                       : __fmul_rn(val[r], P.repeat_penalty);
+    }
+    __syncthreads();  // E and xbuf are done with; F takes the region
+    finish_row<BLOCK, EPT, NR>(val, id, kept, a, P, rs, row, step, flags, keptw, woff, F, tab, sh);
+}
+
+// MAXNR: the largest register list (rows per lane) compiled in; GENERAL: the
+// per-element path for more survivors is compiled in (the launch picks the
+// variant from the survivor capacity, so lean variants carry no unused code).
+template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
+__global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
+    __shared__ Shared sh;
+    __shared__ uint64_t tab[32];
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int64_t g = blockIdx.x;
+    const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
+    const int V = a.n_vocab;
+    const int cap = a.cap;
+    const int W = (V + 31) >> 5;
+    const int Wp = (W + 3) & ~3;
+
+    // LDS: seen[Wp] | keptw[Wp] | woff[Wp] | region, whose use changes:
+    //   top-k:        value histogram u32[2048] + candidates f32[512], or the
+    //                 radix histogram u32[4096]
+    //   fast path:    xbuf u64[2048] (list, cross-wave exchanges), then E f32
+    //   general path: key32 u32[cap] | id16 u16[cap], E aliasing key32
+    //   finish:       F f32[n_final]
+    uint32_t* seen = reinterpret_cast<uint32_t*>(smem);
+    uint32_t* keptw = seen + Wp;
+    uint32_t* woff = keptw + Wp;
+    uint8_t* region = reinterpret_cast<uint8_t*>(woff + Wp);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(region);
+    float* cand = reinterpret_cast<float*>(region + kValueBins * 4);
+    uint64_t* xbuf = reinterpret_cast<uint64_t*>(region);
+    float* E = reinterpret_cast<float*>(region);
+    uint32_t* key32 = reinterpret_cast<uint32_t*>(region);
+    uint16_t* id16 = reinterpret_cast<uint16_t*>(key32 + cap);
+    float* F = reinterpret_cast<float*>(region);
+
+    const cbx_params P = a.params[row];
+    const int64_t rs = (int64_t)step * a.n_rows + row;  // row-step linear id
+
+    // ---- load (all loads first), combine, mask, temperature (main.cpp:733-738) ----
+    // Buffer loads bounded by a resource of V*4 bytes: one lane offset, the
+    // j*BLOCK stride in a scalar offset, ids >= V read 0 (masked below).
+    const float* lrow = a.logits + rs * a.ld_logits;
+    float s[EPT];
+    {
+        const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(lrow), (short)0, V * 4, kBufferWord3);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 rl, tid * 4, j * BLOCK * 4, 0));
+    }
+    if (a.uncond) {
+        const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.uncond + rs * a.ld_logits), (short)0, V * 4, kBufferWord3);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const float un = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(ru, tid * 4, j * BLOCK * 4, 0));
+            s[j] = __fadd_rn(s[j], __fmul_rn(P.cfg_weight, __fsub_rn(s[j], un)));
+        }
+    }
+    if (tid < 32) tab[tid] = kExp2TabDev.t[tid];
+    // history ids -> seen bitmap, overlapped with the logit loads in flight
+    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
+    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
+    for (int w = tid; w < W; w += BLOCK) { keptw[w] = 0u; seen[w] = 0u; }
+    if (tid == 0) sh.flags = 0u;
+    __syncthreads();
+    if (use_pen) {
+        const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
+        for (int j = tid; j < hlen; j += BLOCK) {
+            const int32_t t = hrow[j];
+            if (t >= 0 && t < V) atomicOr(&seen[t >> 5], 1u << (t & 31));
+        }
+    }
+    const uint32_t* arow = a.allowed ? a.allowed + (int64_t)row * a.ld_allowed : nullptr;
+    const bool fstop = a.force_stop && a.force_stop[rs];
+    const bool scale = P.temp > 0.0f && P.temp != 1.0f;
+    const float inv_t = __fdiv_rn(1.0f, P.temp);
+    int nonfinite = 0;
+    float lo = kPosInf, hi = kNegInf;
+    // element j of this lane is id j*BLOCK + tid: valid for j < n_mine; its
+    // allowed bit is bit (tid & 31) of word j*BLOCK/32 + tid/32
+    const int n_mine = (V - tid + BLOCK - 1) / BLOCK;
+    __amdgpu_buffer_rsrc_t ra_mask;
+    if (arow)
+        ra_mask = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(arow), (short)0, W * 4,
+                                                    kBufferWord3);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        float v = s[j];
+        bool masked = j >= n_mine;
+        if (arow) {
+            const uint32_t word = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                ra_mask, (tid >> 5) * 4, j * (BLOCK / 32) * 4, 0);
+            masked = masked || !((word >> (tid & 31)) & 1u);
+        }
+        if (fstop) masked = masked || (j * BLOCK + tid) != a.stop_token;
+        v = masked ? kNegInf : v;
+        if (scale) v = __fmul_rn(v, inv_t);
+        nonfinite |= (v != v || v == kPosInf) ? 1 : 0;
+        lo = (v != kNegInf) ? fminf(lo, v) : lo;
+        hi = (v != kNegInf) ? fmaxf(hi, v) : hi;
+        s[j] = v;
+    }
+    int bad;
+    block_minmax<BLOCK>(lo, hi, nonfinite, sh, lo, hi, bad);
+    const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
+
+    // ---- top-k (main.cpp:740-748) ----
+    const bool use_topk = P.top_k > 0 && P.top_k < V;
+    if (use_topk) {
+        float thr;
+        int above;
+        if (bad || !(hi > lo) ||
+            !topk_value_bins<BLOCK, EPT>(s, P.top_k, lo, hi, hist, cand, sh, thr, above)) {
+            thr = okey_inv(radix_select_desc<BLOCK, EPT>(s, V, P.top_k, hist, sh));
+            int n_above = 0;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) n_above += (s[j] > thr) ? 1 : 0;
+            above = block_sum<BLOCK>(n_above, sh);
+        }
+        if (above < P.top_k) thr = __fsub_rn(thr, 1e-10f);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) s[j] = (s[j] <= thr) ? kNegInf : s[j];
+    }
+
+    // ---- survivors (score != -inf): count and compaction offsets ----
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) mine += (s[j] != kNegInf) ? 1 : 0;
+    int n_surv;
+    int off = block_excl_scan<BLOCK>(mine, sh, n_surv);
+    if (n_surv > cap) {
+        if (tid == 0) {
+            a.tokens[rs] = -1;
+            if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
+        }
+        if (a.probs) {
+            float* prow = a.probs + rs * a.ld_probs;
+            for (int i = tid; i < V; i += BLOCK) prow[i] = 0.0f;
+        }
+        return;
+    }
+    const bool use_topp = P.top_p < 1.0f && n_surv > 0;
+
+    if (n_surv <= MAXNR * BLOCK) {
+        // ================= fast path: survivors in a register list =================
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (s[j] != kNegInf) xbuf[off++] = desc_key(s[j], (uint32_t)(j * BLOCK + tid));
+        __syncthreads();
+        const int rows_needed = uni((max(64, pow2ceil(n_surv)) + BLOCK - 1) / BLOCK);
+        if (rows_needed <= 1) {
+            fast_path<BLOCK, EPT, 1>(a, P, rs, row, step, flags, n_surv, use_topp, use_pen, seen,
+                                     keptw, woff, region, tab, sh);
+        } else if constexpr (MAXNR >= 2) {
+            if (rows_needed == 2) {
+                fast_path<BLOCK, EPT, 2>(a, P, rs, row, step, flags, n_surv, use_topp, use_pen,
+                                         seen, keptw, woff, region, tab, sh);
+            } else if constexpr (MAXNR >= 4) {
+                if (rows_needed <= 4) {
+                    fast_path<BLOCK, EPT, 4>(a, P, rs, row, step, flags, n_surv, use_topp,
+                                             use_pen, seen, keptw, woff, region, tab, sh);
+                } else if constexpr (MAXNR >= 8) {
+                    fast_path<BLOCK, EPT, 8>(a, P, rs, row, step, flags, n_surv, use_topp,
+                                             use_pen, seen, keptw, woff, region, tab, sh);
+                }
+            }
+        }
+        return;
+    }
+    if constexpr (!GENERAL) {
+        return;  // unreachable: the launch capacity never exceeds MAXNR*BLOCK here
+    } else {
+    // ================= general path: scores per element =================
+    // ---- top-p (main.cpp:750-772) ----
+    if (use_topp) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            if (s[j] != kNegInf) {
+                key32[off] = ~okey(s[j]);
+                id16[off] = (uint16_t)(j * BLOCK + tid);
+                ++off;
+            }
+        }
+        const int n2 = uni(max(64, pow2ceil(n_surv)));
+        for (int i = n_surv + tid; i < n2; i += BLOCK) { key32[i] = 0xFFFFFFFFu; id16[i] = 0xFFFFu; }
+        __syncthreads();
+        bitonic_sort_pairs<BLOCK>(key32, id16, n2);
+        const float mx_surv = unif(okey_inv(~key32[0]));
+        __syncthreads();
+        for (int i = tid; i < n_surv; i += BLOCK)
+            E[i] = expf_libm_branchless(__fsub_rn(okey_inv(~key32[i]), mx_surv), tab);
+        __syncthreads();
+        if (wid == 0) {
+            const float ps = wave_chain_sum(E, n_surv, 0.0f);
+            if (lane == 0) sh.psum = ps;
+        }
+        __syncthreads();
+        const float psum = unif(sh.psum);
+        for (int i = tid; i < n_surv; i += BLOCK) E[i] = __fdiv_rn(E[i], psum);
+        __syncthreads();
+        if (wid == 0) {
+            const int last = wave_chain_cross(E, n_surv, P.top_p);
+            if (lane == 0) sh.n_kept = last + 1;
+        }
+        __syncthreads();
+        const int n_kept = uni(sh.n_kept);
+        for (int i = tid; i < n_kept; i += BLOCK) {
+            const uint32_t idx = id16[i];
+            atomicOr(&keptw[idx >> 5], 1u << (idx & 31));
+        }
+        // equal scores straddling the cutoff: read both ids' scores back
+        if (n_kept < n_surv) {
+            const int ia = id16[n_kept - 1], ib = id16[n_kept];
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                const int i = j * BLOCK + tid;
+                if (i == ia) sh.tie[0] = s[j];
+                if (i == ib) sh.tie[1] = s[j];
+            }
+        }
+        if (tid == 0) sh.mx = mx_surv;  // min-p reference: the best survivor
+        __syncthreads();
+        if (tid == 0 && n_kept < n_surv && sh.tie[0] == sh.tie[1]) sh.flags |= CBX_INFO_TOPP_TIE;
+    }
+
+    // kept predicate per register element
+    uint64_t kept = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = j * BLOCK + tid;
+        const bool k = s[j] != kNegInf && (!use_topp || bit_of(keptw, i));
+        kept |= (uint64_t)k << j;
+    }
+
+    // ---- min-p [extension]: drop expf(s - s_max) < min_p ----
+    if (P.min_p > 0.0f) {
+        float m = kNegInf;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) m = ((kept >> j) & 1u) ? fmaxf(m, s[j]) : m;
+        const float mx_kept = use_topp ? unif(sh.mx) : block_max<BLOCK>(m, sh);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (((kept >> j) & 1u) && expf_libm_branchless(__fsub_rn(s[j], mx_kept), tab) < P.min_p)
+                kept &= ~((uint64_t)1 << j);
+    }
+
+    // ---- repetition penalty (main.cpp:774-781), seen bitmap built at load ----
+    if (use_pen) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int i = j * BLOCK + tid;
+            if (((kept >> j) & 1u) && bit_of(seen, i))
+                s[j] = s[j] > 0.0f ? __fdiv_rn(s[j], P.repeat_penalty)
+                                   : __fmul_rn(s[j], P.repeat_penalty);
+        }
+    }
+    __syncthreads();  // every read of the top-p bitmap and lists is done
+    int id[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) id[j] = j * BLOCK + tid;
+    finish_row<BLOCK, EPT, EPT>(s, id, kept, a, P, rs, row, step, flags, keptw, woff, F, tab, sh);
+    }
+}
+
+template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
+hipError_t launch_cfg(const KernelArgs& a, hipStream_t stream) {
+    const size_t lds = lds_bytes_for(a.cap, a.n_vocab);
+    // Dynamic LDS beyond 64 KiB has to be granted per kernel; remember the
+    // largest grant so repeated launches skip the call.
+    static size_t granted = 64 * 1024 - sizeof(Shared) - 256;
+    if (lds > granted) {
+        hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&sample_rows_kernel<BLOCK, EPT, MAXNR, GENERAL>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        granted = lds;
+    }
+    const int64_t rows = (int64_t)a.n_steps * a.n_rows;
+    hipLaunchKernelGGL((sample_rows_kernel<BLOCK, EPT, MAXNR, GENERAL>), dim3((unsigned)rows),
+                       dim3(BLOCK), lds, stream, a);
+    return hipGetLastError();
+}
+
+// Variant by survivor capacity: the smallest register list that holds `cap`
+// survivors, or the full kernel when cap exceeds the register lists.
+template <int BLOCK, int EPT>
+hipError_t launch_for(const KernelArgs& a, hipStream_t stream) {
+    if (a.cap <= BLOCK) return launch_cfg<BLOCK, EPT, 1, false>(a, stream);
+    if constexpr (4 * BLOCK <= kFastMax) {
+        if (a.cap <= 4 * BLOCK) return launch_cfg<BLOCK, EPT, 4, false>(a, stream);
+        if (a.cap <= kFastMax) return launch_cfg<BLOCK, EPT, 8, false>(a, stream);
+        return launch_cfg<BLOCK, EPT, 8, true>(a, stream);
+    } else {
+        if (a.cap <= kFastMax) return launch_cfg<BLOCK, EPT, kFastMax / BLOCK, false>(a, stream);
+        return launch_cfg<BLOCK, EPT, kFastMax / BLOCK, true>(a, stream);
+    }
+}
+
+}  // namespace
+}  // namespace cbx

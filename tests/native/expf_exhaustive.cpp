@@ -1,5 +1,6 @@
 // Compares the restated expf (chatterbox.cpp_amd/csrc/cbx_expf.h, compiled
-// here as host code) with the host libm expf over every binary32 bit pattern
+// here as host code, both the branching and the branch-free form) with the
+// host libm expf over every binary32 bit pattern
 // in [lo_bits, hi_bits).  Prints "<mismatches> <count>" and the first few
 // mismatching inputs.  usage: expf_exhaustive lo_bits hi_bits n_threads
 #include <cmath>
@@ -27,10 +28,12 @@ int main(int argc, char** argv) {
                 float x;
                 std::memcpy(&x, &bits, 4);
                 const float r = std::exp(x), m = cbx::expf_libm(x);
-                uint32_t rb, mb;
+                const float b = cbx::expf_libm_branchless(x);
+                uint32_t rb, mb, bb;
                 std::memcpy(&rb, &r, 4);
                 std::memcpy(&mb, &m, 4);
-                if (rb != mb) {
+                std::memcpy(&bb, &b, 4);
+                if (rb != mb || rb != bb) {
                     if (!bad[t]) first[t] = bits;
                     ++bad[t];
                 }
