@@ -127,6 +127,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_debug_expf.argtypes = [vp, vp, vp, i64, vp]
     lib.cbx_debug_philox.restype = ctypes.c_int
     lib.cbx_debug_philox.argtypes = [vp, u64, vp, u64, i32, vp, vp]
+    lib.cbx_debug_seqsum.restype = ctypes.c_int
+    lib.cbx_debug_seqsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
     lib.cbx_last_error.restype = ctypes.c_char_p
     lib.cbx_last_error.argtypes = []
     _lib = lib
@@ -249,6 +251,12 @@ class Sampler:
     def debug_expf(self, x, out):
         _check(self.lib.cbx_debug_expf(self.handle, x.data_ptr(), out.data_ptr(), x.numel(),
                                        _stream_ptr()))
+
+    def debug_seqsum(self, terms, offsets, thr, sums, hits):
+        _check(self.lib.cbx_debug_seqsum(self.handle, terms.data_ptr(), offsets.data_ptr(),
+                                         None if thr is None else thr.data_ptr(),
+                                         offsets.numel() - 1, sums.data_ptr(), hits.data_ptr(),
+                                         _stream_ptr()))
 
     def debug_philox(self, seed, stream_ids, step, n, out):
         _check(self.lib.cbx_debug_philox(self.handle, seed,

@@ -34,6 +34,10 @@ struct KernelArgs {
 };
 
 constexpr int32_t kMaxVocab = 32768;
+// Survivors after top-k that the one-wave kernel holds; launches whose
+// capacity is at most this (and V <= kWaveMaxVocab) use it.
+constexpr int32_t kWaveCap = 1024;
+constexpr int32_t kWaveMaxVocab = 256 * 33;
 
 // Largest survivor capacity whose lists fit `lds_bytes` of LDS for n_vocab.
 int32_t max_cap_for_lds(int32_t n_vocab, size_t lds_bytes);
@@ -43,6 +47,10 @@ size_t lds_bytes_for(int32_t cap, int32_t n_vocab);
 // Launch the sampler over n_steps * n_rows rows.  Returns a hipError_t.
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream);
 // One vocabulary class each (lanes x scores per lane), used by launch_sample.
+// One-wave kernels, scores per lane 4*Q (V <= 256*Q).
+hipError_t launch_w16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_w26(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_w33(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x26(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x32(const KernelArgs& a, hipStream_t stream);
@@ -50,6 +58,8 @@ hipError_t launch_v1024x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v1024x32(const KernelArgs& a, hipStream_t stream);
 
 hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream);
+hipError_t launch_debug_seqsum(const float* terms, const int32_t* offsets, const float* thr,
+                              int32_t n_cases, float* sum, int32_t* hit, hipStream_t stream);
 hipError_t launch_debug_philox(uint64_t seed, const uint64_t* stream_ids, uint64_t step,
                                int32_t n, double* out, hipStream_t stream);
 

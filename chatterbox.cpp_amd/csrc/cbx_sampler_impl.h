@@ -41,6 +41,21 @@
 #include "cbx_expf.h"
 #include "cbx_internal.h"
 #include "cbx_philox.h"
+#include "cbx_seqsum.h"
+
+// Stage timestamps for a profiling build (CBX_STAGE_CLOCKS defined, one
+// translation unit): wave 0 of each of the first 16384 workgroups records the
+// shader clock at each marker.  Compiled out otherwise.
+#if defined(CBX_STAGE_CLOCKS)
+__device__ unsigned long long cbx_stage_clock[16384 * 16];
+#define CBX_STAMP(n)                                                      \
+    do {                                                                  \
+        if (threadIdx.x == 0 && blockIdx.x < 16384)                       \
+            cbx_stage_clock[blockIdx.x * 16 + (n)] = clock64();           \
+    } while (0)
+#else
+#define CBX_STAMP(n) ((void)0)
+#endif
 
 namespace cbx {
 namespace {
@@ -51,6 +66,8 @@ constexpr int kFastMax = 2048;    // survivors handled on the register-list path
 constexpr int kValueBins = 2048;  // value histogram of the top-k select
 constexpr int kCandMax = 512;     // scores in the selected bin
 constexpr int kRadixBins = 4096;  // 12-bit digits of the fallback radix select
+constexpr int kSortBins = 2048;   // value bins of the survivor counting sort
+constexpr int kSortBinMax = 64;   // largest bin the counting sort ranks directly
 constexpr double kCdfMargin = 1e-9;
 // Word 3 of a raw buffer resource on gfx9-family parts (data format 32-bit,
 // no swizzle): loads past num_records return 0.
@@ -489,6 +506,83 @@ __device__ __forceinline__ void sort_list(uint64_t (&x)[NR], int n2, uint64_t* x
     }
 }
 
+// Counting sort of the register list (positions r*BLOCK + tid, n keys, the
+// rest ~0) into ascending key order (descending score, ascending id).
+// bin(v) = min(NB-1, int((v - blo) * scale)) is non-decreasing in v, so keys
+// order first by descending bin; a key's place inside its bin is the number of
+// smaller keys in the bin.  Every score must lie in [blo, hi].  Returns false,
+// with the list untouched, when the bins cannot be formed or one bin holds more
+// than kSortBinMax keys; the caller then sorts with the bitonic network.
+// LDS: start offsets u32[NB + 4], then the keys u64[n].
+template <int BLOCK, int NR>
+__device__ __forceinline__ bool bin_sort(uint64_t (&x)[NR], int n, float blo, float hi,
+                                         uint8_t* region, Shared& sh) {
+    constexpr int NB = kSortBins;
+    constexpr int BPT = NB / BLOCK;  // bins per lane in the scan
+    const int tid = threadIdx.x;
+    uint32_t* start = reinterpret_cast<uint32_t*>(region);
+    uint64_t* tmp = reinterpret_cast<uint64_t*>(region + (NB + 4) * 4);
+    const float range = __fsub_rn(hi, blo);
+    const float scale = __fdiv_rn((float)NB, range);
+    if (!(range > 0.0f) || !(scale < kPosInf)) return false;
+    for (int b = tid; b < NB + 4; b += BLOCK) start[b] = 0u;
+    __syncthreads();
+    int rb[NR], slot[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r * BLOCK + tid < n) {
+            const float v = desc_key_value(x[r]);
+            const int b = min(NB - 1, (int)__fmul_rn(__fsub_rn(v, blo), scale));
+            rb[r] = NB - 1 - b;  // ascending rb = descending score
+            slot[r] = (int)atomicAdd(&start[rb[r]], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t c[BPT];
+    int local = 0;
+    uint32_t big = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        c[q] = start[tid * BPT + q];
+        local += (int)c[q];
+        big = max(big, c[q]);
+    }
+    int total;
+    int base = block_excl_scan<BLOCK>(local, sh, total);
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        start[tid * BPT + q] = (uint32_t)base;
+        base += (int)c[q];
+    }
+    if (tid == 0) start[NB] = (uint32_t)n;
+    if (__syncthreads_or(big > (uint32_t)kSortBinMax)) return false;
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+        if (r * BLOCK + tid < n) tmp[start[rb[r]] + slot[r]] = x[r];
+    __syncthreads();
+    int fin[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r * BLOCK + tid < n) {
+            const int s0 = (int)start[rb[r]], s1 = (int)start[rb[r] + 1];
+            int rank = 0;
+            for (int k = s0; k < s1; ++k) rank += (tmp[k] < x[r]) ? 1 : 0;
+            fin[r] = s0 + rank;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+        if (r * BLOCK + tid < n) tmp[fin[r]] = x[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int i = r * BLOCK + tid;
+        x[r] = (i < n) ? tmp[i] : ~0ull;
+    }
+    return true;
+}
+
 // Ascending bitonic sort of (key, id) pairs [0, n2) in LDS (large lists).
 template <int BLOCK>
 __device__ __forceinline__ void bitonic_sort_pairs(uint32_t* key, uint16_t* id, int n2) {
@@ -557,6 +651,106 @@ __device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr
         acc = a;
     }
     return n - 1;
+}
+
+// DPP lane moves of a step table (identity where no source lane).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ SeqTab dpp_tab(const SeqTab& x) {
+    SeqTab y;
+    y.d0 = __builtin_amdgcn_update_dpp(0, x.d0, CTRL, ROWMASK, 0xf, false);
+    y.d1 = __builtin_amdgcn_update_dpp(0, x.d1, CTRL, ROWMASK, 0xf, false);
+    y.q = __builtin_amdgcn_update_dpp(2, x.q, CTRL, ROWMASK, 0xf, false);
+    return y;
+}
+
+// Inclusive scan of step tables over the wave (lane 0 first): row shifts by
+// 1, 2, 4, 8 inside each row of 16 lanes, then row broadcasts of lanes 15 and
+// 31 into the following rows.
+__device__ __forceinline__ SeqTab wave_scan_tab(SeqTab T) {
+    T = seq_compose(dpp_tab<0x111, 0xf>(T), T);  // row_shr:1
+    T = seq_compose(dpp_tab<0x112, 0xf>(T), T);  // row_shr:2
+    T = seq_compose(dpp_tab<0x114, 0xf>(T), T);  // row_shr:4
+    T = seq_compose(dpp_tab<0x118, 0xf>(T), T);  // row_shr:8
+    T = seq_compose(dpp_tab<0x142, 0xa>(T), T);  // row_bcast:15 into rows 1, 3
+    T = seq_compose(dpp_tab<0x143, 0xc>(T), T);  // row_bcast:31 into rows 2, 3
+    return T;
+}
+
+// Left-to-right binary32 running sum P + t[i0] + t[i0+1] + ... + t[n-1] of
+// non-negative finite terms, exactly, by one wave (every lane passes the same
+// arguments; n - i0 <= 64*CMAX) with the segment scan of cbx_seqsum.h: per
+// segment each lane loads a contiguous chunk into registers and composes its
+// steps, a wave scan composes the chunks, and the one lane whose chunk holds
+// the segment's end (or the threshold) walks it.  With thr > 0 the walk also
+// stops at the first index whose running sum is >= thr, returned in `hit` (-1
+// when the sum never reaches thr; the returned sum is then the full sum,
+// otherwise meaningless).
+template <int CMAX>
+__device__ __forceinline__ float seq_sum_wave(const float* t, int n, float P, int i0, float thr,
+                                              int& hit) {
+    const int lane = threadIdx.x & 63;
+    hit = -1;
+    n = uni(n);
+    i0 = uni(i0);
+    while (i0 < n) {
+        const int e = seq_unit_exp(P);
+        const int N0 = (int)ldexpf(P, -e);  // exact integer < 2^24
+        const int p0 = N0 & 1;
+        int nthr = kSeqSat;
+        if (thr > 0.0f) nthr = (int)ceilf(fminf(ldexpf(thr, -e), kSeqClamp));
+        const int target = min(nthr, 1 << 24);
+        const int C = uni((n - i0 + 63) >> 6);  // terms per lane, <= CMAX
+        const int first = i0 + lane * C;
+        float tr[CMAX];
+#pragma unroll
+        for (int k = 0; k < CMAX; ++k) {
+            if (k < C) tr[k] = (first + k < n) ? t[first + k] : 0.0f;  // 0: no step
+        }
+        SeqTab T = seq_identity();
+#pragma unroll
+        for (int k = 0; k < CMAX; ++k)
+            if (k < C) T = seq_push(T, seq_step(tr[k], e));
+        T = wave_scan_tab(T);
+        SeqTab X = dpp_tab<0x138, 0xf>(T);  // wave_shr:1 -> exclusive
+        const int d_before = p0 ? X.d1 : X.d0;
+        const int c_before = p0 ? (X.q >> 1) & 1 : X.q & 1;
+        const int n_after = N0 + (p0 ? T.d1 : T.d0);
+        const uint64_t reach = __ballot(n_after >= target);
+        if (reach == 0) {
+            const int total = __builtin_amdgcn_readlane(n_after, 63);
+            return ldexpf((float)total, e);  // total < 2^24: exact
+        }
+        const int L = __builtin_ctzll(reach);
+        int kind = 0, idx = 0, nprev = 0;
+        if (lane == L) {
+            int d = d_before, c = c_before;
+#pragma unroll
+            for (int k = 0; k < CMAX; ++k) {
+                if (k < C && kind == 0) {
+                    const int nb = N0 + d;
+                    seq_apply(d, c, seq_step(tr[k], e));
+                    if (N0 + d >= (1 << 24)) { kind = 1; idx = first + k; nprev = nb; }
+                    else if (N0 + d >= nthr) { kind = 2; idx = first + k; }
+                }
+            }
+        }
+        kind = __builtin_amdgcn_readlane(kind, L);
+        idx = __builtin_amdgcn_readlane(idx, L);
+        nprev = __builtin_amdgcn_readlane(nprev, L);
+        if (kind == 2) {
+            hit = idx;
+            return P;
+        }
+        if (kind == 0) return P;  // unreachable for finite terms; bounds the loop
+        // the term that leaves the binade: one ordinary add of the exact sum
+        P = __fadd_rn(ldexpf((float)nprev, e), t[idx]);
+        if (thr > 0.0f && P >= thr) {
+            hit = idx;
+            return P;
+        }
+        i0 = idx + 1;
+    }
+    return P;
 }
 
 // --------------------------------------------------------------- bitmaps
@@ -700,6 +894,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
         if ((kept >> q) & 1u) atomicOr(&keptw[id[q] >> 5], 1u << (id[q] & 31));
     __syncthreads();
     const int n_final = bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+    CBX_STAMP(9);
 
     // softmax (main.cpp:783-793)
     float m = kNegInf;
@@ -720,6 +915,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
     }
     __syncthreads();
     const float psum2 = unif(sh.psum);
+    CBX_STAMP(10);
     const bool empty = (psum2 == 0.0f);
     if (!empty) {
 #pragma unroll
@@ -759,8 +955,10 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
             u = a.uniforms[rs];
         }
         token = draw_token<BLOCK>(F, n_final, keptw, woff, W, V, u, sh);
+        CBX_STAMP(11);
     }
 
+    CBX_STAMP(12);
     if (tid == 0) {
         a.tokens[rs] = token;
         if (a.info) a.info[rs] = flags | sh.flags;
@@ -782,6 +980,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
 template <int BLOCK, int EPT, int NR>
 __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params& P, int64_t rs,
                                           int row, int step, uint32_t flags, int n_surv,
+                                          float blo, float bhi,
                                           bool use_topp, bool use_pen, const uint32_t* seen,
                                           uint32_t* keptw, uint32_t* woff, uint8_t* region,
                                           const uint64_t* tab, Shared& sh) {
@@ -801,10 +1000,12 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
     float mx_surv = kNegInf;
     // ---- top-p (main.cpp:750-772) ----
     if (use_topp) {
-        sort_list<BLOCK, NR>(x, n2, xbuf);
+        if (!bin_sort<BLOCK, NR>(x, n_surv, blo, bhi, region, sh)) sort_list<BLOCK, NR>(x, n2, xbuf);
+        CBX_STAMP(4);
         if (tid == 0) sh.mx = desc_key_value(x[0]);
         __syncthreads();
         mx_surv = unif(sh.mx);
+        // E (the bin sort's offsets area) does not overlap the keys still read
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             const int i = r * BLOCK + tid;
@@ -812,23 +1013,35 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
                 E[i] = expf_libm_branchless(__fsub_rn(desc_key_value(x[r]), mx_surv), tab);
         }
         __syncthreads();
+        CBX_STAMP(5);
         if (wid == 0) {
-            const float ps = wave_chain_sum(E, n_surv, 0.0f);
-            if (lane == 0) sh.psum = ps;
-        }
-        __syncthreads();
-        const float psum = unif(sh.psum);
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int i = r * BLOCK + tid;
-            if (i < n_surv) E[i] = __fdiv_rn(E[i], psum);
-        }
-        __syncthreads();
-        if (wid == 0) {
-            const int last = wave_chain_cross(E, n_surv, P.top_p);
+            // psum = 0 + e_0 + e_1 + ... (e_0 = 1), then q_i = e_i / psum in place,
+            // then the first i with q_0 + ... + q_i >= top_p.  Rows holding NaN or
+            // +inf take the term-by-term chains (the segment scan needs finite terms).
+            const bool scan = !(flags & CBX_INFO_NONFINITE);
+            int hit;
+            const float psum = scan ? seq_sum_wave<kFastMax / 64>(E, n_surv, E[0], 1, 0.0f, hit)
+                                    : wave_chain_sum(E, n_surv, 0.0f);
+            CBX_STAMP(6);
+            for (int i = lane; i < n_surv; i += 64) E[i] = __fdiv_rn(E[i], psum);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            int last;
+            if (scan) {
+                const float q0 = E[0];
+                last = 0;
+                if (!(q0 >= P.top_p)) {
+                    (void)seq_sum_wave<kFastMax / 64>(E, n_surv, q0, 1, P.top_p, hit);
+                    last = hit < 0 ? n_surv - 1 : hit;
+                }
+            } else {
+                last = wave_chain_cross(E, n_surv, P.top_p);
+            }
             if (lane == 0) sh.n_kept = last + 1;
         }
         __syncthreads();
+        CBX_STAMP(7);
         const int n_kept = uni(sh.n_kept);
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
@@ -872,6 +1085,7 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
                                        : __fmul_rn(val[r], P.repeat_penalty);
     }
     __syncthreads();  // E and xbuf are done with; F takes the region
+    CBX_STAMP(8);
     finish_row<BLOCK, EPT, NR>(val, id, kept, a, P, rs, row, step, flags, keptw, woff, F, tab, sh);
 }
 
@@ -912,6 +1126,7 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
 
     const cbx_params P = a.params[row];
     const int64_t rs = (int64_t)step * a.n_rows + row;  // row-step linear id
+    CBX_STAMP(0);
 
     // ---- load (all loads first), combine, mask, temperature (main.cpp:733-738) ----
     // Buffer loads bounded by a resource of V*4 bytes: one lane offset, the
@@ -982,10 +1197,12 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
     }
     int bad;
     block_minmax<BLOCK>(lo, hi, nonfinite, sh, lo, hi, bad);
+    CBX_STAMP(1);
     const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
 
     // ---- top-k (main.cpp:740-748) ----
     const bool use_topk = P.top_k > 0 && P.top_k < V;
+    float sblo = lo;  // every survivor lies in [sblo, hi]
     if (use_topk) {
         float thr;
         int above;
@@ -998,11 +1215,13 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
             above = block_sum<BLOCK>(n_above, sh);
         }
         if (above < P.top_k) thr = __fsub_rn(thr, 1e-10f);
+        sblo = fmaxf(thr, lo);
 #pragma unroll
         for (int j = 0; j < EPT; ++j) s[j] = (s[j] <= thr) ? kNegInf : s[j];
     }
 
     // ---- survivors (score != -inf): count and compaction offsets ----
+    CBX_STAMP(2);
     int mine = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) mine += (s[j] != kNegInf) ? 1 : 0;
@@ -1027,20 +1246,21 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
         for (int j = 0; j < EPT; ++j)
             if (s[j] != kNegInf) xbuf[off++] = desc_key(s[j], (uint32_t)(j * BLOCK + tid));
         __syncthreads();
+        CBX_STAMP(3);
         const int rows_needed = uni((max(64, pow2ceil(n_surv)) + BLOCK - 1) / BLOCK);
         if (rows_needed <= 1) {
-            fast_path<BLOCK, EPT, 1>(a, P, rs, row, step, flags, n_surv, use_topp, use_pen, seen,
-                                     keptw, woff, region, tab, sh);
+            fast_path<BLOCK, EPT, 1>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp, use_pen,
+                                     seen, keptw, woff, region, tab, sh);
         } else if constexpr (MAXNR >= 2) {
             if (rows_needed == 2) {
-                fast_path<BLOCK, EPT, 2>(a, P, rs, row, step, flags, n_surv, use_topp, use_pen,
+                fast_path<BLOCK, EPT, 2>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp, use_pen,
                                          seen, keptw, woff, region, tab, sh);
             } else if constexpr (MAXNR >= 4) {
                 if (rows_needed <= 4) {
-                    fast_path<BLOCK, EPT, 4>(a, P, rs, row, step, flags, n_surv, use_topp,
+                    fast_path<BLOCK, EPT, 4>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp,
                                              use_pen, seen, keptw, woff, region, tab, sh);
                 } else if constexpr (MAXNR >= 8) {
-                    fast_path<BLOCK, EPT, 8>(a, P, rs, row, step, flags, n_surv, use_topp,
+                    fast_path<BLOCK, EPT, 8>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp,
                                              use_pen, seen, keptw, woff, region, tab, sh);
                 }
             }

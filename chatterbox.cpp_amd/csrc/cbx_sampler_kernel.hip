@@ -21,6 +21,24 @@ __global__ void debug_philox_kernel(uint64_t seed, const uint64_t* sid, uint64_t
     if (i < n) out[i] = philox_uniform(seed, sid ? sid[i] : (uint64_t)i, step);
 }
 
+// One wave per case: the exact left-to-right binary32 sum of the case's terms
+// (starting from its first term; at most 2048 terms are read) and, for thr > 0, the first index whose
+// running sum reaches thr.
+__global__ __launch_bounds__(64) void debug_seqsum_kernel(const float* t, const int32_t* off,
+                                                          const float* thr, float* sum,
+                                                          int32_t* hit) {
+    const int c = blockIdx.x;
+    const int b = off[c], n = off[c + 1] - b;
+    if (n <= 0) return;
+    int h;
+    const float th = thr ? thr[c] : 0.0f;
+    const float s = seq_sum_wave<kFastMax / 64>(t + b, min(n, kFastMax), t[b], 1, th, h);
+    if (threadIdx.x == 0) {
+        sum[c] = s;
+        hit[c] = (th > 0.0f && t[b] >= th) ? 0 : h;
+    }
+}
+
 }  // namespace
 
 size_t lds_bytes_for(int32_t cap, int32_t n_vocab) {
@@ -28,8 +46,9 @@ size_t lds_bytes_for(int32_t cap, int32_t n_vocab) {
     size_t region = (size_t)kRadixBins * 4;                             // radix histogram
     const size_t bins = (size_t)kValueBins * 4 + (size_t)kCandMax * 4;  // value bins + candidates
     if (bins > region) region = bins;
-    const size_t fast = 8 * (size_t)(cap < kFastMax ? (cap < 64 ? 64 : cap) : kFastMax);
-    if (fast > region) region = fast;                                   // register-list exchange
+    const size_t list = (size_t)(cap < kFastMax ? (cap < 64 ? 64 : cap) : kFastMax);
+    const size_t fast = (size_t)(kSortBins + 4) * 4 + 8 * list;        // counting sort / list
+    if (fast > region) region = fast;
     if ((size_t)cap * 6 > region) region = (size_t)cap * 6;             // LDS-sorted pairs / F
     return 3 * Wp * 4 + region;
 }
@@ -41,6 +60,12 @@ int32_t max_cap_for_lds(int32_t n_vocab, size_t lds_bytes) {
 }
 
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
+    // one wave per row while the survivors fit its list
+    if (a.cap <= kWaveCap) {
+        if (a.n_vocab <= 256 * 16) return launch_w16(a, stream);
+        if (a.n_vocab <= 256 * 26) return launch_w26(a, stream);
+        if (a.n_vocab <= kWaveMaxVocab) return launch_w33(a, stream);
+    }
     // registers per lane sized to the vocabulary (6563 -> 26 per lane)
     if (a.n_vocab <= 256 * 16) return launch_v256x16(a, stream);
     if (a.n_vocab <= 256 * 26) return launch_v256x26(a, stream);
@@ -52,6 +77,13 @@ hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
 hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream) {
     const int64_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(debug_expf_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_seqsum(const float* terms, const int32_t* offsets, const float* thr,
+                              int32_t n_cases, float* sum, int32_t* hit, hipStream_t stream) {
+    hipLaunchKernelGGL(debug_seqsum_kernel, dim3(n_cases), dim3(64), 0, stream, terms, offsets,
+                       thr, sum, hit);
     return hipGetLastError();
 }
 

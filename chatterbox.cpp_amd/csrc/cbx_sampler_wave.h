@@ -1,0 +1,840 @@
+// cbx_sampler_wave.h -- the one-wavefront-per-row sampler (vocabularies up to
+// 256*Q ids, at most kWaveCap survivors after top-k).
+//
+// A row of a few thousand logits is small: one 64-lane wave holds it in
+// registers (4*Q scores per lane, loaded as 16-byte vectors: element 4j + c of
+// lane l is id 256j + 4l + c), and every reduction, scan and compaction is a
+// wave operation (DPP, ballot/mbcnt) with no workgroup barrier.  Each
+// workgroup is a single wave, so a CU keeps many rows in flight while others
+// wait on HBM.  Stage order and arithmetic follow sample_next_token_ex
+// (src/main.cpp:726-801), exactly as the workgroup kernel in
+// cbx_sampler_impl.h does:
+//
+//   load + CFG combine + masks + temperature (main.cpp:733-738)
+//   top-k (main.cpp:740-748): value-bin histogram over [min, max] (a monotone
+//          map), exact selection among the scores of the bin holding rank k;
+//          rows with NaN/+inf or degenerate ranges use an 8-bit radix select
+//   survivors -> LDS list of (descending score, ascending id) keys; counting
+//          sort by value bin, each key placed by its rank inside its bin
+//   top-p (main.cpp:750-772): the binary32 running sums psum and cum by the
+//          exact segment scan (cbx_seqsum.h); min-p [extension]; repetition
+//          penalty from an LDS bitmap of the history (main.cpp:774-781)
+//   softmax + draw (main.cpp:783-800): the kept exp terms in id order; the
+//          token is located on the parallel binary64 prefix of the exp terms
+//          when the uniform is more than kDrawMargin (relative) from both
+//          neighbouring boundaries -- the reference's cumulative values differ
+//          from that prefix ratio by less than 2^-23 relative, whatever its
+//          float normaliser -- otherwise, and for greedy rows or when
+//          probabilities are requested, the reference's float normaliser is
+//          summed term by term and its double CDF replayed.
+//
+// Per-element work is written without branches (spare histogram bins and
+// list slots take what is dropped): the unrolled element loops would
+// otherwise keep one exec mask per element alive.
+#pragma once
+
+#include "cbx_sampler_impl.h"
+
+namespace cbx {
+namespace {
+
+constexpr int kWaveBins = 1024;   // value bins: top-k select, survivor sort
+constexpr int kWaveCand = 512;    // scores in the selected top-k bin
+constexpr int kWaveSortMax = 64;  // largest bin the counting sort ranks directly
+constexpr int kWaveRows = kWaveCap / 64;
+constexpr double kDrawMargin = 3e-7;
+
+template <int Q>
+struct WaveSmem {
+    uint64_t tab[32];
+    uint32_t seen[8 * Q];       // history ids (penalty)
+    uint32_t keptw[8 * Q + 1];  // kept ids after every filter (+ spare word)
+    uint32_t woff[8 * Q];       // kept ids before each word
+    union {
+        uint32_t hist[kWaveBins + 4];  // value bins (+ spare), then sort offsets
+        float cand[kWaveCand + 1];     // scores of the top-k bin (+ spare slot)
+        float E[kWaveCap];             // exp terms in sorted order, then q_i
+        float F[kWaveCap];             // kept exp terms in id order
+    } u;
+    uint64_t list[kWaveCap + 1];  // survivors (+ spare slot): raw, then keys
+    int rk;
+};
+
+// ------------------------------------------------------------ wave helpers
+
+template <int CTRL, int RM>
+__device__ __forceinline__ int dpp_i(int old, int x) {
+    return __builtin_amdgcn_update_dpp(old, x, CTRL, RM, 0xf, false);
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ float dpp_f(float old, float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, x), CTRL,
+                                                                 RM, 0xf, false));
+}
+
+// Reductions and scans over the wave by DPP: row shifts 1, 2, 4, 8 inside
+// rows of 16 lanes, then row broadcasts of lanes 15 and 31.  Lane 63 ends
+// with the total (inclusive scans: every lane its prefix).
+__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
+    x += dpp_i<0x111, 0xf>(0, x);
+    x += dpp_i<0x112, 0xf>(0, x);
+    x += dpp_i<0x114, 0xf>(0, x);
+    x += dpp_i<0x118, 0xf>(0, x);
+    x += dpp_i<0x142, 0xa>(0, x);
+    x += dpp_i<0x143, 0xc>(0, x);
+    return x;
+}
+__device__ __forceinline__ int wave_excl_scan_i(int v, int& total) {
+    const int incl = wave_incl_scan_dpp(v);
+    total = __builtin_amdgcn_readlane(incl, 63);
+    return incl - v;
+}
+__device__ __forceinline__ int wave_sum_dpp(int x) {
+    return __builtin_amdgcn_readlane(wave_incl_scan_dpp(x), 63);
+}
+__device__ __forceinline__ float wave_max_dpp(float x) {
+    x = fmaxf(x, dpp_f<0x111, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x112, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x114, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x118, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x142, 0xa>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x143, 0xc>(kNegInf, x));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+__device__ __forceinline__ float wave_min_dpp(float x) {
+    x = fminf(x, dpp_f<0x111, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x112, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x114, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x118, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x142, 0xa>(kPosInf, x));
+    x = fminf(x, dpp_f<0x143, 0xc>(kPosInf, x));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+__device__ __forceinline__ int wave_min_i_dpp(int x) {
+    x = min(x, dpp_i<0x111, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x112, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x114, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x118, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x142, 0xa>(0x7fffffff, x));
+    x = min(x, dpp_i<0x143, 0xc>(0x7fffffff, x));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Four consecutive words of a raw buffer (one 16-byte load).  The vector is
+// copied out as bytes: subscripting the builtin's vector result directly
+// makes this compiler emit a single-word load.
+__device__ __forceinline__ void load4(const __amdgpu_buffer_rsrc_t& r, int voff, int soff,
+                                      float* out) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    __builtin_memcpy(out, &v, 16);
+}
+
+// Position of this lane's item among the lanes whose bit is set in m.
+__device__ __forceinline__ int ballot_rank(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// An opaque copy of a uniform value: predicates built on it in one pass are
+// not merged with (and kept alive for) those of another pass.
+__device__ __forceinline__ int fresh(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+// The same for a float (held in a vector register: values derived from it
+// are recomputed where used).
+__device__ __forceinline__ float fresh_v(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// What turns a row's logits into its scores (main.cpp:733-738 and the
+// extensions): CFG combine, allowed mask, forced stop, temperature.
+struct RowScores {
+    __amdgpu_buffer_rsrc_t rl, ru, ra;
+    bool uncond, masked_ids, fstop, scale;
+    float cfg_w, inv_t;
+    int V, stop;
+
+    // CFG combine of raw logits v with the unconditional ones.
+    __device__ __forceinline__ void combine4(float* v, const float* un) const {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(v[c], __fmul_rn(cfg_w, __fsub_rn(v[c], un[c])));
+    }
+    // Scores of ids 256j + 4*lane + c (c < 4) from combined logits.
+    __device__ __forceinline__ void finish4(int j, int lane, float* v, int Vm) const {
+        uint32_t word = 0xffffffffu;
+        if (masked_ids)
+            word = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ra, (8 * j + (lane >> 3)) * 4,
+                                                                  0, 0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float x = v[c];
+            const int id = 256 * j + 4 * lane + c;
+            const bool m = (id >= Vm) | !((word >> (4 * (lane & 7) + c)) & 1u) |
+                           (fstop & (id != stop));
+            x = m ? kNegInf : x;
+            if (scale) x = __fmul_rn(x, inv_t);
+            v[c] = x;
+        }
+    }
+    // The same scores again, reloaded (for the rare passes that would
+    // otherwise keep a second copy of the row in registers).
+    __device__ __forceinline__ void reload4(int j, int lane, float* v, int Vm) const {
+        load4(rl, lane * 16, j * 1024, v);
+        if (uncond) {
+            float un[4];
+            load4(ru, lane * 16, j * 1024, un);
+            combine4(v, un);
+        }
+        finish4(j, lane, v, Vm);
+    }
+};
+
+// One 8-bit radix pass of the (rem+1)-th largest okey among ids < V, over
+// scores reloaded vector by vector.
+template <int Q>
+__device__ __forceinline__ void wave_radix_pass(const RowScores& rsc, int shift, uint32_t& prefix,
+                                                uint32_t& pmask, uint32_t& rem, uint32_t* hist) {
+    const int lane = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hist[lane * 4 + q] = 0u;
+    if (lane == 0) hist[256] = 0u;
+    __syncthreads();
+#pragma unroll 1
+    for (int j = 0; j < Q; ++j) {
+        float v[4];
+        rsc.reload4(j, lane, v, rsc.V);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int id = 256 * j + 4 * lane + c;
+            const uint32_t k = okey(v[c]);
+            const bool in = (id < rsc.V) & ((k & pmask) == prefix);
+            atomicAdd(&hist[in ? (k >> shift) & 255u : 256u], 1u);  // 256: spare
+        }
+    }
+    __syncthreads();
+    uint32_t cnt[4];
+    int tot = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        cnt[q] = hist[255 - (lane * 4 + q)];  // descending digits
+        tot += (int)cnt[q];
+    }
+    int all;
+    const uint32_t excl = (uint32_t)wave_excl_scan_i(tot, all);
+    int digit = 0;
+    uint32_t above = 0;
+    const bool mine = excl <= rem && rem < excl + (uint32_t)tot;
+    if (mine) {
+        uint32_t run = excl;
+        bool found = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (!found && run + cnt[q] > rem) {
+                digit = 255 - (lane * 4 + q);
+                above = run;
+                found = true;
+            }
+            run += cnt[q];
+        }
+    }
+    const int L = __builtin_ctzll(__ballot(mine));
+    digit = __builtin_amdgcn_readlane(digit, L);
+    above = (uint32_t)__builtin_amdgcn_readlane((int)above, L);
+    prefix |= (uint32_t)digit << shift;
+    pmask |= 255u << shift;
+    rem -= above;
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ kernel
+
+template <int Q>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sample_rows_wave(
+    KernelArgs a) {
+    __shared__ WaveSmem<Q> sm;
+    constexpr int EPL = 4 * Q;  // scores per lane
+    constexpr int R = kWaveRows;
+    const int lane = threadIdx.x;
+    const int64_t g = blockIdx.x;
+    const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
+    const int V = a.n_vocab;
+    const int W = (V + 31) >> 5;
+    const int cap = min(a.cap, kWaveCap);
+    const cbx_params P = a.params[row];
+    const int64_t rs = (int64_t)step * a.n_rows + row;
+
+    // ---- load: 16-byte buffer loads bounded at V floats (main.cpp:733) ----
+    // The range check of a raw buffer load is per dword, so the vector that
+    // straddles V returns its in-range words and zeros (masked below).
+    const uint32_t* arow = a.allowed ? a.allowed + (int64_t)row * a.ld_allowed : nullptr;
+    RowScores rsc;
+    rsc.rl = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.logits + rs * a.ld_logits),
+                                               (short)0, V * 4, kBufferWord3);
+    rsc.uncond = a.uncond != nullptr;
+    rsc.ru = rsc.rl;
+    if (rsc.uncond)
+        rsc.ru = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.uncond + rs * a.ld_logits), (short)0, V * 4, kBufferWord3);
+    rsc.masked_ids = arow != nullptr;
+    rsc.ra = rsc.rl;
+    if (arow)
+        rsc.ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(arow), (short)0, W * 4,
+                                                   kBufferWord3);
+    rsc.fstop = a.force_stop && a.force_stop[rs];
+    rsc.scale = P.temp > 0.0f && P.temp != 1.0f;
+    rsc.cfg_w = P.cfg_weight;
+    rsc.inv_t = __fdiv_rn(1.0f, P.temp);
+    rsc.V = V;
+    rsc.stop = a.stop_token;
+    float s[EPL];
+#pragma unroll
+    for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
+    if (rsc.uncond) {
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            float un[4];
+            load4(rsc.ru, lane * 16, j * 1024, un);
+            rsc.combine4(&s[4 * j], un);
+        }
+    }
+    if (lane < 32) sm.tab[lane] = kExp2TabDev.t[lane];
+    for (int w = lane; w < 8 * Q + 1; w += 64) {
+        sm.seen[min(w, 8 * Q - 1)] = 0u;
+        sm.keptw[w] = 0u;
+    }
+    __syncthreads();
+    // ---- history ids -> seen bitmap (main.cpp:775), loads batched 4 deep ----
+    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
+    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
+    if (use_pen) {
+        const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
+        for (int b = 0; b < hlen; b += 256) {
+            int t[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = b + u * 64 + lane;
+                t[u] = j < hlen ? hrow[j] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (t[u] >= 0 && t[u] < V) atomicOr(&sm.seen[t[u] >> 5], 1u << (t[u] & 31));
+        }
+    }
+    // ---- masks and temperature (main.cpp:735-738) ----
+    int nonfinite = 0;
+    float lo = kPosInf, hi = kNegInf;
+    {
+        const int Vm = fresh(V);
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            rsc.finish4(j, lane, &s[4 * j], Vm);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float v = s[4 * j + c];
+                nonfinite |= ((v != v) | (v == kPosInf)) ? 1 : 0;
+                lo = fminf(lo, v == kNegInf ? kPosInf : v);
+                hi = fmaxf(hi, v);
+            }
+        }
+    }
+    lo = wave_min_dpp(lo);
+    hi = wave_max_dpp(hi);
+    const int bad = wave_sum_dpp(nonfinite) != 0;
+    const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
+
+    // ---- top-k (main.cpp:740-748) ----
+    const int k = P.top_k;
+    const bool use_topk = k > 0 && k < V;
+    float thr = kNegInf;  // survivors: s > thr
+    if (use_topk) {
+        int above = 0;
+        bool done = false;
+        const float range = __fsub_rn(hi, lo);
+        const float bscale = __fdiv_rn((float)kWaveBins, range);
+        if (!bad && range > 0.0f && bscale < kPosInf) {
+            // bin(v) = fma(v, scale, -lo*scale) clamped to [0, NB-1] is
+            // non-decreasing in v; -inf goes to the spare bin NB
+            const float nlo = -__fmul_rn(lo, bscale);
+            auto bin_of = [&](float v) -> int {
+                const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bscale, nlo), 0.0f,
+                                                           (float)(kWaveBins - 1));
+                return v == kNegInf ? kWaveBins : b;
+            };
+#pragma unroll
+            for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
+            if (lane == 0) sm.u.hist[kWaveBins] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) atomicAdd(&sm.u.hist[bin_of(s[e])], 1u);
+            __syncthreads();
+            constexpr int BPL = kWaveBins / 64;
+            uint32_t cnt[BPL];
+            int tot = 0;
+#pragma unroll
+            for (int q = 0; q < BPL; ++q) {
+                cnt[q] = sm.u.hist[kWaveBins - 1 - (lane * BPL + q)];  // descending bins
+                tot += (int)cnt[q];
+            }
+            int n_fin;
+            const int excl = wave_excl_scan_i(tot, n_fin);
+            if (n_fin <= k) {
+                thr = kNegInf;  // at most k finite scores: nothing is removed
+                above = n_fin;
+                done = true;
+            } else {
+                const bool mine = excl <= k && k < excl + tot;
+                int bsel = 0, above_bins = 0;
+                if (mine) {
+                    int run = excl;
+                    bool found = false;
+#pragma unroll
+                    for (int q = 0; q < BPL; ++q) {
+                        if (!found && run + (int)cnt[q] > k) {
+                            bsel = kWaveBins - 1 - (lane * BPL + q);
+                            above_bins = run;
+                            found = true;
+                        }
+                        run += (int)cnt[q];
+                    }
+                }
+                const int L = __builtin_ctzll(__ballot(mine));
+                bsel = __builtin_amdgcn_readlane(bsel, L);
+                above_bins = __builtin_amdgcn_readlane(above_bins, L);
+                __syncthreads();  // histogram reads done: the candidates reuse it
+                // recompute the bins (keeping 4*Q bin values live costs as many registers)
+                const float bscale2 = fresh_v(bscale), nlo2 = fresh_v(nlo);
+                auto bin2_of = [&](float v) -> int {
+                    const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bscale2, nlo2), 0.0f,
+                                                               (float)(kWaveBins - 1));
+                    return v == kNegInf ? kWaveBins : b;
+                };
+                int nc = 0;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const bool in = bin2_of(s[e]) == bsel;
+                    const uint64_t m = __ballot(in);
+                    const int at = nc + ballot_rank(m);
+                    sm.u.cand[(in && at < kWaveCand) ? at : kWaveCand] = s[e];
+                    nc += __popcll(m);
+                }
+                __syncthreads();
+                if (nc <= kWaveCand) {
+                    const int rem = k - above_bins;  // 0 <= rem < nc
+                    float tv = kNegInf;
+                    int tgt = 0;
+                    bool hitc = false;
+                    for (int c0 = lane; c0 < nc; c0 += 64) {
+                        const float v = sm.u.cand[c0];
+                        int gt = 0, ge = 0;
+                        for (int t = 0; t < nc; ++t) {
+                            const float w = sm.u.cand[t];
+                            gt += (w > v) ? 1 : 0;
+                            ge += (w >= v) ? 1 : 0;
+                        }
+                        if (gt <= rem && rem < ge) { tv = v; tgt = gt; hitc = true; }
+                    }
+                    const int L2 = __builtin_ctzll(__ballot(hitc));
+                    thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                         __builtin_bit_cast(int, tv), L2));
+                    above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
+                    done = true;
+                }
+            }
+        }
+        if (!done) {
+            // 8-bit radix select over all ids (NaN / inf / degenerate rows)
+            uint32_t prefix = 0, pmask = 0, rem = (uint32_t)k;
+            wave_radix_pass<Q>(rsc, 24, prefix, pmask, rem, sm.u.hist);
+            wave_radix_pass<Q>(rsc, 16, prefix, pmask, rem, sm.u.hist);
+            wave_radix_pass<Q>(rsc, 8, prefix, pmask, rem, sm.u.hist);
+            wave_radix_pass<Q>(rsc, 0, prefix, pmask, rem, sm.u.hist);
+            thr = okey_inv(prefix);
+            int n_above = 0;
+#pragma unroll 1
+            for (int j = 0; j < Q; ++j) {
+                float v[4];
+                rsc.reload4(j, lane, v, V);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) n_above += (v[c] > thr) ? 1 : 0;
+            }
+            above = wave_sum_dpp(n_above);
+        }
+        if (above < k) thr = __fsub_rn(thr, 1e-10f);
+    }
+
+    // ---- survivors -> LDS list of (score bits << 32 | id) ----
+    // keep = score != -inf and not (top-k and score <= thr); without NaN that
+    // is score > thr (thr = -inf when nothing is cut).  Dropped items and
+    // items past the list write its spare slot.
+    int n_surv;
+    {
+        int n = 0;
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float v = s[4 * j + c];
+                const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
+                const uint64_t m = __ballot(keep);
+                const int at = n + ballot_rank(m);
+                const int slot = (keep && at < kWaveCap) ? at : kWaveCap;
+                sm.list[slot] = ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) |
+                                (uint32_t)(256 * j + 4 * lane + c);
+                n += __popcll(m);
+            }
+        }
+        n_surv = n;
+    }
+    if (n_surv > cap) {
+        if (lane == 0) {
+            a.tokens[rs] = -1;
+            if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
+        }
+        if (a.probs) {
+            float* prow = a.probs + rs * a.ld_probs;
+            for (int i = lane; i < V; i += 64) prow[i] = 0.0f;
+        }
+        return;
+    }
+    __syncthreads();
+    // raw entries -> composite keys (descending score, ascending id), in place;
+    // positions [n_surv, 64*nr) become the maximum key
+    const int nr = (n_surv + 63) >> 6;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (r < nr) {
+            const int i = r * 64 + lane;
+            const uint64_t w = sm.list[i];
+            const uint64_t key =
+                desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w);
+            sm.list[i] = (i < n_surv) ? key : ~0ull;
+        }
+    }
+    __syncthreads();
+
+    uint32_t rflags = flags;
+    const bool use_topp = P.top_p < 1.0f && n_surv > 0;
+    int n_kept = n_surv;  // kept: list positions [0, n_kept)
+    float mx_surv = hi;
+    if (use_topp) {
+        // ---- counting sort of the keys by value bin over [min survivor, max] ----
+        const float slo = use_topk ? fmaxf(thr, lo) : lo;
+        const float srange = __fsub_rn(hi, slo);
+        const float sscale = __fdiv_rn((float)kWaveBins, srange);
+        bool sorted = false;
+        if (!bad && srange > 0.0f && sscale < kPosInf) {
+            const float nslo = -__fmul_rn(slo, sscale);
+            uint64_t x[R];
+            int rb[R], slot[R];
+#pragma unroll
+            for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
+            if (lane < 4) sm.u.hist[kWaveBins + lane] = 0u;
+            __syncthreads();
+            const int nv = fresh(n_surv);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (r < nr) {
+                    const int i = r * 64 + lane;
+                    x[r] = sm.list[i];
+                    const float v = desc_key_value(x[r]);
+                    const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, sscale, nslo), 0.0f,
+                                                               (float)(kWaveBins - 1));
+                    rb[r] = (i < nv) ? kWaveBins - 1 - b : kWaveBins;  // NB: spare
+                    slot[r] = (int)atomicAdd(&sm.u.hist[rb[r]], 1u);
+                }
+            }
+            __syncthreads();
+            constexpr int BPL = kWaveBins / 64;
+            uint32_t cnt[BPL];
+            int tot = 0;
+            uint32_t big = 0;
+#pragma unroll
+            for (int q = 0; q < BPL; ++q) {
+                cnt[q] = sm.u.hist[lane * BPL + q];
+                tot += (int)cnt[q];
+                big = max(big, cnt[q]);
+            }
+            int all;
+            int base = wave_excl_scan_i(tot, all);
+#pragma unroll
+            for (int q = 0; q < BPL; ++q) {
+                sm.u.hist[lane * BPL + q] = (uint32_t)base;
+                base += (int)cnt[q];
+            }
+            if (lane < 2) sm.u.hist[kWaveBins + lane] = (uint32_t)n_surv;  // spare: empty
+            if (__ballot(big > (uint32_t)kWaveSortMax) == 0) {
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (r < nr) {
+                        const int dst = rb[r] < kWaveBins ? (int)sm.u.hist[rb[r]] + slot[r]
+                                                          : kWaveCap;
+                        sm.list[dst] = x[r];
+                    }
+                __syncthreads();
+                int fin[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (r < nr) {
+                        const int s0 = (int)sm.u.hist[rb[r]], s1 = (int)sm.u.hist[rb[r] + 1];
+                        int rank = 0;
+                        for (int t = s0; t < s1; ++t) rank += (sm.list[t] < x[r]) ? 1 : 0;
+                        fin[r] = rb[r] < kWaveBins ? s0 + rank : kWaveCap;
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (r < nr) sm.list[fin[r]] = x[r];
+                sorted = true;
+            }
+        }
+        if (!sorted) {
+            // bitonic sort of the list in LDS (NaN rows, crowded bins)
+            const int n2 = max(64, pow2ceil(n_surv));
+            __syncthreads();
+            for (int i = n_surv + lane; i < n2; i += 64) sm.list[i] = ~0ull;
+            __syncthreads();
+            for (int kk = 2; kk <= n2; kk <<= 1) {
+                for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+                    for (int i = lane; i < n2; i += 64) {
+                        const int p = i ^ jj;
+                        if (p > i) {
+                            const uint64_t ka = sm.list[i], kb = sm.list[p];
+                            const bool up = (i & kk) == 0;
+                            if ((ka > kb) == up) { sm.list[i] = kb; sm.list[p] = ka; }
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+        }
+        __syncthreads();
+        // ---- top-p (main.cpp:750-772) ----
+        mx_surv = desc_key_value(sm.list[0]);  // sorted[0]
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < nr) {
+                const int i = r * 64 + lane;
+                sm.u.E[i] = expf_libm_branchless(__fsub_rn(desc_key_value(sm.list[i]), mx_surv),
+                                                 sm.tab);
+            }
+        }
+        __syncthreads();
+        int hit;
+        int last;
+        if (!bad) {
+            const float psum = seq_sum_wave<R>(sm.u.E, n_surv, sm.u.E[0], 1, 0.0f, hit);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r < nr) sm.u.E[r * 64 + lane] = __fdiv_rn(sm.u.E[r * 64 + lane], psum);
+            __syncthreads();
+            const float q0 = sm.u.E[0];
+            last = 0;
+            if (!(q0 >= P.top_p)) {
+                (void)seq_sum_wave<R>(sm.u.E, n_surv, q0, 1, P.top_p, hit);
+                last = hit < 0 ? n_surv - 1 : hit;
+            }
+        } else {
+            const float psum = wave_chain_sum(sm.u.E, n_surv, 0.0f);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r < nr) sm.u.E[r * 64 + lane] = __fdiv_rn(sm.u.E[r * 64 + lane], psum);
+            __syncthreads();
+            last = wave_chain_cross(sm.u.E, n_surv, P.top_p);
+        }
+        n_kept = uni(last + 1);
+        if (n_kept < n_surv &&
+            desc_key_value(sm.list[n_kept - 1]) == desc_key_value(sm.list[n_kept]))
+            rflags |= CBX_INFO_TOPP_TIE;
+        __syncthreads();
+    }
+
+    // ---- min-p [extension], repetition penalty (main.cpp:774-781) ----
+    // kept entries: list positions [0, n_kept); per entry in registers
+    const int nk = (n_kept + 63) >> 6;
+    float val[R];
+    int idr[R];
+    uint32_t kept = 0;
+    {
+        const int nkv = fresh(n_kept);
+        const float mx_kept = mx_surv;  // the best kept score before the penalty
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < nk) {
+                const int i = r * 64 + lane;
+                const uint64_t key = sm.list[i];
+                bool kp = i < nkv;
+                float v = desc_key_value(key);
+                const int id = kp ? (int)(uint32_t)key : 0;
+                if (P.min_p > 0.0f)
+                    kp = kp && !(expf_libm_branchless(__fsub_rn(v, mx_kept), sm.tab) < P.min_p);
+                if (use_pen && kp && bit_of(sm.seen, id))
+                    v = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty) : __fmul_rn(v, P.repeat_penalty);
+                val[r] = v;
+                idr[r] = id;
+                kept |= (kp ? 1u : 0u) << r;
+                atomicOr(&sm.keptw[kp ? id >> 5 : 8 * Q], 1u << (id & 31));  // else: spare
+            }
+        }
+    }
+    // ---- softmax (main.cpp:783-793) ----
+    float m2 = kNegInf;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < nk) m2 = ((kept >> r) & 1u) ? fmaxf(m2, val[r]) : m2;
+    const float mx2 = wave_max_dpp(m2);
+    __syncthreads();
+    // id-order ranks of the kept ids: word offsets
+    constexpr int WPL = (8 * Q + 63) / 64;
+    int n_final;
+    {
+        int cw[WPL];
+        int loc = 0;
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) {
+            const int w = lane * WPL + q;
+            cw[q] = (w < W) ? __popc(sm.keptw[w]) : 0;
+            loc += cw[q];
+        }
+        int basew = wave_excl_scan_i(loc, n_final);
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) {
+            const int w = lane * WPL + q;
+            if (w < W) sm.woff[w] = (uint32_t)basew;
+            basew += cw[q];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (r < nk && ((kept >> r) & 1u))
+            sm.u.F[rank_of(sm.keptw, sm.woff, idr[r])] =
+                expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
+    }
+    __syncthreads();
+
+    // ---- greedy or draw (main.cpp:795-800) ----
+    int token = 0;
+    uint32_t oflags = rflags;
+    const bool empty = n_final == 0;  // else psum >= expf(0) = 1
+    float psum2 = 0.0f;
+    bool have_psum2 = false;
+    auto exact_psum2 = [&]() {
+        if (!have_psum2) {
+            psum2 = wave_chain_sum(sm.u.F, n_final, 0.0f);
+            have_psum2 = true;
+        }
+        return psum2;
+    };
+    if (empty) {
+        oflags |= CBX_INFO_EMPTY;
+    } else if (P.temp <= 0.0f) {
+        // first argmax of p_i = e_i / psum over ids (main.cpp:795-797)
+        const float ps = exact_psum2();
+        float best = -1.0f;
+        int first = 0x7fffffff;
+        for (int i = lane; i < n_final; i += 64) {
+            const float p = __fdiv_rn(sm.u.F[i], ps);
+            if (p > best) { best = p; first = i; }  // ascending i: keeps the first
+        }
+        const float b = wave_max_dpp(best);
+        const int rk = wave_min_i_dpp(best == b ? first : 0x7fffffff);
+        token = rk == 0x7fffffff ? 0 : id_of_rank(sm.keptw, sm.woff, W, rk);
+        oflags |= CBX_INFO_GREEDY;
+    } else if (V >= 2) {
+        oflags |= CBX_INFO_DREW;
+        double u;
+        if (a.draw_mode == CBX_DRAW_PHILOX) {
+            const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
+            u = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
+        } else {
+            u = a.uniforms[rs];
+        }
+        const bool last_kept = bit_of(sm.keptw, V - 1);
+        // binary64 prefix of the exp terms in id order, contiguous chunks
+        const int C = (n_final + 63) >> 6;
+        const int r0 = min(lane * C, n_final), r1 = min(r0 + C, n_final);
+        double part = 0.0;
+        for (int r = r0; r < r1; ++r) part = __dadd_rn(part, (double)sm.u.F[r]);
+        double cp = wave_incl_scan_f64(part, lane);
+        const double total = readlane_f64(cp, 63);
+        cp = __dsub_rn(cp, part);  // exclusive
+        const double target = __dmul_rn(u, total);
+        int found = 0x7fffffff;
+        double blo = 0.0, bhi = 0.0;
+        for (int r = r0; r < r1; ++r) {
+            const double before = cp;
+            cp = __dadd_rn(cp, (double)sm.u.F[r]);
+            if (cp >= target) { found = r; blo = before; bhi = cp; break; }
+        }
+        const int rank = wave_min_i_dpp(found);
+        bool certain = false;
+        if (!(u > 0.0)) {
+            token = 0;  // lower_bound of 0 is the first entry
+            certain = true;
+        } else if (rank != 0x7fffffff) {
+            const int L = __builtin_ctzll(__ballot(found == rank));
+            const double inv = __ddiv_rn(1.0, total);
+            const double clo = __dmul_rn(readlane_f64(blo, L), inv);
+            const double chi = __dmul_rn(readlane_f64(bhi, L), inv);
+            const bool lo_ok = rank == 0 || __dsub_rn(u, clo) > kDrawMargin * clo + 1e-30;
+            const bool hi_ok = (rank == n_final - 1 && last_kept) ||
+                               __dsub_rn(chi, u) > kDrawMargin * chi + 1e-30;
+            certain = lo_ok && hi_ok;
+            token = id_of_rank(sm.keptw, sm.woff, W, rank);
+        }
+        if (!certain) {
+            // the reference's arithmetic: float normaliser, double CDF (rare)
+            const float ps = exact_psum2();
+            if (lane == 0) {
+                double sum = 0.0;
+                for (int r = 0; r < n_final; ++r)
+                    sum = __dadd_rn(sum, (double)__fdiv_rn(sm.u.F[r], ps));
+                double acc = 0.0;
+                int rk = -1;
+                for (int r = 0; r < n_final; ++r) {
+                    acc = __dadd_rn(acc, __ddiv_rn((double)__fdiv_rn(sm.u.F[r], ps), sum));
+                    const double c = (r == n_final - 1 && last_kept) ? 1.0 : acc;
+                    if (c >= u) { rk = r; break; }
+                }
+                sm.rk = rk;
+            }
+            __syncthreads();
+            const int rk = sm.rk;
+            token = rk < 0 ? V - 1 : id_of_rank(sm.keptw, sm.woff, W, rk);
+        }
+    }
+    if (lane == 0) {
+        a.tokens[rs] = token;
+        if (a.info) a.info[rs] = oflags;
+    }
+    if (a.probs) {
+        const float ps = empty ? 0.0f : exact_psum2();
+        float* prow = a.probs + rs * a.ld_probs;
+        for (int i = lane; i < V; i += 64)
+            prow[i] = (!empty && bit_of(sm.keptw, i))
+                          ? __fdiv_rn(sm.u.F[rank_of(sm.keptw, sm.woff, i)], ps)
+                          : 0.0f;
+    }
+}
+
+template <int Q>
+hipError_t launch_wave(const KernelArgs& a, hipStream_t stream) {
+    const int64_t rows = (int64_t)a.n_steps * a.n_rows;
+    hipLaunchKernelGGL((sample_rows_wave<Q>), dim3((unsigned)rows), dim3(64), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace cbx

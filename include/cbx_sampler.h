@@ -142,6 +142,14 @@ int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream);
 int cbx_debug_expf(cbx_sampler* s, const float* in, float* out, int64_t n, void* stream);
 int cbx_debug_philox(cbx_sampler* s, uint64_t seed, const uint64_t* stream_ids,
                      uint64_t step, int32_t n, double* out, void* stream);
+/* Diagnostics: the device's exact left-to-right binary32 running sum (the
+ * evaluation the sampler uses for the reference's float accumulations,
+ * main.cpp:759-768 and :786-790).  Case c sums terms[offsets[c] ..
+ * offsets[c+1]) (finite, >= 0, 1 to 2048 of them) into sum[c]; when thr is given
+ * and thr[c] > 0, hit[c] is the first index (from the case's start) whose
+ * running sum is >= thr[c], else -1.  Device memory, async. */
+int cbx_debug_seqsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
+                     const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream);
 
 /* Thread-local description of the last error on this thread ("" if none). */
 const char* cbx_last_error(void);

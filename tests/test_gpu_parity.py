@@ -118,6 +118,28 @@ def test_device_expf_exhaustive(cbx, torch_cuda):
     assert bad == 0
 
 
+def test_device_running_sum_scan(cbx, torch_cuda):
+    # The device's exact segment scan against numpy's left-to-right float32
+    # accumulation, bit for bit, and the threshold index of the top-p search.
+    import seqsum_cases
+    torch = torch_cuda
+    mod, s = cbx
+    t, off, thr, want_sum, want_hit = seqsum_cases.make_cases(6000, 11)
+    say(f"running-sum scan: {len(off) - 1} cases, {t.size} terms")
+    dt = torch.from_numpy(t).cuda()
+    doff = torch.from_numpy(off).cuda()
+    dthr = torch.from_numpy(thr).cuda()
+    sums = torch.zeros(len(off) - 1, dtype=torch.float32, device="cuda")
+    hits = torch.full((len(off) - 1,), -9, dtype=torch.int32, device="cuda")
+    s.debug_seqsum(dt, doff, dthr, sums, hits)
+    torch.cuda.synchronize()
+    got_sum = sums.cpu().numpy()
+    got_hit = hits.cpu().numpy()
+    has_thr = thr > 0
+    assert np.array_equal(got_sum[~has_thr].view(np.uint32), want_sum[~has_thr].view(np.uint32))
+    assert np.array_equal(got_hit[has_thr], want_hit[has_thr])
+
+
 def test_device_philox_matches_oracle(cbx, torch_cuda):
     torch = torch_cuda
     mod, s = cbx
@@ -247,6 +269,40 @@ def test_masked_stress(cbx, torch_cuda):
     assert np.all(tg[d["force_stop"] == 1] == d["stop"])
 
 
+@pytest.mark.parametrize("V", [6563, 8194, 3000])
+def test_masked_one_wave(cbx, torch_cuda, V):
+    """Allowed bitmask, forced stop, min-p and penalty at vocabularies the
+    one-wave kernel takes (survivor capacity 1024)."""
+    w = pkg.workloads()
+    d = w.masked_stress(B=256, V=V, seed=0x5EED5 + V)
+    u = O.mt_canonical(11 + V, d["B"])
+    say(f"masked one-wave B=256 V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], allowed=d["allowed"], force_stop=d["force_stop"],
+                           stop=d["stop"], max_survivors=1024)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"],
+                             allowed=d["allowed"], force_stop=d["force_stop"], stop=d["stop"])
+    parity.compare(f"masked_one_wave_{V}", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_cfg_pair_one_wave(cbx, torch_cuda):
+    """CFG combine on the one-wave kernel: V=8194 cond/uncond rows with top-k
+    1000 (so the survivors fit its list), fixed history."""
+    w = pkg.workloads()
+    d = w.cfg_pair(steps=256, seed=0x5EED22)
+    p = dict(d["params"])
+    p["top_k"] = 1000
+    rng = np.random.default_rng(3)
+    hist = rng.integers(0, 8194, size=(1, 700)).astype(np.int32)
+    hl = np.array([700], np.int32)
+    u = O.mt_canonical(77, 256)
+    say("cfg_pair one-wave 256 steps")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["cond"], [p], u, hist, hl, n_steps=256,
+                           uncond=d["uncond"], max_survivors=1024)
+    tr, ir, pr = oracle_rows(d["cond"], [p], u, hist, hl, uncond=d["uncond"])
+    parity.compare("cfg_pair_one_wave", tg, ig, tr, ir, u, pg, pr)
+
+
 EDGE_CASES = [
     # name, V, params, logits builder, u
     ("all_masked", 64, dict(top_k=10, top_p=0.9, temp=0.8, repeat_penalty=1.2),
@@ -308,6 +364,27 @@ def test_edge_cases(cbx, torch_cuda, case):
     assert tok == tg[0] and info == ig[0]
     if not (ir[0] & parity.INFO_TOPP_TIE):
         assert tok == tr[0]
+
+
+# cases whose survivors after top-k fit the one-wave kernel's list
+WAVE_EDGE = [c for c in EDGE_CASES if c[1] <= 1024 or 0 < c[2].get("top_k", 0) <= 1024]
+
+
+@pytest.mark.parametrize("case", WAVE_EDGE, ids=[c[0] for c in WAVE_EDGE])
+def test_edge_cases_one_wave(cbx, torch_cuda, case):
+    """The same rows through the one-wave kernel (survivor capacity 1024)."""
+    name, V, p, build, u = case
+    rng = np.random.default_rng(abs(hash(name)) % 2**32)
+    pd = dict(min_p=0.0, cfg_weight=0.0)
+    pd.update(p)
+    x = build(V, rng)[None, :]
+    hist = rng.integers(-5, V + 5, size=(1, 64)).astype(np.int32)
+    hl = np.array([64], np.int32)
+    uu = np.array([u])
+    say(f"edge one-wave {name} V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, [pd], uu, hist, hl, max_survivors=1024)
+    tr, ir, pr = oracle_rows(x, [pd], uu, hist, hl)
+    parity.compare(f"edge_wave_{name}", tg, ig, tr, ir, uu, pg, pr)
 
 
 def test_row_api_extensions(cbx, torch_cuda):
