@@ -753,6 +753,75 @@ __device__ __forceinline__ float seq_sum_wave(const float* t, int n, float P, in
     return P;
 }
 
+// The same running sum with the terms already in registers: lane l holds
+// terms [l*C, l*C + C) in tr[0, C) (C <= CM, zeros past n), for every
+// segment; terms before i0 count as zero (the identity step).
+template <int CM>
+__device__ __forceinline__ float seq_sum_regs(const float (&tr)[CM], int C, int n, float P, int i0,
+                                              float thr, int& hit) {
+    const int lane = threadIdx.x & 63;
+    hit = -1;
+    n = uni(n);
+    i0 = uni(i0);
+    C = uni(C);
+    const int first = lane * C;
+    while (i0 < n) {
+        const int e = seq_unit_exp(P);
+        const int N0 = (int)ldexpf(P, -e);  // exact integer < 2^24
+        const int p0 = N0 & 1;
+        int nthr = kSeqSat;
+        if (thr > 0.0f) nthr = (int)ceilf(fminf(ldexpf(thr, -e), kSeqClamp));
+        const int target = min(nthr, 1 << 24);
+        SeqTab T = seq_identity();
+#pragma unroll
+        for (int k = 0; k < CM; ++k)
+            if (k < C) T = seq_push(T, seq_step(first + k >= i0 ? tr[k] : 0.0f, e));
+        T = wave_scan_tab(T);
+        SeqTab X = dpp_tab<0x138, 0xf>(T);  // wave_shr:1 -> exclusive
+        const int d_before = p0 ? X.d1 : X.d0;
+        const int c_before = p0 ? (X.q >> 1) & 1 : X.q & 1;
+        const int n_after = N0 + (p0 ? T.d1 : T.d0);
+        const uint64_t reach = __ballot(n_after >= target);
+        if (reach == 0) {
+            const int total = __builtin_amdgcn_readlane(n_after, 63);
+            return ldexpf((float)total, e);  // total < 2^24: exact
+        }
+        const int L = __builtin_ctzll(reach);
+        int kind = 0, idx = 0, nprev = 0;
+        float tc = 0.0f;
+        if (lane == L) {
+            int d = d_before, c = c_before;
+#pragma unroll
+            for (int k = 0; k < CM; ++k) {
+                if (k < C && kind == 0) {
+                    const float t = first + k >= i0 ? tr[k] : 0.0f;
+                    const int nb = N0 + d;
+                    seq_apply(d, c, seq_step(t, e));
+                    if (N0 + d >= (1 << 24)) { kind = 1; idx = first + k; nprev = nb; tc = t; }
+                    else if (N0 + d >= nthr) { kind = 2; idx = first + k; }
+                }
+            }
+        }
+        kind = __builtin_amdgcn_readlane(kind, L);
+        idx = __builtin_amdgcn_readlane(idx, L);
+        nprev = __builtin_amdgcn_readlane(nprev, L);
+        tc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tc), L));
+        if (kind == 2) {
+            hit = idx;
+            return P;
+        }
+        if (kind == 0) return P;  // unreachable for finite terms; bounds the loop
+        // the term that leaves the binade: one ordinary add of the exact sum
+        P = __fadd_rn(ldexpf((float)nprev, e), tc);
+        if (thr > 0.0f && P >= thr) {
+            hit = idx;
+            return P;
+        }
+        i0 = idx + 1;
+    }
+    return P;
+}
+
 // --------------------------------------------------------------- bitmaps
 
 __device__ __forceinline__ int pow2ceil(int n) {

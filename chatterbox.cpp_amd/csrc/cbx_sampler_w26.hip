@@ -2,5 +2,5 @@
 #include "cbx_sampler_wave.h"
 
 namespace cbx {
-hipError_t launch_w26(const KernelArgs& a, hipStream_t stream) { return launch_wave<26>(a, stream); }
+hipError_t launch_w26(const KernelArgs& a, hipStream_t stream) { return launch_wave<26, 16>(a, stream); }
 }  // namespace cbx

@@ -2,5 +2,5 @@
 #include "cbx_sampler_wave.h"
 
 namespace cbx {
-hipError_t launch_w33(const KernelArgs& a, hipStream_t stream) { return launch_wave<33>(a, stream); }
+hipError_t launch_w33(const KernelArgs& a, hipStream_t stream) { return launch_wave<33, 26>(a, stream); }
 }  // namespace cbx

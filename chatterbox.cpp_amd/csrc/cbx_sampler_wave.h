@@ -33,6 +33,8 @@
 // otherwise keep one exec mask per element alive.
 #pragma once
 
+#include <type_traits>
+
 #include "cbx_sampler_impl.h"
 
 namespace cbx {
@@ -53,8 +55,9 @@ struct WaveSmem {
     union {
         uint32_t hist[kWaveBins + 4];  // value bins (+ spare), then sort offsets
         float cand[kWaveCand + 1];     // scores of the top-k bin (+ spare slot)
+        uint64_t candk[kWaveCand];     // (score bits << 32 | id) of the top-k bin
         float E[kWaveCap];             // exp terms in sorted order, then q_i
-        float F[kWaveCap];             // kept exp terms in id order
+        float F[kWaveCap + 1];         // kept exp terms in id order (+ spare slot)
     } u;
     uint64_t list[kWaveCap + 1];  // survivors (+ spare slot): raw, then keys
     int rk;
@@ -119,6 +122,24 @@ __device__ __forceinline__ int wave_min_i_dpp(int x) {
     x = min(x, dpp_i<0x142, 0xa>(0x7fffffff, x));
     x = min(x, dpp_i<0x143, 0xc>(0x7fffffff, x));
     return __builtin_amdgcn_readlane(x, 63);
+}
+
+template <int CTRL, int RM>
+__device__ __forceinline__ double dpp_d(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)dpp_i<CTRL, RM>(0, (int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)dpp_i<CTRL, RM>(0, (int)(uint32_t)(b >> 32));
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// Inclusive scan of doubles over the wave (lanes without a source add +0).
+__device__ __forceinline__ double wave_incl_scan_f64_dpp(double x) {
+    x = __dadd_rn(x, dpp_d<0x111, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x112, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x114, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x118, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x142, 0xa>(x));
+    x = __dadd_rn(x, dpp_d<0x143, 0xc>(x));
+    return x;
 }
 
 __device__ __forceinline__ double readlane_f64(double v, int l) {
@@ -258,7 +279,7 @@ __device__ __forceinline__ void wave_radix_pass(const RowScores& rsc, int shift,
 
 // ------------------------------------------------------------------ kernel
 
-template <int Q>
+template <int Q, int JT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sample_rows_wave(
     KernelArgs a) {
     __shared__ WaveSmem<Q> sm;
@@ -272,6 +293,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     const int cap = min(a.cap, kWaveCap);
     const cbx_params P = a.params[row];
     const int64_t rs = (int64_t)step * a.n_rows + row;
+    CBX_STAMP(0);
 
     // ---- load: 16-byte buffer loads bounded at V floats (main.cpp:733) ----
     // The range check of a raw buffer load is per dword, so the vector that
@@ -296,6 +318,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     rsc.inv_t = __fdiv_rn(1.0f, P.temp);
     rsc.V = V;
     rsc.stop = a.stop_token;
+    // the history ids (first 1024) are requested first: their bitmap is
+    // built while the logits are still arriving
+    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
+    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
+    const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
+    constexpr int HB = 16;  // history ids per lane per batch
+    int hid[HB];
+    if (use_pen) {
+        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
+#pragma unroll
+        for (int u = 0; u < HB; ++u)
+            hid[u] = (u * 64 + lane < hlen)
+                         ? __builtin_amdgcn_raw_buffer_load_b32(rh, (u * 64 + lane) * 4, 0, 0)
+                         : -1;
+    }
     float s[EPL];
 #pragma unroll
     for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
@@ -313,12 +351,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
         sm.keptw[w] = 0u;
     }
     __syncthreads();
-    // ---- history ids -> seen bitmap (main.cpp:775), loads batched 4 deep ----
-    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
-    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
+    // ---- history ids -> seen bitmap (main.cpp:775) ----
     if (use_pen) {
-        const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
-        for (int b = 0; b < hlen; b += 256) {
+#pragma unroll
+        for (int u = 0; u < HB; ++u) {
+            const int t = hid[u];
+            const bool ok = t >= 0 && t < V;
+            atomicOr(&sm.seen[ok ? t >> 5 : 0], ok ? 1u << (t & 31) : 0u);
+        }
+        for (int b = HB * 64; b < hlen; b += 256) {  // histories past 1024 ids
             int t[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -331,9 +372,60 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
         }
     }
     // ---- masks and temperature (main.cpp:735-738) ----
-    int nonfinite = 0;
+    CBX_STAMP(1);
+    // Plain rows (no allowed mask, no forced stop) mask only ids >= V, which
+    // this instantiation meets in vectors j >= JT alone (V > 256*JT); the
+    // others need 4 operations per score and no predicate.
+    const bool plain = !rsc.masked_ids && !rsc.fstop;
     float lo = kPosInf, hi = kNegInf;
-    {
+    bool bad = false, neg_inf = false;  // NaN/+inf seen; -inf among unmasked scores
+    if (plain) {
+        // acc = sum of (v - v): 0 while every unmasked score is finite, NaN
+        // once one is NaN or infinite
+        float acc = 0.0f;
+        const int Vm = fresh(V);
+        auto pass = [&](auto scaled) {
+#pragma unroll
+            for (int j = 0; j < Q; ++j) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float v = s[4 * j + c];
+                    if (decltype(scaled)::value) v = __fmul_rn(v, rsc.inv_t);
+                    if (j < JT) {
+                        acc = __fadd_rn(acc, __fsub_rn(v, v));
+                        lo = fminf(lo, v);
+                    } else {
+                        const bool pad = 256 * j + 4 * lane + c >= Vm;
+                        acc = __fadd_rn(acc, pad ? 0.0f : __fsub_rn(v, v));
+                        v = pad ? kNegInf : v;
+                        lo = fminf(lo, pad ? kPosInf : v);
+                    }
+                    hi = fmaxf(hi, v);
+                    s[4 * j + c] = v;
+                }
+            }
+        };
+        if (rsc.scale) pass(std::true_type{});
+        else pass(std::false_type{});
+        const bool spec = __ballot(acc != 0.0f) != 0;  // NaN != 0
+        if (spec) {
+            // rare: tell NaN/+inf (reported) from -inf logits, and take the
+            // minimum over finite scores only
+            int nf = 0, ni = 0;
+            lo = kPosInf;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float v = s[e];
+                const bool pad = (e >> 2) >= JT && 256 * (e >> 2) + 4 * lane + (e & 3) >= Vm;
+                nf |= (!pad && (v != v || v == kPosInf)) ? 1 : 0;
+                ni |= (!pad && v == kNegInf) ? 1 : 0;
+                lo = fminf(lo, v == kNegInf ? kPosInf : v);
+            }
+            bad = wave_sum_dpp(nf) != 0;
+            neg_inf = wave_sum_dpp(ni) != 0;
+        }
+    } else {
+        int nonfinite = 0;
         const int Vm = fresh(V);
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
@@ -346,25 +438,185 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
                 hi = fmaxf(hi, v);
             }
         }
+        bad = wave_sum_dpp(nonfinite) != 0;
+        neg_inf = true;  // masked ids are -inf
     }
     lo = wave_min_dpp(lo);
     hi = wave_max_dpp(hi);
-    const int bad = wave_sum_dpp(nonfinite) != 0;
     const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
+    CBX_STAMP(2);
 
     // ---- top-k (main.cpp:740-748) ----
     const int k = P.top_k;
     const bool use_topk = k > 0 && k < V;
     float thr = kNegInf;  // survivors: s > thr
+    int n_surv = -1;      // >= 0 once the survivor list is built
     if (use_topk) {
         int above = 0;
         bool done = false;
         const float range = __fsub_rn(hi, lo);
         const float bscale = __fdiv_rn((float)kWaveBins, range);
-        if (!bad && range > 0.0f && bscale < kPosInf) {
-            // bin(v) = fma(v, scale, -lo*scale) clamped to [0, NB-1] is
-            // non-decreasing in v; -inf goes to the spare bin NB
-            const float nlo = -__fmul_rn(lo, bscale);
+        const float nlo = -__fmul_rn(lo, bscale);
+        if (!bad && !neg_inf && range > 0.0f && bscale < kPosInf) {
+            // Plain rows: bin(v) = trunc(med3(fma(v, scale, -lo*scale), 0, NB-1))
+            // is non-decreasing in v; the V..256Q padding (-inf) lands in bin 0
+            // and is taken off its count.
+#pragma unroll
+            for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < EPL; ++e)
+                atomicAdd(&sm.u.hist[(int)__builtin_amdgcn_fmed3f(__fmaf_rn(s[e], bscale, nlo),
+                                                                   0.0f, (float)(kWaveBins - 1))],
+                          1u);
+            __syncthreads();
+                        constexpr int BPL = kWaveBins / 64;
+            uint32_t cnt[BPL];
+            int tot = 0;
+#pragma unroll
+            for (int q = 0; q < BPL; ++q) {
+                const int b = kWaveBins - 1 - (lane * BPL + q);  // descending bins
+                cnt[q] = sm.u.hist[b] - (b == 0 ? (uint32_t)(256 * Q - V) : 0u);
+                tot += (int)cnt[q];
+            }
+            int n_fin;
+            const int excl = wave_excl_scan_i(tot, n_fin);
+            if (n_fin <= k) {
+                thr = kNegInf;  // at most k finite scores: nothing is removed
+                above = n_fin;
+                done = true;
+            } else {
+                const bool mine = excl <= k && k < excl + tot;
+                int bsel = 0, above_bins = 0, nsel = 0;
+                if (mine) {
+                    int run = excl;
+                    bool found = false;
+#pragma unroll
+                    for (int q = 0; q < BPL; ++q) {
+                        if (!found && run + (int)cnt[q] > k) {
+                            bsel = kWaveBins - 1 - (lane * BPL + q);
+                            above_bins = run;
+                            nsel = (int)cnt[q];
+                            found = true;
+                        }
+                        run += (int)cnt[q];
+                    }
+                }
+                const int L = __builtin_ctzll(__ballot(mine));
+                bsel = __builtin_amdgcn_readlane(bsel, L);
+                above_bins = __builtin_amdgcn_readlane(above_bins, L);
+                nsel = __builtin_amdgcn_readlane(nsel, L);
+                // Score boundaries of the selected bin: B0 = least float with
+                // bin >= bsel, B1 = least float with bin >= bsel + 1 (+inf past
+                // the top bin).  bin(v) >= b  <=>  fma(v, scale, -lo*scale) >= b,
+                // probed over 64 consecutive floats around the real root.
+                auto boundary = [&](int b, float& B) -> bool {
+                    const float v0 = (float)(((double)b - (double)nlo) / (double)bscale);
+                    const float v = okey_inv(okey(v0) + (uint32_t)(lane - 32));
+                    const uint64_t m = __ballot(__fmaf_rn(v, bscale, nlo) >= (float)b);
+                    if (m == 0 || m == ~0ull) return false;
+                    const int L0 = __builtin_ctzll(m);
+                    if (m != (~0ull << L0)) return false;
+                    B = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                      __builtin_bit_cast(int, v), L0));
+                    return true;
+                };
+                float B0 = kNegInf, B1 = kPosInf;
+                const bool have_b = bsel >= 1 && nsel <= kWaveCand && boundary(bsel, B0) &&
+                                    (bsel == kWaveBins - 1 || boundary(bsel + 1, B1));
+                __syncthreads();  // histogram reads done: the candidates reuse it
+                                if (have_b && above_bins + nsel <= kWaveCap) {
+                    // One pass, no exec-mask changes: every score >= B0 (the
+                    // survivors >= B1 and the selected bin's candidates) joins
+                    // the list; the rest write its spare slot.
+                    auto val_of = [](uint64_t pk) {
+                        return __builtin_bit_cast(float, (uint32_t)(pk >> 32));
+                    };
+                    int n = 0;
+#pragma unroll
+                    for (int j = 0; j < Q; ++j) {
+                        const float B0j = fresh_v(B0);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const float v = s[4 * j + c];
+                            const bool ge = v >= B0j;
+                            const uint64_t m = __ballot(ge);
+                            const int at = ballot_rank(m) + n;
+                            sm.list[ge ? at : kWaveCap] =
+                                ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) |
+                                (uint32_t)(256 * j + 4 * lane + c);
+                            n += __popcll(m);
+                        }
+                    }
+                    __syncthreads();
+                                        const int nr0 = (n + 63) >> 6;
+                    int nc = 0;
+                    uint64_t x[kWaveRows];  // the list, read once
+#pragma unroll
+                    for (int g = 0; g < kWaveRows; g += 4) {
+                        if (g < nr0) {
+#pragma unroll
+                            for (int r = g; r < g + 4; ++r) x[r] = sm.list[r * 64 + lane];
+                        }
+                    }
+                    if (n == above_bins + nsel) {
+                        // the candidates: list entries below B1
+#pragma unroll
+                        for (int r = 0; r < kWaveRows; ++r) {
+                            if (r < nr0) {
+                                const int i = r * 64 + lane;
+                                const bool inb = i < n && val_of(x[r]) < B1;
+                                const uint64_t m = __ballot(inb);
+                                const int at = ballot_rank(m) + nc;
+                                sm.u.candk[(inb && at < kWaveCand) ? at : kWaveCand] = x[r];
+                                nc += __popcll(m);
+                            }
+                        }
+                    }
+                    __syncthreads();
+                    if (n == above_bins + nsel && nc == nsel) {
+                        const int rem = k - above_bins;  // 0 <= rem < nc
+                        float tv = kNegInf;
+                        int tgt = 0;
+                        bool hitc = false;
+                        for (int c0 = lane; c0 < nc; c0 += 64) {
+                            const float v = val_of(sm.u.candk[c0]);
+                            int gt = 0, ge = 0;
+                            for (int t = 0; t < nc; ++t) {
+                                const float w = val_of(sm.u.candk[t]);
+                                gt += (w > v) ? 1 : 0;
+                                ge += (w >= v) ? 1 : 0;
+                            }
+                            if (gt <= rem && rem < ge) { tv = v; tgt = gt; hitc = true; }
+                        }
+                        const int L2 = __builtin_ctzll(__ballot(hitc));
+                        thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                             __builtin_bit_cast(int, tv), L2));
+                        above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
+                        if (above < k) thr = __fsub_rn(thr, 1e-10f);
+                        if (!(thr < B0)) {
+                            // survivors: entries > thr, compacted in place
+                            int n2 = 0;
+#pragma unroll
+                            for (int r = 0; r < kWaveRows; ++r) {
+                                if (r < nr0) {
+                                    const bool keep = r * 64 + lane < n && val_of(x[r]) > thr;
+                                    const uint64_t m = __ballot(keep);
+                                    const int at = ballot_rank(m) + n2;
+                                    sm.list[keep ? at : kWaveCap] = x[r];
+                                    n2 += __popcll(m);
+                                }
+                            }
+                            n_surv = n2;
+                        }
+                        done = true;  // thr < B0 (nudge past the bin): the full pass below
+                    }
+                    __syncthreads();
+                }
+            }
+        }
+        if (!done && !bad && range > 0.0f && bscale < kPosInf) {
+            // bins with -inf sent to the spare bin NB (masked rows, -inf logits)
             auto bin_of = [&](float v) -> int {
                 const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bscale, nlo), 0.0f,
                                                            (float)(kWaveBins - 1));
@@ -450,6 +702,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
                     done = true;
                 }
             }
+            if (done) {
+                if (above < k) thr = __fsub_rn(thr, 1e-10f);
+            }
         }
         if (!done) {
             // 8-bit radix select over all ids (NaN / inf / degenerate rows)
@@ -468,16 +723,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
                 for (int c = 0; c < 4; ++c) n_above += (v[c] > thr) ? 1 : 0;
             }
             above = wave_sum_dpp(n_above);
+            if (above < k) thr = __fsub_rn(thr, 1e-10f);
         }
-        if (above < k) thr = __fsub_rn(thr, 1e-10f);
     }
+    CBX_STAMP(3);
 
     // ---- survivors -> LDS list of (score bits << 32 | id) ----
     // keep = score != -inf and not (top-k and score <= thr); without NaN that
     // is score > thr (thr = -inf when nothing is cut).  Dropped items and
     // items past the list write its spare slot.
-    int n_surv;
-    {
+    if (n_surv < 0) {
         int n = 0;
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
@@ -495,6 +750,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
         }
         n_surv = n;
     }
+    CBX_STAMP(4);
     if (n_surv > cap) {
         if (lane == 0) {
             a.tokens[rs] = -1;
@@ -509,18 +765,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     __syncthreads();
     // raw entries -> composite keys (descending score, ascending id), in place;
     // positions [n_surv, 64*nr) become the maximum key
+    // Rows of the list are handled 4 at a time under one uniform branch, so
+    // their LDS accesses overlap; rows past the list only touch unused slots.
     const int nr = (n_surv + 63) >> 6;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r < nr) {
-            const int i = r * 64 + lane;
-            const uint64_t w = sm.list[i];
-            const uint64_t key =
-                desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w);
-            sm.list[i] = (i < n_surv) ? key : ~0ull;
+    for (int g = 0; g < R; g += 4) {
+        if (g < nr) {
+#pragma unroll
+            for (int r = g; r < g + 4; ++r) {
+                const int i = r * 64 + lane;
+                const uint64_t w = sm.list[i];
+                const uint64_t key =
+                    desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w);
+                sm.list[i] = (i < n_surv) ? key : ~0ull;
+            }
         }
     }
     __syncthreads();
+    CBX_STAMP(5);
 
     uint32_t rflags = flags;
     const bool use_topp = P.top_p < 1.0f && n_surv > 0;
@@ -542,18 +804,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             __syncthreads();
             const int nv = fresh(n_surv);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if (r < nr) {
-                    const int i = r * 64 + lane;
-                    x[r] = sm.list[i];
-                    const float v = desc_key_value(x[r]);
-                    const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, sscale, nslo), 0.0f,
-                                                               (float)(kWaveBins - 1));
-                    rb[r] = (i < nv) ? kWaveBins - 1 - b : kWaveBins;  // NB: spare
-                    slot[r] = (int)atomicAdd(&sm.u.hist[rb[r]], 1u);
+            for (int g = 0; g < R; g += 4) {
+                if (g < nr) {
+#pragma unroll
+                    for (int r = g; r < g + 4; ++r) {
+                        const int i = r * 64 + lane;
+                        x[r] = sm.list[i];
+                        const float v = desc_key_value(x[r]);
+                        const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, sscale, nslo),
+                                                                   0.0f, (float)(kWaveBins - 1));
+                        rb[r] = (i < nv) ? kWaveBins - 1 - b : kWaveBins;  // NB: spare
+                        slot[r] = (int)atomicAdd(&sm.u.hist[rb[r]], 1u);
+                    }
                 }
             }
             __syncthreads();
+            CBX_STAMP(13);
             constexpr int BPL = kWaveBins / 64;
             uint32_t cnt[BPL];
             int tot = 0;
@@ -574,28 +840,43 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             if (lane < 2) sm.u.hist[kWaveBins + lane] = (uint32_t)n_surv;  // spare: empty
             if (__ballot(big > (uint32_t)kWaveSortMax) == 0) {
                 __syncthreads();
+                CBX_STAMP(14);
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    if (r < nr) {
-                        const int dst = rb[r] < kWaveBins ? (int)sm.u.hist[rb[r]] + slot[r]
-                                                          : kWaveCap;
-                        sm.list[dst] = x[r];
+                for (int g = 0; g < R; g += 4)
+                    if (g < nr) {
+#pragma unroll
+                        for (int r = g; r < g + 4; ++r) {
+                            const int dst = rb[r] < kWaveBins ? (int)sm.u.hist[rb[r]] + slot[r]
+                                                              : kWaveCap;
+                            sm.list[dst] = x[r];
+                        }
                     }
                 __syncthreads();
+                CBX_STAMP(15);
                 int fin[R];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    if (r < nr) {
+                    if (r < ((nr + 3) & ~3)) {
                         const int s0 = (int)sm.u.hist[rb[r]], s1 = (int)sm.u.hist[rb[r] + 1];
                         int rank = 0;
-                        for (int t = s0; t < s1; ++t) rank += (sm.list[t] < x[r]) ? 1 : 0;
+                        for (int t = s0; t < s1; t += 4) {  // 4 reads in flight
+                            const uint64_t k0 = sm.list[t];
+                            const uint64_t k1 = sm.list[min(t + 1, kWaveCap)];
+                            const uint64_t k2 = sm.list[min(t + 2, kWaveCap)];
+                            const uint64_t k3 = sm.list[min(t + 3, kWaveCap)];
+                            rank += (k0 < x[r]) + (t + 1 < s1 && k1 < x[r]) +
+                                    (t + 2 < s1 && k2 < x[r]) + (t + 3 < s1 && k3 < x[r]);
+                        }
                         fin[r] = rb[r] < kWaveBins ? s0 + rank : kWaveCap;
                     }
                 }
                 __syncthreads();
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    if (r < nr) sm.list[fin[r]] = x[r];
+                for (int g = 0; g < R; g += 4)
+                    if (g < nr) {
+#pragma unroll
+                        for (int r = g; r < g + 4; ++r) sm.list[fin[r]] = x[r];
+                    }
                 sorted = true;
             }
         }
@@ -621,31 +902,81 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
         }
         __syncthreads();
         // ---- top-p (main.cpp:750-772) ----
+        CBX_STAMP(6);
         mx_surv = desc_key_value(sm.list[0]);  // sorted[0]
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nr) {
-                const int i = r * 64 + lane;
-                sm.u.E[i] = expf_libm_branchless(__fsub_rn(desc_key_value(sm.list[i]), mx_surv),
-                                                 sm.tab);
-            }
-        }
-        __syncthreads();
         int hit;
         int last;
         if (!bad) {
-            const float psum = seq_sum_wave<R>(sm.u.E, n_surv, sm.u.E[0], 1, 0.0f, hit);
+            // e_i in registers, lane l holding sorted positions [l*C, l*C + C)
+            // (C odd: the strided LDS reads fall in distinct banks)
+            constexpr int CM = kWaveRows + 1;
+            const int C = ((n_surv + 63) >> 6) | 1;
+            float ev[CM];
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r < nr) sm.u.E[r * 64 + lane] = __fdiv_rn(sm.u.E[r * 64 + lane], psum);
-            __syncthreads();
-            const float q0 = sm.u.E[0];
-            last = 0;
-            if (!(q0 >= P.top_p)) {
-                (void)seq_sum_wave<R>(sm.u.E, n_surv, q0, 1, P.top_p, hit);
-                last = hit < 0 ? n_surv - 1 : hit;
+            for (int q = 0; q < CM; ++q) {
+                if (q < C) {
+                    const int i = lane * C + q;
+                    const float v = desc_key_value(sm.list[min(i, kWaveCap)]);
+                    ev[q] = i < n_surv ? expf_libm_branchless(__fsub_rn(v, mx_surv), sm.tab) : 0.0f;
+                }
+            }
+            CBX_STAMP(7);
+            const float e0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                           __builtin_bit_cast(int, ev[0]), 0));
+            const float psum = seq_sum_regs<CM>(ev, C, n_surv, e0, 1, 0.0f, hit);
+            CBX_STAMP(8);
+#pragma unroll
+            for (int q = 0; q < CM; ++q)
+                if (q < C) ev[q] = __fdiv_rn(ev[q], psum);  // 0 stays 0
+            // First i with cum_i = q_0 + ... + q_i (binary32, in order) >= top_p.
+            // The binary64 prefix X_i of the same q's differs from cum_i by at
+            // most i half-ulps of cum_i (one rounding per add): where X_i is
+            // further than that from top_p for the deciding indices the answer
+            // is certain; otherwise the exact running sum decides.
+            const double p = (double)P.top_p;
+            double part = 0.0;
+#pragma unroll
+            for (int q = 0; q < CM; ++q)
+                if (q < C) part = __dadd_rn(part, (double)ev[q]);
+            double x = __dsub_rn(wave_incl_scan_f64_dpp(part), part);
+            int c_hi = 0x7fffffff, c_lo = 0x7fffffff;
+#pragma unroll
+            for (int q = 0; q < CM; ++q) {
+                if (q < C) {
+                    const int i = lane * C + q;
+                    x = __dadd_rn(x, (double)ev[q]);
+                    const double cmax = __dmul_rn(x, 1.0 + 0x1p-12);
+                    const int ex = (int)((__builtin_bit_cast(uint64_t, cmax) >> 52) & 0x7ff) - 1023;
+                    const double err = __dadd_rn(
+                        __dmul_rn((double)i, ldexp(1.0, max(ex, -126) - 24)), 1e-12);
+                    const bool in = i < n_surv;
+                    c_hi = (in && c_hi == 0x7fffffff && __dadd_rn(x, err) >= p) ? i : c_hi;
+                    c_lo = (in && c_lo == 0x7fffffff && __dsub_rn(x, err) >= p) ? i : c_lo;
+                }
+            }
+            c_hi = wave_min_i_dpp(c_hi);
+            c_lo = wave_min_i_dpp(c_lo);
+            if (c_hi == c_lo) {
+                last = c_hi == 0x7fffffff ? n_surv - 1 : c_hi;
+            } else {
+                const float q0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                               __builtin_bit_cast(int, ev[0]), 0));
+                last = 0;
+                if (!(q0 >= P.top_p)) {
+                    (void)seq_sum_regs<CM>(ev, C, n_surv, q0, 1, P.top_p, hit);
+                    last = hit < 0 ? n_surv - 1 : hit;
+                }
             }
         } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (r < nr) {
+                    const int i = r * 64 + lane;
+                    sm.u.E[i] = expf_libm_branchless(
+                        __fsub_rn(desc_key_value(sm.list[i]), mx_surv), sm.tab);
+                }
+            }
+            __syncthreads();
             const float psum = wave_chain_sum(sm.u.E, n_surv, 0.0f);
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -654,6 +985,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             last = wave_chain_cross(sm.u.E, n_surv, P.top_p);
         }
         n_kept = uni(last + 1);
+        CBX_STAMP(9);
         if (n_kept < n_surv &&
             desc_key_value(sm.list[n_kept - 1]) == desc_key_value(sm.list[n_kept]))
             rflags |= CBX_INFO_TOPP_TIE;
@@ -670,21 +1002,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
         const int nkv = fresh(n_kept);
         const float mx_kept = mx_surv;  // the best kept score before the penalty
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nk) {
-                const int i = r * 64 + lane;
-                const uint64_t key = sm.list[i];
-                bool kp = i < nkv;
-                float v = desc_key_value(key);
-                const int id = kp ? (int)(uint32_t)key : 0;
-                if (P.min_p > 0.0f)
-                    kp = kp && !(expf_libm_branchless(__fsub_rn(v, mx_kept), sm.tab) < P.min_p);
-                if (use_pen && kp && bit_of(sm.seen, id))
-                    v = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty) : __fmul_rn(v, P.repeat_penalty);
-                val[r] = v;
-                idr[r] = id;
-                kept |= (kp ? 1u : 0u) << r;
-                atomicOr(&sm.keptw[kp ? id >> 5 : 8 * Q], 1u << (id & 31));  // else: spare
+        for (int g = 0; g < R; g += 4) {
+            if (g < nk) {
+#pragma unroll
+                for (int r = g; r < g + 4; ++r) {
+                    const int i = r * 64 + lane;
+                    const uint64_t key = sm.list[i];
+                    bool kp = i < nkv;
+                    float v = desc_key_value(key);
+                    const int id = kp ? (int)(uint32_t)key : 0;
+                    if (P.min_p > 0.0f)
+                        kp = kp &&
+                             !(expf_libm_branchless(__fsub_rn(v, mx_kept), sm.tab) < P.min_p);
+                    if (use_pen) {
+                        const bool hit = kp && bit_of(sm.seen, id);
+                        const float pv = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty)
+                                                  : __fmul_rn(v, P.repeat_penalty);
+                        v = hit ? pv : v;
+                    }
+                    val[r] = v;
+                    idr[r] = id;
+                    kept |= (kp ? 1u : 0u) << r;
+                    atomicOr(&sm.keptw[kp ? id >> 5 : 8 * Q], kp ? 1u << (id & 31) : 0u);
+                }
             }
         }
     }
@@ -692,8 +1032,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     float m2 = kNegInf;
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        if (r < nk) m2 = ((kept >> r) & 1u) ? fmaxf(m2, val[r]) : m2;
+        if (r < ((nk + 3) & ~3)) m2 = ((kept >> r) & 1u) ? fmaxf(m2, val[r]) : m2;
     const float mx2 = wave_max_dpp(m2);
+    CBX_STAMP(10);
     __syncthreads();
     // id-order ranks of the kept ids: word offsets
     constexpr int WPL = (8 * Q + 63) / 64;
@@ -717,12 +1058,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r < nk && ((kept >> r) & 1u))
-            sm.u.F[rank_of(sm.keptw, sm.woff, idr[r])] =
-                expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
+    for (int g = 0; g < R; g += 4) {
+        if (g < nk) {
+#pragma unroll
+            for (int r = g; r < g + 4; ++r) {
+                const bool kp = (kept >> r) & 1u;
+                const int at = kp ? rank_of(sm.keptw, sm.woff, idr[r]) : kWaveCap;  // spare
+                sm.u.F[at] = expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
+            }
+        }
     }
     __syncthreads();
+    CBX_STAMP(11);
 
     // ---- greedy or draw (main.cpp:795-800) ----
     int token = 0;
@@ -815,6 +1162,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             token = rk < 0 ? V - 1 : id_of_rank(sm.keptw, sm.woff, W, rk);
         }
     }
+    CBX_STAMP(12);
     if (lane == 0) {
         a.tokens[rs] = token;
         if (a.info) a.info[rs] = oflags;
@@ -829,10 +1177,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     }
 }
 
-template <int Q>
+// Q: scores per lane / 4 (V <= 256*Q); JT: V > 256*JT for every launch.
+template <int Q, int JT>
 hipError_t launch_wave(const KernelArgs& a, hipStream_t stream) {
     const int64_t rows = (int64_t)a.n_steps * a.n_rows;
-    hipLaunchKernelGGL((sample_rows_wave<Q>), dim3((unsigned)rows), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((sample_rows_wave<Q, JT>), dim3((unsigned)rows), dim3(64), 0, stream, a);
     return hipGetLastError();
 }
 
