@@ -46,6 +46,12 @@ constexpr int kWaveSortMax = 64;  // largest bin the counting sort ranks directl
 constexpr int kWaveRows = kWaveCap / 64;
 constexpr double kDrawMargin = 3e-7;
 
+// Waves per SIMD the register allocation aims for (the row's scores take
+// 4*Q registers; the rest of the kernel is kept within the same budget).
+#ifndef WAVE_WPE
+#define WAVE_WPE 3
+#endif
+
 template <int Q>
 struct WaveSmem {
     uint64_t tab[32];
@@ -280,7 +286,7 @@ __device__ __forceinline__ void wave_radix_pass(const RowScores& rsc, int shift,
 // ------------------------------------------------------------------ kernel
 
 template <int Q, int JT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sample_rows_wave(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) void sample_rows_wave(
     KernelArgs a) {
     __shared__ WaveSmem<Q> sm;
     constexpr int EPL = 4 * Q;  // scores per lane
@@ -373,13 +379,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     }
     // ---- masks and temperature (main.cpp:735-738) ----
     CBX_STAMP(1);
-    // Plain rows (no allowed mask, no forced stop) mask only ids >= V, which
+    // Masked rows first set the ids the mask drops to -inf (the allowed row
+    // is staged in LDS, in the kept-bitmap words that are cleared again after).
+    // Then every row takes the same pass: only ids >= V are padding, which
     // this instantiation meets in vectors j >= JT alone (V > 256*JT); the
     // others need 4 operations per score and no predicate.
     const bool plain = !rsc.masked_ids && !rsc.fstop;
     float lo = kPosInf, hi = kNegInf;
     bool bad = false, neg_inf = false;  // NaN/+inf seen; -inf among unmasked scores
-    if (plain) {
+    if (!plain) {
+        if (rsc.masked_ids)
+            for (int w = lane; w < W; w += 64)
+                sm.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t word = rsc.masked_ids ? sm.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int id = 256 * j + 4 * lane + c;
+                const bool m = !((word >> (4 * (lane & 7) + c)) & 1u) |
+                               (rsc.fstop & (id != rsc.stop));
+                s[4 * j + c] = m ? kNegInf : s[4 * j + c];
+            }
+        }
+        __syncthreads();
+        for (int w = lane; w < 8 * Q + 1; w += 64) sm.keptw[w] = 0u;
+    }
+    {
         // acc = sum of (v - v): 0 while every unmasked score is finite, NaN
         // once one is NaN or infinite
         float acc = 0.0f;
@@ -424,27 +451,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             bad = wave_sum_dpp(nf) != 0;
             neg_inf = wave_sum_dpp(ni) != 0;
         }
-    } else {
-        int nonfinite = 0;
-        const int Vm = fresh(V);
-#pragma unroll
-        for (int j = 0; j < Q; ++j) {
-            rsc.finish4(j, lane, &s[4 * j], Vm);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float v = s[4 * j + c];
-                nonfinite |= ((v != v) | (v == kPosInf)) ? 1 : 0;
-                lo = fminf(lo, v == kNegInf ? kPosInf : v);
-                hi = fmaxf(hi, v);
-            }
-        }
-        bad = wave_sum_dpp(nonfinite) != 0;
-        neg_inf = true;  // masked ids are -inf
     }
     lo = wave_min_dpp(lo);
     hi = wave_max_dpp(hi);
     const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
     CBX_STAMP(2);
+    // The scores again, reloaded four at a time, for the passes after the
+    // fast top-k path (so the register copy of the row need not stay live).
+    auto each_score = [&](auto&& f) {
+#pragma unroll 1
+        for (int j = 0; j < Q; ++j) {
+            float v[4];
+            rsc.reload4(j, lane, v, V);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) f(v[c], 256 * j + 4 * lane + c);
+        }
+    };
 
     // ---- top-k (main.cpp:740-748) ----
     const int k = P.top_k;
@@ -626,8 +648,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
             if (lane == 0) sm.u.hist[kWaveBins] = 0u;
             __syncthreads();
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) atomicAdd(&sm.u.hist[bin_of(s[e])], 1u);
+            each_score([&](float v, int) { atomicAdd(&sm.u.hist[bin_of(v)], 1u); });
             __syncthreads();
             constexpr int BPL = kWaveBins / 64;
             uint32_t cnt[BPL];
@@ -663,22 +684,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
                 bsel = __builtin_amdgcn_readlane(bsel, L);
                 above_bins = __builtin_amdgcn_readlane(above_bins, L);
                 __syncthreads();  // histogram reads done: the candidates reuse it
-                // recompute the bins (keeping 4*Q bin values live costs as many registers)
-                const float bscale2 = fresh_v(bscale), nlo2 = fresh_v(nlo);
-                auto bin2_of = [&](float v) -> int {
-                    const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bscale2, nlo2), 0.0f,
-                                                               (float)(kWaveBins - 1));
-                    return v == kNegInf ? kWaveBins : b;
-                };
                 int nc = 0;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    const bool in = bin2_of(s[e]) == bsel;
+                each_score([&](float v, int) {
+                    const bool in = bin_of(v) == bsel;
                     const uint64_t m = __ballot(in);
                     const int at = nc + ballot_rank(m);
-                    sm.u.cand[(in && at < kWaveCand) ? at : kWaveCand] = s[e];
+                    sm.u.cand[(in && at < kWaveCand) ? at : kWaveCand] = v;
                     nc += __popcll(m);
-                }
+                });
                 __syncthreads();
                 if (nc <= kWaveCand) {
                     const int rem = k - above_bins;  // 0 <= rem < nc
@@ -715,13 +728,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
             wave_radix_pass<Q>(rsc, 0, prefix, pmask, rem, sm.u.hist);
             thr = okey_inv(prefix);
             int n_above = 0;
-#pragma unroll 1
-            for (int j = 0; j < Q; ++j) {
-                float v[4];
-                rsc.reload4(j, lane, v, V);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) n_above += (v[c] > thr) ? 1 : 0;
-            }
+            each_score([&](float v, int) { n_above += (v > thr) ? 1 : 0; });
             above = wave_sum_dpp(n_above);
             if (above < k) thr = __fsub_rn(thr, 1e-10f);
         }
@@ -734,20 +741,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sa
     // items past the list write its spare slot.
     if (n_surv < 0) {
         int n = 0;
-#pragma unroll
-        for (int j = 0; j < Q; ++j) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float v = s[4 * j + c];
-                const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
-                const uint64_t m = __ballot(keep);
-                const int at = n + ballot_rank(m);
-                const int slot = (keep && at < kWaveCap) ? at : kWaveCap;
-                sm.list[slot] = ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) |
-                                (uint32_t)(256 * j + 4 * lane + c);
-                n += __popcll(m);
-            }
-        }
+        each_score([&](float v, int id) {
+            const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
+            const uint64_t m = __ballot(keep);
+            const int at = n + ballot_rank(m);
+            const int slot = (keep && at < kWaveCap) ? at : kWaveCap;
+            sm.list[slot] = ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)id;
+            n += __popcll(m);
+        });
         n_surv = n;
     }
     CBX_STAMP(4);
