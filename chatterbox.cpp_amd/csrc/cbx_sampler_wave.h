@@ -41,7 +41,7 @@ namespace cbx {
 namespace {
 
 constexpr int kWaveBins = 1024;   // value bins: top-k select, survivor sort
-constexpr int kWaveCand = 512;    // scores in the selected top-k bin
+constexpr int kWaveCand = 256;    // scores in the selected top-k bin
 constexpr int kWaveSortMax = 64;  // largest bin the counting sort ranks directly
 constexpr int kWaveRows = kWaveCap / 64;
 constexpr double kDrawMargin = 3e-7;
@@ -52,21 +52,31 @@ constexpr double kDrawMargin = 3e-7;
 #define WAVE_WPE 3
 #endif
 
+// LDS of one row (~11 KB at Q = 26, so a CU holds as many rows as registers
+// allow).  Phases reuse storage:
+//   list:  the top-k histogram (u32 bins) until the survivors are written;
+//          the survivor keys; the kept exp terms F in id order at the end
+//   u:     the sort's bin offsets (two u16 per word); the top-k bin's
+//          candidates; the allowed row of masked rows at the start; the kept
+//          bitmap and its word offsets at the end
 template <int Q>
 struct WaveSmem {
     uint64_t tab[32];
-    uint32_t seen[8 * Q];       // history ids (penalty)
-    uint32_t keptw[8 * Q + 1];  // kept ids after every filter (+ spare word)
-    uint32_t woff[8 * Q];       // kept ids before each word
+    uint32_t seen[8 * Q];  // history ids (penalty)
     union {
-        uint32_t hist[kWaveBins + 4];  // value bins (+ spare), then sort offsets
-        float cand[kWaveCand + 1];     // scores of the top-k bin (+ spare slot)
-        uint64_t candk[kWaveCand];     // (score bits << 32 | id) of the top-k bin
-        float E[kWaveCap];             // exp terms in sorted order, then q_i
-        float F[kWaveCap + 1];         // kept exp terms in id order (+ spare slot)
+        uint32_t hist16[kWaveBins / 2 + 2];  // sort offsets, u16 pairs (+ spare bins)
+        float cand[kWaveCand + 1];           // scores of the top-k bin (+ spare slot)
+        uint64_t candk[kWaveCand + 1];       // (score bits << 32 | id), same bin
+        struct {
+            uint32_t keptw[8 * Q + 1];  // kept ids after every filter (+ spare word)
+            uint32_t woff[8 * Q];       // kept ids before each word
+        } b;
     } u;
-    uint64_t list[kWaveCap + 1];  // survivors (+ spare slot): raw, then keys
+    uint64_t list[kWaveCap + 1];  // survivors (+ spare slot)
     int rk;
+
+    __device__ uint32_t* khist() { return reinterpret_cast<uint32_t*>(list); }
+    __device__ float* F() { return reinterpret_cast<float*>(list); }
 };
 
 // ------------------------------------------------------------ wave helpers
@@ -283,6 +293,36 @@ __device__ __forceinline__ void wave_radix_pass(const RowScores& rsc, int shift,
     __syncthreads();
 }
 
+// 0 + t_0 + t_1 + ... + t_{n-1} in order, binary32, where lane l holds terms
+// l*C .. l*C + C - 1 in t[0, C): one dependent add per term (rows with NaN or
+// infinite terms, where the segment scan does not apply).
+template <int CM>
+__device__ __forceinline__ float chain_sum_regs(const float (&t)[CM], int C, int n) {
+    float acc = 0.0f;
+    for (int l = 0; l < 64 && l * C < n; ++l) {
+#pragma unroll
+        for (int q = 0; q < CM; ++q)
+            if (q < C && l * C + q < n)
+                acc = __fadd_rn(acc, lane_term(__builtin_bit_cast(int, t[q]), l));
+    }
+    return acc;
+}
+// First i with 0 + t_0 + ... + t_i >= thr (binary32, in order), n-1 if none.
+template <int CM>
+__device__ __forceinline__ int chain_cross_regs(const float (&t)[CM], int C, int n, float thr) {
+    float acc = 0.0f;
+    for (int l = 0; l < 64 && l * C < n; ++l) {
+#pragma unroll
+        for (int q = 0; q < CM; ++q) {
+            if (q < C && l * C + q < n) {
+                acc = __fadd_rn(acc, lane_term(__builtin_bit_cast(int, t[q]), l));
+                if (acc >= thr) return l * C + q;
+            }
+        }
+    }
+    return n - 1;
+}
+
 // ------------------------------------------------------------------ kernel
 
 template <int Q, int JT>
@@ -352,10 +392,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
     }
     if (lane < 32) sm.tab[lane] = kExp2TabDev.t[lane];
-    for (int w = lane; w < 8 * Q + 1; w += 64) {
-        sm.seen[min(w, 8 * Q - 1)] = 0u;
-        sm.keptw[w] = 0u;
-    }
+    for (int w = lane; w < 8 * Q; w += 64) sm.seen[w] = 0u;
     __syncthreads();
     // ---- history ids -> seen bitmap (main.cpp:775) ----
     if (use_pen) {
@@ -390,11 +427,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     if (!plain) {
         if (rsc.masked_ids)
             for (int w = lane; w < W; w += 64)
-                sm.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
+                sm.u.b.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            const uint32_t word = rsc.masked_ids ? sm.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
+            const uint32_t word = rsc.masked_ids ? sm.u.b.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int id = 256 * j + 4 * lane + c;
@@ -404,7 +441,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
         }
         __syncthreads();
-        for (int w = lane; w < 8 * Q + 1; w += 64) sm.keptw[w] = 0u;
     }
     {
         // acc = sum of (v - v): 0 while every unmasked score is finite, NaN
@@ -483,12 +519,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             // Plain rows: bin(v) = trunc(med3(fma(v, scale, -lo*scale), 0, NB-1))
             // is non-decreasing in v; the V..256Q padding (-inf) lands in bin 0
             // and is taken off its count.
+            uint32_t* hist = sm.khist();
 #pragma unroll
-            for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
+            for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
             __syncthreads();
 #pragma unroll
             for (int e = 0; e < EPL; ++e)
-                atomicAdd(&sm.u.hist[(int)__builtin_amdgcn_fmed3f(__fmaf_rn(s[e], bscale, nlo),
+                atomicAdd(&hist[(int)__builtin_amdgcn_fmed3f(__fmaf_rn(s[e], bscale, nlo),
                                                                    0.0f, (float)(kWaveBins - 1))],
                           1u);
             __syncthreads();
@@ -498,7 +535,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
             for (int q = 0; q < BPL; ++q) {
                 const int b = kWaveBins - 1 - (lane * BPL + q);  // descending bins
-                cnt[q] = sm.u.hist[b] - (b == 0 ? (uint32_t)(256 * Q - V) : 0u);
+                cnt[q] = hist[b] - (b == 0 ? (uint32_t)(256 * Q - V) : 0u);
                 tot += (int)cnt[q];
             }
             int n_fin;
@@ -644,18 +681,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                                            (float)(kWaveBins - 1));
                 return v == kNegInf ? kWaveBins : b;
             };
+            uint32_t* hist = sm.khist();
 #pragma unroll
-            for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
-            if (lane == 0) sm.u.hist[kWaveBins] = 0u;
+            for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
+            if (lane == 0) hist[kWaveBins] = 0u;
             __syncthreads();
-            each_score([&](float v, int) { atomicAdd(&sm.u.hist[bin_of(v)], 1u); });
+            each_score([&](float v, int) { atomicAdd(&hist[bin_of(v)], 1u); });
             __syncthreads();
             constexpr int BPL = kWaveBins / 64;
             uint32_t cnt[BPL];
             int tot = 0;
 #pragma unroll
             for (int q = 0; q < BPL; ++q) {
-                cnt[q] = sm.u.hist[kWaveBins - 1 - (lane * BPL + q)];  // descending bins
+                cnt[q] = hist[kWaveBins - 1 - (lane * BPL + q)];  // descending bins
                 tot += (int)cnt[q];
             }
             int n_fin;
@@ -722,10 +760,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         if (!done) {
             // 8-bit radix select over all ids (NaN / inf / degenerate rows)
             uint32_t prefix = 0, pmask = 0, rem = (uint32_t)k;
-            wave_radix_pass<Q>(rsc, 24, prefix, pmask, rem, sm.u.hist);
-            wave_radix_pass<Q>(rsc, 16, prefix, pmask, rem, sm.u.hist);
-            wave_radix_pass<Q>(rsc, 8, prefix, pmask, rem, sm.u.hist);
-            wave_radix_pass<Q>(rsc, 0, prefix, pmask, rem, sm.u.hist);
+            wave_radix_pass<Q>(rsc, 24, prefix, pmask, rem, sm.khist());
+            wave_radix_pass<Q>(rsc, 16, prefix, pmask, rem, sm.khist());
+            wave_radix_pass<Q>(rsc, 8, prefix, pmask, rem, sm.khist());
+            wave_radix_pass<Q>(rsc, 0, prefix, pmask, rem, sm.khist());
             thr = okey_inv(prefix);
             int n_above = 0;
             each_score([&](float v, int) { n_above += (v > thr) ? 1 : 0; });
@@ -799,9 +837,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             const float nslo = -__fmul_rn(slo, sscale);
             uint64_t x[R];
             int rb[R], slot[R];
+            // bin offsets as u16 pairs: bin b in half (b & 1) of word b >> 1
+            uint32_t* h16 = sm.u.hist16;
+            auto get16 = [&](int b) { return (int)((h16[b >> 1] >> ((b & 1) * 16)) & 0xffffu); };
 #pragma unroll
-            for (int q = 0; q < kWaveBins / 64; ++q) sm.u.hist[lane * (kWaveBins / 64) + q] = 0u;
-            if (lane < 4) sm.u.hist[kWaveBins + lane] = 0u;
+            for (int q = 0; q < kWaveBins / 128; ++q) h16[lane * (kWaveBins / 128) + q] = 0u;
+            if (lane < 2) h16[kWaveBins / 2 + lane] = 0u;
             __syncthreads();
             const int nv = fresh(n_surv);
 #pragma unroll
@@ -815,30 +856,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, sscale, nslo),
                                                                    0.0f, (float)(kWaveBins - 1));
                         rb[r] = (i < nv) ? kWaveBins - 1 - b : kWaveBins;  // NB: spare
-                        slot[r] = (int)atomicAdd(&sm.u.hist[rb[r]], 1u);
+                        const uint32_t old16 =
+                            atomicAdd(&h16[rb[r] >> 1], (rb[r] & 1) ? 0x10000u : 1u);
+                        slot[r] = (int)((old16 >> ((rb[r] & 1) * 16)) & 0xffffu);
                     }
                 }
             }
             __syncthreads();
             CBX_STAMP(13);
-            constexpr int BPL = kWaveBins / 64;
-            uint32_t cnt[BPL];
+            constexpr int WPL16 = kWaveBins / 128;  // words (bin pairs) per lane
+            uint32_t wv[WPL16];
             int tot = 0;
             uint32_t big = 0;
 #pragma unroll
-            for (int q = 0; q < BPL; ++q) {
-                cnt[q] = sm.u.hist[lane * BPL + q];
-                tot += (int)cnt[q];
-                big = max(big, cnt[q]);
+            for (int q = 0; q < WPL16; ++q) {
+                wv[q] = h16[lane * WPL16 + q];
+                const uint32_t c0 = wv[q] & 0xffffu, c1 = wv[q] >> 16;
+                tot += (int)(c0 + c1);
+                big = max(big, max(c0, c1));
             }
             int all;
             int base = wave_excl_scan_i(tot, all);
 #pragma unroll
-            for (int q = 0; q < BPL; ++q) {
-                sm.u.hist[lane * BPL + q] = (uint32_t)base;
-                base += (int)cnt[q];
+            for (int q = 0; q < WPL16; ++q) {
+                const uint32_t c0 = wv[q] & 0xffffu;
+                h16[lane * WPL16 + q] = (uint32_t)base | ((uint32_t)(base + (int)c0) << 16);
+                base += (int)(c0 + (wv[q] >> 16));
             }
-            if (lane < 2) sm.u.hist[kWaveBins + lane] = (uint32_t)n_surv;  // spare: empty
+            // spare bin NB and the sentinel NB + 1: both start at n_surv (empty)
+            if (lane == 0) h16[kWaveBins / 2] = (uint32_t)n_surv | ((uint32_t)n_surv << 16);
             if (__ballot(big > (uint32_t)kWaveSortMax) == 0) {
                 __syncthreads();
                 CBX_STAMP(14);
@@ -847,8 +893,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     if (g < nr) {
 #pragma unroll
                         for (int r = g; r < g + 4; ++r) {
-                            const int dst = rb[r] < kWaveBins ? (int)sm.u.hist[rb[r]] + slot[r]
-                                                              : kWaveCap;
+                            const int dst = rb[r] < kWaveBins ? get16(rb[r]) + slot[r] : kWaveCap;
                             sm.list[dst] = x[r];
                         }
                     }
@@ -858,7 +903,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     if (r < ((nr + 3) & ~3)) {
-                        const int s0 = (int)sm.u.hist[rb[r]], s1 = (int)sm.u.hist[rb[r] + 1];
+                        const int s0 = get16(rb[r]), s1 = get16(rb[r] + 1);
                         int rank = 0;
                         for (int t = s0; t < s1; t += 4) {  // 4 reads in flight
                             const uint64_t k0 = sm.list[t];
@@ -969,21 +1014,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 }
             }
         } else {
+            // rows holding NaN or +inf: the reference's sums term by term
+            constexpr int CM = kWaveRows + 1;
+            const int C = ((n_surv + 63) >> 6) | 1;
+            float ev[CM];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if (r < nr) {
-                    const int i = r * 64 + lane;
-                    sm.u.E[i] = expf_libm_branchless(
-                        __fsub_rn(desc_key_value(sm.list[i]), mx_surv), sm.tab);
+            for (int q = 0; q < CM; ++q) {
+                if (q < C) {
+                    const int i = lane * C + q;
+                    const float v = desc_key_value(sm.list[min(i, kWaveCap)]);
+                    ev[q] = i < n_surv ? expf_libm_branchless(__fsub_rn(v, mx_surv), sm.tab) : 0.0f;
                 }
             }
-            __syncthreads();
-            const float psum = wave_chain_sum(sm.u.E, n_surv, 0.0f);
+            const float psum = chain_sum_regs<CM>(ev, C, n_surv);
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r < nr) sm.u.E[r * 64 + lane] = __fdiv_rn(sm.u.E[r * 64 + lane], psum);
-            __syncthreads();
-            last = wave_chain_cross(sm.u.E, n_surv, P.top_p);
+            for (int q = 0; q < CM; ++q)
+                if (q < C) ev[q] = __fdiv_rn(ev[q], psum);
+            last = chain_cross_regs<CM>(ev, C, n_surv, P.top_p);
         }
         n_kept = uni(last + 1);
         CBX_STAMP(9);
@@ -995,6 +1042,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 
     // ---- min-p [extension], repetition penalty (main.cpp:774-781) ----
     // kept entries: list positions [0, n_kept); per entry in registers
+    for (int w = lane; w < 8 * Q + 1; w += 64) sm.u.b.keptw[w] = 0u;
+    __syncthreads();
     const int nk = (n_kept + 63) >> 6;
     float val[R];
     int idr[R];
@@ -1024,7 +1073,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     val[r] = v;
                     idr[r] = id;
                     kept |= (kp ? 1u : 0u) << r;
-                    atomicOr(&sm.keptw[kp ? id >> 5 : 8 * Q], kp ? 1u << (id & 31) : 0u);
+                    atomicOr(&sm.u.b.keptw[kp ? id >> 5 : 8 * Q], kp ? 1u << (id & 31) : 0u);
                 }
             }
         }
@@ -1046,14 +1095,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
             const int w = lane * WPL + q;
-            cw[q] = (w < W) ? __popc(sm.keptw[w]) : 0;
+            cw[q] = (w < W) ? __popc(sm.u.b.keptw[w]) : 0;
             loc += cw[q];
         }
         int basew = wave_excl_scan_i(loc, n_final);
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
             const int w = lane * WPL + q;
-            if (w < W) sm.woff[w] = (uint32_t)basew;
+            if (w < W) sm.u.b.woff[w] = (uint32_t)basew;
             basew += cw[q];
         }
     }
@@ -1064,8 +1113,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
             for (int r = g; r < g + 4; ++r) {
                 const bool kp = (kept >> r) & 1u;
-                const int at = kp ? rank_of(sm.keptw, sm.woff, idr[r]) : kWaveCap;  // spare
-                sm.u.F[at] = expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
+                const int at = kp ? rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r]) : kWaveCap;  // spare
+                sm.F()[at] = expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
             }
         }
     }
@@ -1080,7 +1129,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     bool have_psum2 = false;
     auto exact_psum2 = [&]() {
         if (!have_psum2) {
-            psum2 = wave_chain_sum(sm.u.F, n_final, 0.0f);
+            psum2 = wave_chain_sum(sm.F(), n_final, 0.0f);
             have_psum2 = true;
         }
         return psum2;
@@ -1093,12 +1142,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         float best = -1.0f;
         int first = 0x7fffffff;
         for (int i = lane; i < n_final; i += 64) {
-            const float p = __fdiv_rn(sm.u.F[i], ps);
+            const float p = __fdiv_rn(sm.F()[i], ps);
             if (p > best) { best = p; first = i; }  // ascending i: keeps the first
         }
         const float b = wave_max_dpp(best);
         const int rk = wave_min_i_dpp(best == b ? first : 0x7fffffff);
-        token = rk == 0x7fffffff ? 0 : id_of_rank(sm.keptw, sm.woff, W, rk);
+        token = rk == 0x7fffffff ? 0 : id_of_rank(sm.u.b.keptw, sm.u.b.woff, W, rk);
         oflags |= CBX_INFO_GREEDY;
     } else if (V >= 2) {
         oflags |= CBX_INFO_DREW;
@@ -1109,12 +1158,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         } else {
             u = a.uniforms[rs];
         }
-        const bool last_kept = bit_of(sm.keptw, V - 1);
+        const bool last_kept = bit_of(sm.u.b.keptw, V - 1);
         // binary64 prefix of the exp terms in id order, contiguous chunks
         const int C = (n_final + 63) >> 6;
         const int r0 = min(lane * C, n_final), r1 = min(r0 + C, n_final);
         double part = 0.0;
-        for (int r = r0; r < r1; ++r) part = __dadd_rn(part, (double)sm.u.F[r]);
+        for (int r = r0; r < r1; ++r) part = __dadd_rn(part, (double)sm.F()[r]);
         double cp = wave_incl_scan_f64(part, lane);
         const double total = readlane_f64(cp, 63);
         cp = __dsub_rn(cp, part);  // exclusive
@@ -1123,7 +1172,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         double blo = 0.0, bhi = 0.0;
         for (int r = r0; r < r1; ++r) {
             const double before = cp;
-            cp = __dadd_rn(cp, (double)sm.u.F[r]);
+            cp = __dadd_rn(cp, (double)sm.F()[r]);
             if (cp >= target) { found = r; blo = before; bhi = cp; break; }
         }
         const int rank = wave_min_i_dpp(found);
@@ -1140,7 +1189,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             const bool hi_ok = (rank == n_final - 1 && last_kept) ||
                                __dsub_rn(chi, u) > kDrawMargin * chi + 1e-30;
             certain = lo_ok && hi_ok;
-            token = id_of_rank(sm.keptw, sm.woff, W, rank);
+            token = id_of_rank(sm.u.b.keptw, sm.u.b.woff, W, rank);
         }
         if (!certain) {
             // the reference's arithmetic: float normaliser, double CDF (rare)
@@ -1148,11 +1197,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             if (lane == 0) {
                 double sum = 0.0;
                 for (int r = 0; r < n_final; ++r)
-                    sum = __dadd_rn(sum, (double)__fdiv_rn(sm.u.F[r], ps));
+                    sum = __dadd_rn(sum, (double)__fdiv_rn(sm.F()[r], ps));
                 double acc = 0.0;
                 int rk = -1;
                 for (int r = 0; r < n_final; ++r) {
-                    acc = __dadd_rn(acc, __ddiv_rn((double)__fdiv_rn(sm.u.F[r], ps), sum));
+                    acc = __dadd_rn(acc, __ddiv_rn((double)__fdiv_rn(sm.F()[r], ps), sum));
                     const double c = (r == n_final - 1 && last_kept) ? 1.0 : acc;
                     if (c >= u) { rk = r; break; }
                 }
@@ -1160,7 +1209,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
             __syncthreads();
             const int rk = sm.rk;
-            token = rk < 0 ? V - 1 : id_of_rank(sm.keptw, sm.woff, W, rk);
+            token = rk < 0 ? V - 1 : id_of_rank(sm.u.b.keptw, sm.u.b.woff, W, rk);
         }
     }
     CBX_STAMP(12);
@@ -1172,8 +1221,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         const float ps = empty ? 0.0f : exact_psum2();
         float* prow = a.probs + rs * a.ld_probs;
         for (int i = lane; i < V; i += 64)
-            prow[i] = (!empty && bit_of(sm.keptw, i))
-                          ? __fdiv_rn(sm.u.F[rank_of(sm.keptw, sm.woff, i)], ps)
+            prow[i] = (!empty && bit_of(sm.u.b.keptw, i))
+                          ? __fdiv_rn(sm.F()[rank_of(sm.u.b.keptw, sm.u.b.woff, i)], ps)
                           : 0.0f;
     }
 }
