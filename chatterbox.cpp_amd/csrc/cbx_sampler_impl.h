@@ -24,9 +24,10 @@
 //          or the libstdc++ discrete_distribution CDF (main.cpp:795-800;
 //          random.tcc:2657-2712)
 //
-// Exactness.  The binary32 running sums are evaluated in the reference's order
-// by one wave: 64 terms per load, then a chain of dependent IEEE adds reading
-// each lane's term (v_readlane), so every partial sum is the reference's.
+// Exactness.  The binary32 running sums take the reference's values: on the
+// fast path by the exact segment scan of cbx_seqsum.h (finite terms), else by
+// one wave reading 64 terms per load and chaining dependent IEEE adds over
+// the lanes (v_readlane), so every partial sum is the reference's.
 // The binary64 CDF is located in parallel with a certified margin: the
 // parallel cumulative values differ from the reference's sequential ones by
 // < 1.5e-11, so when the uniform lies more than 1e-9 from both neighbouring

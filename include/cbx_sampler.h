@@ -92,7 +92,9 @@ typedef struct cbx_batch {
     int32_t         draw_mode;  /* CBX_DRAW_UNIFORM or CBX_DRAW_PHILOX              */
     int32_t         max_survivors; /* host hint: bound on ids left by top-k (e.g. the
                                    largest active top_k); 0 = n_vocab.  Rows that
-                                   exceed it report CBX_INFO_OVERFLOW              */
+                                   exceed it report CBX_INFO_OVERFLOW.  At most
+                                   1024 with n_vocab <= 8448 runs one wavefront
+                                   per row (the fastest form)                      */
     const double*   uniforms;   /* CBX_DRAW_UNIFORM: [n_steps][n_rows] in [0,1)      */
     uint64_t        seed;       /* CBX_DRAW_PHILOX key                              */
     const uint64_t* stream_ids; /* CBX_DRAW_PHILOX: [n_rows]; NULL = row index      */
