@@ -48,11 +48,11 @@
 // translation unit): wave 0 of each of the first 16384 workgroups records the
 // shader clock at each marker.  Compiled out otherwise.
 #if defined(CBX_STAGE_CLOCKS)
-__device__ unsigned long long cbx_stage_clock[16384 * 16];
+__device__ unsigned long long cbx_stage_clock[16384 * 32];
 #define CBX_STAMP(n)                                                      \
     do {                                                                  \
         if (threadIdx.x == 0 && blockIdx.x < 16384)                       \
-            cbx_stage_clock[blockIdx.x * 16 + (n)] = clock64();           \
+            cbx_stage_clock[blockIdx.x * 32 + (n)] = clock64();           \
     } while (0)
 #else
 #define CBX_STAMP(n) ((void)0)

@@ -62,17 +62,17 @@ constexpr double kDrawMargin = 3e-7;
 template <int Q>
 struct WaveSmem {
     uint64_t tab[32];
-    uint32_t seen[8 * Q];  // history ids (penalty)
+    uint32_t seen[8 * Q + 64];  // history ids (penalty) (+ a spare word per lane)
     union {
         uint32_t hist16[kWaveBins / 2 + 2];  // sort offsets, u16 pairs (+ spare bins)
-        float cand[kWaveCand + 1];           // scores of the top-k bin (+ spare slot)
-        uint64_t candk[kWaveCand + 1];       // (score bits << 32 | id), same bin
+        float cand[kWaveCand + 64];          // scores of the top-k bin (+ spare slots)
+        uint64_t candk[kWaveCand + 64];      // (score bits << 32 | id), same bin
         struct {
-            uint32_t keptw[8 * Q + 1];  // kept ids after every filter (+ spare word)
+            uint32_t keptw[8 * Q + 64];  // kept ids after every filter (+ spare words)
             uint32_t woff[8 * Q];       // kept ids before each word
         } b;
     } u;
-    uint64_t list[kWaveCap + 1];  // survivors (+ spare slot)
+    uint64_t list[kWaveCap + 64];  // survivors (+ spare slots)
     int rk;
 
     __device__ uint32_t* khist() { return reinterpret_cast<uint32_t*>(list); }
@@ -293,34 +293,58 @@ __device__ __forceinline__ void wave_radix_pass(const RowScores& rsc, int shift,
     __syncthreads();
 }
 
-// 0 + t_0 + t_1 + ... + t_{n-1} in order, binary32, where lane l holds terms
-// l*C .. l*C + C - 1 in t[0, C): one dependent add per term (rows with NaN or
-// infinite terms, where the segment scan does not apply).
-template <int CM>
-__device__ __forceinline__ float chain_sum_regs(const float (&t)[CM], int C, int n) {
-    float acc = 0.0f;
-    for (int l = 0; l < 64 && l * C < n; ++l) {
+// The binary32 running sum 0 + t_0 + t_1 + ... in order, where lane l holds
+// terms l*C .. l*C + C - 1 in t[0, C) (zeros past the last term), by sweeps
+// of the wave: a sweep adds each lane's terms, one after the other, to the
+// sum carried in from the lane below (a wave_shr:1 DPP operand; lane 0 starts
+// from 0), so after sweep s the sums of lanes 0..s are final.  These are the
+// reference's adds in the reference's order (NaN and infinities included);
+// a sweep costs C + 1 instructions.  nl: lanes holding terms (1..64).
+// Returns the final sum of lane nl - 1.  With THR, stops once a lane's final
+// sum reaches thr: `hit` is then the first term index whose running sum is
+// >= thr (otherwise -1).
+template <int C, bool THR, int CM>
+__device__ __forceinline__ float chain_sweeps(const float (&t)[CM], int nl, float thr, int& hit) {
+    static_assert(C <= CM, "terms per lane");
+    const int lane = threadIdx.x & 63;
+    hit = -1;
+    float s = 0.0f;
+    for (int sw = 0; sw < nl; ++sw) {
+        const float in = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x138, 0xf, 0xf, true));
+        float acc = __fadd_rn(in, t[0]);
 #pragma unroll
-        for (int q = 0; q < CM; ++q)
-            if (q < C && l * C + q < n)
-                acc = __fadd_rn(acc, lane_term(__builtin_bit_cast(int, t[q]), l));
-    }
-    return acc;
-}
-// First i with 0 + t_0 + ... + t_i >= thr (binary32, in order), n-1 if none.
-template <int CM>
-__device__ __forceinline__ int chain_cross_regs(const float (&t)[CM], int C, int n, float thr) {
-    float acc = 0.0f;
-    for (int l = 0; l < 64 && l * C < n; ++l) {
+        for (int k = 1; k < C; ++k) acc = __fadd_rn(acc, t[k]);
+        s = acc;
+        if (THR && ((__ballot(s >= thr) >> sw) & 1ull)) {
+            // lane sw holds the first crossing: walk its terms from its start
+            float w = in;
+            int first = C;
 #pragma unroll
-        for (int q = 0; q < CM; ++q) {
-            if (q < C && l * C + q < n) {
-                acc = __fadd_rn(acc, lane_term(__builtin_bit_cast(int, t[q]), l));
-                if (acc >= thr) return l * C + q;
+            for (int k = 0; k < C; ++k) {
+                w = __fadd_rn(w, t[k]);
+                first = (first == C && w >= thr) ? k : first;
             }
+            hit = sw * C + __builtin_amdgcn_readlane(first, sw);
+            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), sw));
         }
     }
-    return n - 1;
+    (void)lane;
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), nl - 1));
+}
+
+// Calls f(std::integral_constant<int, C>) for the odd C in [c, CM] equal to
+// the run-time C (terms per lane are odd, so lane-strided LDS reads of the
+// sorted list fall in distinct banks).
+template <int c, int CM, typename F>
+__device__ __forceinline__ void with_odd_c(int C, F&& f) {
+    if constexpr (c <= CM) {
+        if (C == c) {
+            f(std::integral_constant<int, c>{});
+            return;
+        }
+        with_odd_c<c + 2, CM>(C, f);
+    }
 }
 
 // ------------------------------------------------------------------ kernel
@@ -400,7 +424,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         for (int u = 0; u < HB; ++u) {
             const int t = hid[u];
             const bool ok = t >= 0 && t < V;
-            atomicOr(&sm.seen[ok ? t >> 5 : 0], ok ? 1u << (t & 31) : 0u);
+            if (u * 64 < hlen)  // uniform: batches past the history are skipped
+                atomicOr(&sm.seen[ok ? t >> 5 : 8 * Q + lane], ok ? 1u << (t & 31) : 0u);
         }
         for (int b = HB * 64; b < hlen; b += 256) {  // histories past 1024 ids
             int t[4];
@@ -529,7 +554,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                                                    0.0f, (float)(kWaveBins - 1))],
                           1u);
             __syncthreads();
-                        constexpr int BPL = kWaveBins / 64;
+            CBX_STAMP(16);
+            constexpr int BPL = kWaveBins / 64;
             uint32_t cnt[BPL];
             int tot = 0;
 #pragma unroll
@@ -580,11 +606,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                                       __builtin_bit_cast(int, v), L0));
                     return true;
                 };
+                CBX_STAMP(17);
                 float B0 = kNegInf, B1 = kPosInf;
                 const bool have_b = bsel >= 1 && nsel <= kWaveCand && boundary(bsel, B0) &&
                                     (bsel == kWaveBins - 1 || boundary(bsel + 1, B1));
                 __syncthreads();  // histogram reads done: the candidates reuse it
-                                if (have_b && above_bins + nsel <= kWaveCap) {
+                CBX_STAMP(18);
+                if (have_b && above_bins + nsel <= kWaveCap) {
                     // One pass, no exec-mask changes: every score >= B0 (the
                     // survivors >= B1 and the selected bin's candidates) joins
                     // the list; the rest write its spare slot.
@@ -601,14 +629,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                             const bool ge = v >= B0j;
                             const uint64_t m = __ballot(ge);
                             const int at = ballot_rank(m) + n;
-                            sm.list[ge ? at : kWaveCap] =
+                            sm.list[ge ? at : kWaveCap + lane] =
                                 ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) |
                                 (uint32_t)(256 * j + 4 * lane + c);
                             n += __popcll(m);
                         }
                     }
                     __syncthreads();
-                                        const int nr0 = (n + 63) >> 6;
+                    CBX_STAMP(19);
+                    const int nr0 = (n + 63) >> 6;
                     int nc = 0;
                     uint64_t x[kWaveRows];  // the list, read once
 #pragma unroll
@@ -627,12 +656,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                 const bool inb = i < n && val_of(x[r]) < B1;
                                 const uint64_t m = __ballot(inb);
                                 const int at = ballot_rank(m) + nc;
-                                sm.u.candk[(inb && at < kWaveCand) ? at : kWaveCand] = x[r];
+                                sm.u.candk[(inb && at < kWaveCand) ? at : kWaveCand + lane] = x[r];
                                 nc += __popcll(m);
                             }
                         }
                     }
                     __syncthreads();
+                    CBX_STAMP(20);
                     if (n == above_bins + nsel && nc == nsel) {
                         const int rem = k - above_bins;  // 0 <= rem < nc
                         float tv = kNegInf;
@@ -653,6 +683,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                                              __builtin_bit_cast(int, tv), L2));
                         above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
                         if (above < k) thr = __fsub_rn(thr, 1e-10f);
+                        CBX_STAMP(21);
                         if (!(thr < B0)) {
                             // survivors: entries > thr, compacted in place
                             int n2 = 0;
@@ -662,7 +693,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                     const bool keep = r * 64 + lane < n && val_of(x[r]) > thr;
                                     const uint64_t m = __ballot(keep);
                                     const int at = ballot_rank(m) + n2;
-                                    sm.list[keep ? at : kWaveCap] = x[r];
+                                    sm.list[keep ? at : kWaveCap + lane] = x[r];
                                     n2 += __popcll(m);
                                 }
                             }
@@ -727,7 +758,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     const bool in = bin_of(v) == bsel;
                     const uint64_t m = __ballot(in);
                     const int at = nc + ballot_rank(m);
-                    sm.u.cand[(in && at < kWaveCand) ? at : kWaveCand] = v;
+                    sm.u.cand[(in && at < kWaveCand) ? at : kWaveCand + lane] = v;
                     nc += __popcll(m);
                 });
                 __syncthreads();
@@ -783,7 +814,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
             const uint64_t m = __ballot(keep);
             const int at = n + ballot_rank(m);
-            const int slot = (keep && at < kWaveCap) ? at : kWaveCap;
+            const int slot = (keep && at < kWaveCap) ? at : kWaveCap + lane;
             sm.list[slot] = ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)id;
             n += __popcll(m);
         });
@@ -893,7 +924,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     if (g < nr) {
 #pragma unroll
                         for (int r = g; r < g + 4; ++r) {
-                            const int dst = rb[r] < kWaveBins ? get16(rb[r]) + slot[r] : kWaveCap;
+                            const int dst = rb[r] < kWaveBins ? get16(rb[r]) + slot[r] : kWaveCap + lane;
                             sm.list[dst] = x[r];
                         }
                     }
@@ -913,7 +944,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                             rank += (k0 < x[r]) + (t + 1 < s1 && k1 < x[r]) +
                                     (t + 2 < s1 && k2 < x[r]) + (t + 3 < s1 && k3 < x[r]);
                         }
-                        fin[r] = rb[r] < kWaveBins ? s0 + rank : kWaveCap;
+                        fin[r] = rb[r] < kWaveBins ? s0 + rank : kWaveCap + lane;
                     }
                 }
                 __syncthreads();
@@ -950,87 +981,85 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         // ---- top-p (main.cpp:750-772) ----
         CBX_STAMP(6);
         mx_surv = desc_key_value(sm.list[0]);  // sorted[0]
-        int hit;
-        int last;
-        if (!bad) {
-            // e_i in registers, lane l holding sorted positions [l*C, l*C + C)
-            // (C odd: the strided LDS reads fall in distinct banks)
-            constexpr int CM = kWaveRows + 1;
-            const int C = ((n_surv + 63) >> 6) | 1;
-            float ev[CM];
+        // e_i in registers, lane l holding sorted positions [l*C, l*C + C)
+        // (C odd: the strided LDS reads fall in distinct banks)
+        constexpr int CM = kWaveRows + 1;
+        const int C = uni(((n_surv + 63) >> 6) | 1);
+        const int nl = uni((n_surv + C - 1) / C);  // lanes holding terms
+        float ev[CM];
 #pragma unroll
-            for (int q = 0; q < CM; ++q) {
-                if (q < C) {
-                    const int i = lane * C + q;
-                    const float v = desc_key_value(sm.list[min(i, kWaveCap)]);
-                    ev[q] = i < n_surv ? expf_libm_branchless(__fsub_rn(v, mx_surv), sm.tab) : 0.0f;
-                }
+        for (int q = 0; q < CM; ++q) {
+            if (q < C) {
+                const int i = lane * C + q;
+                const float v = desc_key_value(sm.list[min(i, kWaveCap)]);
+                ev[q] = i < n_surv ? expf_libm_branchless(__fsub_rn(v, mx_surv), sm.tab) : 0.0f;
             }
-            CBX_STAMP(7);
-            const float e0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                           __builtin_bit_cast(int, ev[0]), 0));
-            const float psum = seq_sum_regs<CM>(ev, C, n_surv, e0, 1, 0.0f, hit);
-            CBX_STAMP(8);
-#pragma unroll
-            for (int q = 0; q < CM; ++q)
-                if (q < C) ev[q] = __fdiv_rn(ev[q], psum);  // 0 stays 0
-            // First i with cum_i = q_0 + ... + q_i (binary32, in order) >= top_p.
-            // The binary64 prefix X_i of the same q's differs from cum_i by at
-            // most i half-ulps of cum_i (one rounding per add): where X_i is
-            // further than that from top_p for the deciding indices the answer
-            // is certain; otherwise the exact running sum decides.
+        }
+        CBX_STAMP(7);
+        // psum = 0 + e_0 + e_1 + ... (binary32, sorted order), term by term
+        float psum = 0.0f;
+        with_odd_c<1, CM>(C, [&](auto cc) {
+            int unused;
+            psum = chain_sweeps<decltype(cc)::value, false>(ev, nl, 0.0f, unused);
+        });
+        CBX_STAMP(8);
+        // First i with cum_i = q_0 + ... + q_i >= top_p, q_j = e_j / psum
+        // (binary32, in order).  With Y_i = (e_0 + ... + e_i) / psum in
+        // binary64, |cum_i - Y_i| <= i half-ulps of cum_i (one rounding per
+        // add) + 2^-24 Y_i (the rounding of each q_j): a lane bounds this for
+        // its terms by its last index and the binade of its last Y.  Where
+        // Y_i -/+ that bound puts the first crossing at one index the answer
+        // is certain; otherwise (and for rows holding NaN or +inf) the q's
+        // are formed and summed as the reference does.
+        int last = n_surv - 1;
+        bool certain = false;
+        if (!bad) {
             const double p = (double)P.top_p;
+            const double inv = __ddiv_rn(1.0, (double)psum);
             double part = 0.0;
 #pragma unroll
             for (int q = 0; q < CM; ++q)
                 if (q < C) part = __dadd_rn(part, (double)ev[q]);
-            double x = __dsub_rn(wave_incl_scan_f64_dpp(part), part);
-            int c_hi = 0x7fffffff, c_lo = 0x7fffffff;
+            const double x0 = __dsub_rn(wave_incl_scan_f64_dpp(part), part);
+            const double yl = __dmul_rn(__dadd_rn(x0, part), inv);
+            const double cm = __dmul_rn(yl, 1.0 + 0x1p-12);
+            const int b = __builtin_amdgcn_frexp_exp(cm) - 1;  // cm in [2^b, 2^(b+1))
+            const double err = __dadd_rn(
+                __dadd_rn(__dmul_rn((double)(lane * C + C - 1), ldexp(1.0, max(b, -126) - 24)),
+                          __dmul_rn(yl, 0x1p-23)),
+                1e-12);
+            const double lo_thr = __dsub_rn(p, err), hi_thr = __dadd_rn(p, err);
+            // y is non-decreasing: the first index meeting a bound is the
+            // count of the lane's terms before it
+            int n_hi = 0, n_lo = 0;
+            double x = x0;
 #pragma unroll
             for (int q = 0; q < CM; ++q) {
                 if (q < C) {
-                    const int i = lane * C + q;
                     x = __dadd_rn(x, (double)ev[q]);
-                    const double cmax = __dmul_rn(x, 1.0 + 0x1p-12);
-                    const int ex = (int)((__builtin_bit_cast(uint64_t, cmax) >> 52) & 0x7ff) - 1023;
-                    const double err = __dadd_rn(
-                        __dmul_rn((double)i, ldexp(1.0, max(ex, -126) - 24)), 1e-12);
-                    const bool in = i < n_surv;
-                    c_hi = (in && c_hi == 0x7fffffff && __dadd_rn(x, err) >= p) ? i : c_hi;
-                    c_lo = (in && c_lo == 0x7fffffff && __dsub_rn(x, err) >= p) ? i : c_lo;
+                    const double y = __dmul_rn(x, inv);
+                    n_hi += y < lo_thr ? 1 : 0;
+                    n_lo += y < hi_thr ? 1 : 0;
                 }
             }
-            c_hi = wave_min_i_dpp(c_hi);
-            c_lo = wave_min_i_dpp(c_lo);
+            int c_hi = n_hi < C ? lane * C + n_hi : 0x7fffffff;
+            int c_lo = n_lo < C ? lane * C + n_lo : 0x7fffffff;
+            c_hi = min(wave_min_i_dpp(c_hi), n_surv);  // n_surv: never
+            c_lo = min(wave_min_i_dpp(c_lo), n_surv);
             if (c_hi == c_lo) {
-                last = c_hi == 0x7fffffff ? n_surv - 1 : c_hi;
-            } else {
-                const float q0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                               __builtin_bit_cast(int, ev[0]), 0));
-                last = 0;
-                if (!(q0 >= P.top_p)) {
-                    (void)seq_sum_regs<CM>(ev, C, n_surv, q0, 1, P.top_p, hit);
-                    last = hit < 0 ? n_surv - 1 : hit;
-                }
+                certain = true;
+                last = c_hi == n_surv ? n_surv - 1 : c_hi;
             }
-        } else {
-            // rows holding NaN or +inf: the reference's sums term by term
-            constexpr int CM = kWaveRows + 1;
-            const int C = ((n_surv + 63) >> 6) | 1;
-            float ev[CM];
-#pragma unroll
-            for (int q = 0; q < CM; ++q) {
-                if (q < C) {
-                    const int i = lane * C + q;
-                    const float v = desc_key_value(sm.list[min(i, kWaveCap)]);
-                    ev[q] = i < n_surv ? expf_libm_branchless(__fsub_rn(v, mx_surv), sm.tab) : 0.0f;
-                }
-            }
-            const float psum = chain_sum_regs<CM>(ev, C, n_surv);
+        }
+        if (!certain) {
 #pragma unroll
             for (int q = 0; q < CM; ++q)
-                if (q < C) ev[q] = __fdiv_rn(ev[q], psum);
-            last = chain_cross_regs<CM>(ev, C, n_surv, P.top_p);
+                if (q < C) ev[q] = __fdiv_rn(ev[q], psum);  // 0 stays 0
+            with_odd_c<1, CM>(C, [&](auto cc) {
+                int hit;
+                (void)chain_sweeps<decltype(cc)::value, true>(ev, nl, P.top_p, hit);
+                last = hit < 0 ? n_surv - 1 : hit;
+            });
         }
         n_kept = uni(last + 1);
         CBX_STAMP(9);
@@ -1042,7 +1071,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 
     // ---- min-p [extension], repetition penalty (main.cpp:774-781) ----
     // kept entries: list positions [0, n_kept); per entry in registers
-    for (int w = lane; w < 8 * Q + 1; w += 64) sm.u.b.keptw[w] = 0u;
+    for (int w = lane; w < 8 * Q; w += 64) sm.u.b.keptw[w] = 0u;
     __syncthreads();
     const int nk = (n_kept + 63) >> 6;
     float val[R];
@@ -1073,7 +1102,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     val[r] = v;
                     idr[r] = id;
                     kept |= (kp ? 1u : 0u) << r;
-                    atomicOr(&sm.u.b.keptw[kp ? id >> 5 : 8 * Q], kp ? 1u << (id & 31) : 0u);
+                    atomicOr(&sm.u.b.keptw[kp ? id >> 5 : 8 * Q + lane], kp ? 1u << (id & 31) : 0u);
                 }
             }
         }
@@ -1113,7 +1142,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
             for (int r = g; r < g + 4; ++r) {
                 const bool kp = (kept >> r) & 1u;
-                const int at = kp ? rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r]) : kWaveCap;  // spare
+                const int at = kp ? rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r]) : kWaveCap + lane;  // spare
                 sm.F()[at] = expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
             }
         }
