@@ -180,6 +180,19 @@ __device__ __forceinline__ int ballot_rank(uint64_t m) {
                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// LDS byte offset of a shared-memory object (the low word of its generic
+// address is its offset in the LDS aperture).
+template <typename T>
+__device__ __forceinline__ uint32_t lds_offset(const T* p) {
+    return (uint32_t)(uintptr_t)p;
+}
+
+// One 8-byte LDS store: w0 at byte offset addr, w1 at addr + 4 (two data
+// registers, so no register pair is assembled for it).
+__device__ __forceinline__ void lds_store_pair(uint32_t addr, uint32_t w0, uint32_t w1) {
+    asm volatile("ds_write2_b32 %0, %1, %2 offset1:1" : : "v"(addr), "v"(w0), "v"(w1) : "memory");
+}
+
 // An opaque copy of a uniform value: predicates built on it in one pass are
 // not merged with (and kept alive for) those of another pass.
 __device__ __forceinline__ int fresh(int v) {
@@ -468,29 +481,38 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         __syncthreads();
     }
     {
-        // acc = sum of (v - v): 0 while every unmasked score is finite, NaN
-        // once one is NaN or infinite
+        // acc = sum of v * 0: 0 while every unmasked score is finite, NaN once
+        // one is NaN or infinite.  Vectors j >= JT may hold padding.
         float acc = 0.0f;
         const int Vm = fresh(V);
         auto pass = [&](auto scaled) {
 #pragma unroll
             for (int j = 0; j < Q; ++j) {
+                float w[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    float v = s[4 * j + c];
-                    if (decltype(scaled)::value) v = __fmul_rn(v, rsc.inv_t);
-                    if (j < JT) {
-                        acc = __fadd_rn(acc, __fsub_rn(v, v));
-                        lo = fminf(lo, v);
-                    } else {
-                        const bool pad = 256 * j + 4 * lane + c >= Vm;
-                        acc = __fadd_rn(acc, pad ? 0.0f : __fsub_rn(v, v));
-                        v = pad ? kNegInf : v;
-                        lo = fminf(lo, pad ? kPosInf : v);
-                    }
-                    hi = fmaxf(hi, v);
-                    s[4 * j + c] = v;
+                    w[c] = s[4 * j + c];
+                    if (decltype(scaled)::value) w[c] = __fmul_rn(w[c], rsc.inv_t);
                 }
+                if (j < JT) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc = __fmaf_rn(w[c], 0.0f, acc);
+                    lo = fminf(lo, fminf(w[0], w[1]));
+                    lo = fminf(lo, fminf(w[2], w[3]));
+                    hi = fmaxf(hi, fmaxf(w[0], w[1]));
+                    hi = fmaxf(hi, fmaxf(w[2], w[3]));
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const bool pad = 256 * j + 4 * lane + c >= Vm;
+                        acc = __fmaf_rn(pad ? 0.0f : w[c], 0.0f, acc);
+                        w[c] = pad ? kNegInf : w[c];
+                        lo = fminf(lo, pad ? kPosInf : w[c]);
+                        hi = fmaxf(hi, w[c]);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) s[4 * j + c] = w[c];
             }
         };
         if (rsc.scale) pass(std::true_type{});
@@ -540,19 +562,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         const float range = __fsub_rn(hi, lo);
         const float bscale = __fdiv_rn((float)kWaveBins, range);
         const float nlo = -__fmul_rn(lo, bscale);
-        if (!bad && !neg_inf && range > 0.0f && bscale < kPosInf) {
-            // Plain rows: bin(v) = trunc(med3(fma(v, scale, -lo*scale), 0, NB-1))
-            // is non-decreasing in v; the V..256Q padding (-inf) lands in bin 0
-            // and is taken off its count.
+        // Plain rows: y(v) = fma(v, bs, c0) lands in [2^23, 2^23 + NB) for
+        // every score in [lo, hi] (checked at both ends; y is monotone), where
+        // a float is an integer: bin(v) = bits(y) - bits(2^23) is
+        // non-decreasing in v and costs two operations per score.  The
+        // V..256Q padding (-inf) is raised to bin 0 and taken off its count.
+        const float bs = __fdiv_rn((float)(kWaveBins - 4), range);
+        const float c0 = __fsub_rn(0x1p23f + 2.0f, __fmul_rn(lo, bs));
+        const bool bins_fit = __fmaf_rn(lo, bs, c0) >= 0x1p23f &&
+                              __fmaf_rn(hi, bs, c0) <= 0x1p23f + (float)(kWaveBins - 1);
+        if (!bad && !neg_inf && range > 0.0f && bs < kPosInf && bins_fit) {
             uint32_t* hist = sm.khist();
 #pragma unroll
             for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
             __syncthreads();
 #pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                atomicAdd(&hist[(int)__builtin_amdgcn_fmed3f(__fmaf_rn(s[e], bscale, nlo),
-                                                                   0.0f, (float)(kWaveBins - 1))],
-                          1u);
+            for (int e = 0; e < EPL; ++e) {
+                float y = __fmaf_rn(s[e], bs, c0);
+                if ((e >> 2) >= JT) y = fmaxf(y, 0x1p23f);  // padding: bin 0
+                atomicAdd(&hist[__builtin_bit_cast(uint32_t, y) - 0x4B000000u], 1u);
+            }
             __syncthreads();
             CBX_STAMP(16);
             constexpr int BPL = kWaveBins / 64;
@@ -593,12 +622,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 nsel = __builtin_amdgcn_readlane(nsel, L);
                 // Score boundaries of the selected bin: B0 = least float with
                 // bin >= bsel, B1 = least float with bin >= bsel + 1 (+inf past
-                // the top bin).  bin(v) >= b  <=>  fma(v, scale, -lo*scale) >= b,
-                // probed over 64 consecutive floats around the real root.
+                // the top bin).  bin(v) >= b  <=>  fma(v, bs, c0) >= 2^23 + b,
+                // which (the fma rounding to integers) holds from about
+                // v*bs + c0 = 2^23 + b - 1/2 on; probed over 64 consecutive
+                // floats around that root.
                 auto boundary = [&](int b, float& B) -> bool {
-                    const float v0 = (float)(((double)b - (double)nlo) / (double)bscale);
+                    const float tb = 0x1p23f + (float)b;
+                    const float v0 = (float)(((double)tb - 0.5 - (double)c0) / (double)bs);
                     const float v = okey_inv(okey(v0) + (uint32_t)(lane - 32));
-                    const uint64_t m = __ballot(__fmaf_rn(v, bscale, nlo) >= (float)b);
+                    const uint64_t m = __ballot(__fmaf_rn(v, bs, c0) >= tb);
                     if (m == 0 || m == ~0ull) return false;
                     const int L0 = __builtin_ctzll(m);
                     if (m != (~0ull << L0)) return false;
@@ -619,7 +651,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     auto val_of = [](uint64_t pk) {
                         return __builtin_bit_cast(float, (uint32_t)(pk >> 32));
                     };
-                    int n = 0;
+                    // sb: byte offset of the next free slot (a running scalar)
+                    const uint32_t lbase = lds_offset(&sm.list[0]);
+                    const uint32_t spare = lds_offset(&sm.list[kWaveCap + lane]);
+                    uint32_t sb = lbase;
 #pragma unroll
                     for (int j = 0; j < Q; ++j) {
                         const float B0j = fresh_v(B0);
@@ -628,13 +663,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                             const float v = s[4 * j + c];
                             const bool ge = v >= B0j;
                             const uint64_t m = __ballot(ge);
-                            const int at = ballot_rank(m) + n;
-                            sm.list[ge ? at : kWaveCap + lane] =
-                                ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) |
-                                (uint32_t)(256 * j + 4 * lane + c);
-                            n += __popcll(m);
+                            const uint32_t at = ((uint32_t)ballot_rank(m) << 3) + sb;
+                            lds_store_pair(ge ? at : spare, (uint32_t)(256 * j + 4 * lane + c),
+                                           __builtin_bit_cast(uint32_t, v));
+                            // opaque, so the shift-add is not re-associated
+                            sb = (uint32_t)fresh((int)(sb + 8u * (uint32_t)__popcll(m)));
                         }
                     }
+                    const int n = (int)((sb - lbase) >> 3);
                     __syncthreads();
                     CBX_STAMP(19);
                     const int nr0 = (n + 63) >> 6;
