@@ -497,10 +497,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 if (j < JT) {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) acc = __fmaf_rn(w[c], 0.0f, acc);
-                    lo = fminf(lo, fminf(w[0], w[1]));
-                    lo = fminf(lo, fminf(w[2], w[3]));
-                    hi = fmaxf(hi, fmaxf(w[0], w[1]));
-                    hi = fmaxf(hi, fmaxf(w[2], w[3]));
+                    // running value first: one 3-input min / max per pair
+                    lo = fminf(fminf(lo, w[0]), w[1]);
+                    lo = fminf(fminf(lo, w[2]), w[3]);
+                    hi = fmaxf(fmaxf(hi, w[0]), w[1]);
+                    hi = fmaxf(fmaxf(hi, w[2]), w[3]);
                 } else {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
@@ -964,23 +965,45 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                             sm.list[dst] = x[r];
                         }
                     }
+                // keys after the survivors: the maximum key (4 slots, for the
+                // reads past a bin's end below)
+                if (lane < 4) sm.list[n_surv + lane] = ~0ull;
                 __syncthreads();
                 CBX_STAMP(15);
+                // Rank inside the bin: the keys of the bin below x.  Reads past
+                // the bin's end see later bins (lower scores: larger keys) or
+                // the maximum key, which never count; bins of one key skip.
+                // The first four keys of the bins of four rows are read together
+                // (most bins hold at most four); longer bins loop on.
                 int fin[R];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    if (r < ((nr + 3) & ~3)) {
-                        const int s0 = get16(rb[r]), s1 = get16(rb[r] + 1);
-                        int rank = 0;
-                        for (int t = s0; t < s1; t += 4) {  // 4 reads in flight
-                            const uint64_t k0 = sm.list[t];
-                            const uint64_t k1 = sm.list[min(t + 1, kWaveCap)];
-                            const uint64_t k2 = sm.list[min(t + 2, kWaveCap)];
-                            const uint64_t k3 = sm.list[min(t + 3, kWaveCap)];
-                            rank += (k0 < x[r]) + (t + 1 < s1 && k1 < x[r]) +
-                                    (t + 2 < s1 && k2 < x[r]) + (t + 3 < s1 && k3 < x[r]);
+                for (int g = 0; g < R; g += 4) {
+                    if (g < nr) {
+                        int s0[4], s1[4], rank[4];
+                        uint64_t kk[4][4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            s0[u] = get16(rb[g + u]);
+                            s1[u] = get16(rb[g + u] + 1);
                         }
-                        fin[r] = rb[r] < kWaveBins ? s0 + rank : kWaveCap + lane;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) kk[u][q] = sm.list[s0[u] + q];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            rank[u] = (kk[u][0] < x[g + u]) + (kk[u][1] < x[g + u]) +
+                                      (kk[u][2] < x[g + u]) + (kk[u][3] < x[g + u]);
+                            for (int t = s0[u] + 4; t < s1[u]; t += 4) {
+                                const uint64_t k0 = sm.list[t];
+                                const uint64_t k1 = sm.list[t + 1];
+                                const uint64_t k2 = sm.list[t + 2];
+                                const uint64_t k3 = sm.list[t + 3];
+                                rank[u] += (k0 < x[g + u]) + (k1 < x[g + u]) + (k2 < x[g + u]) +
+                                           (k3 < x[g + u]);
+                            }
+                            fin[g + u] = rb[g + u] < kWaveBins ? s0[u] + rank[u] : kWaveCap + lane;
+                        }
                     }
                 }
                 __syncthreads();
