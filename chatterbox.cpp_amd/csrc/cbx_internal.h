@@ -47,10 +47,14 @@ size_t lds_bytes_for(int32_t cap, int32_t n_vocab);
 // Launch the sampler over n_steps * n_rows rows.  Returns a hipError_t.
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream);
 // One vocabulary class each (lanes x scores per lane), used by launch_sample.
-// One-wave kernels, scores per lane 4*Q (V <= 256*Q).
+// One-wave kernels, scores per lane 4*Q (V <= 256*Q); the *t forms serve
+// V > 256*(Q-1), where only the last vector of each lane holds padding.
 hipError_t launch_w16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w26(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w33(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_w16t(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_w26t(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_w33t(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x26(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x32(const KernelArgs& a, hipStream_t stream);

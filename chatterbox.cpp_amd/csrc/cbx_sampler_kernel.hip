@@ -62,9 +62,10 @@ int32_t max_cap_for_lds(int32_t n_vocab, size_t lds_bytes) {
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
     // one wave per row while the survivors fit its list
     if (a.cap <= kWaveCap) {
-        if (a.n_vocab <= 256 * 16) return launch_w16(a, stream);
-        if (a.n_vocab <= 256 * 26) return launch_w26(a, stream);
-        if (a.n_vocab <= kWaveMaxVocab) return launch_w33(a, stream);
+        if (a.n_vocab <= 256 * 16) return a.n_vocab > 256 * 15 ? launch_w16t(a, stream) : launch_w16(a, stream);
+        if (a.n_vocab <= 256 * 26) return a.n_vocab > 256 * 25 ? launch_w26t(a, stream) : launch_w26(a, stream);
+        if (a.n_vocab <= kWaveMaxVocab)
+            return a.n_vocab > 256 * 32 ? launch_w33t(a, stream) : launch_w33(a, stream);
     }
     // registers per lane sized to the vocabulary (6563 -> 26 per lane)
     if (a.n_vocab <= 256 * 16) return launch_v256x16(a, stream);

@@ -44,12 +44,12 @@ def cfg_pair(steps=1000, seed=0x5EED2):
     return dict(cond=cond, uncond=uncond, params=params, V=V_LLAMA)
 
 
-def batched_streams(B=256, steps=1, seed=0x5EED3, hist_max=1000):
-    """B independent streams, V=6563: logits ~N(0,3) with 5 spikes per row at
-    heights U[6,12]; history lengths U[0, hist_max]; per-row temperature
-    U[0.5,1.2], top_k from {50, 250, 1000}; top_p 0.9, penalty 1.2."""
+def batched_streams(B=256, steps=1, seed=0x5EED3, hist_max=1000, V=V_TURBO):
+    """B independent streams, V=6563 (or V): logits ~N(0,3) with 5 spikes per
+    row at heights U[6,12]; history lengths U[0, hist_max]; per-row
+    temperature U[0.5,1.2], top_k from {50, 250, 1000}; top_p 0.9, penalty
+    1.2."""
     rng = np.random.default_rng(seed)
-    V = V_TURBO
     logits = (rng.standard_normal((steps * B, V)) * 3.0).astype(np.float32)
     for r in range(steps * B):
         idx = rng.choice(V, size=5, replace=False)

@@ -238,6 +238,20 @@ def test_batched_streams(cbx, torch_cuda):
     parity.compare("batched_streams", tg, ig, tr, ir, u, pg, pr)
 
 
+@pytest.mark.parametrize("V", [3000, 4000, 5000, 7000, 8300])
+def test_batched_streams_vocab(cbx, torch_cuda, V):
+    """The batched workload at vocabularies of each one-wave kernel class
+    (padding in several vectors per lane, or in the last one only)."""
+    w = pkg.workloads()
+    d = w.batched_streams(B=256, steps=1, seed=0x5EED40 + V, V=V)
+    u = O.mt_canonical(41 + V, 256)
+    say(f"batched_streams V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], max_survivors=1000)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
+    parity.compare(f"batched_streams_{V}", tg, ig, tr, ir, u, pg, pr)
+
+
 def test_batched_streams_philox(cbx, torch_cuda):
     """Device Philox draws keyed (seed, stream, step) equal the oracle fed the
     oracle's Philox uniforms."""
