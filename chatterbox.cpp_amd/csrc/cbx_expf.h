@@ -158,8 +158,31 @@ CBX_HD float expf_libm_branchless(float x, const uint64_t* tab) {
     return special ? sp : main;
 }
 
+// The branch-free form for arguments x <= 0 (including -inf, not NaN): the
+// only special case left is the underflow to 0 below log(2^-150).  Equal to
+// expf_libm on that domain (checked exhaustively on the host).
+CBX_HD float expf_nonpos(float x, const uint64_t* tab) {
+    using namespace expf_detail;
+    const bool under = x < -0x1.9fe368p6f;
+    const double xd = (double)(under ? 0.0f : x);
+    double kd = fma64(kInvLn2N, xd, kShift);
+    const uint64_t ki = d2u(kd);
+    kd -= kShift;
+    const double r = fma64(kInvLn2N, xd, -kd);
+    uint64_t t = tab[ki % 32];
+    t += ki << (52 - 5);
+    const double s = u2d(t);
+    const double z = fma64(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = fma64(kC2, r, 1.0);
+    y = fma64(z, r2, y);
+    y = y * s;
+    return under ? 0.0f : (float)y;
+}
+
 #if !defined(__HIPCC__)
 inline float expf_libm_branchless(float x) { return expf_libm_branchless(x, kExp2TabHost.t); }
+inline float expf_nonpos(float x) { return expf_nonpos(x, kExp2TabHost.t); }
 #endif
 
 }  // namespace cbx

@@ -870,38 +870,43 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         return;
     }
     __syncthreads();
-    // raw entries -> composite keys (descending score, ascending id), in place;
-    // positions [n_surv, 64*nr) become the maximum key
-    // Rows of the list are handled 4 at a time under one uniform branch, so
-    // their LDS accesses overlap; rows past the list only touch unused slots.
     const int nr = (n_surv + 63) >> 6;
-#pragma unroll
-    for (int g = 0; g < R; g += 4) {
-        if (g < nr) {
-#pragma unroll
-            for (int r = g; r < g + 4; ++r) {
-                const int i = r * 64 + lane;
-                const uint64_t w = sm.list[i];
-                const uint64_t key =
-                    desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w);
-                sm.list[i] = (i < n_surv) ? key : ~0ull;
-            }
-        }
-    }
-    __syncthreads();
-    CBX_STAMP(5);
-
     uint32_t rflags = flags;
     const bool use_topp = P.top_p < 1.0f && n_surv > 0;
     int n_kept = n_surv;  // kept: list positions [0, n_kept)
     float mx_surv = hi;
+    // top-p sorts by a counting sort over [min survivor, max] where it can
+    const float slo = use_topk ? fmaxf(thr, lo) : lo;
+    const float srange = __fsub_rn(hi, slo);
+    const float sscale = __fdiv_rn((float)kWaveBins, srange);
+    const bool csort = use_topp && !bad && srange > 0.0f && sscale < kPosInf;
+    // raw entries -> composite keys (descending score, ascending id), in place;
+    // positions [n_surv, 64*nr) become the maximum key (the counting sort
+    // converts in registers instead).
+    // Rows of the list are handled 4 at a time under one uniform branch, so
+    // their LDS accesses overlap; rows past the list only touch unused slots.
+    if (!csort) {
+#pragma unroll
+        for (int g = 0; g < R; g += 4) {
+            if (g < nr) {
+#pragma unroll
+                for (int r = g; r < g + 4; ++r) {
+                    const int i = r * 64 + lane;
+                    const uint64_t w = sm.list[i];
+                    const uint64_t key =
+                        desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w);
+                    sm.list[i] = (i < n_surv) ? key : ~0ull;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    CBX_STAMP(5);
+
     if (use_topp) {
         // ---- counting sort of the keys by value bin over [min survivor, max] ----
-        const float slo = use_topk ? fmaxf(thr, lo) : lo;
-        const float srange = __fsub_rn(hi, slo);
-        const float sscale = __fdiv_rn((float)kWaveBins, srange);
         bool sorted = false;
-        if (!bad && srange > 0.0f && sscale < kPosInf) {
+        if (csort) {
             const float nslo = -__fmul_rn(slo, sscale);
             uint64_t x[R];
             int rb[R], slot[R];
@@ -919,8 +924,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                     for (int r = g; r < g + 4; ++r) {
                         const int i = r * 64 + lane;
-                        x[r] = sm.list[i];
-                        const float v = desc_key_value(x[r]);
+                        const uint64_t w = sm.list[i];  // raw (score bits << 32 | id)
+                        const float v = __builtin_bit_cast(float, (uint32_t)(w >> 32));
+                        x[r] = (i < nv) ? desc_key(v, (uint32_t)w) : ~0ull;
                         const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, sscale, nslo),
                                                                    0.0f, (float)(kWaveBins - 1));
                         rb[r] = (i < nv) ? kWaveBins - 1 - b : kWaveBins;  // NB: spare
@@ -1014,6 +1020,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         for (int r = g; r < g + 4; ++r) sm.list[fin[r]] = x[r];
                     }
                 sorted = true;
+            } else {
+                // crowded bins: the keys go back in place for the bitonic sort
+                __syncthreads();
+#pragma unroll
+                for (int g = 0; g < R; g += 4)
+                    if (g < nr) {
+#pragma unroll
+                        for (int r = g; r < g + 4; ++r) sm.list[r * 64 + lane] = x[r];
+                    }
             }
         }
         if (!sorted) {
@@ -1046,14 +1061,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         const int C = uni(((n_surv + 63) >> 6) | 1);
         const int nl = uni((n_surv + C - 1) / C);  // lanes holding terms
         float ev[CM];
+        // (every index is inside the list and its spare slots; x <= 0 and not
+        // NaN for rows without NaN / +inf)
+        auto exp_terms = [&](auto nonpos) {
 #pragma unroll
-        for (int q = 0; q < CM; ++q) {
-            if (q < C) {
-                const int i = lane * C + q;
-                const float v = desc_key_value(sm.list[min(i, kWaveCap)]);
-                ev[q] = i < n_surv ? expf_libm_branchless(__fsub_rn(v, mx_surv), sm.tab) : 0.0f;
+            for (int q = 0; q < CM; ++q) {
+                if (q < C) {
+                    const int i = lane * C + q;
+                    const float x = __fsub_rn(desc_key_value(sm.list[i]), mx_surv);
+                    const float e = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
+                                                            : expf_libm_branchless(x, sm.tab);
+                    ev[q] = i < n_surv ? e : 0.0f;
+                }
             }
-        }
+        };
+        if (bad) exp_terms(std::false_type{});
+        else exp_terms(std::true_type{});
         CBX_STAMP(7);
         // psum = 0 + e_0 + e_1 + ... (binary32, sorted order), term by term
         float psum = 0.0f;
@@ -1149,9 +1172,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     bool kp = i < nkv;
                     float v = desc_key_value(key);
                     const int id = kp ? (int)(uint32_t)key : 0;
-                    if (P.min_p > 0.0f)
-                        kp = kp &&
-                             !(expf_libm_branchless(__fsub_rn(v, mx_kept), sm.tab) < P.min_p);
+                    if (P.min_p > 0.0f) {
+                        const float x = __fsub_rn(v, mx_kept);
+                        kp = kp && !((bad ? expf_libm_branchless(x, sm.tab)
+                                          : expf_nonpos(x, sm.tab)) < P.min_p);
+                    }
                     if (use_pen) {
                         const bool hit = kp && bit_of(sm.seen, id);
                         const float pv = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty)
@@ -1195,17 +1220,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
     }
     __syncthreads();
+    // val - mx2 <= 0 and not NaN once mx2 is finite and the row holds no NaN
+    auto f_terms = [&](auto nonpos) {
 #pragma unroll
-    for (int g = 0; g < R; g += 4) {
-        if (g < nk) {
+        for (int g = 0; g < R; g += 4) {
+            if (g < nk) {
 #pragma unroll
-            for (int r = g; r < g + 4; ++r) {
-                const bool kp = (kept >> r) & 1u;
-                const int at = kp ? rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r]) : kWaveCap + lane;  // spare
-                sm.F()[at] = expf_libm_branchless(__fsub_rn(val[r], mx2), sm.tab);
+                for (int r = g; r < g + 4; ++r) {
+                    const bool kp = (kept >> r) & 1u;
+                    const int at = kp ? rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r])
+                                      : kWaveCap + lane;  // spare
+                    const float x = __fsub_rn(val[r], mx2);
+                    sm.F()[at] = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
+                                                         : expf_libm_branchless(x, sm.tab);
+                }
             }
         }
-    }
+    };
+    if (!bad && __builtin_fabsf(mx2) < kPosInf) f_terms(std::true_type{});
+    else f_terms(std::false_type{});
     __syncthreads();
     CBX_STAMP(11);
 

@@ -1,6 +1,7 @@
 // Compares the restated expf (chatterbox.cpp_amd/csrc/cbx_expf.h, compiled
-// here as host code, both the branching and the branch-free form) with the
-// host libm expf over every binary32 bit pattern
+// here as host code: the branching form, the branch-free form, and for x <= 0
+// the non-positive form) with the host libm expf over every binary32 bit
+// pattern
 // in [lo_bits, hi_bits).  Prints "<mismatches> <count>" and the first few
 // mismatching inputs.  usage: expf_exhaustive lo_bits hi_bits n_threads
 #include <cmath>
@@ -29,11 +30,14 @@ int main(int argc, char** argv) {
                 std::memcpy(&x, &bits, 4);
                 const float r = std::exp(x), m = cbx::expf_libm(x);
                 const float b = cbx::expf_libm_branchless(x);
-                uint32_t rb, mb, bb;
+                const bool nonpos = x <= 0.0f;  // -inf included, NaN not
+                const float p = nonpos ? cbx::expf_nonpos(x) : r;
+                uint32_t rb, mb, bb, pb;
                 std::memcpy(&rb, &r, 4);
                 std::memcpy(&mb, &m, 4);
                 std::memcpy(&bb, &b, 4);
-                if (rb != mb || rb != bb) {
+                std::memcpy(&pb, &p, 4);
+                if (rb != mb || rb != bb || rb != pb) {
                     if (!bad[t]) first[t] = bits;
                     ++bad[t];
                 }

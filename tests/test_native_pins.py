@@ -36,6 +36,7 @@ def expf_bin(tmp_path_factory):
                     reason="glibc selects its FMA expf only on FMA+AVX2 hosts")
 @pytest.mark.parametrize("lo,hi", [
     (0x80000000, 0xC2D00001),   # every x in [-104, -0]: all arguments s - max <= 0
+    (0xC2D00001, 0xC4000001),   # (-512, -104): the underflow to 0
     (0x00000000, 0x42B20000),   # [0, 89): positive side, special-case cut-offs
     (0x7F800000, 0x7F800001),   # +inf
     (0xFF800000, 0xFF800001),   # -inf
