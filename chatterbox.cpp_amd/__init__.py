@@ -129,6 +129,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_debug_philox.argtypes = [vp, u64, vp, u64, i32, vp, vp]
     lib.cbx_debug_seqsum.restype = ctypes.c_int
     lib.cbx_debug_seqsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
+    lib.cbx_debug_chainsum.restype = ctypes.c_int
+    lib.cbx_debug_chainsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
     lib.cbx_last_error.restype = ctypes.c_char_p
     lib.cbx_last_error.argtypes = []
     _lib = lib
@@ -257,6 +259,12 @@ class Sampler:
                                          None if thr is None else thr.data_ptr(),
                                          offsets.numel() - 1, sums.data_ptr(), hits.data_ptr(),
                                          _stream_ptr()))
+
+    def debug_chainsum(self, terms, offsets, thr, sums, hits):
+        _check(self.lib.cbx_debug_chainsum(self.handle, terms.data_ptr(), offsets.data_ptr(),
+                                           None if thr is None else thr.data_ptr(),
+                                           offsets.numel() - 1, sums.data_ptr(),
+                                           hits.data_ptr(), _stream_ptr()))
 
     def debug_philox(self, seed, stream_ids, step, n, out):
         _check(self.lib.cbx_debug_philox(self.handle, seed,

@@ -64,6 +64,8 @@ hipError_t launch_v1024x32(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream);
 hipError_t launch_debug_seqsum(const float* terms, const int32_t* offsets, const float* thr,
                               int32_t n_cases, float* sum, int32_t* hit, hipStream_t stream);
+hipError_t launch_debug_chain(const float* terms, const int32_t* offsets, const float* thr,
+                              int32_t n_cases, float* sum, int32_t* hit, hipStream_t stream);
 hipError_t launch_debug_philox(uint64_t seed, const uint64_t* stream_ids, uint64_t step,
                                int32_t n, double* out, hipStream_t stream);
 

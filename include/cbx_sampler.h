@@ -152,6 +152,12 @@ int cbx_debug_philox(cbx_sampler* s, uint64_t seed, const uint64_t* stream_ids,
  * running sum is >= thr[c], else -1.  Device memory, async. */
 int cbx_debug_seqsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
                      const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream);
+/* Diagnostics: the same sums and threshold indices by the one-wavefront
+ * kernel's evaluation (terms in per-lane runs, DPP sweep chains or binade
+ * segments); 1 to 1088 terms per case, otherwise as cbx_debug_seqsum (the
+ * case's sum starts from 0).  Device memory, async. */
+int cbx_debug_chainsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
+                       const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream);
 
 /* Thread-local description of the last error on this thread ("" if none). */
 const char* cbx_last_error(void);

@@ -141,6 +141,36 @@ def test_device_running_sum_scan(cbx, torch_cuda):
     assert np.array_equal(got_hit[has_thr], want_hit[has_thr])
 
 
+def test_device_chain_sums(cbx, torch_cuda):
+    # The one-wave kernel's running sums (sweep chains, binade segments for
+    # long per-lane runs) against numpy's left-to-right float32 accumulation,
+    # bit for bit, and the first index reaching the threshold.
+    import seqsum_cases
+    torch = torch_cuda
+    mod, s = cbx
+    t, off, thr, want_sum, want_hit = seqsum_cases.make_cases(8000, 12)
+    n = np.diff(off)
+    keep = n <= 1088
+    # the cases that fit the one-wave layout, repacked
+    parts = [t[off[c]:off[c + 1]] for c in np.nonzero(keep)[0]]
+    t2 = np.concatenate(parts).astype(np.float32)
+    off2 = np.concatenate([[0], np.cumsum([len(x) for x in parts])]).astype(np.int32)
+    thr2, want_sum, want_hit = thr[keep], want_sum[keep], want_hit[keep]
+    say(f"chain sums: {len(parts)} cases, {t2.size} terms")
+    sums = torch.zeros(len(parts), dtype=torch.float32, device="cuda")
+    hits = torch.full((len(parts),), -9, dtype=torch.int32, device="cuda")
+    s.debug_chainsum(torch.from_numpy(t2).cuda(), torch.from_numpy(off2).cuda(),
+                     torch.from_numpy(thr2).cuda(), sums, hits)
+    torch.cuda.synchronize()
+    got_sum, got_hit = sums.cpu().numpy(), hits.cpu().numpy()
+    has_thr = thr2 > 0
+    bad = np.nonzero(got_sum[~has_thr].view(np.uint32) != want_sum[~has_thr].view(np.uint32))[0]
+    assert bad.size == 0, (bad[:5], got_sum[~has_thr][bad[:5]], want_sum[~has_thr][bad[:5]])
+    assert np.array_equal(got_hit[has_thr], want_hit[has_thr])
+    # long runs (segments) were exercised
+    assert np.sum(np.diff(off2) > 64 * 5) > 100
+
+
 def test_device_philox_matches_oracle(cbx, torch_cuda):
     torch = torch_cuda
     mod, s = cbx
