@@ -1131,96 +1131,92 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         CBX_STAMP(6);
         mx_surv = desc_key_value(sm.list[0]);  // sorted[0]
         // e_i in registers, lane l holding sorted positions [l*C, l*C + C)
-        // (C odd: the strided LDS reads fall in distinct banks)
+        // (C odd: the strided LDS reads fall in distinct banks).  The stage
+        // is compiled per C, so its loops unroll without run-time guards and
+        // every read of a lane's run is in flight at once.
         constexpr int CM = kWaveRows + 1;
         const int C = uni(((n_surv + 63) >> 6) | 1);
         const int nl = uni((n_surv + C - 1) / C);  // lanes holding terms
-        float ev[CM];
-        // (every index is inside the list and its spare slots; x <= 0 and not
-        // NaN for rows without NaN / +inf)
-        auto exp_terms = [&](auto nonpos) {
-#pragma unroll
-            for (int q = 0; q < CM; ++q) {
-                if (q < C) {
-                    const int i = lane * C + q;
-                    const float x = __fsub_rn(desc_key_value(sm.list[i]), mx_surv);
-                    const float e = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
-                                                            : expf_libm_branchless(x, sm.tab);
-                    ev[q] = i < n_surv ? e : 0.0f;
-                }
-            }
-        };
-        if (bad) exp_terms(std::false_type{});
-        else exp_terms(std::true_type{});
-        CBX_STAMP(7);
-        // psum = 0 + e_0 + e_1 + ... (binary32, sorted order), term by term
-        float psum = 0.0f;
+        int last = n_surv - 1;
         with_odd_c<1, CM>(C, [&](auto cc) {
             constexpr int CC = decltype(cc)::value;
+            float ev[CM];
+            // (every index is inside the list and its spare slots; x <= 0 and
+            // not NaN for rows without NaN / +inf)
+            float xs[CC];
+#pragma unroll
+            for (int q = 0; q < CC; ++q)
+                xs[q] = __fsub_rn(desc_key_value(sm.list[lane * CC + q]), mx_surv);
+            if (!bad) {
+#pragma unroll
+                for (int q = 0; q < CC; ++q) ev[q] = expf_nonpos(xs[q], sm.tab);
+            } else {
+#pragma unroll
+                for (int q = 0; q < CC; ++q) ev[q] = expf_libm_branchless(xs[q], sm.tab);
+            }
+#pragma unroll
+            for (int q = 0; q < CC; ++q) ev[q] = lane * CC + q < n_surv ? ev[q] : 0.0f;
+            CBX_STAMP(7);
+            // psum = 0 + e_0 + e_1 + ... (binary32, sorted order), term by term
             int unused;
+            float psum;
             if constexpr (CC >= 7) psum = bad ? chain_sweeps<CC, false>(ev, nl, 0.0f, unused)
                                               : chain_segments<CC>(ev, nl);
             else psum = chain_sweeps<CC, false>(ev, nl, 0.0f, unused);
-        });
-        CBX_STAMP(8);
-        // First i with cum_i = q_0 + ... + q_i >= top_p, q_j = e_j / psum
-        // (binary32, in order).  With Y_i = (e_0 + ... + e_i) / psum in
-        // binary64, |cum_i - Y_i| <= i half-ulps of cum_i (one rounding per
-        // add) + 2^-24 Y_i (the rounding of each q_j): a lane bounds this for
-        // its terms by its last index and the binade of its last Y.  Where
-        // Y_i -/+ that bound puts the first crossing at one index the answer
-        // is certain; otherwise (and for rows holding NaN or +inf) the q's
-        // are formed and summed as the reference does.
-        int last = n_surv - 1;
-        bool certain = false;
-        if (!bad) {
-            const double p = (double)P.top_p;
-            const double inv = __ddiv_rn(1.0, (double)psum);
-            double part = 0.0;
+            CBX_STAMP(8);
+            // First i with cum_i = q_0 + ... + q_i >= top_p, q_j = e_j / psum
+            // (binary32, in order).  With Y_i = (e_0 + ... + e_i) / psum in
+            // binary64, |cum_i - Y_i| <= i half-ulps of cum_i (one rounding
+            // per add) + 2^-24 Y_i (the rounding of each q_j): a lane bounds
+            // this for its terms by its last index and the binade of its last
+            // Y.  Where Y_i -/+ that bound puts the first crossing at one index
+            // the answer is certain; otherwise (and for rows holding NaN or
+            // +inf) the q's are formed and summed as the reference does.
+            bool certain = false;
+            if (!bad) {
+                const double p = (double)P.top_p;
+                const double inv = __ddiv_rn(1.0, (double)psum);
+                double part = 0.0;
 #pragma unroll
-            for (int q = 0; q < CM; ++q)
-                if (q < C) part = __dadd_rn(part, (double)ev[q]);
-            const double x0 = __dsub_rn(wave_incl_scan_f64_dpp(part), part);
-            const double yl = __dmul_rn(__dadd_rn(x0, part), inv);
-            const double cm = __dmul_rn(yl, 1.0 + 0x1p-12);
-            const int b = __builtin_amdgcn_frexp_exp(cm) - 1;  // cm in [2^b, 2^(b+1))
-            const double err = __dadd_rn(
-                __dadd_rn(__dmul_rn((double)(lane * C + C - 1), ldexp(1.0, max(b, -126) - 24)),
-                          __dmul_rn(yl, 0x1p-23)),
-                1e-12);
-            const double lo_thr = __dsub_rn(p, err), hi_thr = __dadd_rn(p, err);
-            // y is non-decreasing: the first index meeting a bound is the
-            // count of the lane's terms before it
-            int n_hi = 0, n_lo = 0;
-            double x = x0;
+                for (int q = 0; q < CC; ++q) part = __dadd_rn(part, (double)ev[q]);
+                const double x0 = __dsub_rn(wave_incl_scan_f64_dpp(part), part);
+                const double yl = __dmul_rn(__dadd_rn(x0, part), inv);
+                const double cm = __dmul_rn(yl, 1.0 + 0x1p-12);
+                const int b = __builtin_amdgcn_frexp_exp(cm) - 1;  // cm in [2^b, 2^(b+1))
+                const double err = __dadd_rn(
+                    __dadd_rn(__dmul_rn((double)(lane * CC + CC - 1),
+                                        ldexp(1.0, max(b, -126) - 24)),
+                              __dmul_rn(yl, 0x1p-23)),
+                    1e-12);
+                const double lo_thr = __dsub_rn(p, err), hi_thr = __dadd_rn(p, err);
+                // y is non-decreasing: the first index meeting a bound is the
+                // count of the lane's terms before it
+                int n_hi = 0, n_lo = 0;
+                double x = x0;
 #pragma unroll
-            for (int q = 0; q < CM; ++q) {
-                if (q < C) {
+                for (int q = 0; q < CC; ++q) {
                     x = __dadd_rn(x, (double)ev[q]);
                     const double y = __dmul_rn(x, inv);
                     n_hi += y < lo_thr ? 1 : 0;
                     n_lo += y < hi_thr ? 1 : 0;
                 }
+                int c_hi = n_hi < CC ? lane * CC + n_hi : 0x7fffffff;
+                int c_lo = n_lo < CC ? lane * CC + n_lo : 0x7fffffff;
+                c_hi = min(wave_min_i_dpp(c_hi), n_surv);  // n_surv: never
+                c_lo = min(wave_min_i_dpp(c_lo), n_surv);
+                if (c_hi == c_lo) {
+                    certain = true;
+                    last = c_hi == n_surv ? n_surv - 1 : c_hi;
+                }
             }
-            int c_hi = n_hi < C ? lane * C + n_hi : 0x7fffffff;
-            int c_lo = n_lo < C ? lane * C + n_lo : 0x7fffffff;
-            c_hi = min(wave_min_i_dpp(c_hi), n_surv);  // n_surv: never
-            c_lo = min(wave_min_i_dpp(c_lo), n_surv);
-            if (c_hi == c_lo) {
-                certain = true;
-                last = c_hi == n_surv ? n_surv - 1 : c_hi;
-            }
-        }
-        if (!certain) {
+            if (!certain) {
 #pragma unroll
-            for (int q = 0; q < CM; ++q)
-                if (q < C) ev[q] = __fdiv_rn(ev[q], psum);  // 0 stays 0
-            with_odd_c<1, CM>(C, [&](auto cc) {
+                for (int q = 0; q < CC; ++q) ev[q] = __fdiv_rn(ev[q], psum);  // 0 stays 0
                 int hit;
-                (void)chain_sweeps<decltype(cc)::value, true>(ev, nl, P.top_p, hit);
+                (void)chain_sweeps<CC, true>(ev, nl, P.top_p, hit);
                 last = hit < 0 ? n_surv - 1 : hit;
-            });
-        }
+            }
+        });
         n_kept = uni(last + 1);
         CBX_STAMP(9);
         if (n_kept < n_surv &&
