@@ -114,8 +114,8 @@ def cpu_baseline(hist, hist_len, params, logits_host, u, gpu_tokens, seconds_1t,
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1280)
-    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--steps", type=int, default=16384)
+    ap.add_argument("--warmup", type=int, default=1024)
     ap.add_argument("--steps-per-launch", type=int, default=64)
     ap.add_argument("--slabs", type=int, default=2)
     ap.add_argument("--single-launch-steps", type=int, default=200,

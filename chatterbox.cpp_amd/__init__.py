@@ -15,7 +15,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libcbx_sampler.so")
+# The in-tree build; CBX_SAMPLER_LIB names another build of the same library.
+LIB_PATH = os.environ.get("CBX_SAMPLER_LIB") or os.path.join(_HERE, "lib", "libcbx_sampler.so")
 
 CBX_OK = 0
 CBX_ERR_INVALID = -1

@@ -1354,22 +1354,41 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             u = a.uniforms[rs];
         }
         const bool last_kept = bit_of(sm.u.b.keptw, V - 1);
-        // binary64 prefix of the exp terms in id order, contiguous chunks
-        const int C = (n_final + 63) >> 6;
-        const int r0 = min(lane * C, n_final), r1 = min(r0 + C, n_final);
-        double part = 0.0;
-        for (int r = r0; r < r1; ++r) part = __dadd_rn(part, (double)sm.F()[r]);
-        double cp = wave_incl_scan_f64(part, lane);
-        const double total = readlane_f64(cp, 63);
-        cp = __dsub_rn(cp, part);  // exclusive
-        const double target = __dmul_rn(u, total);
+        // binary64 prefix of the exp terms in id order: lane l holds the odd
+        // run [l*C, l*C + C) in registers (compiled per C, reads in flight
+        // together, distinct banks)
+        constexpr int CM = kWaveRows + 1;
+        const int C = uni(((n_final + 63) >> 6) | 1);
+        double total = 0.0, blo = 0.0, bhi = 0.0;
         int found = 0x7fffffff;
-        double blo = 0.0, bhi = 0.0;
-        for (int r = r0; r < r1; ++r) {
-            const double before = cp;
-            cp = __dadd_rn(cp, (double)sm.F()[r]);
-            if (cp >= target) { found = r; blo = before; bhi = cp; break; }
-        }
+        with_odd_c<1, CM>(C, [&](auto cc) {
+            constexpr int CC = decltype(cc)::value;
+            float f[CC];
+#pragma unroll
+            for (int q = 0; q < CC; ++q) {
+                const int r = lane * CC + q;  // inside the list's float view
+                const float v = sm.F()[r];
+                f[q] = r < n_final ? v : 0.0f;
+            }
+            double part = 0.0;
+#pragma unroll
+            for (int q = 0; q < CC; ++q) part = __dadd_rn(part, (double)f[q]);
+            double cp = wave_incl_scan_f64(part, lane);
+            total = readlane_f64(cp, 63);
+            cp = __dsub_rn(cp, part);  // exclusive
+            const double target = __dmul_rn(u, total);
+            bool got = false;
+#pragma unroll
+            for (int q = 0; q < CC; ++q) {
+                const double before = cp;
+                cp = __dadd_rn(cp, (double)f[q]);
+                const bool hit = !got && cp >= target && lane * CC + q < n_final;
+                blo = hit ? before : blo;
+                bhi = hit ? cp : bhi;
+                found = hit ? lane * CC + q : found;
+                got = got || hit;
+            }
+        });
         const int rank = wave_min_i_dpp(found);
         bool certain = false;
         if (!(u > 0.0)) {
