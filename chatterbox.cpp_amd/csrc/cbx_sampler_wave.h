@@ -187,10 +187,22 @@ __device__ __forceinline__ uint32_t lds_offset(const T* p) {
     return (uint32_t)(uintptr_t)p;
 }
 
-// One 8-byte LDS store: w0 at byte offset addr, w1 at addr + 4 (two data
-// registers, so no register pair is assembled for it).
-__device__ __forceinline__ void lds_store_pair(uint32_t addr, uint32_t w0, uint32_t w1) {
-    asm volatile("ds_write2_b32 %0, %1, %2 offset1:1" : : "v"(addr), "v"(w0), "v"(w1) : "memory");
+// One 8-byte LDS store (w0 at byte offset addr, w1 at addr + 4: two data
+// registers, so no register pair is assembled) made by the lanes of mask
+// only (a ballot, so a subset of the active lanes): the other lanes are
+// switched off for this one instruction instead of being sent to spare slots
+// by a per-lane select.
+__device__ __forceinline__ void lds_store_pair_lanes(uint32_t addr, uint32_t w0, uint32_t w1,
+                                                     uint64_t mask) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %4\n\t"
+        "ds_write2_b32 %1, %2, %3 offset1:1\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(saved)
+        : "v"(addr), "v"(w0), "v"(w1), "s"(mask)
+        : "memory");
 }
 
 // An opaque copy of a uniform value: predicates built on it in one pass are
@@ -729,7 +741,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     };
                     // sb: byte offset of the next free slot (a running scalar)
                     const uint32_t lbase = lds_offset(&sm.list[0]);
-                    const uint32_t spare = lds_offset(&sm.list[kWaveCap + lane]);
                     uint32_t sb = lbase;
 #pragma unroll
                     for (int j = 0; j < Q; ++j) {
@@ -737,11 +748,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
                             const float v = s[4 * j + c];
-                            const bool ge = v >= B0j;
-                            const uint64_t m = __ballot(ge);
+                            const uint64_t m = __ballot(v >= B0j);
                             const uint32_t at = ((uint32_t)ballot_rank(m) << 3) + sb;
-                            lds_store_pair(ge ? at : spare, (uint32_t)(256 * j + 4 * lane + c),
-                                           __builtin_bit_cast(uint32_t, v));
+                            lds_store_pair_lanes(at, (uint32_t)(256 * j + 4 * lane + c),
+                                                 __builtin_bit_cast(uint32_t, v), m);
                             // opaque, so the shift-add is not re-associated
                             sb = (uint32_t)fresh((int)(sb + 8u * (uint32_t)__popcll(m)));
                         }
