@@ -49,7 +49,7 @@ constexpr double kDrawMargin = 3e-7;
 // Waves per SIMD the register allocation aims for (the row's scores take
 // 4*Q registers; the rest of the kernel is kept within the same budget).
 #ifndef WAVE_WPE
-#define WAVE_WPE 3
+#define WAVE_WPE 4
 #endif
 
 // LDS of one row (~11 KB at Q = 26, so a CU holds as many rows as registers
@@ -62,17 +62,17 @@ constexpr double kDrawMargin = 3e-7;
 template <int Q>
 struct WaveSmem {
     uint64_t tab[32];
-    uint32_t seen[8 * Q + 64];  // history ids (penalty) (+ a spare word per lane)
+    uint32_t seen[8 * Q];  // history ids (penalty)
     union {
         uint32_t hist16[kWaveBins / 2 + 2];  // sort offsets, u16 pairs (+ spare bins)
-        float cand[kWaveCand + 64];          // scores of the top-k bin (+ spare slots)
-        uint64_t candk[kWaveCand + 64];      // (score bits << 32 | id), same bin
+        float cand[kWaveCand];               // scores of the top-k bin
+        uint64_t candk[kWaveCand];           // (score bits << 32 | id), same bin
         struct {
-            uint32_t keptw[8 * Q + 64];  // kept ids after every filter (+ spare words)
+            uint32_t keptw[8 * Q];      // kept ids after every filter
             uint32_t woff[8 * Q];       // kept ids before each word
         } b;
     } u;
-    uint64_t list[kWaveCap + 64];  // survivors (+ spare slots)
+    uint64_t list[kWaveCap + 4];  // survivors (+ padding: maximum keys, one spare slot)
     int rk;
 
     __device__ uint32_t* khist() { return reinterpret_cast<uint32_t*>(list); }
@@ -202,6 +202,41 @@ __device__ __forceinline__ void lds_store_pair_lanes(uint32_t addr, uint32_t w0,
         "s_mov_b64 exec, %0"
         : "=&s"(saved)
         : "v"(addr), "v"(w0), "v"(w1), "s"(mask)
+        : "memory");
+}
+
+// Single LDS stores and ORs made by the lanes of mask only, as above.
+__device__ __forceinline__ void lds_store_b64_lanes(uint32_t addr, uint64_t v, uint64_t mask) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %3\n\t"
+        "ds_write_b64 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(saved)
+        : "v"(addr), "v"(v), "s"(mask)
+        : "memory");
+}
+__device__ __forceinline__ void lds_store_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %3\n\t"
+        "ds_write_b32 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(saved)
+        : "v"(addr), "v"(v), "s"(mask)
+        : "memory");
+}
+__device__ __forceinline__ void lds_or_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b64 exec, %3\n\t"
+        "ds_or_b32 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(saved)
+        : "v"(addr), "v"(v), "s"(mask)
         : "memory");
 }
 
@@ -525,7 +560,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             const int t = hid[u];
             const bool ok = t >= 0 && t < V;
             if (u * 64 < hlen)  // uniform: batches past the history are skipped
-                atomicOr(&sm.seen[ok ? t >> 5 : 8 * Q + lane], ok ? 1u << (t & 31) : 0u);
+                lds_or_b32_lanes(lds_offset(&sm.seen[0]) + ((uint32_t)(t >> 5) << 2),
+                                 1u << (t & 31), __ballot(ok));
         }
         for (int b = HB * 64; b < hlen; b += 256) {  // histories past 1024 ids
             int t[4];
@@ -778,7 +814,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                 const bool inb = i < n && val_of(x[r]) < B1;
                                 const uint64_t m = __ballot(inb);
                                 const int at = ballot_rank(m) + nc;
-                                sm.u.candk[(inb && at < kWaveCand) ? at : kWaveCand + lane] = x[r];
+                                // (more than the array holds: the count check below fails)
+                                if (nc + __popcll(m) <= kWaveCand)
+                                    lds_store_b64_lanes(lds_offset(&sm.u.candk[0]) + 8u * (uint32_t)at,
+                                                        x[r], m);
                                 nc += __popcll(m);
                             }
                         }
@@ -815,7 +854,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                     const bool keep = r * 64 + lane < n && val_of(x[r]) > thr;
                                     const uint64_t m = __ballot(keep);
                                     const int at = ballot_rank(m) + n2;
-                                    sm.list[keep ? at : kWaveCap + lane] = x[r];
+                                    lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)at,
+                                                        x[r], m);
                                     n2 += __popcll(m);
                                 }
                             }
@@ -880,7 +920,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     const bool in = bin_of(v) == bsel;
                     const uint64_t m = __ballot(in);
                     const int at = nc + ballot_rank(m);
-                    sm.u.cand[(in && at < kWaveCand) ? at : kWaveCand + lane] = v;
+                    if (nc + __popcll(m) <= kWaveCand)  // else nc > kWaveCand: not used
+                        lds_store_b32_lanes(lds_offset(&sm.u.cand[0]) + 4u * (uint32_t)at,
+                                            __builtin_bit_cast(uint32_t, v), m);
                     nc += __popcll(m);
                 });
                 __syncthreads();
@@ -928,16 +970,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 
     // ---- survivors -> LDS list of (score bits << 32 | id) ----
     // keep = score != -inf and not (top-k and score <= thr); without NaN that
-    // is score > thr (thr = -inf when nothing is cut).  Dropped items and
-    // items past the list write its spare slot.
+    // is score > thr (thr = -inf when nothing is cut).  Only kept items that
+    // fit the list are stored.
     if (n_surv < 0) {
         int n = 0;
         each_score([&](float v, int id) {
             const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
             const uint64_t m = __ballot(keep);
             const int at = n + ballot_rank(m);
-            const int slot = (keep && at < kWaveCap) ? at : kWaveCap + lane;
-            sm.list[slot] = ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)id;
+            // past the list: the row overflows and its list is not used
+            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)at,
+                                ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)id,
+                                __ballot(keep && at < kWaveCap));
             n += __popcll(m);
         });
         n_surv = n;
@@ -1052,8 +1096,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     if (g < nr) {
 #pragma unroll
                         for (int r = g; r < g + 4; ++r) {
-                            const int dst = rb[r] < kWaveBins ? get16(rb[r]) + slot[r] : kWaveCap + lane;
-                            sm.list[dst] = x[r];
+                            const int dst = get16(rb[r]) + slot[r];  // survivors' lanes only
+                            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)dst, x[r],
+                                                __ballot(rb[r] < kWaveBins));
                         }
                     }
                 // keys after the survivors: the maximum key (4 slots, for the
@@ -1093,7 +1138,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                 rank[u] += (k0 < x[g + u]) + (k1 < x[g + u]) + (k2 < x[g + u]) +
                                            (k3 < x[g + u]);
                             }
-                            fin[g + u] = rb[g + u] < kWaveBins ? s0[u] + rank[u] : kWaveCap + lane;
+                            fin[g + u] = s0[u] + rank[u];
                         }
                     }
                 }
@@ -1102,7 +1147,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 for (int g = 0; g < R; g += 4)
                     if (g < nr) {
 #pragma unroll
-                        for (int r = g; r < g + 4; ++r) sm.list[fin[r]] = x[r];
+                        for (int r = g; r < g + 4; ++r)
+                            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)fin[r], x[r],
+                                                __ballot(rb[r] < kWaveBins));
                     }
                 sorted = true;
             } else {
@@ -1156,7 +1203,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             float xs[CC];
 #pragma unroll
             for (int q = 0; q < CC; ++q)
-                xs[q] = __fsub_rn(desc_key_value(sm.list[lane * CC + q]), mx_surv);
+                xs[q] = __fsub_rn(desc_key_value(sm.list[min(lane * CC + q, kWaveCap)]), mx_surv);
             if (!bad) {
 #pragma unroll
                 for (int q = 0; q < CC; ++q) ev[q] = expf_nonpos(xs[q], sm.tab);
@@ -1270,7 +1317,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     val[r] = v;
                     idr[r] = id;
                     kept |= (kp ? 1u : 0u) << r;
-                    atomicOr(&sm.u.b.keptw[kp ? id >> 5 : 8 * Q + lane], kp ? 1u << (id & 31) : 0u);
+                    lds_or_b32_lanes(lds_offset(&sm.u.b.keptw[0]) + ((uint32_t)(id >> 5) << 2),
+                                     1u << (id & 31), __ballot(kp));
                 }
             }
         }
@@ -1312,11 +1360,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                 for (int r = g; r < g + 4; ++r) {
                     const bool kp = (kept >> r) & 1u;
-                    const int at = kp ? rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r])
-                                      : kWaveCap + lane;  // spare
+                    const int at = rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r]);  // kept lanes
                     const float x = __fsub_rn(val[r], mx2);
-                    sm.F()[at] = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
-                                                         : expf_libm_branchless(x, sm.tab);
+                    const float e = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
+                                                            : expf_libm_branchless(x, sm.tab);
+                    lds_store_b32_lanes(lds_offset(sm.F()) + 4u * (uint32_t)at,
+                                        __builtin_bit_cast(uint32_t, e), __ballot(kp));
                 }
             }
         }
