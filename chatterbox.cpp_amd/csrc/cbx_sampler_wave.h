@@ -72,7 +72,7 @@ struct WaveSmem {
             uint32_t woff[8 * Q];       // kept ids before each word
         } b;
     } u;
-    uint64_t list[kWaveCap + 4];  // survivors (+ padding: maximum keys, one spare slot)
+    alignas(16) uint64_t list[kWaveCap + 4];  // survivors (+ padding: maximum keys)
     int rk;
 
     __device__ uint32_t* khist() { return reinterpret_cast<uint32_t*>(list); }
@@ -523,22 +523,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     rsc.inv_t = __fdiv_rn(1.0f, P.temp);
     rsc.V = V;
     rsc.stop = a.stop_token;
-    // the history ids (first 1024) are requested first: their bitmap is
-    // built while the logits are still arriving
     const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
     const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
     const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
-    constexpr int HB = 16;  // history ids per lane per batch
-    int hid[HB];
-    if (use_pen) {
-        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
-#pragma unroll
-        for (int u = 0; u < HB; ++u)
-            hid[u] = (u * 64 + lane < hlen)
-                         ? __builtin_amdgcn_raw_buffer_load_b32(rh, (u * 64 + lane) * 4, 0, 0)
-                         : -1;
-    }
     float s[EPL];
 #pragma unroll
     for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
@@ -554,25 +541,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     for (int w = lane; w < 8 * Q; w += 64) sm.seen[w] = 0u;
     __syncthreads();
     // ---- history ids -> seen bitmap (main.cpp:775) ----
+    // The id loads are issued after the logits' (memory reads complete in
+    // order, so waiting for them costs nothing beyond the logits' arrival);
+    // loads past the history read 0 and are masked out.
     if (use_pen) {
+        constexpr int HB = 16;  // ids per lane per batch: 1024 per pass
+        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
+        for (int b0 = 0; b0 < hlen; b0 += HB * 64) {
+            int hid[HB];
 #pragma unroll
-        for (int u = 0; u < HB; ++u) {
-            const int t = hid[u];
-            const bool ok = t >= 0 && t < V;
-            if (u * 64 < hlen)  // uniform: batches past the history are skipped
-                lds_or_b32_lanes(lds_offset(&sm.seen[0]) + ((uint32_t)(t >> 5) << 2),
-                                 1u << (t & 31), __ballot(ok));
-        }
-        for (int b = HB * 64; b < hlen; b += 256) {  // histories past 1024 ids
-            int t[4];
+            for (int u = 0; u < HB; ++u)
+                hid[u] = __builtin_amdgcn_raw_buffer_load_b32(rh, (b0 + u * 64 + lane) * 4, 0, 0);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = b + u * 64 + lane;
-                t[u] = j < hlen ? hrow[j] : -1;
+            for (int u = 0; u < HB; ++u) {
+                const int t = hid[u];
+                const bool ok = b0 + u * 64 + lane < hlen && t >= 0 && t < V;
+                if (b0 + u * 64 < hlen)  // uniform: batches past the history are skipped
+                    lds_or_b32_lanes(lds_offset(&sm.seen[0]) + ((uint32_t)(t >> 5) << 2),
+                                     1u << (t & 31), __ballot(ok));
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (t[u] >= 0 && t[u] < V) atomicOr(&sm.seen[t[u] >> 5], 1u << (t[u] & 31));
         }
     }
     // ---- masks and temperature (main.cpp:735-738) ----
@@ -708,14 +696,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
             __syncthreads();
             CBX_STAMP(16);
-            constexpr int BPL = kWaveBins / 64;
-            uint32_t cnt[BPL];
-            int tot = 0;
+            // Lane l owns the 16 bins kWaveBins-1-16l .. kWaveBins-16-16l
+            // (descending scores), contiguous in LDS: their total from four
+            // 16-byte reads.  The padding sits in bin 0 (lane 63).
+            static_assert(kWaveBins == 1024, "16 bins per lane");
+            const uint32_t pad = (uint32_t)(256 * Q - V);
+            int tot;
+            {
+                const uint4* h4 = reinterpret_cast<const uint4*>(hist) + (kWaveBins / 4 - 4 - 4 * lane);
+                uint32_t sum = 0;
 #pragma unroll
-            for (int q = 0; q < BPL; ++q) {
-                const int b = kWaveBins - 1 - (lane * BPL + q);  // descending bins
-                cnt[q] = hist[b] - (b == 0 ? (uint32_t)(256 * Q - V) : 0u);
-                tot += (int)cnt[q];
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 w = h4[i];
+                    sum += (w.x + w.y) + (w.z + w.w);
+                }
+                tot = (int)(sum - (lane == 63 ? pad : 0u));
             }
             int n_fin;
             const int excl = wave_excl_scan_i(tot, n_fin);
@@ -724,26 +719,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 above = n_fin;
                 done = true;
             } else {
-                const bool mine = excl <= k && k < excl + tot;
-                int bsel = 0, above_bins = 0, nsel = 0;
-                if (mine) {
-                    int run = excl;
-                    bool found = false;
-#pragma unroll
-                    for (int q = 0; q < BPL; ++q) {
-                        if (!found && run + (int)cnt[q] > k) {
-                            bsel = kWaveBins - 1 - (lane * BPL + q);
-                            above_bins = run;
-                            nsel = (int)cnt[q];
-                            found = true;
-                        }
-                        run += (int)cnt[q];
-                    }
-                }
-                const int L = __builtin_ctzll(__ballot(mine));
-                bsel = __builtin_amdgcn_readlane(bsel, L);
-                above_bins = __builtin_amdgcn_readlane(above_bins, L);
-                nsel = __builtin_amdgcn_readlane(nsel, L);
+                // the lane whose bins hold rank k; lanes 0..15 take its bins
+                // (q-th largest first) and scan their counts
+                const int L = __builtin_ctzll(__ballot(excl <= k && k < excl + tot));
+                const int exclL = __builtin_amdgcn_readlane(excl, L);
+                const int bq = kWaveBins - 1 - (16 * L + (lane & 15));
+                const int cq = (int)(hist[bq] - (bq == 0 ? pad : 0u));
+                int inc = cq;  // inclusive scan inside lanes 0..15 (row 0)
+                inc += dpp_i<0x111, 0xf>(0, inc);
+                inc += dpp_i<0x112, 0xf>(0, inc);
+                inc += dpp_i<0x114, 0xf>(0, inc);
+                inc += dpp_i<0x118, 0xf>(0, inc);
+                const int Qh = __builtin_ctzll(__ballot(lane < 16 && exclL + inc > k));
+                const int bsel = kWaveBins - 1 - (16 * L + Qh);
+                const int nsel = __builtin_amdgcn_readlane(cq, Qh);
+                const int above_bins = exclL + __builtin_amdgcn_readlane(inc, Qh) - nsel;
                 // Score boundaries of the selected bin: B0 = least float with
                 // bin >= bsel, B1 = least float with bin >= bsel + 1 (+inf past
                 // the top bin).  bin(v) >= b  <=>  fma(v, bs, c0) >= 2^23 + b,
