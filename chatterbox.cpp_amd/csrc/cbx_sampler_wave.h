@@ -187,55 +187,47 @@ __device__ __forceinline__ uint32_t lds_offset(const T* p) {
     return (uint32_t)(uintptr_t)p;
 }
 
-// One 8-byte LDS store (w0 at byte offset addr, w1 at addr + 4: two data
-// registers, so no register pair is assembled) made by the lanes of mask
-// only (a ballot, so a subset of the active lanes): the other lanes are
-// switched off for this one instruction instead of being sent to spare slots
-// by a per-lane select.
+// LDS stores and ORs made by the lanes of `mask` only (a ballot, so a subset
+// of the active lanes): the other lanes are switched off for the one
+// instruction instead of being sent to spare slots by a per-lane select.
+// This kernel runs every lane of its wave on every path (its branches are
+// wave-uniform), so exec is restored to all lanes afterwards.
+//   pair: w0 at byte offset addr, w1 at addr + 4 (two data registers, so no
+//   register pair is assembled for it)
 __device__ __forceinline__ void lds_store_pair_lanes(uint32_t addr, uint32_t w0, uint32_t w1,
                                                      uint64_t mask) {
-    uint64_t saved;
     asm volatile(
-        "s_mov_b64 %0, exec\n\t"
-        "s_mov_b64 exec, %4\n\t"
-        "ds_write2_b32 %1, %2, %3 offset1:1\n\t"
-        "s_mov_b64 exec, %0"
-        : "=&s"(saved)
+        "s_mov_b64 exec, %3\n\t"
+        "ds_write2_b32 %0, %1, %2 offset1:1\n\t"
+        "s_mov_b64 exec, -1"
+        :
         : "v"(addr), "v"(w0), "v"(w1), "s"(mask)
         : "memory");
 }
-
-// Single LDS stores and ORs made by the lanes of mask only, as above.
 __device__ __forceinline__ void lds_store_b64_lanes(uint32_t addr, uint64_t v, uint64_t mask) {
-    uint64_t saved;
     asm volatile(
-        "s_mov_b64 %0, exec\n\t"
-        "s_mov_b64 exec, %3\n\t"
-        "ds_write_b64 %1, %2\n\t"
-        "s_mov_b64 exec, %0"
-        : "=&s"(saved)
+        "s_mov_b64 exec, %2\n\t"
+        "ds_write_b64 %0, %1\n\t"
+        "s_mov_b64 exec, -1"
+        :
         : "v"(addr), "v"(v), "s"(mask)
         : "memory");
 }
 __device__ __forceinline__ void lds_store_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
-    uint64_t saved;
     asm volatile(
-        "s_mov_b64 %0, exec\n\t"
-        "s_mov_b64 exec, %3\n\t"
-        "ds_write_b32 %1, %2\n\t"
-        "s_mov_b64 exec, %0"
-        : "=&s"(saved)
+        "s_mov_b64 exec, %2\n\t"
+        "ds_write_b32 %0, %1\n\t"
+        "s_mov_b64 exec, -1"
+        :
         : "v"(addr), "v"(v), "s"(mask)
         : "memory");
 }
 __device__ __forceinline__ void lds_or_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
-    uint64_t saved;
     asm volatile(
-        "s_mov_b64 %0, exec\n\t"
-        "s_mov_b64 exec, %3\n\t"
-        "ds_or_b32 %1, %2\n\t"
-        "s_mov_b64 exec, %0"
-        : "=&s"(saved)
+        "s_mov_b64 exec, %2\n\t"
+        "ds_or_b32 %0, %1\n\t"
+        "s_mov_b64 exec, -1"
+        :
         : "v"(addr), "v"(v), "s"(mask)
         : "memory");
 }
