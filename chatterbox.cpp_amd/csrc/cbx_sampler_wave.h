@@ -52,19 +52,18 @@ constexpr double kDrawMargin = 3e-7;
 #define WAVE_WPE 4
 #endif
 
-// LDS of one row (~11 KB at Q = 26, so a CU holds as many rows as registers
-// allow).  Phases reuse storage:
+// LDS of one row (~11 KB at Q = 26: 14 rows per CU).  Phases reuse storage:
 //   list:  the top-k histogram (u32 bins) until the survivors are written;
-//          the survivor keys; the kept exp terms F in id order at the end
-//   u:     the sort's bin offsets (two u16 per word); the top-k bin's
-//          candidates; the allowed row of masked rows at the start; the kept
-//          bitmap and its word offsets at the end
+//          the survivor entries; the sort's bin counters and offsets while
+//          the entries are in registers; the sorted keys; the kept exp terms
+//          F in id order at the end
+//   u:     the top-k bin's candidates; the allowed row of masked rows at the
+//          start; the kept bitmap and its word offsets at the end
 template <int Q>
 struct WaveSmem {
     uint64_t tab[32];
     uint32_t seen[8 * Q];  // history ids (penalty)
     union {
-        uint32_t hist16[kWaveBins / 2 + 2];  // sort offsets, u16 pairs (+ spare bins)
         float cand[kWaveCand];               // scores of the top-k bin
         uint64_t candk[kWaveCand];           // (score bits << 32 | id), same bin
         struct {
@@ -989,8 +988,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // top-p sorts by a counting sort over [min survivor, max] where it can
     const float slo = use_topk ? fmaxf(thr, lo) : lo;
     const float srange = __fsub_rn(hi, slo);
-    const float sscale = __fdiv_rn((float)kWaveBins, srange);
-    const bool csort = use_topp && !bad && srange > 0.0f && sscale < kPosInf;
+    // descending sort bins: fma(v, -ss, sc) lands in [2^23, 2^23 + NB) (an
+    // integer) for v in [slo, hi], checked at both ends (the map is monotone)
+    const float ss = __fdiv_rn((float)(kWaveBins - 4), srange);
+    const float sc = __fmaf_rn(hi, ss, 0x1p23f + 2.0f);
+    const bool csort = use_topp && !bad && srange > 0.0f && ss < kPosInf &&
+                       __fmaf_rn(hi, -ss, sc) >= 0x1p23f &&
+                       __fmaf_rn(slo, -ss, sc) <= 0x1p23f + (float)(kWaveBins - 1);
     // raw entries -> composite keys (descending score, ascending id), in place;
     // positions [n_surv, 64*nr) become the maximum key (the counting sort
     // converts in registers instead).
@@ -1016,18 +1020,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 
     if (use_topp) {
         // ---- counting sort of the keys by value bin over [min survivor, max] ----
+        // Every survivor is read into registers first, so the counters and
+        // offsets can use the list's own storage until the keys go back to
+        // their sorted places; each key's bin bounds stay in registers.
         bool sorted = false;
         if (csort) {
-            const float nslo = -__fmul_rn(slo, sscale);
+            // descending bins: rb(v) = bits(fma(v, -ss, sc)) - bits(2^23), in
+            // [0, NB) for v in [slo, hi] (csort checked both ends)
             uint64_t x[R];
-            int rb[R], slot[R];
-            // bin offsets as u16 pairs: bin b in half (b & 1) of word b >> 1
-            uint32_t* h16 = sm.u.hist16;
-            auto get16 = [&](int b) { return (int)((h16[b >> 1] >> ((b & 1) * 16)) & 0xffffu); };
-#pragma unroll
-            for (int q = 0; q < kWaveBins / 128; ++q) h16[lane * (kWaveBins / 128) + q] = 0u;
-            if (lane < 2) h16[kWaveBins / 2 + lane] = 0u;
-            __syncthreads();
+            int rb[R], slot[R], s0[R], s1[R];
+            uint32_t* cnt = reinterpret_cast<uint32_t*>(sm.list);  // NB counters, then per-lane spares
+            constexpr int kSpare = kWaveBins + 8;
             const int nv = fresh(n_surv);
 #pragma unroll
             for (int g = 0; g < R; g += 4) {
@@ -1038,50 +1041,72 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         const uint64_t w = sm.list[i];  // raw (score bits << 32 | id)
                         const float v = __builtin_bit_cast(float, (uint32_t)(w >> 32));
                         x[r] = (i < nv) ? desc_key(v, (uint32_t)w) : ~0ull;
-                        const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, sscale, nslo),
-                                                                   0.0f, (float)(kWaveBins - 1));
-                        rb[r] = (i < nv) ? kWaveBins - 1 - b : kWaveBins;  // NB: spare
-                        const uint32_t old16 =
-                            atomicAdd(&h16[rb[r] >> 1], (rb[r] & 1) ? 0x10000u : 1u);
-                        slot[r] = (int)((old16 >> ((rb[r] & 1) * 16)) & 0xffffu);
+                        const int b = (int)(__builtin_bit_cast(uint32_t, __fmaf_rn(v, -ss, sc)) -
+                                            0x4B000000u);
+                        rb[r] = (i < nv) ? b : kSpare + lane;  // past the list: a spare counter
                     }
                 }
             }
+            __syncthreads();  // the list is in registers: its storage takes the counters
+#pragma unroll
+            for (int q = 0; q < kWaveBins / 64; ++q) cnt[lane * (kWaveBins / 64) + q] = 0u;
+            if (lane < 8) cnt[kWaveBins + lane] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int g = 0; g < R; g += 4)
+                if (g < nr) {
+#pragma unroll
+                    for (int r = g; r < g + 4; ++r) slot[r] = (int)atomicAdd(&cnt[rb[r]], 1u);
+                }
             __syncthreads();
             CBX_STAMP(13);
-            constexpr int WPL16 = kWaveBins / 128;  // words (bin pairs) per lane
-            uint32_t wv[WPL16];
-            int tot = 0;
+            // lane l: bins 16l .. 16l + 15 -> exclusive offsets in place
             uint32_t big = 0;
+            {
+                uint4* c4 = reinterpret_cast<uint4*>(cnt) + 4 * lane;
+                uint4 w4[4];
+                uint32_t loc = 0;
 #pragma unroll
-            for (int q = 0; q < WPL16; ++q) {
-                wv[q] = h16[lane * WPL16 + q];
-                const uint32_t c0 = wv[q] & 0xffffu, c1 = wv[q] >> 16;
-                tot += (int)(c0 + c1);
-                big = max(big, max(c0, c1));
-            }
-            int all;
-            int base = wave_excl_scan_i(tot, all);
+                for (int i = 0; i < 4; ++i) {
+                    w4[i] = c4[i];
+                    big = max(big, max(max(w4[i].x, w4[i].y), max(w4[i].z, w4[i].w)));
+                    loc += (w4[i].x + w4[i].y) + (w4[i].z + w4[i].w);
+                }
+                int all;
+                uint32_t run = (uint32_t)wave_excl_scan_i((int)loc, all);
 #pragma unroll
-            for (int q = 0; q < WPL16; ++q) {
-                const uint32_t c0 = wv[q] & 0xffffu;
-                h16[lane * WPL16 + q] = (uint32_t)base | ((uint32_t)(base + (int)c0) << 16);
-                base += (int)(c0 + (wv[q] >> 16));
+                for (int i = 0; i < 4; ++i) {
+                    uint4 o;
+                    o.x = run; run += w4[i].x;
+                    o.y = run; run += w4[i].y;
+                    o.z = run; run += w4[i].z;
+                    o.w = run; run += w4[i].w;
+                    c4[i] = o;
+                }
+                if (lane == 63) cnt[kWaveBins] = run;  // end of the last bin (= n_surv)
             }
-            // spare bin NB and the sentinel NB + 1: both start at n_surv (empty)
-            if (lane == 0) h16[kWaveBins / 2] = (uint32_t)n_surv | ((uint32_t)n_surv << 16);
             if (__ballot(big > (uint32_t)kWaveSortMax) == 0) {
                 __syncthreads();
+#pragma unroll
+                for (int g = 0; g < R; g += 4)
+                    if (g < nr) {
+#pragma unroll
+                        for (int r = g; r < g + 4; ++r) {  // lanes past the list: empty bins
+                            const bool in = r * 64 + lane < nv;
+                            const int a0 = (int)cnt[rb[r]], a1 = (int)cnt[rb[r] + 1];
+                            s0[r] = in ? a0 : n_surv;
+                            s1[r] = in ? a1 : n_surv;
+                        }
+                    }
+                __syncthreads();  // offsets read: the keys take their bins
                 CBX_STAMP(14);
 #pragma unroll
                 for (int g = 0; g < R; g += 4)
                     if (g < nr) {
 #pragma unroll
-                        for (int r = g; r < g + 4; ++r) {
-                            const int dst = get16(rb[r]) + slot[r];  // survivors' lanes only
-                            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)dst, x[r],
-                                                __ballot(rb[r] < kWaveBins));
-                        }
+                        for (int r = g; r < g + 4; ++r)
+                            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)(s0[r] + slot[r]),
+                                                x[r], __ballot(r * 64 + lane < nv));
                     }
                 // keys after the survivors: the maximum key (4 slots, for the
                 // reads past a bin's end below)
@@ -1090,37 +1115,32 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 CBX_STAMP(15);
                 // Rank inside the bin: the keys of the bin below x.  Reads past
                 // the bin's end see later bins (lower scores: larger keys) or
-                // the maximum key, which never count; bins of one key skip.
-                // The first four keys of the bins of four rows are read together
-                // (most bins hold at most four); longer bins loop on.
+                // the maximum key, which never count.  The first four keys of
+                // the bins of four rows are read together (most bins hold at
+                // most four); longer bins loop on.
                 int fin[R];
 #pragma unroll
                 for (int g = 0; g < R; g += 4) {
                     if (g < nr) {
-                        int s0[4], s1[4], rank[4];
                         uint64_t kk[4][4];
 #pragma unroll
                         for (int u = 0; u < 4; ++u) {
-                            s0[u] = get16(rb[g + u]);
-                            s1[u] = get16(rb[g + u] + 1);
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) kk[u][q] = sm.list[s0[g + u] + q];
                         }
 #pragma unroll
-                        for (int u = 0; u < 4; ++u)
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) kk[u][q] = sm.list[s0[u] + q];
-#pragma unroll
                         for (int u = 0; u < 4; ++u) {
-                            rank[u] = (kk[u][0] < x[g + u]) + (kk[u][1] < x[g + u]) +
-                                      (kk[u][2] < x[g + u]) + (kk[u][3] < x[g + u]);
-                            for (int t = s0[u] + 4; t < s1[u]; t += 4) {
+                            const uint64_t xr = x[g + u];
+                            int rank = (kk[u][0] < xr) + (kk[u][1] < xr) + (kk[u][2] < xr) +
+                                       (kk[u][3] < xr);
+                            for (int t = s0[g + u] + 4; t < s1[g + u]; t += 4) {
                                 const uint64_t k0 = sm.list[t];
                                 const uint64_t k1 = sm.list[t + 1];
                                 const uint64_t k2 = sm.list[t + 2];
                                 const uint64_t k3 = sm.list[t + 3];
-                                rank[u] += (k0 < x[g + u]) + (k1 < x[g + u]) + (k2 < x[g + u]) +
-                                           (k3 < x[g + u]);
+                                rank += (k0 < xr) + (k1 < xr) + (k2 < xr) + (k3 < xr);
                             }
-                            fin[g + u] = s0[u] + rank[u];
+                            fin[g + u] = s0[g + u] + rank;
                         }
                     }
                 }
@@ -1131,7 +1151,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                         for (int r = g; r < g + 4; ++r)
                             lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)fin[r], x[r],
-                                                __ballot(rb[r] < kWaveBins));
+                                                __ballot(r * 64 + lane < nv));
                     }
                 sorted = true;
             } else {
