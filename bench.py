@@ -267,7 +267,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
                      "traffic": read_traffic(S),
-                     "kernel": "sample_rows_wave<26,16>",
+                     "kernel": "sample_rows_wave<26,25>",
                      "algorithmic_bytes_per_launch": bytes_launch,
                      "avg_launch_ms": round(avg_launch_ms, 5)},
         "cpu_baseline": cpu,
