@@ -988,13 +988,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // top-p sorts by a counting sort over [min survivor, max] where it can
     const float slo = use_topk ? fmaxf(thr, lo) : lo;
     const float srange = __fsub_rn(hi, slo);
-    // descending sort bins: fma(v, -ss, sc) lands in [2^23, 2^23 + NB) (an
-    // integer) for v in [slo, hi], checked at both ends (the map is monotone)
-    const float ss = __fdiv_rn((float)(kWaveBins - 4), srange);
-    const float sc = __fmaf_rn(hi, ss, 0x1p23f + 2.0f);
-    const bool csort = use_topp && !bad && srange > 0.0f && ss < kPosInf &&
-                       __fmaf_rn(hi, -ss, sc) >= 0x1p23f &&
-                       __fmaf_rn(slo, -ss, sc) <= 0x1p23f + (float)(kWaveBins - 1);
+    // descending sort bins, finer where survivors crowd (just above the
+    // threshold): with x = max(0, (hi - v) / range) in [0, ~1], bin =
+    // bits(fma(x*x, NB - 4, 2^23 + 2)) - bits(2^23).  Every step is a
+    // correctly rounded monotone operation, so the bin never decreases as v
+    // falls; the range is checked at both ends.
+    const float sxs = __fdiv_rn(1.0f, srange);
+    const float sxc = __fmul_rn(hi, sxs);
+    auto sort_bin_y = [&](float v) {
+        const float xq = fmaxf(__fmaf_rn(v, -sxs, sxc), 0.0f);
+        return __fmaf_rn(__fmul_rn(xq, xq), (float)(kWaveBins - 4), 0x1p23f + 2.0f);
+    };
+    const bool csort = use_topp && !bad && srange > 0.0f && sxs < kPosInf &&
+                       sort_bin_y(hi) >= 0x1p23f &&
+                       sort_bin_y(slo) <= 0x1p23f + (float)(kWaveBins - 1);
     // raw entries -> composite keys (descending score, ascending id), in place;
     // positions [n_surv, 64*nr) become the maximum key (the counting sort
     // converts in registers instead).
@@ -1025,7 +1032,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         // their sorted places; each key's bin bounds stay in registers.
         bool sorted = false;
         if (csort) {
-            // descending bins: rb(v) = bits(fma(v, -ss, sc)) - bits(2^23), in
+            // descending bins rb(v) = bits(sort_bin_y(v)) - bits(2^23), in
             // [0, NB) for v in [slo, hi] (csort checked both ends)
             uint64_t x[R];
             int rb[R], slot[R], s0[R], s1[R];
@@ -1041,8 +1048,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         const uint64_t w = sm.list[i];  // raw (score bits << 32 | id)
                         const float v = __builtin_bit_cast(float, (uint32_t)(w >> 32));
                         x[r] = (i < nv) ? desc_key(v, (uint32_t)w) : ~0ull;
-                        const int b = (int)(__builtin_bit_cast(uint32_t, __fmaf_rn(v, -ss, sc)) -
-                                            0x4B000000u);
+                        const int b = (int)(__builtin_bit_cast(uint32_t, sort_bin_y(v)) - 0x4B000000u);
                         rb[r] = (i < nv) ? b : kSpare + lane;  // past the list: a spare counter
                     }
                 }
