@@ -990,14 +990,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     const float srange = __fsub_rn(hi, slo);
     // descending sort bins, finer where survivors crowd (just above the
     // threshold): with x = max(0, (hi - v) / range) in [0, ~1], bin =
-    // bits(fma(x*x, NB - 4, 2^23 + 2)) - bits(2^23).  Every step is a
+    // bits(fma(x^3, NB - 4, 2^23 + 2)) - bits(2^23).  Every step is a
     // correctly rounded monotone operation, so the bin never decreases as v
     // falls; the range is checked at both ends.
     const float sxs = __fdiv_rn(1.0f, srange);
     const float sxc = __fmul_rn(hi, sxs);
     auto sort_bin_y = [&](float v) {
         const float xq = fmaxf(__fmaf_rn(v, -sxs, sxc), 0.0f);
-        return __fmaf_rn(__fmul_rn(xq, xq), (float)(kWaveBins - 4), 0x1p23f + 2.0f);
+        return __fmaf_rn(__fmul_rn(__fmul_rn(xq, xq), xq), (float)(kWaveBins - 4), 0x1p23f + 2.0f);
     };
     const bool csort = use_topp && !bad && srange > 0.0f && sxs < kPosInf &&
                        sort_bin_y(hi) >= 0x1p23f &&
