@@ -52,28 +52,31 @@ constexpr double kDrawMargin = 3e-7;
 #define WAVE_WPE 4
 #endif
 
-// LDS of one row (~11 KB at Q = 26: 14 rows per CU).  Phases reuse storage:
+// LDS of one row (9.9 KB at Q = 26, allocated in 512-byte granules as
+// 10 KB: 16 rows per CU, as many as the 128-register budget allows).  Phases
+// reuse storage:
 //   list:  the top-k histogram (u32 bins) until the survivors are written;
-//          the survivor entries; the sort's bin counters and offsets while
-//          the entries are in registers; the sorted keys; the kept exp terms
-//          F in id order at the end
-//   u:     the top-k bin's candidates; the allowed row of masked rows at the
-//          start; the kept bitmap and its word offsets at the end
+//          the survivor entries; the top-k bin's candidates while the
+//          entries are in registers; the sort's bin counters and offsets
+//          while the entries are in registers; the sorted keys; the kept exp
+//          terms F in id order at the end
+//   keptw: the allowed row of masked rows at the start; the kept bitmap at
+//          the end
+//   h:     the history bitmap until the penalty pass has read it; then the
+//          kept bitmap's word offsets
 template <int Q>
 struct WaveSmem {
     uint64_t tab[32];
-    uint32_t seen[8 * Q];  // history ids (penalty)
+    uint32_t keptw[8 * Q];  // kept ids after every filter
     union {
-        float cand[kWaveCand];               // scores of the top-k bin
-        uint64_t candk[kWaveCand];           // (score bits << 32 | id), same bin
-        struct {
-            uint32_t keptw[8 * Q];      // kept ids after every filter
-            uint32_t woff[8 * Q];       // kept ids before each word
-        } b;
-    } u;
+        uint32_t seen[8 * Q];  // history ids (penalty)
+        uint32_t woff[8 * Q];  // kept ids before each word
+    } h;
     alignas(16) uint64_t list[kWaveCap + 4];  // survivors (+ padding: maximum keys)
     int rk;
 
+    __device__ float* cand() { return reinterpret_cast<float*>(list); }  // scores of the top-k bin
+    __device__ uint64_t* candk() { return list; }  // (score bits << 32 | id), same bin
     __device__ uint32_t* khist() { return reinterpret_cast<uint32_t*>(list); }
     __device__ float* F() { return reinterpret_cast<float*>(list); }
 };
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
     }
     if (lane < 32) sm.tab[lane] = kExp2TabDev.t[lane];
-    for (int w = lane; w < 8 * Q; w += 64) sm.seen[w] = 0u;
+    for (int w = lane; w < 8 * Q; w += 64) sm.h.seen[w] = 0u;
     __syncthreads();
     // ---- history ids -> seen bitmap (main.cpp:775) ----
     // The id loads are issued after the logits' (memory reads complete in
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 const int t = hid[u];
                 const bool ok = b0 + u * 64 + lane < hlen && t >= 0 && t < V;
                 if (b0 + u * 64 < hlen)  // uniform: batches past the history are skipped
-                    lds_or_b32_lanes(lds_offset(&sm.seen[0]) + ((uint32_t)(t >> 5) << 2),
+                    lds_or_b32_lanes(lds_offset(&sm.h.seen[0]) + ((uint32_t)(t >> 5) << 2),
                                      1u << (t & 31), __ballot(ok));
             }
         }
@@ -567,11 +570,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     if (!plain) {
         if (rsc.masked_ids)
             for (int w = lane; w < W; w += 64)
-                sm.u.b.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
+                sm.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            const uint32_t word = rsc.masked_ids ? sm.u.b.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
+            const uint32_t word = rsc.masked_ids ? sm.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int id = 256 * j + 4 * lane + c;
@@ -797,7 +800,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                 const int at = ballot_rank(m) + nc;
                                 // (more than the array holds: the count check below fails)
                                 if (nc + __popcll(m) <= kWaveCand)
-                                    lds_store_b64_lanes(lds_offset(&sm.u.candk[0]) + 8u * (uint32_t)at,
+                                    lds_store_b64_lanes(lds_offset(sm.candk()) + 8u * (uint32_t)at,
                                                         x[r], m);
                                 nc += __popcll(m);
                             }
@@ -811,10 +814,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         int tgt = 0;
                         bool hitc = false;
                         for (int c0 = lane; c0 < nc; c0 += 64) {
-                            const float v = val_of(sm.u.candk[c0]);
+                            const float v = val_of(sm.candk()[c0]);
                             int gt = 0, ge = 0;
                             for (int t = 0; t < nc; ++t) {
-                                const float w = val_of(sm.u.candk[t]);
+                                const float w = val_of(sm.candk()[t]);
                                 gt += (w > v) ? 1 : 0;
                                 ge += (w >= v) ? 1 : 0;
                             }
@@ -902,7 +905,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     const uint64_t m = __ballot(in);
                     const int at = nc + ballot_rank(m);
                     if (nc + __popcll(m) <= kWaveCand)  // else nc > kWaveCand: not used
-                        lds_store_b32_lanes(lds_offset(&sm.u.cand[0]) + 4u * (uint32_t)at,
+                        lds_store_b32_lanes(lds_offset(sm.cand()) + 4u * (uint32_t)at,
                                             __builtin_bit_cast(uint32_t, v), m);
                     nc += __popcll(m);
                 });
@@ -913,10 +916,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     int tgt = 0;
                     bool hitc = false;
                     for (int c0 = lane; c0 < nc; c0 += 64) {
-                        const float v = sm.u.cand[c0];
+                        const float v = sm.cand()[c0];
                         int gt = 0, ge = 0;
                         for (int t = 0; t < nc; ++t) {
-                            const float w = sm.u.cand[t];
+                            const float w = sm.cand()[t];
                             gt += (w > v) ? 1 : 0;
                             ge += (w >= v) ? 1 : 0;
                         }
@@ -1292,7 +1295,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 
     // ---- min-p [extension], repetition penalty (main.cpp:774-781) ----
     // kept entries: list positions [0, n_kept); per entry in registers
-    for (int w = lane; w < 8 * Q; w += 64) sm.u.b.keptw[w] = 0u;
+    for (int w = lane; w < 8 * Q; w += 64) sm.keptw[w] = 0u;
     __syncthreads();
     const int nk = (n_kept + 63) >> 6;
     float val[R];
@@ -1317,7 +1320,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                                           : expf_nonpos(x, sm.tab)) < P.min_p);
                     }
                     if (use_pen) {
-                        const bool hit = kp && bit_of(sm.seen, id);
+                        const bool hit = kp && bit_of(sm.h.seen, id);
                         const float pv = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty)
                                                   : __fmul_rn(v, P.repeat_penalty);
                         v = hit ? pv : v;
@@ -1325,7 +1328,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     val[r] = v;
                     idr[r] = id;
                     kept |= (kp ? 1u : 0u) << r;
-                    lds_or_b32_lanes(lds_offset(&sm.u.b.keptw[0]) + ((uint32_t)(id >> 5) << 2),
+                    lds_or_b32_lanes(lds_offset(&sm.keptw[0]) + ((uint32_t)(id >> 5) << 2),
                                      1u << (id & 31), __ballot(kp));
                 }
             }
@@ -1348,14 +1351,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
             const int w = lane * WPL + q;
-            cw[q] = (w < W) ? __popc(sm.u.b.keptw[w]) : 0;
+            cw[q] = (w < W) ? __popc(sm.keptw[w]) : 0;
             loc += cw[q];
         }
         int basew = wave_excl_scan_i(loc, n_final);
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
             const int w = lane * WPL + q;
-            if (w < W) sm.u.b.woff[w] = (uint32_t)basew;
+            if (w < W) sm.h.woff[w] = (uint32_t)basew;
             basew += cw[q];
         }
     }
@@ -1368,7 +1371,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                 for (int r = g; r < g + 4; ++r) {
                     const bool kp = (kept >> r) & 1u;
-                    const int at = rank_of(sm.u.b.keptw, sm.u.b.woff, idr[r]);  // kept lanes
+                    const int at = rank_of(sm.keptw, sm.h.woff, idr[r]);  // kept lanes
                     const float x = __fsub_rn(val[r], mx2);
                     const float e = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
                                                             : expf_libm_branchless(x, sm.tab);
@@ -1409,7 +1412,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
         const float b = wave_max_dpp(best);
         const int rk = wave_min_i_dpp(best == b ? first : 0x7fffffff);
-        token = rk == 0x7fffffff ? 0 : id_of_rank(sm.u.b.keptw, sm.u.b.woff, W, rk);
+        token = rk == 0x7fffffff ? 0 : id_of_rank(sm.keptw, sm.h.woff, W, rk);
         oflags |= CBX_INFO_GREEDY;
     } else if (V >= 2) {
         oflags |= CBX_INFO_DREW;
@@ -1420,7 +1423,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         } else {
             u = a.uniforms[rs];
         }
-        const bool last_kept = bit_of(sm.u.b.keptw, V - 1);
+        const bool last_kept = bit_of(sm.keptw, V - 1);
         // binary64 prefix of the exp terms in id order: lane l holds the odd
         // run [l*C, l*C + C) in registers (compiled per C, reads in flight
         // together, distinct banks)
@@ -1470,7 +1473,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             const bool hi_ok = (rank == n_final - 1 && last_kept) ||
                                __dsub_rn(chi, u) > kDrawMargin * chi + 1e-30;
             certain = lo_ok && hi_ok;
-            token = id_of_rank(sm.u.b.keptw, sm.u.b.woff, W, rank);
+            token = id_of_rank(sm.keptw, sm.h.woff, W, rank);
         }
         if (!certain) {
             // the reference's arithmetic: float normaliser, double CDF (rare)
@@ -1490,7 +1493,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
             __syncthreads();
             const int rk = sm.rk;
-            token = rk < 0 ? V - 1 : id_of_rank(sm.u.b.keptw, sm.u.b.woff, W, rk);
+            token = rk < 0 ? V - 1 : id_of_rank(sm.keptw, sm.h.woff, W, rk);
         }
     }
     CBX_STAMP(12);
@@ -1502,8 +1505,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         const float ps = empty ? 0.0f : exact_psum2();
         float* prow = a.probs + rs * a.ld_probs;
         for (int i = lane; i < V; i += 64)
-            prow[i] = (!empty && bit_of(sm.u.b.keptw, i))
-                          ? __fdiv_rn(sm.F()[rank_of(sm.u.b.keptw, sm.u.b.woff, i)], ps)
+            prow[i] = (!empty && bit_of(sm.keptw, i))
+                          ? __fdiv_rn(sm.F()[rank_of(sm.keptw, sm.h.woff, i)], ps)
                           : 0.0f;
     }
 }
