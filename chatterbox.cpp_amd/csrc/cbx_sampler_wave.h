@@ -520,6 +520,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
     const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
     const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
+    // Loads in the order they are needed (memory reads return in order): the
+    // exp table's words, the row, then the history's first 1024 ids, so no
+    // wait comes between them and one wait covers the row and the ids.
+    const uint64_t tabv = kExp2TabDev.t[lane & 31];
     float s[EPL];
 #pragma unroll
     for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
@@ -531,22 +535,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             rsc.combine4(&s[4 * j], un);
         }
     }
-    if (lane < 32) sm.tab[lane] = kExp2TabDev.t[lane];
-    for (int w = lane; w < 8 * Q; w += 64) sm.h.seen[w] = 0u;
-    __syncthreads();
     // ---- history ids -> seen bitmap (main.cpp:775) ----
-    // The id loads are issued after the logits' (memory reads complete in
-    // order, so waiting for them costs nothing beyond the logits' arrival);
-    // loads past the history read 0 and are masked out.
+    // Loads past the history read 0 and are masked out.
+    constexpr int HB = 16;  // ids per lane per batch: 1024 per pass
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
+    int hid[HB];
     if (use_pen) {
-        constexpr int HB = 16;  // ids per lane per batch: 1024 per pass
-        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
-        for (int b0 = 0; b0 < hlen; b0 += HB * 64) {
-            int hid[HB];
 #pragma unroll
-            for (int u = 0; u < HB; ++u)
-                hid[u] = __builtin_amdgcn_raw_buffer_load_b32(rh, (b0 + u * 64 + lane) * 4, 0, 0);
+        for (int u = 0; u < HB; ++u)
+            hid[u] = __builtin_amdgcn_raw_buffer_load_b32(rh, (u * 64 + lane) * 4, 0, 0);
+    }
+    if (lane < 32) sm.tab[lane] = tabv;
+    for (int w = lane; w < 8 * Q; w += 64) sm.h.seen[w] = 0u;
+    if (use_pen) {
+        for (int b0 = 0; b0 < hlen; b0 += HB * 64) {
+            if (b0 > 0) {
+#pragma unroll
+                for (int u = 0; u < HB; ++u)
+                    hid[u] = __builtin_amdgcn_raw_buffer_load_b32(rh, (b0 + u * 64 + lane) * 4, 0, 0);
+            }
 #pragma unroll
             for (int u = 0; u < HB; ++u) {
                 const int t = hid[u];
