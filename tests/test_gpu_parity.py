@@ -385,6 +385,18 @@ EDGE_CASES = [
      lambda V, r: np.concatenate([[0.0], np.full(V - 1, -95.0)]).astype(F32), 0.999),
     ("huge_spread", 2048, dict(top_k=0, top_p=0.999, temp=0.5, repeat_penalty=1.0),
      lambda V, r: (r.standard_normal(V) * 40).astype(F32), 0.5),
+    # skewed rows: one spike far above the rest (a single score above the
+    # midrange)
+    ("topk_spike_refloor", 6563, dict(top_k=50, top_p=0.9, temp=0.9, repeat_penalty=1.2),
+     lambda V, r: np.concatenate([[60.0], r.standard_normal(V - 1)]).astype(F32), 0.45),
+    # exactly k + 1 scores in the upper half of the range
+    ("topk_floor_edge", 2000, dict(top_k=100, top_p=0.95, temp=1.0, repeat_penalty=1.1),
+     lambda V, r: np.concatenate([r.uniform(5.0, 6.0, 101), r.uniform(-6.0, -5.0, V - 101)
+                                  ]).astype(F32), 0.52),
+    # the k-th score ties with the midrange itself (0.0), 60 times
+    ("topk_floor_tie", 1500, dict(top_k=50, top_p=0.9, temp=1.0, repeat_penalty=1.3),
+     lambda V, r: np.concatenate([[4.0, -4.0], r.uniform(0.5, 3.5, 30), np.zeros(60),
+                                  r.uniform(-3.9, -0.1, V - 92)]).astype(F32), 0.66),
     # 150 equal survivors in one value bin: the sort falls back to the bitonic network
     ("crowded_bin", 600, dict(top_k=500, top_p=0.9, temp=1.0, repeat_penalty=1.2),
      lambda V, r: np.concatenate([np.full(150, 3.0), np.full(200, 2.0), [10.0],
