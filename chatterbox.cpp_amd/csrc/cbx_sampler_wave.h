@@ -224,6 +224,28 @@ __device__ __forceinline__ void lds_store_b32_lanes(uint32_t addr, uint32_t v, u
         : "v"(addr), "v"(v), "s"(mask)
         : "memory");
 }
+// One step of an append: the lanes whose score v is >= b0 store (id, v) at
+// consecutive 8-byte slots from byte offset sb in lane order, and sb moves
+// past them.  v_cmpx writes the lane mask to VCC and EXEC at once; two wait
+// states separate that VALU write of VCC from its VALU reads; exec is all
+// lanes again at the end (the caller's code is wave-uniform).
+__device__ __forceinline__ uint32_t append_ge(uint32_t sb, float b0, float v, uint32_t id) {
+    uint32_t t, cnt;
+    asm volatile(
+        "v_cmpx_le_f32 vcc, %[b0], %[v]\n\t"
+        "s_nop 1\n\t"
+        "v_mbcnt_lo_u32_b32 %[t], vcc_lo, 0\n\t"
+        "v_mbcnt_hi_u32_b32 %[t], vcc_hi, %[t]\n\t"
+        "v_lshl_add_u32 %[t], %[t], 3, %[sb]\n\t"
+        "ds_write2_b32 %[t], %[id], %[v] offset1:1\n\t"
+        "s_mov_b64 exec, -1\n\t"
+        "s_bcnt1_i32_b64 %[cnt], vcc\n\t"
+        "s_lshl3_add_u32 %[sb], %[cnt], %[sb]"
+        : [t] "=&v"(t), [cnt] "=&s"(cnt), [sb] "+s"(sb)
+        : [b0] "s"(b0), [v] "v"(v), [id] "v"(id)
+        : "vcc", "scc", "memory");
+    return sb;
+}
 __device__ __forceinline__ void lds_or_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
     asm volatile(
         "s_mov_b64 exec, %2\n\t"
@@ -761,9 +783,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 __syncthreads();  // histogram reads done: the candidates reuse it
                 CBX_STAMP(18);
                 if (have_b && above_bins + nsel <= kWaveCap) {
-                    // One pass, no exec-mask changes: every score >= B0 (the
-                    // survivors >= B1 and the selected bin's candidates) joins
-                    // the list; the rest write its spare slot.
+                    // One pass: every score >= B0 (the survivors >= B1 and the
+                    // selected bin's candidates) joins the list, in (vector,
+                    // element, lane) order.
                     auto val_of = [](uint64_t pk) {
                         return __builtin_bit_cast(float, (uint32_t)(pk >> 32));
                     };
@@ -772,17 +794,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     uint32_t sb = lbase;
 #pragma unroll
                     for (int j = 0; j < Q; ++j) {
-                        const float B0j = fresh_v(B0);
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            const float v = s[4 * j + c];
-                            const uint64_t m = __ballot(v >= B0j);
-                            const uint32_t at = ((uint32_t)ballot_rank(m) << 3) + sb;
-                            lds_store_pair_lanes(at, (uint32_t)(256 * j + 4 * lane + c),
-                                                 __builtin_bit_cast(uint32_t, v), m);
-                            // opaque, so the shift-add is not re-associated
-                            sb = (uint32_t)fresh((int)(sb + 8u * (uint32_t)__popcll(m)));
-                        }
+                        for (int c = 0; c < 4; ++c)
+                            sb = append_ge(sb, B0, s[4 * j + c], (uint32_t)(256 * j + 4 * lane + c));
                     }
                     const int n = (int)((sb - lbase) >> 3);
                     __syncthreads();
