@@ -269,6 +269,16 @@ __device__ __forceinline__ float fresh_v(float v) {
     return v;
 }
 
+// The same for a wave-uniform double, moved to scalar registers (also keeps
+// its computation where it is written).
+__device__ __forceinline__ double fresh_d(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    int lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    int hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
 // What turns a row's logits into its scores (main.cpp:733-738 and the
 // extensions): CFG combine, allowed mask, forced stop, temperature.
 struct RowScores {
@@ -568,6 +578,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         for (int u = 0; u < HB; ++u)
             hid[u] = __builtin_amdgcn_raw_buffer_load_b32(rh, (u * 64 + lane) * 4, 0, 0);
     }
+    // the draw's uniform, while the loads are in flight (scalar work)
+    double u_draw = 0.0;
+    if (a.draw_mode == CBX_DRAW_PHILOX) {
+        const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
+        u_draw = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
+    } else {
+        u_draw = a.uniforms[rs];
+    }
+    u_draw = fresh_d(u_draw);
     if (lane < 32) sm.tab[lane] = tabv;
     for (int w = lane; w < 8 * Q; w += 64) sm.h.seen[w] = 0u;
     if (use_pen) {
@@ -1367,16 +1386,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // id-order ranks of the kept ids: word offsets
     constexpr int WPL = (8 * Q + 63) / 64;
     int n_final;
+    int cw[WPL];  // kept ids in the lane's words lane*WPL .. lane*WPL + WPL - 1
+    int loc = 0, wbase;
     {
-        int cw[WPL];
-        int loc = 0;
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
             const int w = lane * WPL + q;
             cw[q] = (w < W) ? __popc(sm.keptw[w]) : 0;
             loc += cw[q];
         }
-        int basew = wave_excl_scan_i(loc, n_final);
+        wbase = wave_excl_scan_i(loc, n_final);
+        int basew = wbase;
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
             const int w = lane * WPL + q;
@@ -1384,6 +1404,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             basew += cw[q];
         }
     }
+    // Id of the kept id of id-order rank `rank` (0 <= rank < n_final): the
+    // lane whose words hold it finds the word; lanes 0..31 then count the
+    // word's set bits below their own bit (mbcnt) to find the bit.
+    auto id_of_rank_w = [&](int rank) -> int {
+        const int L = __builtin_ctzll(__ballot(wbase <= rank && rank < wbase + loc));
+        int run = wbase, wq = 0, kq = 0;
+        bool got = false;
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) {
+            const bool in = !got && rank < run + cw[q];
+            wq = in ? lane * WPL + q : wq;
+            kq = in ? rank - run : kq;
+            got = got || in;
+            run += cw[q];
+        }
+        const int w = __builtin_amdgcn_readlane(wq, L);
+        const int kb = __builtin_amdgcn_readlane(kq, L);
+        const uint32_t bits = sm.keptw[w];
+        const bool hit = lane < 32 && ((bits >> (lane & 31)) & 1u) &&
+                         (int)__builtin_amdgcn_mbcnt_lo(bits, 0u) == kb;
+        return w * 32 + __builtin_ctzll(__ballot(hit));
+    };
     __syncthreads();
     // val - mx2 <= 0 and not NaN once mx2 is finite and the row holds no NaN
     auto f_terms = [&](auto nonpos) {
@@ -1434,17 +1476,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
         const float b = wave_max_dpp(best);
         const int rk = wave_min_i_dpp(best == b ? first : 0x7fffffff);
-        token = rk == 0x7fffffff ? 0 : id_of_rank(sm.keptw, sm.h.woff, W, rk);
+        token = rk == 0x7fffffff ? 0 : id_of_rank_w(rk);
         oflags |= CBX_INFO_GREEDY;
     } else if (V >= 2) {
         oflags |= CBX_INFO_DREW;
-        double u;
-        if (a.draw_mode == CBX_DRAW_PHILOX) {
-            const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
-            u = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
-        } else {
-            u = a.uniforms[rs];
-        }
+        const double u = u_draw;
         const bool last_kept = bit_of(sm.keptw, V - 1);
         // binary64 prefix of the exp terms in id order: lane l holds the odd
         // run [l*C, l*C + C) in registers (compiled per C, reads in flight
@@ -1495,7 +1531,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             const bool hi_ok = (rank == n_final - 1 && last_kept) ||
                                __dsub_rn(chi, u) > kDrawMargin * chi + 1e-30;
             certain = lo_ok && hi_ok;
-            token = id_of_rank(sm.keptw, sm.h.woff, W, rank);
+            token = id_of_rank_w(rank);
         }
         if (!certain) {
             // the reference's arithmetic: float normaliser, double CDF (rare)
@@ -1515,7 +1551,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
             __syncthreads();
             const int rk = sm.rk;
-            token = rk < 0 ? V - 1 : id_of_rank(sm.keptw, sm.h.woff, W, rk);
+            token = rk < 0 ? V - 1 : id_of_rank_w(rk);
         }
     }
     CBX_STAMP(12);
