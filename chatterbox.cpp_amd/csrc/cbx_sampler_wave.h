@@ -560,11 +560,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
     for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
     if (rsc.uncond) {
+        // CFG rows: the uncond vectors stream through a ring of UD register
+        // quads, UD - 1 loads ahead of the combine (the waits are in order)
+        constexpr int UD = 3;
+        float un[UD][4];
+#pragma unroll
+        for (int j = 0; j < UD - 1; ++j) load4(rsc.ru, lane * 16, j * 1024, un[j]);
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            float un[4];
-            load4(rsc.ru, lane * 16, j * 1024, un);
-            rsc.combine4(&s[4 * j], un);
+            if (j + UD - 1 < Q) load4(rsc.ru, lane * 16, (j + UD - 1) * 1024, un[(j + UD - 1) % UD]);
+            rsc.combine4(&s[4 * j], un[j % UD]);
         }
     }
     // ---- history ids -> seen bitmap (main.cpp:775) ----
