@@ -640,8 +640,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         __syncthreads();
     }
     {
-        // acc = sum of v * 0: 0 while every unmasked score is finite, NaN once
-        // one is NaN or infinite.  Vectors j >= JT may hold padding.
+        // acc = sum of the products of score pairs: finite while every
+        // unmasked score is finite, NaN or infinite once one is NaN or
+        // infinite (or, for huge scores, when the sum overflows: the check
+        // below then finds no such score).  Vectors j >= JT may hold padding.
         float acc = 0.0f;
         const int Vm = fresh(V);
         auto pass = [&](auto scaled) {
@@ -654,8 +656,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     if (decltype(scaled)::value) w[c] = __fmul_rn(w[c], rsc.inv_t);
                 }
                 if (j < JT) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) acc = __fmaf_rn(w[c], 0.0f, acc);
+                    acc = __fmaf_rn(w[0], w[1], acc);
+                    acc = __fmaf_rn(w[2], w[3], acc);
                     // running value first: one 3-input min / max per pair
                     lo = fminf(fminf(lo, w[0]), w[1]);
                     lo = fminf(fminf(lo, w[2]), w[3]);
@@ -677,7 +679,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         };
         if (rsc.scale) pass(std::true_type{});
         else pass(std::false_type{});
-        const bool spec = __ballot(acc != 0.0f) != 0;  // NaN != 0
+        const bool spec = __ballot(!(__builtin_fabsf(acc) < kPosInf)) != 0;
         if (spec) {
             // rare: tell NaN/+inf (reported) from -inf logits, and take the
             // minimum over finite scores only

@@ -397,6 +397,12 @@ EDGE_CASES = [
     ("topk_floor_tie", 1500, dict(top_k=50, top_p=0.9, temp=1.0, repeat_penalty=1.3),
      lambda V, r: np.concatenate([[4.0, -4.0], r.uniform(0.5, 3.5, 30), np.zeros(60),
                                   r.uniform(-3.9, -0.1, V - 92)]).astype(F32), 0.66),
+    # finite scores whose pairwise products overflow binary32
+    ("huge_scores", 6563, dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.2),
+     lambda V, r: (r.standard_normal(V) * 1e19).astype(F32), 0.4),
+    # -inf logits among finite ones (10% of the ids)
+    ("some_neg_inf", 6563, dict(top_k=250, top_p=0.9, temp=1.1, repeat_penalty=1.2),
+     lambda V, r: np.where(r.random(V) < 0.1, -np.inf, r.standard_normal(V) * 3).astype(F32), 0.6),
     # 150 equal survivors in one value bin: the sort falls back to the bitonic network
     ("crowded_bin", 600, dict(top_k=500, top_p=0.9, temp=1.0, repeat_penalty=1.2),
      lambda V, r: np.concatenate([np.full(150, 3.0), np.full(200, 2.0), [10.0],
@@ -446,6 +452,34 @@ def test_edge_cases_one_wave(cbx, torch_cuda, case):
     tg, ig, pg = gpu_batch(cbx, torch_cuda, x, [pd], uu, hist, hl, max_survivors=1024)
     tr, ir, pr = oracle_rows(x, [pd], uu, hist, hl)
     parity.compare(f"edge_wave_{name}", tg, ig, tr, ir, uu, pg, pr)
+
+
+@pytest.mark.parametrize("max_survivors", [0, 1024])
+def test_nonfinite_rows_flagged(cbx, torch_cuda, max_survivors):
+    """NaN or +inf logits are outside the reference's contract: such rows are
+    flagged CBX_INFO_NONFINITE and still return an id in range (or -1 on
+    overflow); rows of the same batch without them keep parity."""
+    V = 6563
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((6, V)) * 3).astype(F32)
+    x[0, 17] = np.nan
+    x[1, 3000] = np.inf
+    x[2, 5] = np.nan
+    x[2, 6] = -np.inf
+    x[3, :] = np.nan
+    # rows 4 and 5 stay finite
+    plist = [dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.2, min_p=0.0, cfg_weight=0.0)] * 6
+    u = rng.random(6)
+    hist = rng.integers(0, V, size=(6, 64)).astype(np.int32)
+    hl = np.full(6, 64, np.int32)
+    say(f"nonfinite rows max_survivors={max_survivors}")
+    tg, ig, _ = gpu_batch(cbx, torch_cuda, x, plist, u, hist, hl, max_survivors=max_survivors)
+    for r in range(4):
+        assert ig[r] & parity.INFO_NONFINITE, (r, ig[r])
+        assert -1 <= tg[r] < V
+    assert not np.any(ig[4:] & parity.INFO_NONFINITE)
+    tr, ir, _ = oracle_rows(x[4:], plist[4:], u[4:], hist[4:], hl[4:])
+    assert list(tg[4:]) == list(tr)
 
 
 def test_row_api_extensions(cbx, torch_cuda):
