@@ -1082,7 +1082,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         // offsets can use the list's own storage until the keys go back to
         // their sorted places; each key's bin bounds stay in registers.
         bool sorted = false;
-        if (csort) {
+        if (n_surv <= 64) {
+            // one row of entries: each lane's key ranked against the others
+            // by readlane (no LDS round trips), then one store each; the
+            // lanes past the list write the maximum key in place.  Keys are
+            // distinct (the ids are), so the ranks are 0 .. n_surv - 1.
+            const uint64_t w = sm.list[lane];  // raw entry, or its key (!csort)
+            uint64_t key = w;
+            if (csort)
+                key = lane < n_surv
+                          ? desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w)
+                          : ~0ull;
+            int rank = 0;
+#pragma unroll 4
+            for (int t = 0; t < n_surv; ++t) {
+                const uint64_t kt =
+                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), t) << 32) |
+                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, t);
+                rank += (kt < key) ? 1 : 0;
+            }
+            __syncthreads();  // every entry read: the sorted keys take the list
+            sm.list[lane < n_surv ? rank : lane] = key;
+            sorted = true;
+        } else if (csort) {
             // descending bins rb(v) = bits(sort_bin_y(v)) - bits(2^23), in
             // [0, NB) for v in [slo, hi] (csort checked both ends)
             uint64_t x[R];
