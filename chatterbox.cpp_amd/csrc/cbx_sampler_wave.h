@@ -508,6 +508,20 @@ __device__ __forceinline__ void with_odd_c(int C, F&& f) {
     }
 }
 
+// f(rows) for each group of four list rows g = 0, 4, .. N - 4 that holds
+// entries (g < n): f takes the group's first row and its row count (1 when
+// the group's first row is the last one, else 4) as compile-time values.
+template <int G, int N, class F>
+__device__ __forceinline__ void for_row_groups(int n, F&& f) {
+    if constexpr (G < N) {
+        if (G < n) {
+            if (G + 1 == n) f(std::integral_constant<int, G>{}, std::integral_constant<int, 1>{});
+            else f(std::integral_constant<int, G>{}, std::integral_constant<int, 4>{});
+        }
+        for_row_groups<G + 4, N>(n, f);
+    }
+}
+
 // ------------------------------------------------------------------ kernel
 
 template <int Q, int JT>
@@ -1375,34 +1389,37 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         const int nkv = fresh(n_kept);
         const float mx_kept = mx_surv;  // the best kept score before the penalty
 #pragma unroll
-        for (int g = 0; g < R; g += 4) {
-            if (g < nk) {
-#pragma unroll
-                for (int r = g; r < g + 4; ++r) {
-                    const int i = r * 64 + lane;
-                    const uint64_t key = sm.list[i];
-                    bool kp = i < nkv;
-                    float v = desc_key_value(key);
-                    const int id = kp ? (int)(uint32_t)key : 0;
-                    if (P.min_p > 0.0f) {
-                        const float x = __fsub_rn(v, mx_kept);
-                        kp = kp && !((bad ? expf_libm_branchless(x, sm.tab)
-                                          : expf_nonpos(x, sm.tab)) < P.min_p);
-                    }
-                    if (use_pen) {
-                        const bool hit = kp && bit_of(sm.h.seen, id);
-                        const float pv = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty)
-                                                  : __fmul_rn(v, P.repeat_penalty);
-                        v = hit ? pv : v;
-                    }
-                    val[r] = v;
-                    idr[r] = id;
-                    kept |= (kp ? 1u : 0u) << r;
-                    lds_or_b32_lanes(lds_offset(&sm.keptw[0]) + ((uint32_t)(id >> 5) << 2),
-                                     1u << (id & 31), __ballot(kp));
-                }
-            }
+        for (int r = 0; r < R; ++r) {
+            val[r] = kNegInf;
+            idr[r] = 0;
         }
+        for_row_groups<0, R>(nk, [&](auto gc, auto cc) {
+            constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+            for (int r = g; r < g + rows; ++r) {
+                const int i = r * 64 + lane;
+                const uint64_t key = sm.list[i];
+                bool kp = i < nkv;
+                float v = desc_key_value(key);
+                const int id = kp ? (int)(uint32_t)key : 0;
+                if (P.min_p > 0.0f) {
+                    const float x = __fsub_rn(v, mx_kept);
+                    kp = kp && !((bad ? expf_libm_branchless(x, sm.tab)
+                                      : expf_nonpos(x, sm.tab)) < P.min_p);
+                }
+                if (use_pen) {
+                    const bool hit = kp && bit_of(sm.h.seen, id);
+                    const float pv = v > 0.0f ? __fdiv_rn(v, P.repeat_penalty)
+                                              : __fmul_rn(v, P.repeat_penalty);
+                    v = hit ? pv : v;
+                }
+                val[r] = v;
+                idr[r] = id;
+                kept |= (kp ? 1u : 0u) << r;
+                lds_or_b32_lanes(lds_offset(&sm.keptw[0]) + ((uint32_t)(id >> 5) << 2),
+                                 1u << (id & 31), __ballot(kp));
+            }
+        });
     }
     // ---- softmax (main.cpp:783-793) ----
     float m2 = kNegInf;
@@ -1458,21 +1475,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     __syncthreads();
     // val - mx2 <= 0 and not NaN once mx2 is finite and the row holds no NaN
     auto f_terms = [&](auto nonpos) {
+        for_row_groups<0, R>(nk, [&](auto gc, auto cc) {
+            constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
 #pragma unroll
-        for (int g = 0; g < R; g += 4) {
-            if (g < nk) {
-#pragma unroll
-                for (int r = g; r < g + 4; ++r) {
-                    const bool kp = (kept >> r) & 1u;
-                    const int at = rank_of(sm.keptw, sm.h.woff, idr[r]);  // kept lanes
-                    const float x = __fsub_rn(val[r], mx2);
-                    const float e = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
-                                                            : expf_libm_branchless(x, sm.tab);
-                    lds_store_b32_lanes(lds_offset(sm.F()) + 4u * (uint32_t)at,
-                                        __builtin_bit_cast(uint32_t, e), __ballot(kp));
-                }
+            for (int r = g; r < g + rows; ++r) {
+                const bool kp = (kept >> r) & 1u;
+                const int at = rank_of(sm.keptw, sm.h.woff, idr[r]);  // kept lanes
+                const float x = __fsub_rn(val[r], mx2);
+                const float e = decltype(nonpos)::value ? expf_nonpos(x, sm.tab)
+                                                        : expf_libm_branchless(x, sm.tab);
+                lds_store_b32_lanes(lds_offset(sm.F()) + 4u * (uint32_t)at,
+                                    __builtin_bit_cast(uint32_t, e), __ballot(kp));
             }
-        }
+        });
     };
     if (!bad && __builtin_fabsf(mx2) < kPosInf) f_terms(std::true_type{});
     else f_terms(std::false_type{});
