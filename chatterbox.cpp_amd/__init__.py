@@ -83,6 +83,25 @@ class Batch(ctypes.Structure):
     ]
 
 
+CBX_WTYPE_F16, CBX_WTYPE_Q4_0, CBX_WTYPE_Q8_0 = 1, 2, 8
+
+
+class Head(ctypes.Structure):
+    """cbx_head (include/cbx_sampler.h): the speech_head projection."""
+
+    _fields_ = [
+        ("weights", ctypes.c_void_p),
+        ("wtype", ctypes.c_int32),
+        ("n_embd", ctypes.c_int32),
+        ("bias", ctypes.c_void_p),
+        ("hidden", ctypes.c_void_p),
+        ("hidden_uncond", ctypes.c_void_p),
+        ("ld_hidden", ctypes.c_int64),
+        ("logits", ctypes.c_void_p),
+        ("logits_uncond", ctypes.c_void_p),
+    ]
+
+
 class CbxError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"cbx error {code}: {msg}")
@@ -125,6 +144,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_sample_batch.restype = ctypes.c_int
     lib.cbx_sample_batch.argtypes = [vp, ctypes.POINTER(Batch), vp]
     lib.cbx_debug_expf.restype = ctypes.c_int
+    lib.cbx_head_logits.restype = ctypes.c_int
+    lib.cbx_head_logits.argtypes = [vp, ctypes.POINTER(Head), i32, i32, i64, vp]
+    lib.cbx_head_sample_batch.restype = ctypes.c_int
+    lib.cbx_head_sample_batch.argtypes = [vp, ctypes.POINTER(Head), ctypes.POINTER(Batch), vp]
     lib.cbx_debug_expf.argtypes = [vp, vp, vp, i64, vp]
     lib.cbx_debug_philox.restype = ctypes.c_int
     lib.cbx_debug_philox.argtypes = [vp, u64, vp, u64, i32, vp, vp]
@@ -213,7 +236,7 @@ class Sampler:
                      logits_uncond=None, history=None, history_len=None, allowed=None,
                      force_stop=None, stop_token=0, info=None, probs=None,
                      draw_mode=None, seed=0, stream_ids=None, step0=0, max_survivors=0,
-                     n_vocab=None, stream=None):
+                     n_vocab=None, stream=None, head=None):
         """logits: device float32 [n_steps*n_rows, ld] (or [n_steps, n_rows, ld]);
         params: device uint8 tensor from params_tensor(); tokens: device int32.
         n_vocab defaults to ld (the row stride)."""
@@ -249,7 +272,40 @@ class Sampler:
         b.probs = None if probs is None else probs.data_ptr()
         b.ld_probs = 0 if probs is None else probs.shape[-1]
         st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
-        _check(self.lib.cbx_sample_batch(self.handle, ctypes.byref(b), st))
+        if head is None:
+            _check(self.lib.cbx_sample_batch(self.handle, ctypes.byref(b), st))
+        else:
+            _check(self.lib.cbx_head_sample_batch(self.handle, ctypes.byref(head), ctypes.byref(b),
+                                                  st))
+
+    @staticmethod
+    def head(weights, wtype, n_embd, hidden, logits, *, bias=None, hidden_uncond=None,
+             logits_uncond=None):
+        """A cbx_head over device tensors: weights (uint8 bytes of the wtype
+        layout), hidden [rows, ld] float32, logits [rows, ld] float32 out."""
+        h = Head()
+        h.weights = weights.data_ptr()
+        h.wtype = wtype
+        h.n_embd = n_embd
+        h.bias = None if bias is None else bias.data_ptr()
+        h.hidden = hidden.data_ptr()
+        h.hidden_uncond = None if hidden_uncond is None else hidden_uncond.data_ptr()
+        h.ld_hidden = hidden.shape[-1]
+        h.logits = logits.data_ptr()
+        h.logits_uncond = None if logits_uncond is None else logits_uncond.data_ptr()
+        # the structure holds raw addresses: keep the tensors alive with it
+        h._tensors = (weights, bias, hidden, hidden_uncond, logits, logits_uncond)
+        return h
+
+    def head_logits(self, head, n_rows, n_vocab, ld_logits, stream=None):
+        st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
+        _check(self.lib.cbx_head_logits(self.handle, ctypes.byref(head), n_rows, n_vocab,
+                                        ld_logits, st))
+
+    def head_sample_batch(self, head, logits, params, tokens, **kw):
+        """cbx_head_sample_batch: the projection into head.logits (whose
+        shape gives the row stride), then sample_batch's sampling."""
+        self.sample_batch(logits, params, tokens, head=head, **kw)
 
     def debug_expf(self, x, out):
         _check(self.lib.cbx_debug_expf(self.handle, x.data_ptr(), out.data_ptr(), x.numel(),

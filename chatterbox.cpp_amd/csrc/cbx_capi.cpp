@@ -318,6 +318,71 @@ int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
     return CBX_OK;
 }
 
+namespace {
+int check_head(const char* fn, const cbx_head* h, int32_t n_rows, int32_t n_vocab,
+               int64_t ld_logits) {
+    if (!h || !h->weights || !h->hidden || !h->logits)
+        return fail(CBX_ERR_INVALID, "%s: NULL head, weights, hidden or logits", fn);
+    if (h->wtype != CBX_WTYPE_F16 && h->wtype != CBX_WTYPE_Q4_0 && h->wtype != CBX_WTYPE_Q8_0)
+        return fail(CBX_ERR_INVALID, "%s: unknown wtype %d", fn, h->wtype);
+    if (h->n_embd < 32 || h->n_embd > 16384 || h->n_embd % 32)
+        return fail(CBX_ERR_INVALID, "%s: n_embd %d not a multiple of 32 in [32, 16384]", fn,
+                    h->n_embd);
+    if (h->ld_hidden < h->n_embd)
+        return fail(CBX_ERR_INVALID, "%s: ld_hidden %lld < n_embd %d", fn,
+                    (long long)h->ld_hidden, h->n_embd);
+    if (h->hidden_uncond && !h->logits_uncond)
+        return fail(CBX_ERR_INVALID, "%s: hidden_uncond without logits_uncond", fn);
+    if (n_rows < 1 || n_vocab < 1 || n_vocab > cbx::kMaxVocab || ld_logits < n_vocab)
+        return fail(CBX_ERR_INVALID, "%s: n_rows %d, n_vocab %d, ld_logits %lld", fn, n_rows,
+                    n_vocab, (long long)ld_logits);
+    // the kernel's buffer descriptors address the weights and rows in 32 bits
+    const int64_t bpb = h->wtype == CBX_WTYPE_F16 ? 64 : (h->wtype == CBX_WTYPE_Q4_0 ? 18 : 34);
+    if ((int64_t)n_vocab * (h->n_embd / 32) * bpb > 0x7fffffffLL ||
+        ((int64_t)n_rows * h->ld_hidden + h->n_embd) * 4 > 0x7fffffffLL)
+        return fail(CBX_ERR_UNSUPPORTED, "%s: weights or hidden rows past 2 GiB", fn);
+    return CBX_OK;
+}
+
+int run_head(const cbx_head* h, int32_t n_rows, int32_t n_vocab, int64_t ld_logits,
+             hipStream_t st) {
+    CBX_HIP(cbx::launch_head(h->weights, h->wtype, h->bias, h->hidden, h->ld_hidden, h->logits,
+                             ld_logits, n_rows, n_vocab, h->n_embd, st));
+    if (h->hidden_uncond)
+        CBX_HIP(cbx::launch_head(h->weights, h->wtype, h->bias, h->hidden_uncond, h->ld_hidden,
+                                 h->logits_uncond, ld_logits, n_rows, n_vocab, h->n_embd, st));
+    return CBX_OK;
+}
+}  // namespace
+
+int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n_vocab,
+                    int64_t ld_logits, void* stream) {
+    if (!s) return fail(CBX_ERR_INVALID, "cbx_head_logits: NULL handle");
+    const int rc = check_head("cbx_head_logits", h, n_rows, n_vocab, ld_logits);
+    if (rc != CBX_OK) return rc;
+    DeviceGuard g(s->device);
+    return run_head(h, n_rows, n_vocab, ld_logits, (hipStream_t)stream);
+}
+
+int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream) {
+    if (!s || !b) return fail(CBX_ERR_INVALID, "cbx_head_sample_batch: NULL handle or batch");
+    if (b->n_rows < 1 || b->n_steps < 1 || (int64_t)b->n_rows * b->n_steps > 0x7fffffffLL)
+        return fail(CBX_ERR_INVALID, "cbx_head_sample_batch: n_rows %d, n_steps %d", b->n_rows,
+                    b->n_steps);
+    const int32_t rows = b->n_rows * b->n_steps;
+    const int rc = check_head("cbx_head_sample_batch", h, rows, b->n_vocab, b->ld_logits);
+    if (rc != CBX_OK) return rc;
+    cbx_batch bb = *b;
+    bb.logits = h->logits;
+    if (h->hidden_uncond) bb.logits_uncond = h->logits_uncond;
+    {
+        DeviceGuard g(s->device);
+        const int rh = run_head(h, rows, b->n_vocab, b->ld_logits, (hipStream_t)stream);
+        if (rh != CBX_OK) return rh;
+    }
+    return cbx_sample_batch(s, &bb, stream);
+}
+
 int cbx_debug_expf(cbx_sampler* s, const float* in, float* out, int64_t n, void* stream) {
     if (!s || !in || !out || n < 0) return fail(CBX_ERR_INVALID, "cbx_debug_expf: bad argument");
     if (n == 0) return CBX_OK;

@@ -138,6 +138,44 @@ int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_u
  * streams.  Replaces n_steps x n_rows calls of sample_next_token_ex. */
 int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream);
 
+/* Weight formats of the speech_head projection (ggml type ids; rows of n_embd
+ * weights, one per vocab id, ggml ne = [n_embd, n_vocab]). */
+#define CBX_WTYPE_F16  1 /* 2 bytes per weight                                    */
+#define CBX_WTYPE_Q4_0 2 /* 18-byte blocks of 32: fp16 d, 16 bytes of nibbles
+                            (element j < 16 low nibble of byte j, j + 16 high);
+                            w = (q - 8) * d                                       */
+#define CBX_WTYPE_Q8_0 8 /* 34-byte blocks of 32: fp16 d, 32 int8; w = q * d     */
+
+/* The T3 speech_head projection, logits = W h + b (src/main.cpp:577; weights
+ * chatterbox/speech_head and chatterbox/speech_head_bias, main.cpp:394-395,
+ * written by scripts/convert-t3-turbo-to-gguf.py:65-104).  Device pointers. */
+typedef struct cbx_head {
+    const void*  weights;       /* [n_vocab] rows in the wtype layout             */
+    int32_t      wtype;         /* CBX_WTYPE_*                                    */
+    int32_t      n_embd;        /* 32 .. 16384, a multiple of 32                  */
+    const float* bias;          /* optional [n_vocab]                             */
+    const float* hidden;        /* [rows][ld_hidden] fp32 (the ln_f output)       */
+    const float* hidden_uncond; /* optional CFG uncond rows, same layout          */
+    int64_t      ld_hidden;     /* >= n_embd                                      */
+    float*       logits;        /* out [rows][ld_logits]                          */
+    float*       logits_uncond; /* out, required with hidden_uncond               */
+} cbx_head;
+
+/* The projection alone for n_rows rows of hidden (and hidden_uncond) into
+ * logits (and logits_uncond), row stride ld_logits >= n_vocab; fp32 weights
+ * as the format defines them, fp32 matrix-core products and sums.
+ * Replaces the speech_head mul_mat of the T3 step (main.cpp:577).  Async. */
+int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n_vocab,
+                    int64_t ld_logits, void* stream);
+
+/* Fused variant of cbx_sample_batch: the projection of the batch's
+ * n_steps * n_rows hidden rows into h->logits (row stride b->ld_logits; with
+ * hidden_uncond also h->logits_uncond), then the sampler over them, both on
+ * `stream`.  b->logits is ignored; b->logits_uncond is used only when
+ * h->hidden_uncond is NULL.  Replaces the speech_head mul_mat, the logits
+ * hand-off (main.cpp:706-708) and sample_next_token_ex of one T3 step. */
+int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream);
+
 /* Diagnostics: the device exponential used by the sampler (the glibc expf
  * algorithm restated for the GPU) applied elementwise, and the device Philox
  * uniforms for (seed, stream_ids[i] or i, step).  Device memory, async. */

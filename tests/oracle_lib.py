@@ -183,3 +183,50 @@ def stdlib_draw(probs, x0, x1):
     L.cbx_oracle_stdlib_draw.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32,
                                          ctypes.c_uint32]
     return L.cbx_oracle_stdlib_draw(p.ctypes.data, p.size, x0, x1)
+
+
+# ---- speech_head formats (oracle/cbx_oracle.cpp) ----
+WTYPE_F16, WTYPE_Q4_0, WTYPE_Q8_0 = 1, 2, 8
+BLOCK_BYTES = {WTYPE_Q4_0: 18, WTYPE_Q8_0: 34}
+
+
+def quantize(w, wtype):
+    """fp32 [rows, n_embd] -> uint8 [rows, n_embd/32 * block bytes] (ggml rules);
+    F16 rows are the IEEE binary16 bytes."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, n = w.shape
+    if wtype == WTYPE_F16:
+        return w.astype(np.float16).view(np.uint8).reshape(rows, n * 2).copy()
+    out = np.zeros((rows, n // 32 * BLOCK_BYTES[wtype]), np.uint8)
+    lib().cbx_oracle_quantize(w.ctypes.data, rows, n, wtype, out.ctypes.data)
+    return out
+
+
+def dequantize(blocks, wtype, n_embd):
+    """uint8 [rows, bytes] -> fp32 [rows, n_embd], the values the format defines."""
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    rows = blocks.shape[0]
+    if wtype == WTYPE_F16:
+        return blocks.view(np.float16).reshape(rows, n_embd).astype(np.float32)
+    out = np.zeros((rows, n_embd), np.float32)
+    for r in range(rows):
+        lib().cbx_oracle_dequant_row(blocks[r].ctypes.data, wtype, n_embd,
+                                     out[r].ctypes.data)
+    return out
+
+
+def head_f64(blocks, wtype, bias, hidden, n_vocab, n_embd):
+    """logits [rows, n_vocab] in binary64: sum_k deq(W[v][k]) h[r][k] + b[v]
+    (F16 rows through dequantize and a binary64 product)."""
+    hidden = np.ascontiguousarray(hidden, np.float32)
+    if wtype == WTYPE_F16:
+        wd = dequantize(blocks, wtype, n_embd).astype(np.float64)
+        out = hidden.astype(np.float64) @ wd.T
+        return out + (0.0 if bias is None else bias.astype(np.float64))
+    rows = hidden.shape[0]
+    out = np.zeros((rows, n_vocab), np.float64)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().cbx_oracle_head_f64(np.ascontiguousarray(blocks).ctypes.data, wtype,
+                              None if b is None else b.ctypes.data, hidden.ctypes.data, rows,
+                              n_vocab, n_embd, out.ctypes.data)
+    return out

@@ -1,0 +1,161 @@
+"""GPU parity of the fused speech_head variant (cbx_head_logits /
+cbx_head_sample_batch, chatterbox.cpp_amd/csrc/cbx_head.hip) against the
+oracle: the projection against the oracle's binary64 head (W dequantized
+exactly as the format defines, main.cpp:577) within a bound on binary32
+accumulation, and the fused call's tokens against the oracle sampler run on
+the logits the GPU projected (bit-exact, as for any logits).
+
+Tolerance: |gpu - ref| <= 1e-5 * sum_k |w_vk h_rk| + 1e-6 per logit (fp32
+products and sums over n_embd terms; a term lost or misplaced moves a logit
+by about sum |w h| / n_embd, a hundred times the bound).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import pkg
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+@pytest.fixture(scope="module")
+def cbx(torch_cuda):
+    mod = pkg.load()
+    s = mod.Sampler(0, 32768, 1024)
+    yield mod, s
+    s.close()
+
+
+def _problem(rng, V, K, R, wtype, scale=0.05):
+    w = (rng.standard_normal((V, K)) * scale).astype(np.float32)
+    blocks = O.quantize(w, wtype)
+    bias = (rng.standard_normal(V) * 0.1).astype(np.float32)
+    h = rng.standard_normal((R, K)).astype(np.float32)
+    return blocks, bias, h
+
+
+def _bound(blocks, wtype, h, K):
+    deq = np.abs(O.dequantize(blocks, wtype, K)).astype(np.float64)
+    return np.abs(h).astype(np.float64) @ deq.T
+
+
+def _gpu_head(cbx, torch, blocks, wtype, bias, h, V, K, ld, ld_h=None):
+    mod, s = cbx
+    R = h.shape[0]
+    ld_h = K if ld_h is None else ld_h
+    hp = np.zeros((R, ld_h), np.float32)
+    hp[:, :K] = h
+    dW = torch.from_numpy(np.ascontiguousarray(blocks).reshape(-1)).cuda()
+    dh = torch.from_numpy(hp).cuda()
+    db = None if bias is None else torch.from_numpy(bias).cuda()
+    out = torch.full((R, ld), -7.0, dtype=torch.float32, device="cuda")
+    head = mod.Sampler.head(dW, wtype, K, dh, out, bias=db)
+    s.head_logits(head, R, V, ld)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+CASES = [
+    # wtype, V, K, R, ld
+    (O.WTYPE_Q4_0, 6563, 1024, 128, 6563),   # B=64 CFG pairs of the Turbo vocab
+    (O.WTYPE_Q8_0, 6563, 1024, 128, 6576),
+    (O.WTYPE_F16, 6563, 1024, 40, 6563),
+    (O.WTYPE_Q4_0, 8194, 1024, 2, 8194),     # one CFG pair, the Llama vocab
+    (O.WTYPE_Q8_0, 300, 64, 17, 301),        # ragged tiles on both axes
+    (O.WTYPE_F16, 33, 32, 1, 40),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"w{c[0]}_V{c[1]}_K{c[2]}_R{c[3]}" for c in CASES])
+def test_head_logits_against_f64(cbx, torch_cuda, case):
+    wtype, V, K, R, ld = case
+    rng = np.random.default_rng(V * 7 + R + wtype)
+    blocks, bias, h = _problem(rng, V, K, R, wtype)
+    say(f"head wtype={wtype} V={V} K={K} R={R}")
+    got = _gpu_head(cbx, torch_cuda, blocks, wtype, bias, h, V, K, ld, ld_h=K + 3 * (R % 2))
+    ref = O.head_f64(blocks, wtype, bias, h, V, K)
+    tol = 1e-5 * _bound(blocks, wtype, h, K) + 1e-6
+    err = np.abs(got[:, :V].astype(np.float64) - ref)
+    assert np.all(err <= tol), f"max err {err.max():.3g}, worst ratio {(err / tol).max():.3g}"
+    if ld > V:
+        assert np.all(got[:, V:] == -7.0), "stores past n_vocab"
+
+
+def test_head_without_bias(cbx, torch_cuda):
+    rng = np.random.default_rng(5)
+    blocks, _, h = _problem(rng, 500, 256, 20, O.WTYPE_Q4_0)
+    got = _gpu_head(cbx, torch_cuda, blocks, O.WTYPE_Q4_0, None, h, 500, 256, 500)
+    ref = O.head_f64(blocks, O.WTYPE_Q4_0, None, h, 500, 256)
+    tol = 1e-5 * _bound(blocks, O.WTYPE_Q4_0, h, 256) + 1e-6
+    assert np.all(np.abs(got - ref) <= tol)
+
+
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0])
+def test_fused_head_sample_cfg(cbx, torch_cuda, wtype):
+    """B=64 CFG streams, two steps: projection of cond and uncond hidden rows,
+    then the sampler (k 1000, p 0.95, T 0.8, pen 1.2, w 0.5) in one call."""
+    torch = torch_cuda
+    mod, s = cbx
+    V, K, B, S = 6563, 1024, 64, 2
+    rng = np.random.default_rng(77 + wtype)
+    blocks, bias, h = _problem(rng, V, K, B * S, wtype, scale=0.1)
+    hu = (h + 0.5 * rng.standard_normal(h.shape)).astype(np.float32)
+    hist = rng.integers(0, V, size=(B, 300)).astype(np.int32)
+    hl = rng.integers(0, 301, size=B).astype(np.int32)
+    plist = [dict(top_k=1000, top_p=0.95, temp=0.8, repeat_penalty=1.2, min_p=0.0,
+                  cfg_weight=0.5)] * B
+    u = rng.random(B * S)
+    w = pkg.workloads()
+    dW = torch.from_numpy(blocks.reshape(-1)).cuda()
+    dh, dhu = torch.from_numpy(h).cuda(), torch.from_numpy(hu).cuda()
+    lc = torch.zeros((B * S, V), dtype=torch.float32, device="cuda")
+    lu = torch.zeros_like(lc)
+    head = mod.Sampler.head(dW, wtype, K, dh, lc, bias=torch.from_numpy(bias).cuda(),
+                            hidden_uncond=dhu, logits_uncond=lu)
+    prm = torch.from_numpy(w.pack_params(plist)).cuda()
+    tok = torch.full((B * S,), -5, dtype=torch.int32, device="cuda")
+    info = torch.zeros(B * S, dtype=torch.int32, device="cuda")
+    say(f"fused head+sample wtype={wtype} B={B} S={S}")
+    s.head_sample_batch(head, lc, prm, tok, n_steps=S, info=info,
+                        uniforms=torch.from_numpy(u).cuda(),
+                        history=torch.from_numpy(hist).cuda(),
+                        history_len=torch.from_numpy(hl).cuda(), max_survivors=1024)
+    torch.cuda.synchronize()
+    got = tok.cpu().numpy()
+    lcn, lun = lc.cpu().numpy(), lu.cpu().numpy()
+    # the projection is the head's
+    for x, hh in ((lcn, h), (lun, hu)):
+        ref = O.head_f64(blocks, wtype, bias, hh, V, K)
+        assert np.all(np.abs(x - ref) <= 1e-5 * _bound(blocks, wtype, hh, K) + 1e-6)
+    # and the tokens are the oracle sampler's on those logits
+    op = [O.params(**p) for p in plist] * S
+    want = np.array([O.sample_row(lcn[r], hist[r % B][: hl[r % B]], op[r], u[r],
+                                  uncond=lun[r])[0] for r in range(B * S)])
+    assert np.array_equal(got, want), np.nonzero(got != want)[0][:8]
+
+
+def test_head_rejects_bad_arguments(cbx, torch_cuda):
+    torch = torch_cuda
+    mod, s = cbx
+    dW = torch.zeros(18 * 32, dtype=torch.uint8, device="cuda")
+    dh = torch.zeros((2, 64), dtype=torch.float32, device="cuda")
+    out = torch.zeros((2, 16), dtype=torch.float32, device="cuda")
+    for wtype, K in ((3, 64), (O.WTYPE_Q4_0, 48), (O.WTYPE_Q4_0, 0)):
+        head = mod.Sampler.head(dW, wtype, K, dh, out)
+        with pytest.raises(mod.CbxError):
+            s.head_logits(head, 2, 16, 16)
+    head = mod.Sampler.head(dW, O.WTYPE_Q4_0, 64, dh, out)
+    with pytest.raises(mod.CbxError):
+        s.head_logits(head, 2, 16, 8)  # ld_logits < n_vocab

@@ -1,0 +1,88 @@
+"""Pins of the oracle's speech_head weight formats (oracle/cbx_oracle.cpp):
+ggml's Q4_0 / Q8_0 blocks of 32 (fp16 scale d first; Q4_0 element j < 16 in
+the low nibble of byte j, element j + 16 in its high nibble, w = (q - 8) d;
+Q8_0 w = q d), quantized with ggml's reference rules (Q4_0: d = the signed
+largest-magnitude value / -8, q = min(15, trunc(x / d + 8.5)); Q8_0:
+d = max|x| / 127, q = round half away from zero), the rules the reference's
+converter gets from gguf.quants.quantize (scripts/convert-t3-turbo-to-gguf.py:
+86-104).  Known-answer blocks worked by hand, the error bounds the rules
+imply on random rows, and the binary64 head against a direct product.
+"""
+import numpy as np
+
+import oracle_lib as O
+
+
+def test_q4_0_known_block():
+    # x_j = (j - 16) / 4: the largest magnitude is x_0 = -4, so d = 0.5 and
+    # q_j = trunc(j / 2 + 0.5) = 0,1,1,2,2,...,15,15, with 16 clipped to 15
+    x = ((np.arange(32) - 16) / 4.0).astype(np.float32)[None, :]
+    b = O.quantize(x, O.WTYPE_Q4_0)[0]
+    want = bytes([0x00, 0x38,  # d = 0.5 in binary16
+                  0x80, 0x91, 0x91, 0xA2, 0xA2, 0xB3, 0xB3, 0xC4,
+                  0xC4, 0xD5, 0xD5, 0xE6, 0xE6, 0xF7, 0xF7, 0xF8])
+    assert bytes(b) == want
+    q = [0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5, 6, 6, 7, 7, 8,
+         8, 9, 9, 10, 10, 11, 11, 12, 12, 13, 13, 14, 14, 15, 15, 15]
+    deq = O.dequantize(b[None, :], O.WTYPE_Q4_0, 32)[0]
+    assert list(deq) == [(v - 8) * 0.5 for v in q]
+
+
+def test_q8_0_known_blocks():
+    # |x| <= 127 integers with 127 present: d = 1 and q = x; halved: d = 0.5
+    x = np.array([-127, -100, -64, -3, -1, 0, 1, 2, 5, 9, 17, 33, 50, 63, 64, 65,
+                  70, 80, 90, 99, 101, 110, 111, 112, 113, 120, 121, 122, 123, 124, 126, 127],
+                 np.float32)
+    rows = np.stack([x, x / 2]).astype(np.float32)
+    b = O.quantize(rows, O.WTYPE_Q8_0)
+    assert bytes(b[0][:2]) == bytes([0x00, 0x3C])  # d = 1.0
+    assert bytes(b[1][:2]) == bytes([0x00, 0x38])  # d = 0.5
+    assert list(b[0][2:].view(np.int8)) == list(x.astype(np.int8))
+    assert list(b[1][2:].view(np.int8)) == list(x.astype(np.int8))
+    deq = O.dequantize(b, O.WTYPE_Q8_0, 32)
+    assert np.array_equal(deq, rows)
+
+
+def _scales(blocks, wtype, n_embd):
+    bb = O.BLOCK_BYTES[wtype]
+    nb = n_embd // 32
+    raw = blocks.reshape(blocks.shape[0], nb, bb)[:, :, :2].copy()
+    return raw.view(np.float16)[..., 0].astype(np.float32)
+
+
+def test_quantize_error_bounds():
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((64, 256)) * 0.05).astype(np.float32)
+    w[3, :32] = 0.0  # an all-zero block: d = 0, every weight 0
+    for wtype, frac, qmax in ((O.WTYPE_Q4_0, 1.0, 8), (O.WTYPE_Q8_0, 0.5, 127)):
+        b = O.quantize(w, wtype)
+        assert b.shape == (64, 256 // 32 * O.BLOCK_BYTES[wtype])
+        d = np.abs(_scales(b, wtype, 256))
+        deq = O.dequantize(b, wtype, 256)
+        err = np.abs(deq - w).reshape(64, 8, 32).max(axis=-1)
+        # Q4_0 rounds to the nearest step except the clipped +8 step (one d);
+        # Q8_0 to the nearest step; the binary16 scale (quantization divides
+        # by the binary32 one) moves a weight q d by up to |q| d 2^-11
+        assert np.all(err <= d * (frac + (qmax + 1) * 2.0 ** -11) + 1e-12)
+        assert np.all(deq[3, :32] == 0.0)
+        # the largest-magnitude weight of each Q4_0 block is exact (q = 0)
+        if wtype == O.WTYPE_Q4_0:
+            blk = w.reshape(64, 8, 32)
+            i = np.abs(blk).argmax(axis=-1)
+            mx = np.take_along_axis(blk, i[..., None], -1)[..., 0]
+            dq = np.take_along_axis(deq.reshape(64, 8, 32), i[..., None], -1)[..., 0]
+            assert np.allclose(dq, mx, rtol=2.0 ** -10, atol=0)
+
+
+def test_head_f64_matches_direct_product():
+    rng = np.random.default_rng(12)
+    V, K, R = 37, 64, 3
+    w = (rng.standard_normal((V, K)) * 0.1).astype(np.float32)
+    h = rng.standard_normal((R, K)).astype(np.float32)
+    bias = rng.standard_normal(V).astype(np.float32)
+    for wtype in (O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16):
+        b = O.quantize(w, wtype)
+        got = O.head_f64(b, wtype, bias, h, V, K)
+        deq = O.dequantize(b, wtype, K).astype(np.float64)
+        want = h.astype(np.float64) @ deq.T + bias.astype(np.float64)
+        assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
