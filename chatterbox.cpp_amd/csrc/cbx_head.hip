@@ -6,8 +6,12 @@
 // of nibbles, element j < 16 in the low nibble of byte j and element j + 16
 // in its high nibble, w = (q - 8) d; Q8_0 blocks are d and 32 int8, w = q d).
 //
-// One wavefront per workgroup computes a tile of 32 vocab ids x 16 rows with
-// v_mfma_f32_16x16x4_f32 (two 16x16 accumulators).  Lane l feeds A[l%16][l/16]
+// A workgroup of KS wavefronts computes a tile of 32 vocab ids x 16 rows with
+// v_mfma_f32_16x16x4_f32 (two 16x16 accumulators per wave); wave w takes the
+// w-th of KS runs of 32-weight blocks along n_embd, and the KS partial tiles
+// are added in wave order through LDS (a fixed order: results do not depend
+// on scheduling).  KS waves per tile keep enough waves in flight to cover the
+// loads' latency.  Lane l feeds A[l%16][l/16]
 // and B[l/16][l%16] and holds D[4(l/16)+i][l%16] in accumulator register i.
 // Inside a 32-weight block, step s (0..7) and lane group g = l/16 carry
 // k = 8g + s, so each lane dequantizes 8 consecutive weights of one block per
@@ -33,59 +37,81 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t hb) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
 }
 
-__device__ __forceinline__ uint32_t ld_u16(const __amdgpu_buffer_rsrc_t& r, uint32_t off) {
-    return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-
-// The 8 weights k = 8g .. 8g + 7 of block kb of vocab row v.
+// Raw bytes of the 8 weights k = 8g .. 8g + 7 of block kb of vocab row v:
+// F16 four dwords; Q4_0 / Q8_0 the fp16 scale in q[4] and the 8 bytes of
+// nibbles or int8 in q[0..1].  Blocks are 18 or 34 bytes, so only 2-byte
+// alignment holds: the bytes come from dword-aligned loads (the dword holding
+// the scale, three dwords holding the 8 bytes) shifted into place.
 template <int WT>
-__device__ __forceinline__ void weights8(const __amdgpu_buffer_rsrc_t& rw, int v, int kb, int g,
-                                         int n_embd, float* w) {
+__device__ __forceinline__ void load_w(const __amdgpu_buffer_rsrc_t& rw, int v, int kb, int g,
+                                       int n_embd, uint32_t* q) {
     if constexpr (WT == CBX_WTYPE_F16) {
         const uint32_t off = (uint32_t)(((int64_t)v * n_embd + kb * 32 + 8 * g) * 2);
-        const uint32_t u0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, off, 0, 0);
-        const uint32_t u1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, off + 4, 0, 0);
-        const uint32_t u2 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, off + 8, 0, 0);
-        const uint32_t u3 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, off + 12, 0, 0);
-        const uint32_t u[4] = {u0, u1, u2, u3};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w[2 * i] = half_bits_to_float(u[i] & 0xffffu);
-            w[2 * i + 1] = half_bits_to_float(u[i] >> 16);
-        }
+        const auto u = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+        q[0] = u[0]; q[1] = u[1]; q[2] = u[2]; q[3] = u[3];
     } else {
         constexpr int BB = WT == CBX_WTYPE_Q4_0 ? 18 : 34;  // bytes per block
         const uint32_t blk = (uint32_t)(((int64_t)v * (n_embd / 32) + kb) * BB);
-        const float d = half_bits_to_float(ld_u16(rw, blk));
-        // Q4_0: bytes 8(g&1) .. +7 of the nibbles, low nibbles for g < 2;
-        // Q8_0: int8 values 8g .. 8g + 7
+        // Q4_0: bytes 8(g&1) .. +7 of the nibbles; Q8_0: int8 values 8g .. 8g + 7
         const uint32_t qoff = blk + 2 + (WT == CBX_WTYPE_Q4_0 ? 8 * (g & 1) : 8 * g);
-        uint32_t p[4];
+        const uint32_t dw = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, blk & ~3u, 0, 0);
+        q[4] = (dw >> (8 * (blk & 3u))) & 0xffffu;
+        const auto t = __builtin_amdgcn_raw_buffer_load_b96(rw, qoff & ~3u, 0, 0);
+        const uint32_t sh = 8 * (qoff & 3u);
+        q[0] = __builtin_amdgcn_alignbit(t[1], t[0], sh);
+        q[1] = __builtin_amdgcn_alignbit(t[2], t[1], sh);
+    }
+}
+
+__device__ __forceinline__ float ubyte(uint32_t x, int i) { return (float)((x >> (8 * i)) & 0xffu); }
+
+// The fp32 weights the format defines, from load_w's bytes.  Q4_0: nibble
+// n = q + 8 and w = (n - 8) d = fma(n, d, -8d), exact (n d and -8d are exact
+// and their sum is representable); Q8_0: u = q + 128 (sign bit flipped) and
+// w = fma(u, d, -128d), exact for the same reason.
+template <int WT>
+__device__ __forceinline__ void dequant(const uint32_t* q, int g, float* w) {
+    if constexpr (WT == CBX_WTYPE_F16) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = ld_u16(rw, qoff + 2 * i);
+        for (int i = 0; i < 4; ++i) {
+            w[2 * i] = half_bits_to_float(q[i] & 0xffffu);
+            w[2 * i + 1] = half_bits_to_float(q[i] >> 16);
+        }
+    } else {
+        const float d = half_bits_to_float(q[4]);
+        uint32_t x0, x1;
+        float off;
+        if constexpr (WT == CBX_WTYPE_Q4_0) {
+            const int sh = g < 2 ? 0 : 4;
+            x0 = (q[0] >> sh) & 0x0f0f0f0fu;
+            x1 = (q[1] >> sh) & 0x0f0f0f0fu;
+            off = __fmul_rn(d, -8.0f);
+        } else {
+            x0 = q[0] ^ 0x80808080u;
+            x1 = q[1] ^ 0x80808080u;
+            off = __fmul_rn(d, -128.0f);
+        }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t byte = (p[i >> 1] >> (8 * (i & 1))) & 0xffu;
-            if constexpr (WT == CBX_WTYPE_Q4_0) {
-                const int q = (int)(g < 2 ? (byte & 0xfu) : (byte >> 4)) - 8;
-                w[i] = __fmul_rn((float)q, d);
-            } else {
-                w[i] = __fmul_rn((float)(int8_t)byte, d);
-            }
+        for (int i = 0; i < 4; ++i) {
+            w[i] = __fmaf_rn(ubyte(x0, i), d, off);
+            w[4 + i] = __fmaf_rn(ubyte(x1, i), d, off);
         }
     }
 }
 
+constexpr int KS = 4;  // waves per tile (runs of blocks along n_embd)
+
 template <int WT>
-__global__ __launch_bounds__(64) void head_mfma(const void* W, const float* bias,
-                                                const float* hidden, int64_t ld_hidden,
-                                                float* out, int64_t ld_out, int n_rows,
-                                                int n_vocab, int n_embd) {
-    const int lane = threadIdx.x;
+__global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float* bias,
+                                                     const float* hidden, int64_t ld_hidden,
+                                                     float* out, int64_t ld_out, int n_rows,
+                                                     int n_vocab, int n_embd) {
+    __shared__ f4 part[KS - 1][2][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, g = lane >> 4;
     const int v0 = blockIdx.x * 32, r0 = blockIdx.y * 16;
-    constexpr int64_t kRowBytesNum = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
-    const int64_t wbytes = (int64_t)n_vocab * (n_embd / 32) * kRowBytesNum;
+    constexpr int64_t kBlockBytes = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
+    const int64_t wbytes = (int64_t)n_vocab * (n_embd / 32) * kBlockBytes;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
@@ -96,20 +122,46 @@ __global__ __launch_bounds__(64) void head_mfma(const void* W, const float* bias
     const int va_c = va < n_vocab ? va : n_vocab, vb_c = vb < n_vocab ? vb : n_vocab;
     const int64_t hrow = rr < n_rows ? (int64_t)rr * ld_hidden : ((int64_t)n_rows * ld_hidden + n_embd);
     f4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
-    const int nb = n_embd / 32;
-#pragma unroll 1
-    for (int kb = 0; kb < nb; ++kb) {
-        float wa[8], wb[8], hv[8];
-        weights8<WT>(rw, va_c, kb, g, n_embd, wa);
-        weights8<WT>(rw, vb_c, kb, g, n_embd, wb);
+    const int nball = n_embd / 32;
+    const int kb0 = nball * wave / KS, kb1 = nball * (wave + 1) / KS;
+    // block kb + 1's loads are in flight while block kb's products run
+    uint32_t qa[5], qb[5];
+    f4 h0, h1;
+    auto load = [&](int kb) {
+        load_w<WT>(rw, va_c, kb, g, n_embd, qa);
+        load_w<WT>(rw, vb_c, kb, g, n_embd, qb);
         const uint32_t hoff = (uint32_t)((hrow + kb * 32 + 8 * g) * 4);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            hv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rh, hoff + 4 * i, 0, 0));
+        h0 = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rh, hoff, 0, 0));
+        h1 = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rh, hoff + 16, 0, 0));
+    };
+    if (kb0 < kb1) load(kb0);
+#pragma unroll 1
+    for (int kb = kb0; kb < kb1; ++kb) {
+        float wa[8], wb[8];
+        dequant<WT>(qa, g, wa);
+        dequant<WT>(qb, g, wb);
+        const float hv[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+        if (kb + 1 < kb1) load(kb + 1);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], hv[s], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wb[s], hv[s], acc1, 0, 0, 0);
+        }
+    }
+    // the partial tiles of waves 1 .. KS-1 join wave 0's in wave order
+    if (wave > 0) {
+        part[wave - 1][0][lane] = acc0;
+        part[wave - 1][1][lane] = acc1;
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < KS - 1; ++w) {
+        const f4 p0 = part[w][0][lane], p1 = part[w][1][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc0[i] = __fadd_rn(acc0[i], p0[i]);
+            acc1[i] = __fadd_rn(acc1[i], p1[i]);
         }
     }
     if (rr >= n_rows) return;
@@ -130,15 +182,15 @@ hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const fl
     const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_rows + 15) / 16));
     switch (wtype) {
         case CBX_WTYPE_F16:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_F16>, grid, dim3(64), 0, stream, W, bias, hidden,
+            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_F16>, grid, dim3(64 * KS), 0, stream, W, bias, hidden,
                                ld_hidden, out, ld_out, n_rows, n_vocab, n_embd);
             break;
         case CBX_WTYPE_Q4_0:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q4_0>, grid, dim3(64), 0, stream, W, bias, hidden,
+            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q4_0>, grid, dim3(64 * KS), 0, stream, W, bias, hidden,
                                ld_hidden, out, ld_out, n_rows, n_vocab, n_embd);
             break;
         case CBX_WTYPE_Q8_0:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q8_0>, grid, dim3(64), 0, stream, W, bias, hidden,
+            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q8_0>, grid, dim3(64 * KS), 0, stream, W, bias, hidden,
                                ld_hidden, out, ld_out, n_rows, n_vocab, n_embd);
             break;
         default:
