@@ -1108,7 +1108,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                           ? desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w)
                           : ~0ull;
             int rank = 0;
-#pragma unroll 4
             for (int t = 0; t < n_surv; ++t) {
                 const uint64_t kt =
                     ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), t) << 32) |
