@@ -111,6 +111,73 @@ def cpu_baseline(hist, hist_len, params, logits_host, u, gpu_tokens, seconds_1t,
     return out
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+HEAD_EMBD, HEAD_B = 1024, 64
+
+
+def fused_head_bench(torch, mod, sampler, stream, steps, dev):
+    """Q4_0 head + sampler, B=64 CFG pairs (128 projected rows): synthetic
+    blocks (random nibbles, fp16 scales of a 0.05-scale weight row) and
+    hidden rows, resident in HBM; HIP events on the launch stream."""
+    rng = np.random.default_rng(0x4EAD)
+    nb = HEAD_EMBD // 32
+    blocks = rng.integers(0, 256, size=(V, nb, 18), dtype=np.uint8)
+    d = (rng.uniform(0.004, 0.01, size=(V, nb))).astype(np.float16)
+    blocks[:, :, :2] = d.view(np.uint8).reshape(V, nb, 2)
+    d_w = torch.from_numpy(blocks.reshape(-1)).to(dev)
+    d_b = torch.from_numpy((rng.standard_normal(V) * 0.1).astype(np.float32)).to(dev)
+    hc = torch.from_numpy(rng.standard_normal((HEAD_B, HEAD_EMBD)).astype(np.float32)).to(dev)
+    hu = torch.from_numpy(rng.standard_normal((HEAD_B, HEAD_EMBD)).astype(np.float32)).to(dev)
+    lc = torch.empty((HEAD_B, V), dtype=torch.float32, device=dev)
+    lu = torch.empty_like(lc)
+    head = mod.Sampler.head(d_w, mod.CBX_WTYPE_Q4_0, HEAD_EMBD, hc, lc, bias=d_b,
+                            hidden_uncond=hu, logits_uncond=lu)
+    w = pkg_workloads()
+    plist = [dict(top_k=1000, top_p=0.95, temp=0.8, repeat_penalty=1.2, min_p=0.05,
+                  cfg_weight=0.5)] * HEAD_B
+    d_par = torch.from_numpy(w.pack_params(plist)).to(dev)
+    hist = torch.from_numpy(rng.integers(0, V, size=(HEAD_B, 1000)).astype(np.int32)).to(dev)
+    hlen = torch.from_numpy(rng.integers(0, 1001, size=HEAD_B).astype(np.int32)).to(dev)
+    tok = torch.empty(HEAD_B, dtype=torch.int32, device=dev)
+
+    def fused_step(i):
+        sampler.head_sample_batch(head, lc, d_par, tok, history=hist, history_len=hlen,
+                                  draw_mode=mod.CBX_DRAW_PHILOX, seed=7, step0=i,
+                                  max_survivors=1000)
+
+    def head_only(i):
+        sampler.head_logits(head, HEAD_B, V, V)
+
+    res = {}
+    for name, fn in (("head", head_only), ("fused", fused_step)):
+        for i in range(20):
+            fn(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(steps):
+            fn(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / steps
+    flops = 2.0 * 2 * HEAD_B * V * HEAD_EMBD  # cond and uncond rows
+    tf = flops / (res["head"] / 1e3) / 1e12
+    return {"workload": "fused Q4_0 speech_head (V=6563 x 1024) + sampler, B=64 CFG pairs "
+                        "(128 projected rows), k 1000, p 0.95, T 0.8, pen 1.2, min_p 0.05",
+            "steps": steps, "ms_per_step": round(res["fused"], 5),
+            "tokens_per_s": round(HEAD_B / (res["fused"] / 1e3), 1),
+            "head_ms": round(res["head"], 5),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                         "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
+                         "kernel": "head_mfma<Q4_0>", "flops_per_launch": flops}}
+
+
+def pkg_workloads():
+    import pkg
+    return pkg.workloads()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +188,8 @@ def main():
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
+    ap.add_argument("--head-steps", type=int, default=200,
+                    help="timed steps of the fused speech_head variant (0: skip)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run a plain device copy of this many MiB (3 times) so "
@@ -206,6 +275,13 @@ def main():
         ms = a.elapsed_time(b) / args.single_launch_steps
         single = {"ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1)}
 
+    # the fused speech_head variant on the B=64 CFG shape: 128 hidden rows
+    # (64 cond + 64 uncond) through Q4_0 weights of the Turbo head
+    # (V=6563 x 1024), then the sampler over the 64 CFG pairs
+    fused = None
+    if args.head_steps > 0:
+        fused = fused_head_bench(torch, mod, sampler, stream, args.head_steps, dev)
+
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -273,6 +349,7 @@ def main():
         "cpu_baseline": cpu,
         "single_launch_per_step": single,
         "parity_vs_oracle": parity,
+        "fused_head": fused,
     }
     print(json.dumps(out), flush=True)
     sampler.close()

@@ -346,11 +346,9 @@ int check_head(const char* fn, const cbx_head* h, int32_t n_rows, int32_t n_voca
 
 int run_head(const cbx_head* h, int32_t n_rows, int32_t n_vocab, int64_t ld_logits,
              hipStream_t st) {
-    CBX_HIP(cbx::launch_head(h->weights, h->wtype, h->bias, h->hidden, h->ld_hidden, h->logits,
-                             ld_logits, n_rows, n_vocab, h->n_embd, st));
-    if (h->hidden_uncond)
-        CBX_HIP(cbx::launch_head(h->weights, h->wtype, h->bias, h->hidden_uncond, h->ld_hidden,
-                                 h->logits_uncond, ld_logits, n_rows, n_vocab, h->n_embd, st));
+    CBX_HIP(cbx::launch_head(h->weights, h->wtype, h->bias, h->hidden, h->hidden_uncond,
+                             h->ld_hidden, h->logits, h->logits_uncond, ld_logits, n_rows,
+                             n_vocab, h->n_embd, st));
     return CBX_OK;
 }
 }  // namespace

@@ -103,10 +103,14 @@ constexpr int KS = 4;  // waves per tile (runs of blocks along n_embd)
 
 template <int WT>
 __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float* bias,
-                                                     const float* hidden, int64_t ld_hidden,
-                                                     float* out, int64_t ld_out, int n_rows,
-                                                     int n_vocab, int n_embd) {
+                                                     const float* hidden0, const float* hidden1,
+                                                     int64_t ld_hidden, float* out0, float* out1,
+                                                     int64_t ld_out, int n_rows, int n_vocab,
+                                                     int n_embd) {
     __shared__ f4 part[KS - 1][2][64];
+    // blockIdx.z: the first (cond) or second (uncond) set of rows
+    const float* hidden = blockIdx.z ? hidden1 : hidden0;
+    float* out = blockIdx.z ? out1 : out0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, g = lane >> 4;
     const int v0 = blockIdx.x * 32, r0 = blockIdx.y * 16;
@@ -176,22 +180,27 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
 
 }  // namespace
 
-hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden,
-                       int64_t ld_hidden, float* out, int64_t ld_out, int32_t n_rows,
-                       int32_t n_vocab, int32_t n_embd, hipStream_t stream) {
-    const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_rows + 15) / 16));
+hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
+                       const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                       int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                       hipStream_t stream) {
+    const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_rows + 15) / 16),
+                    hidden1 ? 2u : 1u);
     switch (wtype) {
         case CBX_WTYPE_F16:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_F16>, grid, dim3(64 * KS), 0, stream, W, bias, hidden,
-                               ld_hidden, out, ld_out, n_rows, n_vocab, n_embd);
+            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_F16>, grid, dim3(64 * KS), 0, stream, W, bias,
+                               hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
+                               n_embd);
             break;
         case CBX_WTYPE_Q4_0:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q4_0>, grid, dim3(64 * KS), 0, stream, W, bias, hidden,
-                               ld_hidden, out, ld_out, n_rows, n_vocab, n_embd);
+            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q4_0>, grid, dim3(64 * KS), 0, stream, W, bias,
+                               hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
+                               n_embd);
             break;
         case CBX_WTYPE_Q8_0:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q8_0>, grid, dim3(64 * KS), 0, stream, W, bias, hidden,
-                               ld_hidden, out, ld_out, n_rows, n_vocab, n_embd);
+            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q8_0>, grid, dim3(64 * KS), 0, stream, W, bias,
+                               hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
+                               n_embd);
             break;
         default:
             return hipErrorInvalidValue;

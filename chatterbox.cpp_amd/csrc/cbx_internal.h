@@ -69,10 +69,12 @@ hipError_t launch_debug_chain(const float* terms, const int32_t* offsets, const 
 hipError_t launch_debug_philox(uint64_t seed, const uint64_t* stream_ids, uint64_t step,
                                int32_t n, double* out, hipStream_t stream);
 
-// The speech_head projection (cbx_head.hip): out[r][v] = W[v] . hidden[r] + bias[v]
-// for r < n_rows, v < n_vocab.
-hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden,
-                       int64_t ld_hidden, float* out, int64_t ld_out, int32_t n_rows,
-                       int32_t n_vocab, int32_t n_embd, hipStream_t stream);
+// The speech_head projection (cbx_head.hip): out0[r][v] = W[v] . hidden0[r] + bias[v]
+// for r < n_rows, v < n_vocab, and the same from hidden1 into out1 in the same
+// launch when hidden1 is given.
+hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
+                       const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                       int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                       hipStream_t stream);
 
 }  // namespace cbx
