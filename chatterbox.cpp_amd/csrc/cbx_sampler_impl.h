@@ -1200,7 +1200,8 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
 
     // ---- load (all loads first), combine, mask, temperature (main.cpp:733-738) ----
     // Buffer loads bounded by a resource of V*4 bytes: one lane offset, the
-    // j*BLOCK stride in a scalar offset, ids >= V read 0 (masked below).
+    // j*BLOCK stride in a scalar offset, ids >= V read 0 (masked below);
+    // non-temporal (cache policy nt): each row's logits are read once.
     const float* lrow = a.logits + rs * a.ld_logits;
     float s[EPT];
     {
@@ -1209,7 +1210,7 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
             s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                 rl, tid * 4, j * BLOCK * 4, 0));
+                                                 rl, tid * 4, j * BLOCK * 4, 2));
     }
     if (a.uncond) {
         const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
@@ -1217,7 +1218,7 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             const float un = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(ru, tid * 4, j * BLOCK * 4, 0));
+                float, __builtin_amdgcn_raw_buffer_load_b32(ru, tid * 4, j * BLOCK * 4, 2));
             s[j] = __fadd_rn(s[j], __fmul_rn(P.cfg_weight, __fsub_rn(s[j], un)));
         }
     }

@@ -172,7 +172,8 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 // makes this compiler emit a single-word load.
 __device__ __forceinline__ void load4(const __amdgpu_buffer_rsrc_t& r, int voff, int soff,
                                       float* out) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    // non-temporal (cache policy nt): each row's logits are read once
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
     __builtin_memcpy(out, &v, 16);
 }
 
