@@ -1108,12 +1108,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 key = lane < n_surv
                           ? desc_key(__builtin_bit_cast(float, (uint32_t)(w >> 32)), (uint32_t)w)
                           : ~0ull;
+            // four lanes per step (lanes past the list hold the maximum key,
+            // which is never below another)
+            auto key_of = [&](int t) -> uint64_t {
+                return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), t)
+                        << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, t);
+            };
             int rank = 0;
-            for (int t = 0; t < n_surv; ++t) {
-                const uint64_t kt =
-                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), t) << 32) |
-                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, t);
-                rank += (kt < key) ? 1 : 0;
+            for (int t = 0; t < n_surv; t += 4) {
+                const uint64_t k0 = key_of(t), k1 = key_of(t + 1), k2 = key_of(t + 2),
+                               k3 = key_of(t + 3);
+                rank += ((k0 < key) ? 1 : 0) + ((k1 < key) ? 1 : 0) + ((k2 < key) ? 1 : 0) +
+                        ((k3 < key) ? 1 : 0);
             }
             __syncthreads();  // every entry read: the sorted keys take the list
             sm.list[lane < n_surv ? rank : lane] = key;
