@@ -606,50 +606,190 @@ __device__ __forceinline__ void bitonic_sort_pairs(uint32_t* key, uint16_t* id, 
 
 // ------------------------------------------------------ reference-order sums
 
-__device__ __forceinline__ float lane_term(int xi, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, l));
+
+template <int CTRL, int RM>
+__device__ __forceinline__ int dpp_i(int old, int x) {
+    return __builtin_amdgcn_update_dpp(old, x, CTRL, RM, 0xf, false);
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ float dpp_f(float old, float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, x), CTRL,
+                                                                 RM, 0xf, false));
 }
 
-// acc + v[0] + ... + v[n-1] in index order, binary32, by one wave: 64 terms
-// per load, then a chain of dependent adds reading each lane's term.
-__device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc) {
+// The binary32 running sum acc0 + t_0 + t_1 + ... in order, where lane l holds
+// terms l*C .. l*C + C - 1 in t[0, C) (zeros past the last term), by sweeps
+// of the wave: a sweep adds each lane's terms, one after the other, to the
+// sum carried in from the lane below (a wave_shr:1 DPP operand; lane 0 starts
+// from acc0), so after sweep s the sums of lanes 0..s are final.  These are the
+// reference's adds in the reference's order (NaN and infinities included);
+// a sweep costs C + 1 instructions.  nl: lanes holding terms (1..64).
+// Returns the final sum of lane nl - 1.  With THR, stops once a lane's final
+// sum reaches thr: `hit` is then the first term index whose running sum is
+// >= thr (otherwise -1).
+template <int C, bool THR, int CM, bool ACC = false>
+__device__ __forceinline__ float chain_sweeps(const float (&t)[CM], int nl, float thr, int& hit,
+                                             float acc0 = 0.0f) {
+    static_assert(C <= CM, "terms per lane");
+    const int lane = threadIdx.x & 63;
+    hit = -1;
+    float s = 0.0f;
+    for (int sw = 0; sw < nl; ++sw) {
+        float in = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x138, 0xf, 0xf, true));
+        if constexpr (ACC) in = lane == 0 ? acc0 : in;  // else lane 0 reads 0 (bound_ctrl)
+        float acc = __fadd_rn(in, t[0]);
+#pragma unroll
+        for (int k = 1; k < C; ++k) acc = __fadd_rn(acc, t[k]);
+        s = acc;
+        if (THR && ((__ballot(s >= thr) >> sw) & 1ull)) {
+            // lane sw holds the first crossing: walk its terms from its start
+            float w = in;
+            int first = C;
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                w = __fadd_rn(w, t[k]);
+                first = (first == C && w >= thr) ? k : first;
+            }
+            hit = sw * C + __builtin_amdgcn_readlane(first, sw);
+            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), sw));
+        }
+    }
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), nl - 1));
+}
+
+// The same sum 0 + t_0 + t_1 + ... (finite terms >= 0, t_0 > 0) with fewer
+// dependent steps, for long lanes.  While the running sum P = N*u stays in
+// one binade [2^b, 2^(b+1)) (u = 2^(b-23), N an integer), each add moves N by
+// an amount that depends on the term and on N's parity only (round to nearest
+// even).  A lane's whole run of terms is therefore a two-entry table
+// (increment from an even N, from an odd N), read off two real float chains
+// started at 2^b and 2^b + u; tables compose, so one DPP scan gives every
+// lane's exact starting N.  The first lane whose run leaves the binade then
+// adds its terms from that exact start as the reference does (any number of
+// binade changes inside), and the next round starts after it.  Lane 0 begins
+// from 0 directly.  Exactly the reference's adds' results.
+template <int C, int CM>
+__device__ __forceinline__ float chain_segments(const float (&t)[CM], int nl, float acc0 = 0.0f) {
+    static_assert(C <= CM, "terms per lane");
+    const int lane = threadIdx.x & 63;
+    constexpr int kSat = 1 << 24;
+    float a = acc0;
+#pragma unroll
+    for (int k = 0; k < C; ++k) a = __fadd_rn(a, t[k]);
+    float P = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
+    int lstart = 1;
+    while (lstart < nl) {
+        if (!(P >= 0x1p-100f)) {  // tiny sums (not seen for softmax terms): one add each
+            int unused;
+            return chain_sweeps<C, false, CM, true>(t, nl, 0.0f, unused, acc0);
+        }
+        const uint32_t pb = __builtin_bit_cast(uint32_t, P);
+        const uint32_t bb = pb & 0x7f800000u;  // bits of 2^b
+        const float base = __builtin_bit_cast(float, bb);
+        const float lim = __builtin_bit_cast(float, bb + 0x00800000u);  // 2^(b+1)
+        const int N0 = (int)((pb & 0x7fffffu) | 0x800000u);            // P / u
+        const int p0 = N0 & 1;
+        float A0 = base, A1 = __builtin_bit_cast(float, bb + 1u);  // N = 2^23, 2^23 + 1
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            A0 = __fadd_rn(A0, t[k]);
+            A1 = __fadd_rn(A1, t[k]);
+        }
+        // increments in units of u (same binade: the bit difference), or saturated
+        int d0 = A0 < lim ? (int)(__builtin_bit_cast(uint32_t, A0) - bb) : kSat;
+        int d1 = A1 < lim ? (int)(__builtin_bit_cast(uint32_t, A1) - bb) - 1 : kSat;
+        d0 = lane < lstart ? 0 : d0;  // lanes already summed: identity
+        d1 = lane < lstart ? 0 : d1;
+        // inclusive scan; composing an earlier table a with this lane's:
+        // from an even start the parity after a is a0 & 1, from an odd one
+        // (1 + a1) & 1
+        auto step = [&](int a0, int a1) {
+            const int n0 = a0 + ((a0 & 1) ? d1 : d0);
+            const int n1 = a1 + ((a1 & 1) ? d0 : d1);
+            d0 = n0;
+            d1 = n1;
+        };
+        step(dpp_i<0x111, 0xf>(0, d0), dpp_i<0x111, 0xf>(0, d1));  // row_shr:1
+        step(dpp_i<0x112, 0xf>(0, d0), dpp_i<0x112, 0xf>(0, d1));  // row_shr:2
+        step(dpp_i<0x114, 0xf>(0, d0), dpp_i<0x114, 0xf>(0, d1));  // row_shr:4
+        step(dpp_i<0x118, 0xf>(0, d0), dpp_i<0x118, 0xf>(0, d1));  // row_shr:8
+        step(dpp_i<0x142, 0xa>(0, d0), dpp_i<0x142, 0xa>(0, d1));  // row_bcast:15
+        step(dpp_i<0x143, 0xc>(0, d0), dpp_i<0x143, 0xc>(0, d1));  // row_bcast:31
+        const int x0 = dpp_i<0x138, 0xf>(0, d0), x1 = dpp_i<0x138, 0xf>(0, d1);  // exclusive
+        const int din = p0 ? x1 : x0, dout = p0 ? d1 : d0;
+        const uint64_t reach = __ballot(N0 + dout >= (1 << 24));
+        if (reach == 0) {
+            // no lane leaves the binade: the total is N0 + the last increment
+            return __builtin_bit_cast(float, pb + (uint32_t)__builtin_amdgcn_readlane(dout, 63));
+        }
+        const int L = (int)__builtin_ctzll(reach);
+        float w = __builtin_bit_cast(float, pb + (uint32_t)din);  // lane's exact start
+#pragma unroll
+        for (int k = 0; k < C; ++k) w = __fadd_rn(w, t[k]);
+        P = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), L));
+        lstart = L + 1;
+    }
+    return P;
+}
+
+// acc + v[0] + ... + v[n-1] in index order, binary32, by one wave, in chunks
+// of 64 x 17 terms (lane l holding terms l*17 .. l*17 + 16 of a chunk: odd
+// strides, distinct banks).  finite: every term finite and >= 0 and acc
+// finite, so the binade segments apply (chain_segments); otherwise sweeps,
+// exact for NaN and infinities too.
+constexpr int kChainC = 17;
+__device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc, bool finite = true) {
     const int lane = threadIdx.x & 63;
     n = uni(n);
-    int base = 0;
-    for (; base + 64 <= n; base += 64) {
-        const int xi = __builtin_bit_cast(int, v[base + lane]);
+    for (int base = 0; base < n; base += 64 * kChainC) {
+        float t[kChainC];
 #pragma unroll
-        for (int l = 0; l < 64; ++l) acc = __fadd_rn(acc, lane_term(xi, l));
-    }
-    if (base < n) {
-        const int xi = __builtin_bit_cast(int, base + lane < n ? v[base + lane] : 0.0f);
-        const int m = n - base;
-        for (int l = 0; l < m; ++l) acc = __fadd_rn(acc, lane_term(xi, l));
+        for (int q = 0; q < kChainC; ++q) {
+            const int i = base + lane * kChainC + q;
+            t[q] = i < n ? v[i] : 0.0f;
+        }
+        const int nl = min(64, (n - base + kChainC - 1) / kChainC);
+        if (finite) {
+            acc = chain_segments<kChainC>(t, nl, acc);
+        } else {
+            int unused;
+            acc = chain_sweeps<kChainC, false, kChainC, true>(t, nl, 0.0f, unused, acc);
+        }
     }
     return acc;
 }
 
 // First i with (0 + v[0] + ... + v[i]) >= thr (binary32, index order), or
 // n-1 when the running sum never reaches thr.  One wave.  Terms are
-// non-negative, so the running sum never decreases: a 64-term chunk is redone
-// term by term only when its end value reaches thr.
-__device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr) {
+// non-negative, so the running sum never decreases: a chunk is searched only
+// when its end value reaches thr.
+__device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr, bool finite = true) {
     const int lane = threadIdx.x & 63;
     n = uni(n);
     float acc = 0.0f;
-    for (int base = 0; base < n; base += 64) {
-        const int m = min(64, n - base);
-        const int xi = __builtin_bit_cast(int, lane < m ? v[base + lane] : 0.0f);
-        float a = acc;
+    for (int base = 0; base < n; base += 64 * kChainC) {
+        float t[kChainC];
 #pragma unroll
-        for (int l = 0; l < 64; ++l) a = __fadd_rn(a, lane_term(xi, l));
-        if (a >= thr) {
-            for (int l = 0; l < m; ++l) {
-                acc = __fadd_rn(acc, lane_term(xi, l));
-                if (acc >= thr) return base + l;
-            }
+        for (int q = 0; q < kChainC; ++q) {
+            const int i = base + lane * kChainC + q;
+            t[q] = i < n ? v[i] : 0.0f;
         }
-        acc = a;
+        const int nl = min(64, (n - base + kChainC - 1) / kChainC);
+        int hit = -1;
+        float end;
+        if (finite) {
+            end = chain_segments<kChainC>(t, nl, acc);
+        } else {
+            int unused;
+            end = chain_sweeps<kChainC, false, kChainC, true>(t, nl, 0.0f, unused, acc);
+        }
+        if (end >= thr) {
+            (void)chain_sweeps<kChainC, true, kChainC, true>(t, nl, thr, hit, acc);
+            if (hit >= 0) return base + hit;
+        }
+        acc = end;
     }
     return n - 1;
 }
@@ -980,7 +1120,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
     }
     __syncthreads();
     if (wid == 0) {
-        const float ps = wave_chain_sum(F, n_final, 0.0f);
+        const float ps = wave_chain_sum(F, n_final, 0.0f, !(flags & CBX_INFO_NONFINITE));
         if (lane == 0) sh.psum = ps;
     }
     __syncthreads();
@@ -1091,7 +1231,7 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
             const bool scan = !(flags & CBX_INFO_NONFINITE);
             int hit;
             const float psum = scan ? seq_sum_wave<kFastMax / 64>(E, n_surv, E[0], 1, 0.0f, hit)
-                                    : wave_chain_sum(E, n_surv, 0.0f);
+                                    : wave_chain_sum(E, n_surv, 0.0f, false);
             CBX_STAMP(6);
             for (int i = lane; i < n_surv; i += 64) E[i] = __fdiv_rn(E[i], psum);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1106,7 +1246,7 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
                     last = hit < 0 ? n_surv - 1 : hit;
                 }
             } else {
-                last = wave_chain_cross(E, n_surv, P.top_p);
+                last = wave_chain_cross(E, n_surv, P.top_p, false);
             }
             if (lane == 0) sh.n_kept = last + 1;
         }
@@ -1355,22 +1495,25 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
         const int n2 = uni(max(64, pow2ceil(n_surv)));
         for (int i = n_surv + tid; i < n2; i += BLOCK) { key32[i] = 0xFFFFFFFFu; id16[i] = 0xFFFFu; }
         __syncthreads();
+        CBX_STAMP(13);
         bitonic_sort_pairs<BLOCK>(key32, id16, n2);
+        CBX_STAMP(14);
         const float mx_surv = unif(okey_inv(~key32[0]));
         __syncthreads();
         for (int i = tid; i < n_surv; i += BLOCK)
             E[i] = expf_libm_branchless(__fsub_rn(okey_inv(~key32[i]), mx_surv), tab);
         __syncthreads();
         if (wid == 0) {
-            const float ps = wave_chain_sum(E, n_surv, 0.0f);
+            const float ps = wave_chain_sum(E, n_surv, 0.0f, !bad);
             if (lane == 0) sh.psum = ps;
         }
         __syncthreads();
+        CBX_STAMP(15);
         const float psum = unif(sh.psum);
         for (int i = tid; i < n_surv; i += BLOCK) E[i] = __fdiv_rn(E[i], psum);
         __syncthreads();
         if (wid == 0) {
-            const int last = wave_chain_cross(E, n_surv, P.top_p);
+            const int last = wave_chain_cross(E, n_surv, P.top_p, !bad);
             if (lane == 0) sh.n_kept = last + 1;
         }
         __syncthreads();

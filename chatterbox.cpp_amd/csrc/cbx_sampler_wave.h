@@ -83,16 +83,6 @@ struct WaveSmem {
 
 // ------------------------------------------------------------ wave helpers
 
-template <int CTRL, int RM>
-__device__ __forceinline__ int dpp_i(int old, int x) {
-    return __builtin_amdgcn_update_dpp(old, x, CTRL, RM, 0xf, false);
-}
-template <int CTRL, int RM>
-__device__ __forceinline__ float dpp_f(float old, float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
-                                                                 __builtin_bit_cast(int, x), CTRL,
-                                                                 RM, 0xf, false));
-}
 
 // Reductions and scans over the wave by DPP: row shifts 1, 2, 4, 8 inside
 // rows of 16 lanes, then row broadcasts of lanes 15 and 31.  Lane 63 ends
@@ -380,120 +370,6 @@ __device__ __forceinline__ void wave_radix_pass(const RowScores& rsc, int shift,
     __syncthreads();
 }
 
-// The binary32 running sum 0 + t_0 + t_1 + ... in order, where lane l holds
-// terms l*C .. l*C + C - 1 in t[0, C) (zeros past the last term), by sweeps
-// of the wave: a sweep adds each lane's terms, one after the other, to the
-// sum carried in from the lane below (a wave_shr:1 DPP operand; lane 0 starts
-// from 0), so after sweep s the sums of lanes 0..s are final.  These are the
-// reference's adds in the reference's order (NaN and infinities included);
-// a sweep costs C + 1 instructions.  nl: lanes holding terms (1..64).
-// Returns the final sum of lane nl - 1.  With THR, stops once a lane's final
-// sum reaches thr: `hit` is then the first term index whose running sum is
-// >= thr (otherwise -1).
-template <int C, bool THR, int CM>
-__device__ __forceinline__ float chain_sweeps(const float (&t)[CM], int nl, float thr, int& hit) {
-    static_assert(C <= CM, "terms per lane");
-    const int lane = threadIdx.x & 63;
-    hit = -1;
-    float s = 0.0f;
-    for (int sw = 0; sw < nl; ++sw) {
-        const float in = __builtin_bit_cast(
-            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x138, 0xf, 0xf, true));
-        float acc = __fadd_rn(in, t[0]);
-#pragma unroll
-        for (int k = 1; k < C; ++k) acc = __fadd_rn(acc, t[k]);
-        s = acc;
-        if (THR && ((__ballot(s >= thr) >> sw) & 1ull)) {
-            // lane sw holds the first crossing: walk its terms from its start
-            float w = in;
-            int first = C;
-#pragma unroll
-            for (int k = 0; k < C; ++k) {
-                w = __fadd_rn(w, t[k]);
-                first = (first == C && w >= thr) ? k : first;
-            }
-            hit = sw * C + __builtin_amdgcn_readlane(first, sw);
-            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), sw));
-        }
-    }
-    (void)lane;
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), nl - 1));
-}
-
-// The same sum 0 + t_0 + t_1 + ... (finite terms >= 0, t_0 > 0) with fewer
-// dependent steps, for long lanes.  While the running sum P = N*u stays in
-// one binade [2^b, 2^(b+1)) (u = 2^(b-23), N an integer), each add moves N by
-// an amount that depends on the term and on N's parity only (round to nearest
-// even).  A lane's whole run of terms is therefore a two-entry table
-// (increment from an even N, from an odd N), read off two real float chains
-// started at 2^b and 2^b + u; tables compose, so one DPP scan gives every
-// lane's exact starting N.  The first lane whose run leaves the binade then
-// adds its terms from that exact start as the reference does (any number of
-// binade changes inside), and the next round starts after it.  Lane 0 begins
-// from 0 directly.  Exactly the reference's adds' results.
-template <int C, int CM>
-__device__ __forceinline__ float chain_segments(const float (&t)[CM], int nl) {
-    static_assert(C <= CM, "terms per lane");
-    const int lane = threadIdx.x & 63;
-    constexpr int kSat = 1 << 24;
-    float a = 0.0f;
-#pragma unroll
-    for (int k = 0; k < C; ++k) a = __fadd_rn(a, t[k]);
-    float P = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
-    int lstart = 1;
-    while (lstart < nl) {
-        if (!(P >= 0x1p-100f)) {  // tiny sums (not seen for softmax terms): one add each
-            int unused;
-            return chain_sweeps<C, false>(t, nl, 0.0f, unused);
-        }
-        const uint32_t pb = __builtin_bit_cast(uint32_t, P);
-        const uint32_t bb = pb & 0x7f800000u;  // bits of 2^b
-        const float base = __builtin_bit_cast(float, bb);
-        const float lim = __builtin_bit_cast(float, bb + 0x00800000u);  // 2^(b+1)
-        const int N0 = (int)((pb & 0x7fffffu) | 0x800000u);            // P / u
-        const int p0 = N0 & 1;
-        float A0 = base, A1 = __builtin_bit_cast(float, bb + 1u);  // N = 2^23, 2^23 + 1
-#pragma unroll
-        for (int k = 0; k < C; ++k) {
-            A0 = __fadd_rn(A0, t[k]);
-            A1 = __fadd_rn(A1, t[k]);
-        }
-        // increments in units of u (same binade: the bit difference), or saturated
-        int d0 = A0 < lim ? (int)(__builtin_bit_cast(uint32_t, A0) - bb) : kSat;
-        int d1 = A1 < lim ? (int)(__builtin_bit_cast(uint32_t, A1) - bb) - 1 : kSat;
-        d0 = lane < lstart ? 0 : d0;  // lanes already summed: identity
-        d1 = lane < lstart ? 0 : d1;
-        // inclusive scan; composing an earlier table a with this lane's:
-        // from an even start the parity after a is a0 & 1, from an odd one
-        // (1 + a1) & 1
-        auto step = [&](int a0, int a1) {
-            const int n0 = a0 + ((a0 & 1) ? d1 : d0);
-            const int n1 = a1 + ((a1 & 1) ? d0 : d1);
-            d0 = n0;
-            d1 = n1;
-        };
-        step(dpp_i<0x111, 0xf>(0, d0), dpp_i<0x111, 0xf>(0, d1));  // row_shr:1
-        step(dpp_i<0x112, 0xf>(0, d0), dpp_i<0x112, 0xf>(0, d1));  // row_shr:2
-        step(dpp_i<0x114, 0xf>(0, d0), dpp_i<0x114, 0xf>(0, d1));  // row_shr:4
-        step(dpp_i<0x118, 0xf>(0, d0), dpp_i<0x118, 0xf>(0, d1));  // row_shr:8
-        step(dpp_i<0x142, 0xa>(0, d0), dpp_i<0x142, 0xa>(0, d1));  // row_bcast:15
-        step(dpp_i<0x143, 0xc>(0, d0), dpp_i<0x143, 0xc>(0, d1));  // row_bcast:31
-        const int x0 = dpp_i<0x138, 0xf>(0, d0), x1 = dpp_i<0x138, 0xf>(0, d1);  // exclusive
-        const int din = p0 ? x1 : x0, dout = p0 ? d1 : d0;
-        const uint64_t reach = __ballot(N0 + dout >= (1 << 24));
-        if (reach == 0) {
-            // no lane leaves the binade: the total is N0 + the last increment
-            return __builtin_bit_cast(float, pb + (uint32_t)__builtin_amdgcn_readlane(dout, 63));
-        }
-        const int L = (int)__builtin_ctzll(reach);
-        float w = __builtin_bit_cast(float, pb + (uint32_t)din);  // lane's exact start
-#pragma unroll
-        for (int k = 0; k < C; ++k) w = __fadd_rn(w, t[k]);
-        P = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), L));
-        lstart = L + 1;
-    }
-    return P;
-}
 
 // Calls f(std::integral_constant<int, C>) for the odd C in [c, CM] equal to
 // the run-time C (terms per lane are odd, so lane-strided LDS reads of the
@@ -1509,7 +1385,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     bool have_psum2 = false;
     auto exact_psum2 = [&]() {
         if (!have_psum2) {
-            psum2 = wave_chain_sum(sm.F(), n_final, 0.0f);
+            psum2 = wave_chain_sum(sm.F(), n_final, 0.0f, !bad);
             have_psum2 = true;
         }
         return psum2;
