@@ -8,8 +8,11 @@ U[0,1000], temperature U[0.5,1.2], top_k in {50,250,1000}, top_p 0.9,
 repetition penalty 1.2, the draw's uniform from the device Philox keyed
 (seed, stream, step).  Inputs are synthetic and resident in HBM before timing.
 Steps are issued `--steps-per-launch` at a time (one launch samples that many
-independent batches); logits rotate over slabs totalling > 2x the 256 MB
-Infinity Cache so every step reads its logits from HBM.
+independent batches; 256 by default, so that the fill at a launch's start and
+the drain at its end, about 18% of the time at 64 steps per launch, stay
+small); logits rotate over slabs totalling > 2x the 256 MB Infinity Cache so
+every step reads its logits from HBM.  `launch_shapes` in the output times
+the same kernel at other launch sizes over views of the same slabs.
 
 Prints one JSON line (rank 0) with the headline value, the roofline of the
 sampling kernel (algorithmic bytes / measured launch time vs 8 TB/s) and the
@@ -183,7 +186,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=16384)
     ap.add_argument("--warmup", type=int, default=1024)
-    ap.add_argument("--steps-per-launch", type=int, default=64)
+    ap.add_argument("--steps-per-launch", type=int, default=256)
     ap.add_argument("--slabs", type=int, default=2)
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
@@ -191,6 +194,9 @@ def main():
     ap.add_argument("--head-steps", type=int, default=200,
                     help="timed steps of the fused speech_head variant (0: skip)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--shape-steps", type=str, default="16,64",
+                    help="also time launches of these many steps (comma list, each dividing "
+                         "--steps-per-launch; empty: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run a plain device copy of this many MiB (3 times) so "
                          "a counter run can scale FETCH_SIZE / WRITE_SIZE by known bytes")
@@ -252,6 +258,36 @@ def main():
     bytes_step = algorithmic_bytes_per_step(hist_len)
     bytes_launch = bytes_step * S
     achieved = bytes_launch / (avg_launch_ms / 1e3) / 1e9
+
+    # the same kernel at smaller launch sizes, over views of the same slabs
+    shapes = {}
+    tokens2 = torch.empty_like(tokens)  # `tokens` keeps the last timed launch for the parity check
+    for s2 in [int(x) for x in args.shape_steps.split(",") if x.strip()]:
+        if s2 <= 0 or S % s2:
+            continue
+        per = S // s2
+        n2 = max(args.steps // s2, 2 * per)
+
+        def launch2(i):
+            sl = slabs[(i // per) % args.slabs][(i % per) * s2 * B:((i % per) + 1) * s2 * B]
+            sampler.sample_batch(sl, d_par, tokens2, n_steps=s2, history=d_hist,
+                                 history_len=d_hlen, draw_mode=mod.CBX_DRAW_PHILOX,
+                                 seed=philox_seed, step0=i * s2, max_survivors=1000)
+        for i in range(per):
+            launch2(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(n2):
+            launch2(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b)
+        tps = n2 * s2 * B / (ms / 1e3)
+        ach = bytes_step * s2 * n2 / (ms / 1e3) / 1e9
+        shapes["s%d" % s2] = {"steps_per_launch": s2, "tokens_per_s": round(tps, 1),
+                              "hbm_frac": round(ach / HBM_PEAK_GBS, 5),
+                              "ms_per_launch": round(ms / n2, 5)}
 
     # one launch per step: the decode-loop shape (launch latency included)
     single = None
@@ -347,6 +383,7 @@ def main():
                      "algorithmic_bytes_per_launch": bytes_launch,
                      "avg_launch_ms": round(avg_launch_ms, 5)},
         "cpu_baseline": cpu,
+        "launch_shapes": shapes,
         "single_launch_per_step": single,
         "parity_vs_oracle": parity,
         "fused_head": fused,
