@@ -102,6 +102,28 @@ class Head(ctypes.Structure):
     ]
 
 
+class HeadFile(ctypes.Structure):
+    """cbx_head_file (include/cbx_gguf.h): the speech_head of a T3 GGUF."""
+
+    _fields_ = [
+        ("n_vocab", ctypes.c_int32),
+        ("n_embd", ctypes.c_int32),
+        ("wtype", ctypes.c_int32),
+        ("has_bias", ctypes.c_int32),
+        ("speech_vocab_size", ctypes.c_int32),
+        ("start_speech_token", ctypes.c_int32),
+        ("stop_speech_token", ctypes.c_int32),
+        ("gguf_version", ctypes.c_int32),
+        ("weight_offset", ctypes.c_uint64),
+        ("weight_bytes", ctypes.c_uint64),
+        ("bias_offset", ctypes.c_uint64),
+        ("bias_bytes", ctypes.c_uint64),
+    ]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 class CbxError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"cbx error {code}: {msg}")
@@ -155,6 +177,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_debug_seqsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
     lib.cbx_debug_chainsum.restype = ctypes.c_int
     lib.cbx_debug_chainsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
+    lib.cbx_gguf_read_head.restype = ctypes.c_int
+    lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
+    lib.cbx_gguf_load_head.restype = ctypes.c_int
+    lib.cbx_gguf_load_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile), vp, vp]
     lib.cbx_last_error.restype = ctypes.c_char_p
     lib.cbx_last_error.argtypes = []
     _lib = lib
@@ -173,6 +199,27 @@ def _ptr(t):
 def _stream_ptr():
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def read_head_gguf(path) -> HeadFile:
+    """cbx_gguf_read_head: parse the speech_head of a T3 GGUF (host only)."""
+    lib = load_library()
+    info = HeadFile()
+    _check(lib.cbx_gguf_read_head(os.fsencode(path), ctypes.byref(info)))
+    return info
+
+
+def load_head_gguf(path, device="cuda"):
+    """cbx_gguf_load_head into new device tensors: returns (info, weights as
+    uint8 bytes of the wtype layout, bias float32 or None), ready for
+    Sampler.head."""
+    import torch
+    info = read_head_gguf(path)
+    w = torch.empty(int(info.weight_bytes), dtype=torch.uint8, device=device)
+    b = torch.empty(info.n_vocab, dtype=torch.float32, device=device) if info.has_bias else None
+    _check(_lib.cbx_gguf_load_head(os.fsencode(path), ctypes.byref(info),
+                                   ctypes.c_void_p(w.data_ptr()), _ptr(b)))
+    return info, w, b
 
 
 def params_tensor(rows, device="cuda"):

@@ -110,6 +110,16 @@ bool params_ok(const cbx_params* p) {
 
 }  // namespace
 
+namespace cbx {
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+}  // namespace cbx
+
 extern "C" {
 
 const char* cbx_last_error(void) { return g_err; }

@@ -8,6 +8,9 @@
 
 namespace cbx {
 
+// Record the message cbx_last_error() returns on this thread; returns code.
+int set_error(int code, const char* fmt, ...);
+
 // Device-side view of one cbx_batch launch (all pointers device addresses).
 struct KernelArgs {
     int32_t n_rows, n_vocab, n_steps, stop_token;

@@ -93,6 +93,37 @@ def test_head_logits_against_f64(cbx, torch_cuda, case):
         assert np.all(got[:, V:] == -7.0), "stores past n_vocab"
 
 
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+def test_head_from_gguf(cbx, torch_cuda, tmp_path, wtype):
+    """cbx_gguf_read_head + cbx_gguf_load_head (csrc/cbx_gguf.cpp) put the
+    file's speech_head and bias in device memory byte for byte, and the
+    projection of the loaded head matches the oracle's."""
+    import gguf_writer as G
+    mod, s = cbx
+    torch = torch_cuda
+    V, K, R = 700, 256, 24
+    rng = np.random.default_rng(40 + wtype)
+    blocks, bias, h = _problem(rng, V, K, R, wtype)
+    gt = {O.WTYPE_Q4_0: G.GGML_Q4_0, O.WTYPE_Q8_0: G.GGML_Q8_0, O.WTYPE_F16: G.GGML_F16}[wtype]
+    data, _, _ = G.t3_head_file(blocks, gt, K, bias, stop=V - 1, start=V - 2)
+    path = tmp_path / "head.gguf"
+    path.write_bytes(data)
+    say(f"gguf head wtype={wtype} V={V} K={K}")
+    info, dW, db = mod.load_head_gguf(str(path))
+    assert (info.n_vocab, info.n_embd, info.wtype, info.stop_speech_token) == (V, K, wtype, V - 1)
+    assert dW.cpu().numpy().tobytes() == np.ascontiguousarray(blocks).tobytes()
+    assert np.array_equal(db.cpu().numpy(), bias)
+    dh = torch.from_numpy(h).cuda()
+    out = torch.full((R, V), -7.0, dtype=torch.float32, device="cuda")
+    head = mod.Sampler.head(dW, info.wtype, info.n_embd, dh, out, bias=db)
+    s.head_logits(head, R, info.n_vocab, V)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = O.head_f64(blocks, wtype, bias, h, V, K)
+    tol = 1e-5 * _bound(blocks, wtype, h, K) + 1e-6
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= tol)
+
+
 def test_head_without_bias(cbx, torch_cuda):
     rng = np.random.default_rng(5)
     blocks, _, h = _problem(rng, 500, 256, 20, O.WTYPE_Q4_0)
