@@ -124,6 +124,14 @@ class HeadFile(ctypes.Structure):
         return {f: getattr(self, f) for f, _ in self._fields_}
 
 
+class Retry(ctypes.Structure):
+    """cbx_retry (include/cbx_retry.h): the early-stop retry policy of one segment."""
+
+    _fields_ = [(f, ctypes.c_int32) for f in (
+        "min_tokens", "max_retries", "attempt", "done", "best_attempt", "best_len",
+        "kept_attempt", "kept_len")]
+
+
 class CbxError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"cbx error {code}: {msg}")
@@ -181,6 +189,12 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
     lib.cbx_gguf_load_head.restype = ctypes.c_int
     lib.cbx_gguf_load_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile), vp, vp]
+    lib.cbx_retry_init.restype = ctypes.c_int
+    lib.cbx_retry_init.argtypes = [ctypes.POINTER(Retry), i32]
+    lib.cbx_retry_stream_id.restype = u64
+    lib.cbx_retry_stream_id.argtypes = [u64, i32]
+    lib.cbx_retry_record.restype = ctypes.c_int
+    lib.cbx_retry_record.argtypes = [ctypes.POINTER(Retry), i32, i32]
     lib.cbx_last_error.restype = ctypes.c_char_p
     lib.cbx_last_error.argtypes = []
     _lib = lib
@@ -220,6 +234,26 @@ def load_head_gguf(path, device="cuda"):
     _check(_lib.cbx_gguf_load_head(os.fsencode(path), ctypes.byref(info),
                                    ctypes.c_void_p(w.data_ptr()), _ptr(b)))
     return info, w, b
+
+
+def retry_start(n_text_tokens) -> Retry:
+    """cbx_retry_init: the retry policy for a segment of n_text_tokens."""
+    r = Retry()
+    _check(load_library().cbx_retry_init(ctypes.byref(r), n_text_tokens))
+    return r
+
+
+def retry_record(r: Retry, n_tokens, stopped_by_stop_token) -> bool:
+    """cbx_retry_record: True if another attempt should run (r.attempt)."""
+    rc = _lib.cbx_retry_record(ctypes.byref(r), n_tokens, 1 if stopped_by_stop_token else 0)
+    if rc < 0:
+        _check(rc)
+    return rc == 1
+
+
+def retry_stream_id(stream, attempt) -> int:
+    """cbx_retry_stream_id: the Philox stream id of a stream's attempt."""
+    return int(load_library().cbx_retry_stream_id(stream, attempt))
 
 
 def params_tensor(rows, device="cuda"):
