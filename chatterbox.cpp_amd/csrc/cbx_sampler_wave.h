@@ -113,6 +113,15 @@ __device__ __forceinline__ float wave_max_dpp(float x) {
     x = fmaxf(x, dpp_f<0x143, 0xc>(kNegInf, x));
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
+__device__ __forceinline__ float wave_sum_f_dpp(float x) {
+    x += dpp_f<0x111, 0xf>(0.0f, x);
+    x += dpp_f<0x112, 0xf>(0.0f, x);
+    x += dpp_f<0x114, 0xf>(0.0f, x);
+    x += dpp_f<0x118, 0xf>(0.0f, x);
+    x += dpp_f<0x142, 0xa>(0.0f, x);
+    x += dpp_f<0x143, 0xc>(0.0f, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
 __device__ __forceinline__ float wave_min_dpp(float x) {
     x = fminf(x, dpp_f<0x111, 0xf>(kPosInf, x));
     x = fminf(x, dpp_f<0x112, 0xf>(kPosInf, x));
@@ -511,6 +520,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // others need 4 operations per score and no predicate.
     const bool plain = !rsc.masked_ids && !rsc.fstop;
     float lo = kPosInf, hi = kNegInf;
+    float msum = 0.0f;  // this lane's 4 scores of vector 0 (padding-free when JT >= 1)
     bool bad = false, neg_inf = false;  // NaN/+inf seen; -inf among unmasked scores
     if (!plain) {
         if (rsc.masked_ids)
@@ -538,6 +548,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         float acc = 0.0f;
         const int Vm = fresh(V);
         auto pass = [&](auto scaled) {
+            msum = 0.0f;
 #pragma unroll
             for (int j = 0; j < Q; ++j) {
                 float w[4];
@@ -547,6 +558,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     if (decltype(scaled)::value) w[c] = __fmul_rn(w[c], rsc.inv_t);
                 }
                 if (j < JT) {
+                    if (j == 0) msum = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
                     acc = __fmaf_rn(w[0], w[1], acc);
                     acc = __fmaf_rn(w[2], w[3], acc);
                     // running value first: one 3-input min / max per pair
@@ -620,28 +632,41 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         // a float is an integer: bin(v) = bits(y) - bits(2^23) is
         // non-decreasing in v and costs two operations per score.  The
         // V..256Q padding (-inf) is raised to bin 0 and taken off its count.
-        const float bs = __fdiv_rn((float)(kWaveBins - 4), range);
-        const float c0 = __fsub_rn(0x1p23f + 2.0f, __fmul_rn(lo, bs));
-        const bool bins_fit = __fmaf_rn(lo, bs, c0) >= 0x1p23f &&
+        // The bins cover [hlo, hi]: for k < V/4 the (k+1)-th largest score
+        // lies, for any ordinary row, above the mean of the 256 scores of
+        // vector 0, so the bins start there (half the atomics, bins twice as
+        // fine).  Scores below hlo land in bins 0..1 (some, within two bins
+        // of hlo) or in a dump word of their own lane below the histogram
+        // (y below 2^23, where floats step by 1/2: y = 2^23 - (l + 1)/2 has
+        // bits(y) - bits(2^23) = -(l + 1)), as does the padding (-inf).  So
+        // the counts of bins >= 2 are exact, and a row whose rank-k bin is
+        // below 2 (or holding fewer than k + 1 binned scores) takes the
+        // full-range pass further down.
+        const bool partial = JT >= 1 && 4 * k < V && !bad && !neg_inf;
+        const float hlo =
+            partial ? fmaxf(lo, __fmul_rn(wave_sum_f_dpp(msum), 1.0f / 256.0f)) : lo;
+        const float hrange = __fsub_rn(hi, hlo);
+        const float bs = __fdiv_rn((float)(kWaveBins - 4), hrange);
+        const float c0 = __fsub_rn(0x1p23f + 2.0f, __fmul_rn(hlo, bs));
+        const bool bins_fit = __fmaf_rn(hlo, bs, c0) >= 0x1p23f &&
                               __fmaf_rn(hi, bs, c0) <= 0x1p23f + (float)(kWaveBins - 1);
-        if (!bad && !neg_inf && range > 0.0f && bs < kPosInf && bins_fit) {
-            uint32_t* hist = sm.khist();
+        if (!bad && !neg_inf && hrange > 0.0f && bs < kPosInf && bins_fit) {
+            uint32_t* hist = sm.khist() + 64;  // words -64..-1: the lanes' dump words
+            const float dump_y = 0x1p23f - 0.5f * (float)(lane + 1);
 #pragma unroll
             for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
             __syncthreads();
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                float y = __fmaf_rn(s[e], bs, c0);
-                if ((e >> 2) >= JT) y = fmaxf(y, 0x1p23f);  // padding: bin 0
-                atomicAdd(&hist[__builtin_bit_cast(uint32_t, y) - 0x4B000000u], 1u);
+                const float y = fmaxf(__fmaf_rn(s[e], bs, c0), dump_y);
+                atomicAdd(&hist[(int)(__builtin_bit_cast(uint32_t, y) - 0x4B000000u)], 1u);
             }
             __syncthreads();
             CBX_STAMP(16);
             // Lane l owns the 16 bins kWaveBins-1-16l .. kWaveBins-16-16l
             // (descending scores), contiguous in LDS: their total from four
-            // 16-byte reads.  The padding sits in bin 0 (lane 63).
+            // 16-byte reads.
             static_assert(kWaveBins == 1024, "16 bins per lane");
-            const uint32_t pad = (uint32_t)(256 * Q - V);
             int tot;
             {
                 const uint4* h4 = reinterpret_cast<const uint4*>(hist) + (kWaveBins / 4 - 4 - 4 * lane);
@@ -651,21 +676,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     const uint4 w = h4[i];
                     sum += (w.x + w.y) + (w.z + w.w);
                 }
-                tot = (int)(sum - (lane == 63 ? pad : 0u));
+                tot = (int)sum;
             }
             int n_fin;
             const int excl = wave_excl_scan_i(tot, n_fin);
             if (n_fin <= k) {
-                thr = kNegInf;  // at most k finite scores: nothing is removed
-                above = n_fin;
-                done = true;
+                if (!partial) {
+                    thr = kNegInf;  // at most k finite scores: nothing is removed
+                    above = n_fin;
+                    done = true;
+                }  // else fewer than k + 1 scores above hlo: the full-range pass
             } else {
                 // the lane whose bins hold rank k; lanes 0..15 take its bins
                 // (q-th largest first) and scan their counts
                 const int L = __builtin_ctzll(__ballot(excl <= k && k < excl + tot));
                 const int exclL = __builtin_amdgcn_readlane(excl, L);
                 const int bq = kWaveBins - 1 - (16 * L + (lane & 15));
-                const int cq = (int)(hist[bq] - (bq == 0 ? pad : 0u));
+                const int cq = (int)hist[bq];
                 int inc = cq;  // inclusive scan inside lanes 0..15 (row 0)
                 inc += dpp_i<0x111, 0xf>(0, inc);
                 inc += dpp_i<0x112, 0xf>(0, inc);
@@ -695,7 +722,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 };
                 CBX_STAMP(17);
                 float B0 = kNegInf, B1 = kPosInf;
-                const bool have_b = bsel >= 1 && nsel <= kWaveCand && boundary(bsel, B0) &&
+                const bool have_b = bsel >= (partial ? 2 : 1) && nsel <= kWaveCand &&
+                                    boundary(bsel, B0) &&
                                     (bsel == kWaveBins - 1 || boundary(bsel + 1, B1));
                 __syncthreads();  // histogram reads done: the candidates reuse it
                 CBX_STAMP(18);

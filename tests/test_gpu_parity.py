@@ -403,6 +403,17 @@ EDGE_CASES = [
     # -inf logits among finite ones (10% of the ids)
     ("some_neg_inf", 6563, dict(top_k=250, top_p=0.9, temp=1.1, repeat_penalty=1.2),
      lambda V, r: np.where(r.random(V) < 0.1, -np.inf, r.standard_normal(V) * 3).astype(F32), 0.6),
+    # the one-wave top-k histogram starts at the mean of ids 0..255: here that
+    # mean (100.004) is above every score but one, so fewer than k + 1 scores
+    # are binned and the full-range pass decides
+    ("topk_mean_above_rank", 6563, dict(top_k=1000, top_p=0.9, temp=1.0, repeat_penalty=1.2),
+     lambda V, r: np.concatenate([np.full(255, 100.0), [101.0],
+                                  r.standard_normal(V - 256)]).astype(F32), 0.3),
+    # ... and here (mean 3.906) the 201st largest score, 3.85 held 300 times,
+    # lies within the two bins below the mean, whose counts are partial
+    ("topk_rank_below_mean_bins", 6563, dict(top_k=200, top_p=0.9, temp=1.0, repeat_penalty=1.2),
+     lambda V, r: np.concatenate([np.full(10, 100.0), np.zeros(246), np.full(300, 3.85),
+                                  -5.0 - r.random(V - 556)]).astype(F32), 0.7),
     # 150 equal survivors in one value bin: the sort falls back to the bitonic network
     ("crowded_bin", 600, dict(top_k=500, top_p=0.9, temp=1.0, repeat_penalty=1.2),
      lambda V, r: np.concatenate([np.full(150, 3.0), np.full(200, 2.0), [10.0],
