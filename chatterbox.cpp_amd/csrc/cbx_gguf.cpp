@@ -225,10 +225,9 @@ int parse(const char* path, cbx_head_file* out) {
     uint64_t boff = 0, bbytes = 0;
     if (bias.found) {
         if (bias.type != kTF32) return invalid(path, "speech_head_bias is not F32");
-        uint64_t elems = 1;
-        for (uint32_t d = 0; d < bias.n_dims; ++d) elems *= bias.ne[d] ? bias.ne[d] : 0;
-        if (bias.ne[0] != n_vocab || elems != n_vocab)
-            return invalid(path, "speech_head_bias does not hold n_vocab values");
+        bool column = bias.ne[0] == n_vocab;  // [n_vocab] or [n_vocab, 1, ...]
+        for (uint32_t d = 1; d < bias.n_dims; ++d) column = column && bias.ne[d] == 1;
+        if (!column) return invalid(path, "speech_head_bias does not hold n_vocab values");
         if (bias.offset % alignment) return invalid(path, "speech_head_bias data is not aligned");
         bbytes = 4 * n_vocab;
         if (bias.offset > r.size - data0 || bbytes > r.size - data0 - bias.offset)
@@ -267,7 +266,8 @@ int copy_to_device(const char* path, uint64_t off, uint64_t n, void* dst) {
         return cbx::set_error(CBX_ERR_NOMEM, "cbx_gguf_load_head: host buffer");
     }
     int rc = CBX_OK;
-    if (fseeko(f, (off_t)off, SEEK_SET) != 0) rc = CBX_ERR_INVALID;
+    if (fseeko(f, (off_t)off, SEEK_SET) != 0)
+        rc = cbx::set_error(CBX_ERR_INVALID, "cbx_gguf_load_head: %s: cannot seek", path);
     for (uint64_t done = 0; rc == CBX_OK && done < n;) {
         const size_t c = (size_t)(n - done < buf.size() ? n - done : buf.size());
         if (fread(buf.data(), 1, c, f) != c) {
@@ -282,7 +282,6 @@ int copy_to_device(const char* path, uint64_t off, uint64_t n, void* dst) {
         done += c;
     }
     fclose(f);
-    if (rc == CBX_ERR_INVALID) return cbx::set_error(rc, "cbx_gguf_load_head: %s: cannot read", path);
     return rc;
 }
 

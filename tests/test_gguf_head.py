@@ -141,6 +141,11 @@ def test_rejects_damaged_and_mismatched_files(mod, tmp_path):
                                       blocks.tobytes()),
                                      ("chatterbox/speech_head_bias", (7,), G.GGML_F32,
                                       b"\0" * 28)])[0], CBX_ERR_INVALID),
+        "bias of 2 x 2^63+1": (G.build([], [("chatterbox/speech_head", (64, 8), G.GGML_Q4_0,
+                                             blocks.tobytes()),
+                                            ("chatterbox/speech_head_bias",
+                                             (8, (1 << 63) + 1, (1 << 63) + 1), G.GGML_F32,
+                                             b"\0" * 32)])[0], CBX_ERR_INVALID),
         "bias F16": (G.build([], [("chatterbox/speech_head", (64, 8), G.GGML_Q4_0,
                                    blocks.tobytes()),
                                   ("chatterbox/speech_head_bias", (8,), G.GGML_F16,
