@@ -38,35 +38,36 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t hb) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
 }
 
-// Raw bytes of the 8 weights k = 8g .. 8g + 7 of block kb of vocab row v:
-// F16 four dwords; Q4_0 / Q8_0 the fp16 scale in q[4] and the 8 bytes of
-// nibbles or int8 in q[0..1].  Blocks are 18 or 34 bytes, so only 2-byte
-// alignment holds: the bytes come from dword-aligned loads (the dword holding
-// the scale, three dwords holding the 8 bytes) shifted into place.
+// Raw bytes of the 8 weights k = 8g .. 8g + 7 of one block of a vocab row,
+// from the row's chunk staged in LDS: F16 four dwords; Q4_0 / Q8_0 the fp16
+// scale in q[4] and the 8 bytes of nibbles or int8 in q[0..1].  Blocks are
+// 18 or 34 bytes, so only 2-byte alignment holds: `off` (the block's byte
+// offset in the staged row) is read as dwords shifted into place.
 template <int WT>
-__device__ __forceinline__ void load_w(const __amdgpu_buffer_rsrc_t& rw, int v, int kb, int g,
-                                       int n_embd, uint32_t* q) {
+__device__ __forceinline__ void lds_w(const uint32_t* srow, int off, int g, uint32_t* q) {
     if constexpr (WT == CBX_WTYPE_F16) {
-        const uint32_t off = (uint32_t)(((int64_t)v * n_embd + kb * 32 + 8 * g) * 2);
-        const auto u = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
-        q[0] = u[0]; q[1] = u[1]; q[2] = u[2]; q[3] = u[3];
+        const int b = off + 16 * g;
+        const uint32_t* p = srow + (b >> 2);
+        const uint32_t sh = 8u * (uint32_t)(b & 3);
+        const uint32_t t0 = p[0], t1 = p[1], t2 = p[2], t3 = p[3], t4 = p[4];
+        q[0] = __builtin_amdgcn_alignbit(t1, t0, sh);
+        q[1] = __builtin_amdgcn_alignbit(t2, t1, sh);
+        q[2] = __builtin_amdgcn_alignbit(t3, t2, sh);
+        q[3] = __builtin_amdgcn_alignbit(t4, t3, sh);
     } else {
-        constexpr int BB = WT == CBX_WTYPE_Q4_0 ? 18 : 34;  // bytes per block
-        const uint32_t blk = (uint32_t)(((int64_t)v * (n_embd / 32) + kb) * BB);
-        // Q4_0: bytes 8(g&1) .. +7 of the nibbles; Q8_0: int8 values 8g .. 8g + 7
-        const uint32_t qoff = blk + 2 + (WT == CBX_WTYPE_Q4_0 ? 8 * (g & 1) : 8 * g);
-        const uint32_t dw = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, blk & ~3u, 0, 0);
-        q[4] = (dw >> (8 * (blk & 3u))) & 0xffffu;
-        const auto t = __builtin_amdgcn_raw_buffer_load_b96(rw, qoff & ~3u, 0, 0);
-        const uint32_t sh = 8 * (qoff & 3u);
-        q[0] = __builtin_amdgcn_alignbit(t[1], t[0], sh);
-        q[1] = __builtin_amdgcn_alignbit(t[2], t[1], sh);
+        q[4] = (srow[off >> 2] >> (8 * (off & 3))) & 0xffffu;
+        const int qoff = off + 2 + (WT == CBX_WTYPE_Q4_0 ? 8 * (g & 1) : 8 * g);
+        const uint32_t* p = srow + (qoff >> 2);
+        const uint32_t sh = 8u * (uint32_t)(qoff & 3);
+        const uint32_t t0 = p[0], t1 = p[1], t2 = p[2];
+        q[0] = __builtin_amdgcn_alignbit(t1, t0, sh);
+        q[1] = __builtin_amdgcn_alignbit(t2, t1, sh);
     }
 }
 
 __device__ __forceinline__ float ubyte(uint32_t x, int i) { return (float)((x >> (8 * i)) & 0xffu); }
 
-// The fp32 weights the format defines, from load_w's bytes.  Q4_0: nibble
+// The fp32 weights the format defines, from lds_w's bytes.  Q4_0: nibble
 // n = q + 8 and w = (n - 8) d = fma(n, d, -8d), exact (n d and -8d are exact
 // and their sum is representable); Q8_0: u = q + 128 (sign bit flipped) and
 // w = fma(u, d, -128d), exact for the same reason.
@@ -113,6 +114,16 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
                                                      int64_t ld_hidden, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
                                                      int n_embd) {
+    constexpr int BB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
+    // Weights are staged per wave in chunks of CB blocks: for each of the 32
+    // vocab rows the chunk's CB * BB bytes are contiguous, so whole-row dword
+    // loads touch two or three lines each (the per-block loads of the 18-byte
+    // pieces of 16 rows 576 bytes apart touched up to 32 lines each, and the
+    // texture-address path was the measured limit).  RSW dwords per staged
+    // row: the bytes from the dword holding the first, plus one.
+    constexpr int CB = WT == CBX_WTYPE_F16 ? 4 : 8;
+    constexpr int RSW = (CB * BB + 6) / 4 + 1;
+    __shared__ uint32_t stage[KS][32 * RSW];
     __shared__ f4 part[KS - 1][2 * NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, g = lane >> 4;
@@ -156,8 +167,6 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     uint32_t qa[5], qb[5];
     f4 h0[NT], h1[NT];
     auto load = [&](int kb) {
-        load_w<WT>(rw, va_c, kb, g, n_embd, qa);
-        load_w<WT>(rw, vb_c, kb, g, n_embd, qb);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int T = blockIdx.y * NT + t;
@@ -168,8 +177,39 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
         }
     };
     if (kb0 < kb1) load(kb0);
+    uint32_t* const sw = stage[wave];
 #pragma unroll 1
-    for (int kb = kb0; kb < kb1; ++kb) {
+    for (int kbc = kb0; kbc < kb1; kbc += CB) {
+        const int nb = min(CB, kb1 - kbc);
+        // stage rows v0 .. v0 + 31 (rows past the table read zeros): the
+        // dwords from the one holding the chunk's first byte
+        const int ndw = (3 + nb * BB + 3) >> 2;  // <= RSW - 1
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        {
+            int rr = lane / ndw, d = lane % ndw;
+            const int q64 = 64 / ndw, r64 = 64 % ndw;
+            for (int i = lane; i < 32 * ndw; i += 64) {
+                const int v = v0 + rr < n_vocab ? v0 + rr : n_vocab;
+                const uint32_t a0 = (uint32_t)(((int64_t)v * nball + kbc) * BB) & ~3u;
+                sw[rr * RSW + d] =
+                    (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, a0 + 4u * (uint32_t)d, 0, 0);
+                d += r64;
+                rr += q64;
+                if (d >= ndw) {
+                    d -= ndw;
+                    ++rr;
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const int sha = (int)((((int64_t)va_c * nball + kbc) * BB) & 3);
+        const int shb = (int)((((int64_t)vb_c * nball + kbc) * BB) & 3);
+#pragma unroll 1
+    for (int kb = kbc; kb < kbc + nb; ++kb) {
+        lds_w<WT>(sw + m * RSW, sha + (kb - kbc) * BB, g, qa);
+        lds_w<WT>(sw + (16 + m) * RSW, shb + (kb - kbc) * BB, g, qb);
         float wa[8], wb[8];
         dequant<WT>(qa, g, wa);
         dequant<WT>(qb, g, wb);
@@ -191,6 +231,7 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
                 acc1[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb[s], hv[t][s], acc1[t], 0, 0, 0);
             }
         }
+    }
     }
     // the partial tiles of waves 1 .. KS-1 join wave 0's in wave order
     if (wave > 0) {
