@@ -3,20 +3,27 @@
 streams, V=6563 (GPT-2-medium T3 Turbo speech vocabulary), on one MI355X.
 
 A step is one pass of the sampler over one batch: 256 independent streams,
-each row 6563 fp32 logits ~N(0,3) with 5 spikes at U[6,12], history length
-U[0,1000], temperature U[0.5,1.2], top_k in {50,250,1000}, top_p 0.9,
-repetition penalty 1.2, the draw's uniform from the device Philox keyed
-(seed, stream, step).  Inputs are synthetic and resident in HBM before timing.
-Steps are issued `--steps-per-launch` at a time (one launch samples that many
-independent batches; 256 by default, so that the fill at a launch's start and
-the drain at its end, about 18% of the time at 64 steps per launch, stay
-small); logits rotate over slabs totalling > 2x the 256 MB Infinity Cache so
-every step reads its logits from HBM.  `launch_shapes` in the output times
-the same kernel at other launch sizes over views of the same slabs.
+each row 6563 fp32 logits ~N(0,3) with 5 spikes at U[6,12] in random places
+of every row, history length U[0,1000], temperature U[0.5,1.2], top_k in
+{50,250,1000}, top_p 0.9, repetition penalty 1.2, the draw's uniform from the
+device Philox keyed (seed, stream, step).  Inputs are synthetic and resident
+in HBM before timing.  Steps are issued `--steps-per-launch` at a time (one
+launch samples that many independent batches; 256 by default, so that the
+fill at a launch's start and the drain at its end stay small); `--steps` and
+`--warmup` are minimums, rounded up to whole launches (at least 16 timed and
+4 untimed), and the line reports the steps actually timed.  Logits rotate over slabs totalling > 2x the 256 MB
+Infinity Cache so every step reads its logits from HBM.
 
-Prints one JSON line (rank 0) with the headline value, the roofline of the
-sampling kernel (algorithmic bytes / measured launch time vs 8 TB/s) and the
-CPU baseline (the oracle, the reference's algorithm in C++, on host cores).
+Prints one JSON line with the headline value, the roofline of the sampling
+kernel (algorithmic bytes / measured launch time vs 8 TB/s), the CPU baseline
+(the oracle, the reference's algorithm in C++, on host cores) and the other
+measured shapes:
+  launch_shapes           the same kernel at 16 and 64 steps per launch
+  single_launch_per_step  B=256, one launch per step (the decode-loop shape)
+  configs                 single stream (B=1, V=6563, 500 steps), CFG pair
+                          (B=1, V=8194, history growing to 1000), masked
+                          stress (B=1024, V=32768, 20% allowed ids)
+  fused_head              Q4_0 speech_head + sampler, B=64 CFG pairs
 """
 import argparse
 import json
@@ -34,20 +41,59 @@ B = 256
 HIST_MAX = 1000
 HBM_PEAK_GBS = 8000.0
 SEED = 0x5EED3
+# The host cores this one-GPU job may use: the host's CPUs are shared among
+# its GPUs' jobs, 16 each.
+CPU_SHARE = 16
+
+
+# Fewest launches timed (and run before timing): one cold launch of 256
+# steps reads about 7% slow, 16 (half a millisecond each) agree with 64 to
+# within the run-to-run spread.
+MIN_TIMED_LAUNCHES = 16
+MIN_WARMUP_LAUNCHES = 4
+
+
+def launches_for(steps, warmup, steps_per_launch):
+    """Whole launches covering at least `steps` timed and `warmup` untimed
+    steps, and at least MIN_TIMED_LAUNCHES / MIN_WARMUP_LAUNCHES of them:
+    (timed launches, warmup launches)."""
+    if steps_per_launch < 1:
+        raise ValueError("--steps-per-launch must be >= 1")
+    n = max(MIN_TIMED_LAUNCHES, -(-max(0, steps) // steps_per_launch))
+    nw = max(MIN_WARMUP_LAUNCHES, -(-max(0, warmup) // steps_per_launch))
+    return n, nw
+
+
+def host_threads():
+    """(threads used by the CPU baseline, CPUs visible to this process)."""
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        visible = os.cpu_count() or 1
+    return max(1, min(visible, CPU_SHARE)), visible
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 def make_inputs(torch, steps_per_launch, n_slabs, dev):
     g = torch.Generator(device=dev)
     g.manual_seed(SEED)
     slabs = []
+    rows = steps_per_launch * B
     for _ in range(n_slabs):
-        x = torch.randn((steps_per_launch * B, V), generator=g, device=dev) * 3.0
-        pos = torch.stack([torch.randperm(V, generator=g, device=dev)[:5]
-                           for _ in range(8)])  # 8 spike patterns, reused cyclically
-        rows = torch.arange(steps_per_launch * B, device=dev)
-        pat = pos[rows % 8]
-        heights = torch.rand((steps_per_launch * B, 5), generator=g, device=dev) * 6.0 + 6.0
-        x.scatter_(1, pat, heights)
+        x = torch.randn((rows, V), generator=g, device=dev) * 3.0
+        # 5 spikes per row at random ids (a repeated id keeps one spike)
+        pos = torch.randint(0, V, (rows, 5), generator=g, device=dev)
+        heights = torch.rand((rows, 5), generator=g, device=dev) * 6.0 + 6.0
+        x.scatter_(1, pos, heights)
         slabs.append(x.contiguous())
     rng = np.random.default_rng(SEED)
     hist = rng.integers(0, V, size=(B, HIST_MAX)).astype(np.int32)
@@ -75,43 +121,93 @@ def read_traffic(steps_per_launch):
     return None
 
 
-def cpu_baseline(hist, hist_len, params, logits_host, u, gpu_tokens, seconds_1t, seconds_mt):
-    import oracle_lib as O
-    plist = [O.OParams(p["top_k"], p["top_p"], p["temp"], p["repeat_penalty"], p["min_p"],
-                       p["cfg_weight"]) for p in params]
+def oparams(O, p):
+    return O.OParams(p["top_k"], p["top_p"], p["temp"], p["repeat_penalty"], p["min_p"],
+                     p["cfg_weight"])
+
+
+def classify_mismatches(O, rows):
+    """rows: (logits, history, params, u, gpu_token, ref_token[, uncond]) of
+    every row whose tokens differ.  Returns the counts by class: a
+    filter-boundary tie (the oracle flags equal scores across the top-p
+    cutoff), a draw-boundary tie (u within 1e-6 of a cumulative boundary of
+    the oracle's probabilities) or a hard mismatch."""
+    import parity
+    out = {"hard": 0, "filter_ties": 0, "draw_ties": 0}
+    for r in rows:
+        lg, h, p, u, _, _ = r[:6]
+        un = r[6] if len(r) > 6 else None
+        _, info, probs, _ = O.sample_row(lg, h, oparams(O, p), u, uncond=un, want_probs=True)
+        if info & O.INFO_TOPP_TIE:
+            out["filter_ties"] += 1
+        elif parity._near_cdf_boundary(probs, u):
+            out["draw_ties"] += 1
+        else:
+            out["hard"] += 1
+    return out
+
+
+def cpu_baseline(O, hist, hist_len, params, logits_host, u, gpu_tokens, seconds_1t, seconds_mt,
+                 threads):
+    plist = [oparams(O, p) for p in params]
     n_steps = logits_host.shape[0] // B
     out = {}
+    bad_rows = {}
+    checked = set()
+
+    def check(s0, k, toks):
+        want = gpu_tokens[s0 * B:(s0 + k) * B]
+        checked.update(range(s0, s0 + k))
+        for i in np.nonzero(toks != want)[0]:
+            r = s0 * B + int(i)
+            q = r % B
+            bad_rows[r] = (logits_host[r], hist[q][:hist_len[q]], params[q], u[r],
+                           int(want[i]), int(toks[i]))
+
     # one thread: the reference sampler is single-threaded
-    rows = 0
-    spent = 0.0
-    mism = 0
-    s = 0
+    rows, spent, s = 0, 0.0, 0
     while spent < seconds_1t and s < n_steps:
         lg = logits_host[s * B:(s + 1) * B]
         toks, _, secs = O.sample_batch(lg, plist, u[s * B:(s + 1) * B], hist, hist_len,
                                        n_threads=1)
-        mism += int(np.sum(toks != gpu_tokens[s * B:(s + 1) * B]))
+        check(s, 1, toks)
         rows += B
         spent += secs
         s += 1
     out["1t"] = (rows / spent, rows)
-    cores = min(os.cpu_count() or 1, 16)
-    rows = 0
-    spent = 0.0
-    s = 0
-    while spent < seconds_mt and s < n_steps:
-        k = min(4, n_steps - s)
+    # all threads, over the same steps again from the first (and around
+    # again while the time lasts)
+    rows, spent, s = 0, 0.0, 0
+    while spent < seconds_mt:
+        s %= n_steps
+        k = min(16, n_steps - s)
         lg = logits_host[s * B:(s + k) * B]
         toks, _, secs = O.sample_batch(lg, plist * k, u[s * B:(s + k) * B],
                                        np.tile(hist, (k, 1)), np.tile(hist_len, k),
-                                       n_threads=cores)
-        mism += int(np.sum(toks != gpu_tokens[s * B:(s + k) * B]))
+                                       n_threads=threads)
+        check(s, k, toks)
         rows += k * B
         spent += secs
         s += k
-    out["mt"] = (rows / spent, rows, cores)
-    out["mismatches"] = mism
+    out["mt"] = (rows / spent, rows) if rows else (0.0, 0)
+    out["rows_checked"] = len(checked) * B
+    out["mismatch"] = len(bad_rows)
+    out["classes"] = classify_mismatches(O, list(bad_rows.values()))
     return out
+
+
+def timed(torch, stream, fn, n, warm=3):
+    """Mean ms per call of fn(i) over n calls, by HIP events on `stream`."""
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(n):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
 
 
 MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
@@ -121,7 +217,8 @@ HEAD_EMBD, HEAD_B = 1024, 64
 def fused_head_bench(torch, mod, sampler, stream, steps, dev):
     """Q4_0 head + sampler, B=64 CFG pairs (128 projected rows): synthetic
     blocks (random nibbles, fp16 scales of a 0.05-scale weight row) and
-    hidden rows, resident in HBM; HIP events on the launch stream."""
+    hidden rows, resident in HBM; HIP events on the launch stream.  Also the
+    projection of one CFG pair alone (2 rows), the single-stream shape."""
     rng = np.random.default_rng(0x4EAD)
     nb = HEAD_EMBD // 32
     blocks = rng.integers(0, 256, size=(V, nb, 18), dtype=np.uint8)
@@ -151,18 +248,12 @@ def fused_head_bench(torch, mod, sampler, stream, steps, dev):
     def head_only(i):
         sampler.head_logits(head, HEAD_B, V, V)
 
+    def head_pair(i):
+        sampler.head_logits(head, 1, V, V)
+
     res = {}
-    for name, fn in (("head", head_only), ("fused", fused_step)):
-        for i in range(20):
-            fn(i)
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(steps):
-            fn(i)
-        b.record(stream)
-        torch.cuda.synchronize()
-        res[name] = a.elapsed_time(b) / steps
+    for name, fn in (("head", head_only), ("fused", fused_step), ("pair", head_pair)):
+        res[name] = timed(torch, stream, fn, steps, warm=20)
     flops = 2.0 * 2 * HEAD_B * V * HEAD_EMBD  # cond and uncond rows
     tf = flops / (res["head"] / 1e3) / 1e12
     return {"workload": "fused Q4_0 speech_head (V=6563 x 1024) + sampler, B=64 CFG pairs "
@@ -170,6 +261,7 @@ def fused_head_bench(torch, mod, sampler, stream, steps, dev):
             "steps": steps, "ms_per_step": round(res["fused"], 5),
             "tokens_per_s": round(HEAD_B / (res["fused"] / 1e3), 1),
             "head_ms": round(res["head"], 5),
+            "head_one_cfg_pair_ms": round(res["pair"], 5),
             "roofline": {"bound": "mfma", "achieved": round(tf, 2),
                          "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
@@ -181,26 +273,182 @@ def pkg_workloads():
     return pkg.workloads()
 
 
-def main():
+def config_single_stream(torch, mod, sampler, stream, dev, O):
+    """B=1, V=6563, 500 steps, fixed history of 256 ids; k 1000, p 0.95,
+    T 0.8, pen 1.2, min_p 0.05.  Philox draws keyed (seed, stream 0, step)."""
+    w = pkg_workloads()
+    d = w.single_stream(steps=500, min_p=0.05)
+    n = d["logits"].shape[0]
+    lg = torch.from_numpy(d["logits"]).to(dev)
+    hist = torch.from_numpy(d["history"][None, :]).to(dev)
+    hl = torch.tensor([d["history"].size], dtype=torch.int32, device=dev)
+    prm = torch.from_numpy(w.pack_params([d["params"]])).to(dev)
+    tok = torch.empty(n, dtype=torch.int32, device=dev)
+    seed = 0x51
+    u = np.array([O.philox_uniform(seed, 0, t) for t in range(n)]) if O else None
+
+    def step(i):
+        t = i % n
+        sampler.sample_batch(lg[t:t + 1], prm, tok[t:t + 1], history=hist, history_len=hl,
+                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=t)
+
+    ms_batch = timed(torch, stream, step, n)
+    got = tok.cpu().numpy()
+
+    def all_steps(i):
+        sampler.sample_batch(lg, prm, tok, n_steps=n, history=hist, history_len=hl,
+                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=0)
+
+    ms_all = timed(torch, stream, all_steps, 5, warm=1)
+    # the row API: host logits in, token out (PCIe copies included)
+    host = d["logits"]
+    t0 = time.perf_counter()
+    for t in range(100):
+        sampler.sample_row(host[t], d["history"], d["params"], u[t] if u is not None else 0.5)
+    ms_row = (time.perf_counter() - t0) * 1e3 / 100
+    out = {"workload": "B=1, V=6563, 500 steps, history 256, k 1000, p 0.95, T 0.8, pen 1.2, "
+                       "min_p 0.05",
+           "us_per_step_batch_api": round(ms_batch * 1e3, 2),
+           "us_per_step_one_launch_500_steps": round(ms_all * 1e3 / n, 3),
+           "us_per_step_row_api_pcie": round(ms_row * 1e3, 2)}
+    if O is not None:
+        ref, _, secs = O.sample_batch(d["logits"], [oparams(O, d["params"])] * n, u,
+                                      np.tile(d["history"], (n, 1)),
+                                      np.full(n, d["history"].size, np.int32), n_threads=1)
+        bad = [(d["logits"][t], d["history"], d["params"], u[t], int(got[t]), int(ref[t]))
+               for t in np.nonzero(got != ref)[0]]
+        out["cpu_us_per_step_1t"] = round(secs * 1e6 / n, 2)
+        out["parity_vs_oracle"] = dict(rows_checked=n, token_mismatches=len(bad),
+                                       **classify_mismatches(O, bad))
+    return out
+
+
+def config_cfg_pair(torch, mod, sampler, stream, dev, O, steps=1000):
+    """CFG pair, B=1, V=8194, 1000 steps: cond ~N(0,3), uncond = cond + N(0,1),
+    w 0.5, top-k off, p 0.95, T 0.8, pen 1.2, min_p 0.05; the history at step t
+    is the t tokens drawn before it (the oracle's sequence, Philox uniforms)."""
+    w = pkg_workloads()
+    d = w.cfg_pair(steps=steps)
+    seed = 0xCF6
+    p = d["params"]
+    seq = []
+    cpu_s = 0.0
+    if O is not None:
+        op = oparams(O, p)
+        for t in range(steps):
+            t0 = time.perf_counter()
+            tk, _ = O.sample_row(d["cond"][t], seq, op, O.philox_uniform(seed, 0, t),
+                                 uncond=d["uncond"][t])
+            cpu_s += time.perf_counter() - t0
+            seq.append(tk)
+    else:
+        seq = list(np.random.default_rng(1).integers(0, d["V"], size=steps))
+    hist = torch.from_numpy(np.array(seq, np.int32)[None, :]).to(dev)
+    hls = torch.arange(steps, dtype=torch.int32, device=dev)
+    c = torch.from_numpy(d["cond"]).to(dev)
+    un = torch.from_numpy(d["uncond"]).to(dev)
+    prm = torch.from_numpy(w.pack_params([p])).to(dev)
+    tok = torch.empty(steps, dtype=torch.int32, device=dev)
+
+    def step(i):
+        t = i % steps
+        sampler.sample_batch(c[t:t + 1], prm, tok[t:t + 1], logits_uncond=un[t:t + 1],
+                             history=hist, history_len=hls[t:t + 1],
+                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=t)
+
+    ms = timed(torch, stream, step, steps)
+    got = tok.cpu().numpy()
+    out = {"workload": "CFG pair B=1, V=8194, 1000 steps, history growing 0->999, top-k off, "
+                       "p 0.95, T 0.8, pen 1.2, min_p 0.05, w 0.5",
+           "us_per_step_batch_api": round(ms * 1e3, 2)}
+    if O is not None:
+        ref = np.array(seq, np.int32)
+        bad = [(d["cond"][t], seq[:t], p, O.philox_uniform(seed, 0, t), int(got[t]),
+                int(ref[t]), d["uncond"][t]) for t in np.nonzero(got != ref)[0]]
+        out["cpu_us_per_step_1t"] = round(cpu_s * 1e6 / steps, 2)
+        out["parity_vs_oracle"] = dict(rows_checked=steps, token_mismatches=len(bad),
+                                       **classify_mismatches(O, bad))
+    return out
+
+
+def config_masked_stress(torch, mod, sampler, stream, dev, steps=48, n_slabs=4):
+    """B=1024, V=32768 logits ~N(0,4), allowed bitmask with 20% of ids set,
+    forced stop on 1/16 of the rows, history 512, pen 1.3, k 50, p 0.9,
+    min_p 0.02; one launch per step over slabs of 128 MiB rotating through
+    512 MiB (twice the Infinity Cache)."""
+    Bm, Vm, H = 1024, 32768, 512
+    Wm = Vm // 32
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x5EED5)
+    slabs = [(torch.randn((Bm, Vm), generator=g, device=dev) * 4.0).contiguous()
+             for _ in range(n_slabs)]
+    bits = (torch.rand((Bm, Wm, 32), generator=g, device=dev) < 0.2).to(torch.int64)
+    stop = Vm - 1
+    bits[:, stop // 32, stop % 32] = 1
+    words = (bits << torch.arange(32, device=dev, dtype=torch.int64)).sum(-1)
+    allowed = words.to(torch.int64).bitwise_and(0xFFFFFFFF)
+    allowed = torch.where(allowed >= 2**31, allowed - 2**32, allowed).to(torch.int32).contiguous()
+    force = (torch.rand(Bm, generator=g, device=dev) < 1.0 / 16).to(torch.uint8)
+    hist = torch.randint(0, Vm, (Bm, H), generator=g, device=dev, dtype=torch.int32)
+    hl = torch.full((Bm,), H, dtype=torch.int32, device=dev)
+    w = pkg_workloads()
+    prm = torch.from_numpy(w.pack_params([dict(top_k=50, top_p=0.9, temp=0.8,
+                                               repeat_penalty=1.3, min_p=0.02,
+                                               cfg_weight=0.0)] * Bm)).to(dev)
+    tok = torch.empty(Bm, dtype=torch.int32, device=dev)
+    info = torch.zeros(Bm, dtype=torch.int32, device=dev)
+
+    def step(i):
+        sampler.sample_batch(slabs[i % n_slabs], prm, tok, history=hist, history_len=hl,
+                             allowed=allowed, force_stop=force, stop_token=stop, info=info,
+                             draw_mode=mod.CBX_DRAW_PHILOX, seed=5, step0=i, max_survivors=50)
+
+    ms = timed(torch, stream, step, steps, warm=n_slabs)
+    bytes_step = Bm * (4 * Vm + 4 * H + Wm * 4 + 1 + 24 + 8)
+    gbs = bytes_step / (ms / 1e3) / 1e9
+    flags = info.cpu().numpy().view(np.uint32)
+    return {"workload": "masked stress B=1024, V=32768, 20% allowed, forced stop 1/16, "
+                        "history 512, k 50, p 0.9, min_p 0.02, pen 1.3",
+            "us_per_step": round(ms * 1e3, 2),
+            "tokens_per_s": round(Bm / (ms / 1e3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 5),
+                         "algorithmic_bytes_per_step": bytes_step,
+                         "kernel": "sample_rows_kernel<1024,32>"},
+            "overflow_rows": int(np.sum((flags & 0x20) != 0))}
+
+
+def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=16384)
-    ap.add_argument("--warmup", type=int, default=1024)
+    ap.add_argument("--steps", type=int, default=16384,
+                    help="timed steps (at least; rounded up to whole launches)")
+    ap.add_argument("--warmup", type=int, default=1024,
+                    help="untimed steps first (at least; rounded up to whole launches)")
     ap.add_argument("--steps-per-launch", type=int, default=256)
     ap.add_argument("--slabs", type=int, default=2)
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
-    ap.add_argument("--cpu-seconds", type=float, default=6.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0,
+                    help="wall seconds of the single-thread CPU baseline")
+    ap.add_argument("--cpu-mt-seconds", type=float, default=2.0,
+                    help="wall seconds of the all-threads CPU baseline")
     ap.add_argument("--head-steps", type=int, default=200,
                     help="timed steps of the fused speech_head variant (0: skip)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations (single stream, CFG pair, masked)")
     ap.add_argument("--shape-steps", type=str, default="16,64",
-                    help="also time launches of these many steps (comma list, each dividing "
-                         "--steps-per-launch; empty: skip)")
+                    help="also time launches of these many steps (comma list; entries that do "
+                         "not divide --steps-per-launch are skipped; empty: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run a plain device copy of this many MiB (3 times) so "
                          "a counter run can scale FETCH_SIZE / WRITE_SIZE by known bytes")
-    args = ap.parse_args()
+    return ap.parse_args(argv)
+
+
+def main():
+    args = parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU; --gpus %d is not supported "
@@ -208,6 +456,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    t_start = time.perf_counter()
     import torch
     import pkg
 
@@ -215,13 +464,12 @@ def main():
     w = pkg.workloads()
     dev = "cuda:0"
     S = args.steps_per_launch
-    if args.steps % S or args.warmup % S:
-        sys.exit("--steps and --warmup must be multiples of --steps-per-launch")
+    n_launch, n_launch_w = launches_for(args.steps, args.warmup, S)
     slabs, hist, hist_len, params = make_inputs(torch, S, args.slabs, dev)
     d_hist = torch.from_numpy(hist).to(dev)
     d_hlen = torch.from_numpy(hist_len).to(dev)
     d_par = torch.from_numpy(w.pack_params(params)).to(dev)
-    sampler = mod.Sampler(device=0, max_vocab=V, max_history=HIST_MAX)
+    sampler = mod.Sampler(device=0, max_vocab=32768, max_history=HIST_MAX)
     tokens = torch.empty(S * B, dtype=torch.int32, device=dev)
     philox_seed = 0xC0FFEE
 
@@ -230,8 +478,6 @@ def main():
                              history_len=d_hlen, draw_mode=mod.CBX_DRAW_PHILOX, seed=philox_seed,
                              step0=step0, max_survivors=1000)
 
-    n_launch_w = args.warmup // S
-    n_launch = args.steps // S
     for i in range(n_launch_w):
         launch(i % args.slabs, i * S)
     torch.cuda.synchronize()
@@ -245,7 +491,8 @@ def main():
     t_all0.record(stream)
     for i in range(n_launch):
         ev[i][0].record(stream)
-        launch(i % args.slabs, (n_launch_w + i) * S)
+        # the slab after the one the previous launch read
+        launch((n_launch_w + i) % args.slabs, (n_launch_w + i) * S)
         ev[i][1].record(stream)
     t_all1.record(stream)
     torch.cuda.synchronize()
@@ -266,23 +513,14 @@ def main():
         if s2 <= 0 or S % s2:
             continue
         per = S // s2
-        n2 = max(args.steps // s2, 2 * per)
+        n2 = max(4096 // s2, 2 * per)
 
         def launch2(i):
             sl = slabs[(i // per) % args.slabs][(i % per) * s2 * B:((i % per) + 1) * s2 * B]
             sampler.sample_batch(sl, d_par, tokens2, n_steps=s2, history=d_hist,
                                  history_len=d_hlen, draw_mode=mod.CBX_DRAW_PHILOX,
                                  seed=philox_seed, step0=i * s2, max_survivors=1000)
-        for i in range(per):
-            launch2(i)
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(n2):
-            launch2(i)
-        b.record(stream)
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b)
+        ms = timed(torch, stream, launch2, n2, warm=per) * n2
         tps = n2 * s2 * B / (ms / 1e3)
         ach = bytes_step * s2 * n2 / (ms / 1e3) / 1e9
         shapes["s%d" % s2] = {"steps_per_launch": s2, "tokens_per_s": round(tps, 1),
@@ -292,24 +530,25 @@ def main():
     # one launch per step: the decode-loop shape (launch latency included)
     single = None
     if args.single_launch_steps > 0:
-        one = slabs[0][:B]
         tok1 = torch.empty(B, dtype=torch.int32, device=dev)
-        for i in range(10):
-            sampler.sample_batch(one, d_par, tok1, history=d_hist, history_len=d_hlen,
-                                 draw_mode=mod.CBX_DRAW_PHILOX, seed=philox_seed, step0=i,
-                                 max_survivors=1000)
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(args.single_launch_steps):
+
+        def one(i):
             sampler.sample_batch(slabs[i % args.slabs][(i % S) * B:(i % S + 1) * B], d_par, tok1,
                                  history=d_hist, history_len=d_hlen,
                                  draw_mode=mod.CBX_DRAW_PHILOX, seed=philox_seed, step0=i,
                                  max_survivors=1000)
-        b.record(stream)
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / args.single_launch_steps
+        ms = timed(torch, stream, one, args.single_launch_steps, warm=10)
         single = {"ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1)}
+
+    O = None
+    if not args.no_cpu:
+        import oracle_lib as O
+
+    configs = None
+    if not args.no_configs:
+        configs = {"single_stream": config_single_stream(torch, mod, sampler, stream, dev, O),
+                   "cfg_pair": config_cfg_pair(torch, mod, sampler, stream, dev, O),
+                   "masked_stress": config_masked_stress(torch, mod, sampler, stream, dev)}
 
     # the fused speech_head variant on the B=64 CFG shape: 128 hidden rows
     # (64 cond + 64 uncond) through Q4_0 weights of the Turbo head
@@ -329,34 +568,28 @@ def main():
 
     cpu = None
     parity = None
-    if not args.no_cpu:
-        import oracle_lib as O
-        # the last timed launch used slab (n_launch-1) % slabs and these steps:
-        last_slab = (n_launch - 1) % args.slabs
+    if O is not None:
+        # the last timed launch used this slab and these steps:
+        last_slab = (n_launch_w + n_launch - 1) % args.slabs
         step0 = (n_launch_w + n_launch - 1) * S
         gpu_tokens = tokens.cpu().numpy()
         logits_host = slabs[last_slab].cpu().numpy()
         u = np.array([O.philox_uniform(philox_seed, r % B, step0 + r // B)
                       for r in range(S * B)])
-        res = cpu_baseline(hist, hist_len, params, logits_host, u, gpu_tokens,
-                           args.cpu_seconds, args.cpu_seconds)
+        threads, visible = host_threads()
+        res = cpu_baseline(O, hist, hist_len, params, logits_host, u, gpu_tokens,
+                           args.cpu_seconds, args.cpu_mt_seconds, threads)
         import platform
-        model = ""
-        try:
-            for line in open("/proc/cpuinfo"):
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-        except OSError:
-            pass
         cpu = {"value": round(res["mt"][0], 1), "unit": "sampled tokens/s",
-               "cores": res["mt"][2], "kind": "port",
-               "sample": "%d rows (B=256 streams x %d steps of the timed workload) on %d threads; "
-                         "single-thread: %.1f tokens/s over %d rows; %s, %s" % (
-                             res["mt"][1], res["mt"][1] // B, res["mt"][2], res["1t"][0],
-                             res["1t"][1], model, platform.machine()),
+               "cores": threads, "kind": "port",
+               "sample": "%d rows (B=256 streams x %d steps of the timed workload) on %d threads "
+                         "(this GPU's share of the host; %d CPUs visible); single-thread: %.1f "
+                         "tokens/s over %d rows; %s, %s" % (
+                             res["mt"][1], res["mt"][1] // B, threads, visible, res["1t"][0],
+                             res["1t"][1], cpu_model(), platform.machine()),
                "single_thread_value": round(res["1t"][0], 1)}
-        parity = {"rows_checked": res["1t"][1] + res["mt"][1], "token_mismatches": res["mismatches"]}
+        parity = dict(rows_checked=res["rows_checked"], token_mismatches=res["mismatch"],
+                      **res["classes"])
 
     out = {
         "metric": "sampled tokens/sec at B=256, V=6563; achieved HBM GB/s vs 8 TB/s peak",
@@ -365,6 +598,8 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": n_launch_w * S,
+        "steps_requested": args.steps,
+        "warmup_requested": args.warmup,
         "ms_per_step": round(total_ms / steps, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -383,10 +618,12 @@ def main():
                      "algorithmic_bytes_per_launch": bytes_launch,
                      "avg_launch_ms": round(avg_launch_ms, 5)},
         "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
         "launch_shapes": shapes,
         "single_launch_per_step": single,
-        "parity_vs_oracle": parity,
+        "configs": configs,
         "fused_head": fused,
+        "wall_s": round(time.perf_counter() - t_start, 1),
     }
     print(json.dumps(out), flush=True)
     sampler.close()

@@ -195,6 +195,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_retry_stream_id.argtypes = [u64, i32]
     lib.cbx_retry_record.restype = ctypes.c_int
     lib.cbx_retry_record.argtypes = [ctypes.POINTER(Retry), i32, i32]
+    lib.cbx_retry_record_tokens.restype = ctypes.c_int
+    lib.cbx_retry_record_tokens.argtypes = [ctypes.POINTER(Retry), i32, i32, i32, i32]
     lib.cbx_last_error.restype = ctypes.c_char_p
     lib.cbx_last_error.argtypes = []
     _lib = lib
@@ -246,6 +248,16 @@ def retry_start(n_text_tokens) -> Retry:
 def retry_record(r: Retry, n_tokens, stopped_by_stop_token) -> bool:
     """cbx_retry_record: True if another attempt should run (r.attempt)."""
     rc = _lib.cbx_retry_record(ctypes.byref(r), n_tokens, 1 if stopped_by_stop_token else 0)
+    if rc < 0:
+        _check(rc)
+    return rc == 1
+
+
+def retry_record_tokens(r: Retry, n_sampled, last_token, stop_token, n_predict) -> bool:
+    """cbx_retry_record_tokens: the record from the tokens drawn in the
+    attempt; True if another attempt should run (r.attempt)."""
+    rc = _lib.cbx_retry_record_tokens(ctypes.byref(r), n_sampled, last_token, stop_token,
+                                      n_predict)
     if rc < 0:
         _check(rc)
     return rc == 1

@@ -1,8 +1,9 @@
 // cbx_retry.cpp -- the T3 segment loop's early-stop retry policy
 // (include/cbx_retry.h), following src/chatterbox_cli.cpp:1614-1672: the
 // min_tokens floor (:1614), MAX_RETRIES (:1615), the per-attempt RNG offset
-// (:1620-1621, here a Philox stream id per attempt), the longest-attempt
-// fallback (:1651) and the accept test (:1653-1654).
+// (:1620-1621, here a Philox stream id per attempt), the stop flag of the
+// decode loop (:1633-1638) and the pop of a final stop token (:1647-1648),
+// the longest-attempt fallback (:1651) and the accept test (:1653-1654).
 #include "../../include/cbx_retry.h"
 #include "cbx_internal.h"
 
@@ -49,4 +50,16 @@ extern "C" int cbx_retry_record(cbx_retry* r, int32_t n_tokens, int32_t stopped_
     r->kept_attempt = r->best_attempt;
     r->kept_len = r->best_len;
     return 0;
+}
+
+extern "C" int cbx_retry_record_tokens(cbx_retry* r, int32_t n_sampled, int32_t last_token,
+                                       int32_t stop_token, int32_t n_predict) {
+    if (!r || n_sampled < 1 || n_predict < 0 || n_sampled > n_predict + 1)
+        return cbx::set_error(CBX_ERR_INVALID,
+                              "cbx_retry_record_tokens: %d tokens drawn with n_predict %d",
+                              n_sampled, n_predict);
+    const bool last_is_stop = last_token == stop_token;
+    // iteration i (< n_predict) checks the (i+1)-th token drawn
+    const int32_t stopped = last_is_stop && n_sampled <= n_predict ? 1 : 0;
+    return cbx_retry_record(r, n_sampled - (last_is_stop ? 1 : 0), stopped);
 }

@@ -50,11 +50,26 @@ int cbx_retry_init(cbx_retry* r, int32_t n_text_tokens);
 uint64_t cbx_retry_stream_id(uint64_t stream, int32_t attempt);
 
 /* Record the attempt just run: n_tokens speech tokens after popping a final
- * stop token, stopped_by_stop_token != 0 if it ended on the stop token.
- * Returns 1 if another attempt should run (r->attempt is then its number),
- * 0 if r->done (r->kept_attempt / kept_len say which tokens to keep), or a
- * negative CBX_ERR_* for a call after done or bad arguments. */
+ * stop token, and the reference's stopped_by_stop_token flag
+ * (chatterbox_cli.cpp:1633-1638): nonzero only when the loop found the stop
+ * token as the current token at the top of one of its n_predict iterations.
+ * A stop token sampled by the last iteration is popped (:1647-1648) but the
+ * flag stays 0, so such an attempt is kept however short it is; neither does
+ * a loop that ends on a full context set it.  Returns 1 if another attempt
+ * should run (r->attempt is then its number), 0 if r->done (r->kept_attempt /
+ * kept_len say which tokens to keep), or a negative CBX_ERR_* for a call after
+ * done or bad arguments. */
 int cbx_retry_record(cbx_retry* r, int32_t n_tokens, int32_t stopped_by_stop_token);
+
+/* The same record from what a decoder counts: n_sampled tokens drawn in the
+ * attempt (the prompt's token and one per loop iteration run), the last of
+ * them last_token, and the loop's bound n_predict (>= 0).  The loop checks
+ * the token drawn before iteration i (i < n_predict) at that iteration's top,
+ * so the attempt stopped on the stop token exactly when last_token ==
+ * stop_token and n_sampled <= n_predict; n_tokens is n_sampled less the
+ * popped stop token. */
+int cbx_retry_record_tokens(cbx_retry* r, int32_t n_sampled, int32_t last_token,
+                            int32_t stop_token, int32_t n_predict);
 
 #ifdef __cplusplus
 }

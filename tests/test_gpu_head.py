@@ -133,15 +133,16 @@ def test_head_without_bias(cbx, torch_cuda):
     assert np.all(np.abs(got - ref) <= tol)
 
 
-@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
 def test_fused_head_sample_cfg(cbx, torch_cuda, wtype):
-    """B=64 CFG streams, two steps: projection of cond and uncond hidden rows,
-    then the sampler (k 1000, p 0.95, T 0.8, pen 1.2, w 0.5) in one call."""
+    """B=64 CFG streams, two steps: projection of cond and uncond hidden rows
+    (weights from N(0, 0.02), hidden rows N(0, 1)), then the sampler (k 1000,
+    p 0.95, T 0.8, pen 1.2, w 0.5) in one call."""
     torch = torch_cuda
     mod, s = cbx
     V, K, B, S = 6563, 1024, 64, 2
     rng = np.random.default_rng(77 + wtype)
-    blocks, bias, h = _problem(rng, V, K, B * S, wtype, scale=0.1)
+    blocks, bias, h = _problem(rng, V, K, B * S, wtype, scale=0.02)
     hu = (h + 0.5 * rng.standard_normal(h.shape)).astype(np.float32)
     hist = rng.integers(0, V, size=(B, 300)).astype(np.int32)
     hl = rng.integers(0, 301, size=B).astype(np.int32)

@@ -283,19 +283,50 @@ def test_batched_streams_vocab(cbx, torch_cuda, V):
     parity.compare(f"batched_streams_{V}", tg, ig, tr, ir, u, pg, pr)
 
 
-def test_batched_streams_philox(cbx, torch_cuda):
+@pytest.mark.parametrize("max_survivors", [0, 1000])
+def test_batched_streams_philox(cbx, torch_cuda, max_survivors):
     """Device Philox draws keyed (seed, stream, step) equal the oracle fed the
-    oracle's Philox uniforms."""
+    oracle's Philox uniforms, on the workgroup kernel (no survivor bound) and
+    the one-wave kernel (at most 1000 survivors)."""
     w = pkg.workloads()
     d = w.batched_streams(B=256, steps=2, seed=0x5EED33)
     n = d["logits"].shape[0]
     seed, step0 = 0xC0FFEE, 1000
     u = np.array([O.philox_uniform(seed, r % 256, step0 + r // 256) for r in range(n)])
-    say("batched_streams philox")
+    say(f"batched_streams philox max_survivors={max_survivors}")
     tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], None, d["history"],
-                           d["hist_len"], n_steps=2, draw_mode=1, seed=seed, step0=step0)
+                           d["hist_len"], n_steps=2, draw_mode=1, seed=seed, step0=step0,
+                           max_survivors=max_survivors)
     tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
     parity.compare("batched_streams_philox", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_timed_path_retry_stream_ids(cbx, torch_cuda):
+    """The benchmark's kernel and draw: B=256 streams, 16 steps in one launch,
+    at most 1000 survivors (the one-wave kernel), Philox draws keyed by the
+    retry policy's stream ids cbx_retry_stream_id(s, a) for attempts 0..3
+    (ids up to 3 * 2^56 + 255): every token equals the oracle fed the oracle's
+    Philox uniform for that (seed, stream id, step)."""
+    torch = torch_cuda
+    mod, s = cbx
+    w = pkg.workloads()
+    B, S = 256, 16
+    d = w.batched_streams(B=B, steps=S, seed=0x5EED34)
+    n = d["logits"].shape[0]
+    sids = np.array([mod.retry_stream_id(r, r % 4) for r in range(B)], np.uint64)
+    assert sids.max() >= 3 << 56
+    seed, step0 = 0x5EED_F00D, 77
+    u = np.array([O.philox_uniform(seed, int(sids[r % B]), step0 + r // B) for r in range(n)])
+    say(f"timed path: B={B} x {S} steps, max_survivors=1000, retry stream ids")
+    tg, ig, pg = gpu_batch(cbx, torch, d["logits"], d["params"], None, d["history"],
+                           d["hist_len"], n_steps=S, draw_mode=1, seed=seed, step0=step0,
+                           max_survivors=1000,
+                           stream_ids=torch.from_numpy(sids.view(np.int64)).cuda())
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
+    parity.compare("timed_path_retry_ids", tg, ig, tr, ir, u, pg, pr)
+    # the same rows keyed by attempt 0 (the plain stream index) draw differently
+    u0 = np.array([O.philox_uniform(seed, r % B, step0 + r // B) for r in range(n)])
+    assert np.count_nonzero(u0 != u) == n - n // 4
 
 
 def test_masked_stress(cbx, torch_cuda):

@@ -79,3 +79,68 @@ def test_stream_ids(mod):
             for a in range(4)]
     assert len(set(seqs)) == 4
     assert all(0.0 <= u < 1.0 for s in seqs for u in s)
+
+
+STOP = 6562
+
+
+def loop_reference(draws, n_predict, stop=STOP, n_ctx_left=None):
+    """The decode loop of chatterbox_cli.cpp:1627-1648 over a fixed sequence
+    of draws: (tokens kept after the pop, stopped_by_stop_token, tokens drawn)."""
+    it = iter(draws)
+    current = next(it)
+    generated = [current]
+    stopped = False
+    for i in range(n_predict):
+        if current == stop:
+            stopped = True
+            break
+        if n_ctx_left is not None and i >= n_ctx_left:
+            break  # "KV cache full"
+        current = next(it)
+        generated.append(current)
+    n_drawn = len(generated)
+    if generated and generated[-1] == stop:
+        generated.pop()
+    return len(generated), stopped, n_drawn
+
+
+@pytest.mark.parametrize("draws,n_predict,n_ctx_left", [
+    ([1, 2, 3, STOP], 10, None),          # stop drawn early: stopped, retried when short
+    ([1] * 10 + [STOP], 10, None),        # stop drawn by the last iteration: not stopped
+    ([1] * 11, 10, None),                 # n_predict ran out
+    ([STOP], 0, None),                    # n_predict 0: the prompt's token only
+    ([STOP], 5, None),                    # the prompt's token is the stop token
+    ([1, 2, 3, 4, 5], 10, 3),             # context full after 3 iterations
+])
+def test_record_tokens_matches_the_loop(mod, draws, n_predict, n_ctx_left):
+    """cbx_retry_record_tokens derives the reference loop's flag and length
+    from the tokens drawn, including a stop token drawn by the last of the
+    n_predict iterations (popped, but the attempt counts as not stopped)."""
+    n_tok, stopped, n_drawn = loop_reference(draws, n_predict, n_ctx_left=n_ctx_left)
+    last = draws[n_drawn - 1]
+    a = mod.retry_start(4)     # min_tokens 20: every attempt here is short
+    b = mod.retry_start(4)
+    again_a = mod.retry_record(a, n_tok, stopped)
+    again_b = mod.retry_record_tokens(b, n_drawn, last, STOP, n_predict)
+    assert again_a == again_b == stopped
+    assert (a.best_len, a.attempt, a.done) == (b.best_len, b.attempt, b.done)
+
+
+def test_stop_on_last_iteration_is_kept(mod):
+    """A 10-token attempt whose 11th draw (by iteration n_predict - 1) is the
+    stop token is kept although it is shorter than min_tokens: the reference
+    never sets stopped_by_stop_token for it."""
+    r = mod.retry_start(4)
+    assert not mod.retry_record_tokens(r, 11, STOP, STOP, 10)
+    assert r.done == 1 and (r.kept_attempt, r.kept_len) == (0, 10)
+    r = mod.retry_start(4)
+    assert mod.retry_record_tokens(r, 10, STOP, STOP, 10)  # drawn by iteration 8: retried
+    assert r.attempt == 1 and r.best_len == 9
+
+
+def test_record_tokens_rejects_impossible_counts(mod):
+    r = mod.retry_start(1)
+    for n_sampled, n_predict in ((0, 5), (7, 5), (1, -1)):
+        with pytest.raises(mod.CbxError):
+            mod.retry_record_tokens(r, n_sampled, 1, STOP, n_predict)
