@@ -43,6 +43,7 @@
 #include "cbx_internal.h"
 #include "cbx_philox.h"
 #include "cbx_seqsum.h"
+#include "cbx_stdsort.h"
 
 // Stage timestamps for a profiling build (CBX_STAGE_CLOCKS defined, one
 // translation unit): wave 0 of each of the first 16384 workgroups records the
@@ -1261,7 +1262,44 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
             if (i == n_kept && i < n_surv) sh.tie[1] = desc_key_value(x[r]);
         }
         __syncthreads();
-        if (tid == 0 && n_kept < n_surv && sh.tie[0] == sh.tie[1]) sh.flags |= CBX_INFO_TOPP_TIE;
+        const bool tie = n_kept < n_surv && sh.tie[0] == sh.tie[1];
+        if (tid == 0 && tie) sh.flags |= CBX_INFO_TOPP_TIE;
+        if (tie && !(flags & CBX_INFO_NONFINITE)) {
+            // Equal scores straddle the cutoff: the survivors in id order
+            // (ranks from a bitmap of their ids), lane 0 replays the
+            // reference's std::sort, and its first n_kept entries are kept.
+            float* qs = reinterpret_cast<float*>(region);
+            uint16_t* qi = reinterpret_cast<uint16_t*>(qs + NR * BLOCK);
+            const int W = (a.n_vocab + 31) >> 5;
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if (r * BLOCK + tid < n_surv) {
+                    const uint32_t i = (uint32_t)x[r];
+                    atomicOr(&keptw[i >> 5], 1u << (i & 31));
+                }
+            __syncthreads();
+            (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if (r * BLOCK + tid < n_surv) {
+                    const uint32_t i = (uint32_t)x[r];
+                    const int at = rank_of(keptw, woff, (int)i);
+                    qs[at] = desc_key_value(x[r]);
+                    qi[at] = (uint16_t)i;
+                }
+            __syncthreads();
+            if (tid == 0) (void)stdsort_replay(SortSeq<uint16_t>{qs, qi}, n_surv);
+            for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
+            __syncthreads();
+            for (int i = tid; i < n_kept; i += BLOCK) atomicOr(&keptw[qi[i] >> 5], 1u << (qi[i] & 31));
+            __syncthreads();
+            kept = 0;
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if (r * BLOCK + tid < n_surv && bit_of(keptw, (int)(uint32_t)x[r]))
+                    kept |= (uint64_t)1 << r;
+            __syncthreads();  // finish_row clears the bitmap again
+        }
     } else {
 #pragma unroll
         for (int r = 0; r < NR; ++r)
@@ -1534,7 +1572,41 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
         }
         if (tid == 0) sh.mx = mx_surv;  // min-p reference: the best survivor
         __syncthreads();
-        if (tid == 0 && n_kept < n_surv && sh.tie[0] == sh.tie[1]) sh.flags |= CBX_INFO_TOPP_TIE;
+        const bool tie = n_kept < n_surv && sh.tie[0] == sh.tie[1];
+        if (tid == 0 && tie) sh.flags |= CBX_INFO_TOPP_TIE;
+        if (tie && !bad) {
+            // Equal scores straddle the cutoff: the survivors in id order
+            // (ranks from a bitmap of their ids, in the word-offset array's
+            // company), lane 0 replays the reference's std::sort in the sort's
+            // own storage, and its first n_kept ids are the kept ones.
+            float* qs = reinterpret_cast<float*>(key32);
+            __syncthreads();
+            for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < EPT; ++j)
+                if (s[j] != kNegInf) {
+                    const int i = j * BLOCK + tid;
+                    atomicOr(&keptw[i >> 5], 1u << (i & 31));
+                }
+            __syncthreads();
+            (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+#pragma unroll
+            for (int j = 0; j < EPT; ++j)
+                if (s[j] != kNegInf) {
+                    const int i = j * BLOCK + tid;
+                    const int at = rank_of(keptw, woff, i);
+                    qs[at] = s[j];
+                    id16[at] = (uint16_t)i;
+                }
+            __syncthreads();
+            if (tid == 0) (void)stdsort_replay(SortSeq<uint16_t>{qs, id16}, n_surv);
+            for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
+            __syncthreads();
+            for (int i = tid; i < n_kept; i += BLOCK)
+                atomicOr(&keptw[id16[i] >> 5], 1u << (id16[i] & 31));
+            __syncthreads();
+        }
     }
 
     // kept predicate per register element

@@ -1283,8 +1283,60 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         n_kept = uni(last + 1);
         CBX_STAMP(9);
         if (n_kept < n_surv &&
-            desc_key_value(sm.list[n_kept - 1]) == desc_key_value(sm.list[n_kept]))
+            desc_key_value(sm.list[n_kept - 1]) == desc_key_value(sm.list[n_kept])) {
             rflags |= CBX_INFO_TOPP_TIE;
+            // Equal scores straddle the cutoff: which of them the reference
+            // keeps is its std::sort's doing.  The survivors are gathered again
+            // in id order (scores reloaded; survivors are the scores > thr)
+            // and lane 0 replays that sort; its first n_kept entries are the
+            // kept ones.  The running sums, hence n_kept, do not depend on the
+            // order of equal scores.
+            if (!bad) {
+                __syncthreads();
+                float* qs = reinterpret_cast<float*>(sm.list);
+                uint16_t* qi = reinterpret_cast<uint16_t*>(qs + kWaveCap);
+                int base = 0;
+#pragma unroll 1
+                for (int j = 0; j < Q; ++j) {
+                    float v[4];
+                    rsc.reload4(j, lane, v, V);
+                    int c = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) c += v[e] > thr ? 1 : 0;
+                    int tot;
+                    int at = base + wave_excl_scan_i(c, tot);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (v[e] > thr && at < kWaveCap) {  // ascending ids: lane, element
+                            qs[at] = v[e];
+                            qi[at] = (uint16_t)(256 * j + 4 * lane + e);
+                            ++at;
+                        }
+                    }
+                    base += tot;
+                }
+                __syncthreads();
+                if (lane == 0 && base == n_surv)
+                    (void)stdsort_replay(SortSeq<uint16_t>{qs, qi}, n_surv);
+                __syncthreads();
+                // the kept entries back as keys (read out first: the keys'
+                // storage overlaps the arrays)
+                float kv[R];
+                uint32_t ki[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int i = r * 64 + lane;
+                    kv[r] = i < n_kept ? qs[i] : 0.0f;
+                    ki[r] = i < n_kept ? qi[i] : 0u;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int i = r * 64 + lane;
+                    if (i < n_kept) sm.list[i] = desc_key(kv[r], ki[r]);
+                }
+            }
+        }
         __syncthreads();
     }
 

@@ -471,8 +471,7 @@ def test_edge_cases(cbx, torch_cuda, case):
     mod, s = cbx
     tok, info = s.sample_row(x[0], hist[0], pd, u)
     assert tok == tg[0] and info == ig[0]
-    if not (ir[0] & parity.INFO_TOPP_TIE):
-        assert tok == tr[0]
+    assert tok == tr[0]
 
 
 # cases whose survivors after top-k fit the one-wave kernel's list
@@ -559,3 +558,46 @@ def test_golden_fixtures(cbx, torch_cuda):
     tg, ig, pg = gpu_batch(cbx, torch_cuda, g["logits"], plist, g["u"], g["history"],
                            g["hist_len"], allowed=g["allowed"])
     parity.compare("golden", tg, ig, g["tokens"], g["info"], g["u"], pg, g["probs"])
+
+
+def plateau_rows(rng, n, V, plateau, level=8.0):
+    """Rows whose top-p cutoff falls inside a run of equal scores: three
+    spikes (10, 9.5, 9), `plateau` ids at `level` scattered over the row and
+    the rest far below.  At T = 1 and p = 0.5 the cumulative mass crosses p
+    among the plateau's ids."""
+    x = (rng.standard_normal((n, V)) - 6.0).astype(F32)
+    for r in range(n):
+        ids = rng.choice(V, size=plateau + 3, replace=False)
+        x[r, ids[:3]] = [10.0, 9.5, 9.0]
+        x[r, ids[3:]] = level
+    return x
+
+
+TIE_CASES = [
+    # name, V, top_k, plateau, max_survivors (kernel)
+    ("one_wave", 6563, 1000, 200, 1024),      # one-wave kernel, list of 1000
+    ("one_wave_small", 500, 100, 60, 1024),
+    ("wg_fast", 6563, 1000, 300, 0),          # workgroup kernel, register list
+    ("wg_general", 8194, 0, 3000, 0),         # workgroup kernel, LDS pairs (8194 survivors)
+]
+
+
+@pytest.mark.parametrize("case", TIE_CASES, ids=[c[0] for c in TIE_CASES])
+def test_topp_tie_rows(cbx, torch_cuda, case):
+    """Equal scores straddle the top-p cutoff in every row: the kept ids are
+    the ones the reference's std::sort puts first, so tokens and
+    probabilities equal the oracle's (which runs std::sort itself)."""
+    name, V, k, plateau, ms = case
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    n = 4 if name == "wg_general" else 32
+    x = plateau_rows(rng, n, V, plateau)
+    plist = [dict(top_k=k, top_p=0.5, temp=1.0, repeat_penalty=1.3, min_p=0.0,
+                  cfg_weight=0.0)] * n
+    hist = rng.integers(0, V, size=(n, 200)).astype(np.int32)
+    hl = np.full(n, 200, np.int32)
+    u = rng.random(n)
+    say(f"top-p tie rows {name}: n={n} V={V} k={k} plateau={plateau} max_survivors={ms}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, plist, u, hist, hl, max_survivors=ms)
+    tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
+    assert np.count_nonzero(ir & parity.INFO_TOPP_TIE) == n  # every row is a tie row
+    parity.compare(f"topp_tie_{name}", tg, ig, tr, ir, u, pg, pr)

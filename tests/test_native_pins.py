@@ -137,3 +137,18 @@ def test_segment_scan_rules_match_sequential_float_sums(seqsum_bin, seed):
     assert cases == 20000
     assert segments > 2 * cases  # binade changes are exercised, not only one segment
     assert bad_sum == 0 and bad_hit == 0, r.stdout
+
+
+def test_stdsort_replay_matches_libstdcxx(tmp_path):
+    """The one-lane restatement of libstdc++'s std::sort (csrc/cbx_stdsort.h)
+    orders (id, score) pairs exactly as std::sort does with the reference's
+    comparator (main.cpp:752-755): ties, sorted runs and McIlroy adversary
+    inputs that reach the heap-sort fallback."""
+    out = str(tmp_path / "stdsort_replay")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-o", out,
+                    os.path.join(NATIVE, "stdsort_replay.cpp")], check=True)
+    res = subprocess.run([out], capture_output=True, text=True)
+    assert res.returncode == 0, res.stdout + res.stderr
+    cases, bad, heaped = (int(v) for v in res.stdout.split()[-3:])
+    assert cases > 5000 and bad == 0
+    assert heaped > 0  # the depth-limit fallback was exercised
