@@ -31,6 +31,10 @@ struct cbx_sampler {
     int32_t* d_token = nullptr;
     uint32_t* d_info = nullptr;
     float* d_probs = nullptr;
+    // redo lists (rows over a launch's survivor capacity): batched calls, and
+    // the single-row calls on the handle's own stream
+    int32_t* d_redo = nullptr;
+    int32_t* d_redo_row = nullptr;
     // pinned host staging for the small per-call inputs/outputs
     struct Small {
         cbx_params params;
@@ -87,6 +91,8 @@ void release(cbx_sampler* s) {
     (void)hipFree(s->d_token);
     (void)hipFree(s->d_info);
     (void)hipFree(s->d_probs);
+    (void)hipFree(s->d_redo);
+    (void)hipFree(s->d_redo_row);
     if (s->h_small) (void)hipHostFree(s->h_small);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
@@ -100,6 +106,22 @@ int32_t pick_cap(const cbx_sampler* s, int32_t n_vocab, int32_t hint) {
     while (cap < want) cap <<= 1;
     const int32_t lim = cbx::max_cap_for_lds(n_vocab, s->lds_limit);
     return cap < lim ? cap : lim;
+}
+
+// The launch, and after a launch at a survivor capacity below the
+// vocabulary's (a caller's max_survivors hint) the redo pass: rows with more
+// survivors (ties at a tiny top-k threshold, top-k off, a hint below top_k)
+// go on the redo list `redo` and are sampled again, on the same stream, at
+// the largest capacity the device's LDS allows -- the whole vocabulary for
+// every n_vocab <= 32768 on gfx950.
+hipError_t launch_with_redo(int32_t full, cbx::KernelArgs a, int32_t* redo, hipStream_t st) {
+    const int64_t rows = (int64_t)a.n_steps * a.n_rows;
+    a.redo = a.cap < full ? redo : nullptr;
+    a.redo_max = (int32_t)(rows < cbx::kRedoMax ? rows : cbx::kRedoMax);
+    hipError_t e = cbx::launch_sample(a, st);
+    if (e != hipSuccess || !a.redo) return e;
+    a.cap = full;
+    return cbx::launch_redo(a, st);
 }
 
 bool params_ok(const cbx_params* p) {
@@ -166,6 +188,11 @@ int cbx_sampler_create(cbx_sampler** out, int32_t device, int32_t max_vocab, int
     if (e == hipSuccess) e = hipMalloc(&s->d_token, sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc(&s->d_info, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&s->d_probs, sizeof(float) * max_vocab);
+    if (e == hipSuccess) e = hipMalloc(&s->d_redo, sizeof(int32_t) * cbx::kRedoWords);
+    if (e == hipSuccess) e = hipMalloc(&s->d_redo_row, sizeof(int32_t) * 3);
+    // the lists start empty; each redo pass leaves them empty again
+    if (e == hipSuccess) e = hipMemset(s->d_redo, 0, sizeof(int32_t) * cbx::kRedoWords);
+    if (e == hipSuccess) e = hipMemset(s->d_redo_row, 0, sizeof(int32_t) * 3);
     if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_small, sizeof(cbx_sampler::Small));
     if (e != hipSuccess) {
         release(s);
@@ -241,15 +268,7 @@ int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_u
     a.info = s->d_info;
     a.probs = probs_out ? s->d_probs : nullptr;
     a.ld_probs = n_vocab;
-    CBX_HIP(cbx::launch_sample(a, st));
-    CBX_HIP(hipMemcpyAsync(&hs->info, s->d_info, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    CBX_HIP(hipStreamSynchronize(st));
-    if ((hs->info & CBX_INFO_OVERFLOW) && a.cap < pick_cap(s, n_vocab, 0)) {
-        // ties at the top-k threshold left more survivors than k: redo the
-        // row with the largest capacity the device allows
-        a.cap = pick_cap(s, n_vocab, 0);
-        CBX_HIP(cbx::launch_sample(a, st));
-    }
+    CBX_HIP(launch_with_redo(pick_cap(s, n_vocab, 0), a, s->d_redo_row, st));
     CBX_HIP(hipMemcpyAsync(&hs->token, s->d_token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
     CBX_HIP(hipMemcpyAsync(&hs->info, s->d_info, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     if (probs_out)
@@ -324,7 +343,7 @@ int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
     a.info = b->info;
     a.probs = b->probs;
     a.ld_probs = b->ld_probs;
-    CBX_HIP(cbx::launch_sample(a, (hipStream_t)stream));
+    CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, (hipStream_t)stream));
     return CBX_OK;
 }
 

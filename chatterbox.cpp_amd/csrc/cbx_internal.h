@@ -34,7 +34,17 @@ struct KernelArgs {
     uint32_t* info;
     float* probs;
     int64_t ld_probs;
+    // Rows left for the redo pass (more survivors than cap): int32 words
+    // [0] count, [1] redo workgroups finished, [2 ..] row-step ids (the first
+    // redo_max).  NULL when no redo pass follows the launch.
+    int32_t* redo;
+    int32_t redo_max;
 };
+
+// Rows one redo pass takes at most (one workgroup each).
+constexpr int32_t kRedoMax = 4096;
+// int32 words of a redo list.
+constexpr int32_t kRedoWords = 2 + kRedoMax;
 
 constexpr int32_t kMaxVocab = 32768;
 // Survivors after top-k that the one-wave kernel holds; launches whose
@@ -49,6 +59,8 @@ size_t lds_bytes_for(int32_t cap, int32_t n_vocab);
 
 // Launch the sampler over n_steps * n_rows rows.  Returns a hipError_t.
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream);
+// Whether launch_sample runs the one-wave kernel for these arguments.
+bool uses_wave_kernel(const KernelArgs& a);
 // One vocabulary class each (lanes x scores per lane), used by launch_sample.
 // One-wave kernels, scores per lane 4*Q (V <= 256*Q); the *t forms serve
 // V > 256*(Q-1), where only the last vector of each lane holds padding.
@@ -63,6 +75,15 @@ hipError_t launch_v256x26(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v256x32(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v1024x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v1024x32(const KernelArgs& a, hipStream_t stream);
+// After a launch at capacity below the vocabulary's: sample again, at a.cap,
+// the rows it put on its redo list, on the same stream (one workgroup per
+// listed row; the last workgroup clears the list for the next launch).
+hipError_t launch_redo(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v256x16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v256x26(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v256x32(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v1024x16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v1024x32(const KernelArgs& a, hipStream_t stream);
 
 hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream);
 hipError_t launch_debug_seqsum(const float* terms, const int32_t* offsets, const float* thr,

@@ -585,9 +585,9 @@ __device__ __forceinline__ bool bin_sort(uint64_t (&x)[NR], int n, float blo, fl
     return true;
 }
 
-// Ascending bitonic sort of (key, id) pairs [0, n2) in LDS (large lists).
+// Ascending bitonic sort of keys [0, n2) in LDS (n2 a power of two).
 template <int BLOCK>
-__device__ __forceinline__ void bitonic_sort_pairs(uint32_t* key, uint16_t* id, int n2) {
+__device__ __forceinline__ void bitonic_sort_keys(uint32_t* key, int n2) {
     n2 = uni(n2);
     for (int k = 2; k <= n2; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
@@ -596,9 +596,7 @@ __device__ __forceinline__ void bitonic_sort_pairs(uint32_t* key, uint16_t* id, 
                 const int p = i + j;
                 const bool up = (i & k) == 0;
                 const uint32_t ka = key[i], kb = key[p];
-                const uint16_t ia = id[i], ib = id[p];
-                const bool a_gt_b = (ka > kb) || (ka == kb && ia > ib);
-                if (a_gt_b == up) { key[i] = kb; key[p] = ka; id[i] = ib; id[p] = ia; }
+                if ((ka > kb) == up) { key[i] = kb; key[p] = ka; }
             }
             __syncthreads();
         }
@@ -740,8 +738,11 @@ __device__ __forceinline__ float chain_segments(const float (&t)[CM], int nl, fl
 // strides, distinct banks).  finite: every term finite and >= 0 and acc
 // finite, so the binade segments apply (chain_segments); otherwise sweeps,
 // exact for NaN and infinities too.
+// The terms come from term(i) (a load, or a value formed on the spot).
 constexpr int kChainC = 17;
-__device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc, bool finite = true) {
+template <class Term>
+__device__ __forceinline__ float wave_chain_sum_of(Term&& term, int n, float acc,
+                                                   bool finite = true) {
     const int lane = threadIdx.x & 63;
     n = uni(n);
     for (int base = 0; base < n; base += 64 * kChainC) {
@@ -749,7 +750,7 @@ __device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc
 #pragma unroll
         for (int q = 0; q < kChainC; ++q) {
             const int i = base + lane * kChainC + q;
-            t[q] = i < n ? v[i] : 0.0f;
+            t[q] = i < n ? term(i) : 0.0f;
         }
         const int nl = min(64, (n - base + kChainC - 1) / kChainC);
         if (finite) {
@@ -762,11 +763,17 @@ __device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc
     return acc;
 }
 
+__device__ __forceinline__ float wave_chain_sum(const float* v, int n, float acc, bool finite = true) {
+    return wave_chain_sum_of([&](int i) { return v[i]; }, n, acc, finite);
+}
+
 // First i with (0 + v[0] + ... + v[i]) >= thr (binary32, index order), or
 // n-1 when the running sum never reaches thr.  One wave.  Terms are
 // non-negative, so the running sum never decreases: a chunk is searched only
-// when its end value reaches thr.
-__device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr, bool finite = true) {
+// when its end value reaches thr.  The terms come from term(i).
+template <class Term>
+__device__ __forceinline__ int wave_chain_cross_of(Term&& term, int n, float thr,
+                                                   bool finite = true) {
     const int lane = threadIdx.x & 63;
     n = uni(n);
     float acc = 0.0f;
@@ -775,7 +782,7 @@ __device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr
 #pragma unroll
         for (int q = 0; q < kChainC; ++q) {
             const int i = base + lane * kChainC + q;
-            t[q] = i < n ? v[i] : 0.0f;
+            t[q] = i < n ? term(i) : 0.0f;
         }
         const int nl = min(64, (n - base + kChainC - 1) / kChainC);
         int hit = -1;
@@ -793,6 +800,9 @@ __device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr
         acc = end;
     }
     return n - 1;
+}
+__device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr, bool finite = true) {
+    return wave_chain_cross_of([&](int i) { return v[i]; }, n, thr, finite);
 }
 
 // DPP lane moves of a step table (identity where no source lane).
@@ -1016,6 +1026,148 @@ __device__ __forceinline__ int bitmap_offsets(const uint32_t* keptw, uint32_t* w
     }
     __syncthreads();
     return n;
+}
+
+// ------------------------------------------------ std::sort order of a tie
+//
+// The wavefront form of stdsort_tied_order (cbx_stdsort.h): the ids of the
+// elements of rank kT in the order the reference's std::sort leaves them.
+// Each partition is one pass counting the right stops and two passes over
+// the range in 64-element chunks, where ballots give every element its
+// left-stop and right-stop ranks, so a partition of m elements costs about
+// 3m/64 steps instead of m dependent steps on one lane.
+
+// LDS writes made visible to the wavefront's later reads.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int mbcnt64(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// __unguarded_partition_pivot of [f, l) (l - f > 16) over packed words
+// (rank << 16 | id) by one wavefront; tmp holds l - f words.  Returns the
+// cut and whether [f, cut) and [cut, l) hold an element of rank kT.
+__device__ __forceinline__ int wave_partition_counts(uint32_t* w, uint32_t* tmp, int f, int l,
+                                                     uint32_t kT, bool& has_lo, bool& has_hi) {
+    const int lane = threadIdx.x & 63;
+    const int m = l - f, half = (m + 1) / 2;
+    if (lane == 0) stdsort_median_to_first(PackedSeq{w}, f, f + 1, f + m / 2, l - 1);
+    wave_lds_sync();
+    const uint32_t pv = (uint32_t)uni((int)(w[f] >> 16));
+    int n_r = 0;  // right stops: !(pv < rank)
+    for (int p0 = f + 1; p0 < l; p0 += 64) {
+        const int p = p0 + lane;
+        n_r += __popcll(__ballot(p < l && !(pv < (w[min(p, l - 1)] >> 16))));
+    }
+    int lb0 = 0, rb0 = 0, cut = l;
+    for (int p0 = f + 1; p0 < l; p0 += 64) {
+        const int p = p0 + lane;
+        const bool in = p < l;
+        const uint32_t x = w[min(p, l - 1)], k = x >> 16;
+        const bool is_l = in && !(k < pv), is_r = in && !(pv < k);
+        const uint64_t ml = __ballot(is_l), mr = __ballot(is_r);
+        const int lb = lb0 + mbcnt64(ml);
+        const int ra = n_r - (rb0 + mbcnt64(mr) + (is_r ? 1 : 0));
+        int c = 0x7fffffff;
+        if (is_l) {
+            if (ra > lb) tmp[lb] = x;  // swapped left stop, partner rank lb
+            else c = p;                // unswapped left stop
+        }
+        if (is_r && lb > ra) {         // swapped right stop, partner rank ra
+            tmp[half + ra] = x;
+            c = p;
+        }
+        cut = min(cut, wave_min_i(c));
+        lb0 += __popcll(ml);
+        rb0 += __popcll(mr);
+    }
+    cut = uni(cut);
+    wave_lds_sync();
+    bool lo_t = (pv == kT), hi_t = false;  // the pivot stays at f < cut
+    lb0 = 0;
+    rb0 = 0;
+    for (int p0 = f + 1; p0 < l; p0 += 64) {
+        const int p = p0 + lane;
+        const bool in = p < l;
+        const uint32_t x = w[min(p, l - 1)], k = x >> 16;
+        const bool is_l = in && !(k < pv), is_r = in && !(pv < k);
+        const uint64_t ml = __ballot(is_l), mr = __ballot(is_r);
+        const int lb = lb0 + mbcnt64(ml);
+        const int ra = n_r - (rb0 + mbcnt64(mr) + (is_r ? 1 : 0));
+        uint32_t nx = x;
+        if (is_l && ra > lb) nx = tmp[half + lb];
+        else if (is_r && lb > ra) nx = tmp[ra];
+        if (in) {
+            w[p] = nx;
+            if ((nx >> 16) == kT) {
+                lo_t = lo_t || p < cut;
+                hi_t = hi_t || p >= cut;
+            }
+        }
+        lb0 += __popcll(ml);
+        rb0 += __popcll(mr);
+    }
+    has_lo = __ballot(lo_t) != 0;
+    has_hi = __ballot(hi_t) != 0;
+    wave_lds_sync();
+    return cut;
+}
+
+// The ids of rank kT, in the reference's std::sort order, written to tied[]
+// (which may alias tmp); returns their count.  w[0, n): the survivors as
+// (rank << 16 | id) in id order, permuted in place; tmp: n words.  One
+// wavefront; the pending ranges live in lanes 0..31 of two registers.
+__device__ __forceinline__ int wave_tied_order(uint32_t* w, uint32_t* tmp, int n, uint32_t kT,
+                                               uint16_t* tied) {
+    const int lane = threadIdx.x & 63;
+    int lg = 0;
+    while ((n >> (lg + 1)) != 0) ++lg;
+    // lane j of st_range / st_depth: stack entry j (range first | last << 16)
+    int st_range = lane == 0 ? (int)((uint32_t)n << 16) : 0;
+    int st_depth = lane == 0 ? 2 * lg : 0;
+    int top = 1;
+    while (top > 0) {
+        --top;
+        const uint32_t rg = (uint32_t)__builtin_amdgcn_readlane(st_range, top);
+        const int f = (int)(rg & 0xffffu);
+        int l = (int)(rg >> 16);
+        int depth = __builtin_amdgcn_readlane(st_depth, top);
+        bool has = true;  // ranges are pushed only when they hold rank kT
+        while (has && l - f > kStdSortThreshold) {
+            if (depth == 0) {  // __partial_sort: rare (adversarial inputs)
+                if (lane == 0) stdsort_heap_sort(PackedSeq{w}, f, l);
+                wave_lds_sync();
+                break;
+            }
+            --depth;
+            bool lo_t, hi_t;
+            const int cut = wave_partition_counts(w, tmp, f, l, kT, lo_t, hi_t);
+            if (hi_t) {
+                st_range = lane == top ? (int)((uint32_t)cut | ((uint32_t)l << 16)) : st_range;
+                st_depth = lane == top ? depth : st_depth;
+                ++top;
+            }
+            l = cut;
+            has = lo_t;
+        }
+    }
+    // the tied elements in array order
+    int m = 0;
+    for (int p0 = 0; p0 < n; p0 += 64) {
+        const int p = p0 + lane;
+        const uint32_t x = p < n ? w[p] : 0u;
+        const bool t = p < n && (x >> 16) == kT;
+        const uint64_t mt = __ballot(t);
+        if (t) tied[m + mbcnt64(mt)] = (uint16_t)(x & 0xffffu);
+        m += __popcll(mt);
+    }
+    wave_lds_sync();
+    return m;
 }
 
 // ----------------------------------------------------------------- the draw
@@ -1340,14 +1492,11 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
 // MAXNR: the largest register list (rows per lane) compiled in; GENERAL: the
 // per-element path for more survivors is compiled in (the launch picks the
 // variant from the survivor capacity, so lean variants carry no unused code).
+// One workgroup samples row-step g of the launch.
 template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
-__global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
-    __shared__ Shared sh;
-    __shared__ uint64_t tab[32];
-    extern __shared__ __align__(16) uint8_t smem[];
-
+__device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Shared& sh,
+                                              uint64_t* tab, uint8_t* smem) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int64_t g = blockIdx.x;
     const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
     const int V = a.n_vocab;
     const int cap = a.cap;
@@ -1358,7 +1507,8 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
     //   top-k:        value histogram u32[2048] + candidates f32[512], or the
     //                 radix histogram u32[4096]
     //   fast path:    xbuf u64[2048] (list, cross-wave exchanges), then E f32
-    //   general path: key32 u32[cap] | id16 u16[cap], E aliasing key32
+    //   general path: key32 u32[cap] (sorted scores); for a tie at the
+    //                 top-p cutoff, rank u16[cap] | id u16[cap] in its place
     //   finish:       F f32[n_final]
     uint32_t* seen = reinterpret_cast<uint32_t*>(smem);
     uint32_t* keptw = seen + Wp;
@@ -1369,7 +1519,6 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
     uint64_t* xbuf = reinterpret_cast<uint64_t*>(region);
     float* E = reinterpret_cast<float*>(region);
     uint32_t* key32 = reinterpret_cast<uint32_t*>(region);
-    uint16_t* id16 = reinterpret_cast<uint16_t*>(key32 + cap);
     float* F = reinterpret_cast<float*>(region);
 
     const cbx_params P = a.params[row];
@@ -1480,6 +1629,10 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
         if (tid == 0) {
             a.tokens[rs] = -1;
             if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
+            if (a.redo) {  // the redo pass samples the row again at full capacity
+                const int i = atomicAdd(&a.redo[0], 1);
+                if (i < a.redo_max) a.redo[2 + i] = (int32_t)rs;
+            }
         }
         if (a.probs) {
             float* prow = a.probs + rs * a.ld_probs;
@@ -1521,68 +1674,74 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
     } else {
     // ================= general path: scores per element =================
     // ---- top-p (main.cpp:750-772) ----
+    // The survivors' scores alone are sorted (keys ~okey(s), ascending =
+    // descending score: 4 bytes each, so every id of a 32768 vocabulary fits
+    // the LDS).  The cutoff is then a score T: the kept ids are those above
+    // T and, of the ids scoring exactly T, the ones std::sort puts first.
+    float T = kNegInf;
+    bool tie = false;
     if (use_topp) {
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-            if (s[j] != kNegInf) {
-                key32[off] = ~okey(s[j]);
-                id16[off] = (uint16_t)(j * BLOCK + tid);
-                ++off;
-            }
-        }
+        for (int j = 0; j < EPT; ++j)
+            if (s[j] != kNegInf) key32[off++] = ~okey(s[j]);
         const int n2 = uni(max(64, pow2ceil(n_surv)));
-        for (int i = n_surv + tid; i < n2; i += BLOCK) { key32[i] = 0xFFFFFFFFu; id16[i] = 0xFFFFu; }
+        for (int i = n_surv + tid; i < n2; i += BLOCK) key32[i] = 0xFFFFFFFFu;
         __syncthreads();
         CBX_STAMP(13);
-        bitonic_sort_pairs<BLOCK>(key32, id16, n2);
+        bitonic_sort_keys<BLOCK>(key32, n2);
         CBX_STAMP(14);
         const float mx_surv = unif(okey_inv(~key32[0]));
-        __syncthreads();
-        for (int i = tid; i < n_surv; i += BLOCK)
-            E[i] = expf_libm_branchless(__fsub_rn(okey_inv(~key32[i]), mx_surv), tab);
-        __syncthreads();
+        // the exp terms in sorted order, formed where the sums read them
+        auto e_of = [&](int i) {
+            return expf_libm_branchless(__fsub_rn(okey_inv(~key32[i]), mx_surv), tab);
+        };
         if (wid == 0) {
-            const float ps = wave_chain_sum(E, n_surv, 0.0f, !bad);
+            const float ps = wave_chain_sum_of(e_of, n_surv, 0.0f, !bad);
             if (lane == 0) sh.psum = ps;
         }
         __syncthreads();
         CBX_STAMP(15);
         const float psum = unif(sh.psum);
-        for (int i = tid; i < n_surv; i += BLOCK) E[i] = __fdiv_rn(E[i], psum);
-        __syncthreads();
         if (wid == 0) {
-            const int last = wave_chain_cross(E, n_surv, P.top_p, !bad);
+            const int last = wave_chain_cross_of(
+                [&](int i) { return __fdiv_rn(e_of(i), psum); }, n_surv, P.top_p, !bad);
             if (lane == 0) sh.n_kept = last + 1;
         }
         __syncthreads();
         const int n_kept = uni(sh.n_kept);
-        for (int i = tid; i < n_kept; i += BLOCK) {
-            const uint32_t idx = id16[i];
-            atomicOr(&keptw[idx >> 5], 1u << (idx & 31));
+        T = unif(okey_inv(~key32[n_kept - 1]));
+        tie = n_kept < n_surv && unif(okey_inv(~key32[n_kept])) == T;
+        if (tid == 0) {
+            sh.mx = mx_surv;  // min-p reference: the best survivor
+            if (tie) sh.flags |= CBX_INFO_TOPP_TIE;
         }
-        // equal scores straddling the cutoff: read both ids' scores back
-        if (n_kept < n_surv) {
-            const int ia = id16[n_kept - 1], ib = id16[n_kept];
+        if (tie && !bad) {
+            // Equal scores straddle the cutoff.  Each survivor's key becomes
+            // its rank among the sorted scores (the first position holding its
+            // score: same order, same ties, 16 bits), the (rank, id) pairs go
+            // in id order (positions from a bitmap of the survivor ids), lane
+            // 0 replays the reference's std::sort on them, and the ids at its
+            // first n_kept positions are the kept ones.
+            uint32_t rk2[(EPT + 1) / 2];  // two 16-bit ranks per register
+#pragma unroll
+            for (int q = 0; q < (EPT + 1) / 2; ++q) rk2[q] = 0u;
 #pragma unroll
             for (int j = 0; j < EPT; ++j) {
-                const int i = j * BLOCK + tid;
-                if (i == ia) sh.tie[0] = s[j];
-                if (i == ib) sh.tie[1] = s[j];
+                if (s[j] != kNegInf) {
+                    const uint32_t key = ~okey(s[j]);
+                    int lo = 0, hi = n_surv;  // first position with key32 >= key
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (key32[mid] < key) lo = mid + 1;
+                        else hi = mid;
+                    }
+                    rk2[j >> 1] |= (uint32_t)lo << (16 * (j & 1));
+                }
             }
-        }
-        if (tid == 0) sh.mx = mx_surv;  // min-p reference: the best survivor
-        __syncthreads();
-        const bool tie = n_kept < n_surv && sh.tie[0] == sh.tie[1];
-        if (tid == 0 && tie) sh.flags |= CBX_INFO_TOPP_TIE;
-        if (tie && !bad) {
-            // Equal scores straddle the cutoff: the survivors in id order
-            // (ranks from a bitmap of their ids, in the word-offset array's
-            // company), lane 0 replays the reference's std::sort in the sort's
-            // own storage, and its first n_kept ids are the kept ones.
-            float* qs = reinterpret_cast<float*>(key32);
-            __syncthreads();
+            uint16_t* qr = reinterpret_cast<uint16_t*>(region);
+            uint16_t* qi = qr + cap;
             for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
-            __syncthreads();
+            __syncthreads();  // the sorted keys are read: their storage takes the pairs
 #pragma unroll
             for (int j = 0; j < EPT; ++j)
                 if (s[j] != kNegInf) {
@@ -1596,25 +1755,27 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
                 if (s[j] != kNegInf) {
                     const int i = j * BLOCK + tid;
                     const int at = rank_of(keptw, woff, i);
-                    qs[at] = s[j];
-                    id16[at] = (uint16_t)i;
+                    qr[at] = (uint16_t)(rk2[j >> 1] >> (16 * (j & 1)));
+                    qi[at] = (uint16_t)i;
                 }
             __syncthreads();
-            if (tid == 0) (void)stdsort_replay(SortSeq<uint16_t>{qs, id16}, n_surv);
+            if (tid == 0) (void)stdsort_replay(SortSeq<uint16_t, uint16_t>{qr, qi}, n_surv);
             for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
             __syncthreads();
             for (int i = tid; i < n_kept; i += BLOCK)
-                atomicOr(&keptw[id16[i] >> 5], 1u << (id16[i] & 31));
-            __syncthreads();
+                atomicOr(&keptw[qi[i] >> 5], 1u << (qi[i] & 31));
         }
+        __syncthreads();
     }
 
-    // kept predicate per register element
+    // kept predicate per register element: above the cutoff score, or at it
+    // among the ids the replayed sort kept
     uint64_t kept = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int i = j * BLOCK + tid;
-        const bool k = s[j] != kNegInf && (!use_topp || bit_of(keptw, i));
+        const bool at_cut = (tie && !bad) ? bit_of(keptw, i) : s[j] >= T;
+        const bool k = s[j] != kNegInf && (!use_topp || at_cut);
         kept |= (uint64_t)k << j;
     }
 
@@ -1649,11 +1810,59 @@ __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
 }
 
 template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
+__global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
+    __shared__ Shared sh;
+    __shared__ uint64_t tab[32];
+    extern __shared__ __align__(16) uint8_t smem[];
+    sample_row_wg<BLOCK, EPT, MAXNR, GENERAL>(a, blockIdx.x, sh, tab, smem);
+}
+
+// The rows a launch put on its redo list (more ids survived top-k than its
+// capacity held), sampled again here at the vocabulary's capacity:
+// workgroup b takes list entry b, or leaves at once when the list is
+// shorter.  One row per workgroup and no loop around the row's code: in a
+// loop the compiler's allocation of the row's registers spills.  The last of
+// the working workgroups clears the list for the next launch (no memset, so
+// the pair of launches can be captured in a graph).  A workgroup that reads
+// the count after that clear finds 0 and leaves, which is right: every
+// workgroup with a row to do read the count before adding itself to `done`.
+template <int BLOCK, int EPT, int MAXNR>
+__global__ __launch_bounds__(BLOCK) void redo_rows_kernel(KernelArgs a) {
+    __shared__ Shared sh;
+    __shared__ uint64_t tab[32];
+    __shared__ int32_t head[2];
+    extern __shared__ __align__(16) uint8_t smem[];
+    int32_t* const list = a.redo;
+    if (threadIdx.x == 0) {
+        const int n = min(list[0], a.redo_max);
+        head[0] = n;
+        head[1] = (int)blockIdx.x < n ? list[2 + blockIdx.x] : -1;
+    }
+    __syncthreads();
+    const int n = uni(head[0]), row = uni(head[1]);
+    if (row < 0) return;
+    a.redo = nullptr;  // full capacity: nothing more to hand on
+    sample_row_wg<BLOCK, EPT, MAXNR, true>(a, row, sh, tab, smem);
+    if (threadIdx.x == 0) {
+        __threadfence();
+        if (atomicAdd(&list[1], 1) == n - 1) {
+            list[0] = 0;
+            list[1] = 0;
+            __threadfence();
+        }
+    }
+}
+
+// LDS a workgroup kernel declares besides its dynamic share (the redo
+// kernel's row list included).
+constexpr size_t kStaticLds = sizeof(Shared) + 32 * 8 + 64;
+
+template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
 hipError_t launch_cfg(const KernelArgs& a, hipStream_t stream) {
     const size_t lds = lds_bytes_for(a.cap, a.n_vocab);
     // Dynamic LDS beyond 64 KiB has to be granted per kernel; remember the
     // largest grant so repeated launches skip the call.
-    static size_t granted = 64 * 1024 - sizeof(Shared) - 256;
+    static size_t granted = 64 * 1024 - kStaticLds;
     if (lds > granted) {
         hipError_t e = hipFuncSetAttribute(
             reinterpret_cast<const void*>(&sample_rows_kernel<BLOCK, EPT, MAXNR, GENERAL>),
@@ -1665,6 +1874,29 @@ hipError_t launch_cfg(const KernelArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((sample_rows_kernel<BLOCK, EPT, MAXNR, GENERAL>), dim3((unsigned)rows),
                        dim3(BLOCK), lds, stream, a);
     return hipGetLastError();
+}
+
+template <int BLOCK, int EPT, int MAXNR>
+hipError_t launch_redo_cfg(const KernelArgs& a, hipStream_t stream) {
+    const size_t lds = lds_bytes_for(a.cap, a.n_vocab);
+    static size_t granted = 64 * 1024 - kStaticLds;
+    if (lds > granted) {
+        hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&redo_rows_kernel<BLOCK, EPT, MAXNR>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        granted = lds;
+    }
+    hipLaunchKernelGGL((redo_rows_kernel<BLOCK, EPT, MAXNR>), dim3((unsigned)a.redo_max),
+                       dim3(BLOCK), lds, stream, a);
+    return hipGetLastError();
+}
+
+// The redo pass at capacity a.cap (every row of the vocabulary, on gfx950).
+template <int BLOCK, int EPT>
+hipError_t launch_redo_for(const KernelArgs& a, hipStream_t stream) {
+    if constexpr (4 * BLOCK <= kFastMax) return launch_redo_cfg<BLOCK, EPT, 8>(a, stream);
+    else return launch_redo_cfg<BLOCK, EPT, kFastMax / BLOCK>(a, stream);
 }
 
 // Variant by survivor capacity: the smallest register list that holds `cap`

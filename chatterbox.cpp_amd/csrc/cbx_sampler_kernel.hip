@@ -49,19 +49,23 @@ size_t lds_bytes_for(int32_t cap, int32_t n_vocab) {
     const size_t list = (size_t)(cap < kFastMax ? (cap < 64 ? 64 : cap) : kFastMax);
     const size_t fast = (size_t)(kSortBins + 4) * 4 + 8 * list;        // counting sort / list
     if (fast > region) region = fast;
-    if ((size_t)cap * 6 > region) region = (size_t)cap * 6;             // LDS-sorted pairs / F
+    if ((size_t)cap * 4 > region) region = (size_t)cap * 4;             // sorted scores / F
     return 3 * Wp * 4 + region;
 }
 
 int32_t max_cap_for_lds(int32_t n_vocab, size_t lds_bytes) {
     int32_t cap = 1 << 16;
-    while (cap > 64 && lds_bytes_for(cap, n_vocab) + sizeof(Shared) + 256 > lds_bytes) cap >>= 1;
+    while (cap > 64 && lds_bytes_for(cap, n_vocab) + kStaticLds > lds_bytes) cap >>= 1;
     return cap;
+}
+
+bool uses_wave_kernel(const KernelArgs& a) {
+    return a.cap <= kWaveCap && a.n_vocab <= kWaveMaxVocab;
 }
 
 hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
     // one wave per row while the survivors fit its list
-    if (a.cap <= kWaveCap) {
+    if (uses_wave_kernel(a)) {
         if (a.n_vocab <= 256 * 16) return a.n_vocab > 256 * 15 ? launch_w16t(a, stream) : launch_w16(a, stream);
         if (a.n_vocab <= 256 * 26) return a.n_vocab > 256 * 25 ? launch_w26t(a, stream) : launch_w26(a, stream);
         if (a.n_vocab <= kWaveMaxVocab)
@@ -73,6 +77,14 @@ hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
     if (a.n_vocab <= 256 * 32) return launch_v256x32(a, stream);
     if (a.n_vocab <= 1024 * 16) return launch_v1024x16(a, stream);
     return launch_v1024x32(a, stream);
+}
+
+hipError_t launch_redo(const KernelArgs& a, hipStream_t stream) {
+    if (a.n_vocab <= 256 * 16) return launch_redo_v256x16(a, stream);
+    if (a.n_vocab <= 256 * 26) return launch_redo_v256x26(a, stream);
+    if (a.n_vocab <= 256 * 32) return launch_redo_v256x32(a, stream);
+    if (a.n_vocab <= 1024 * 16) return launch_redo_v1024x16(a, stream);
+    return launch_redo_v1024x32(a, stream);
 }
 
 hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream) {

@@ -408,6 +408,128 @@ __device__ __forceinline__ void for_row_groups(int n, F&& f) {
     }
 }
 
+// Inclusive max-scan over the wavefront.
+__device__ __forceinline__ int wave_incl_max_scan(int x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(x, o, 64);
+        if (lane >= o) x = max(x, t);
+    }
+    return x;
+}
+
+// The kept entries of a row whose top-p cutoff falls inside equal scores,
+// in the order the reference's std::sort leaves them.  In: the list holds the
+// n_surv survivors as sorted keys (descending score, ascending id) and the
+// first n_kept are kept.  Out: the list's first n_kept entries are the
+// survivors scoring above the tied score T and, of those scoring T, the ones
+// std::sort puts first.  Steps: each survivor's rank (the first sorted
+// position of its score) and id-order position (from a bitmap of the
+// survivor ids in `keptw`, free at this point); the (rank << 16 | id) words
+// in id order in the list's storage, then wave_tied_order; the entries above
+// T gathered again from the row's scores.
+template <int Q>
+__device__ __forceinline__ void tie_order_wave(WaveSmem<Q>& sm, const RowScores& rsc, int n_surv,
+                                            int n_kept, int V) {
+    constexpr int R = kWaveRows;
+    constexpr int WPL = (8 * Q + 63) / 64;
+    const int lane = threadIdx.x;
+    const int nr = (n_surv + 63) >> 6;
+    const float T = desc_key_value(sm.list[n_kept - 1]);
+    // ranks, ids and the bitmap of survivor ids
+    for (int w = lane; w < 8 * Q; w += 64) sm.keptw[w] = 0u;
+    wave_lds_sync();
+    uint32_t word[R];
+    int carry = 0, kT = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        word[r] = 0u;
+        if (r < nr) {
+            const int i = r * 64 + lane;
+            const bool in = i < n_surv;
+            const uint64_t key = sm.list[min(i, n_surv - 1)];
+            const float v = desc_key_value(key);
+            const float prev = desc_key_value(sm.list[max(i - 1, 0)]);
+            const bool start = in && (i == 0 || v != prev);
+            const int rank = max(carry, wave_incl_max_scan(start ? i : 0));
+            carry = __builtin_amdgcn_readlane(rank, 63);
+            const uint32_t id = (uint32_t)key;
+            word[r] = ((uint32_t)rank << 16) | id;
+            kT += __popcll(__ballot(in && v > T));
+            if (in) atomicOr(&sm.keptw[id >> 5], 1u << (id & 31));
+        }
+    }
+    wave_lds_sync();
+    // id-order position: survivors in the words before the id's, then in its
+    // word below it; lane L holds the prefix counts of words L*WPL ..
+    int base[WPL];
+    {
+        int loc = 0;
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) {
+            const int w = lane * WPL + q;
+            base[q] = loc;
+            loc += w < 8 * Q ? __popc(sm.keptw[w]) : 0;
+        }
+        int all;
+        const int off = wave_excl_scan_i(loc, all);
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) base[q] += off;
+    }
+    int pos[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        pos[r] = -1;
+        if (r < nr) {
+            const uint32_t id = word[r] & 0xffffu;
+            const int wd = (int)(id >> 5), owner = wd / WPL, slot = wd - owner * WPL;
+            int b = 0;
+#pragma unroll
+            for (int q = 0; q < WPL; ++q) {
+                const int bq = __builtin_amdgcn_ds_bpermute(owner << 2, base[q]);
+                b = q == slot ? bq : b;
+            }
+            const int p = b + __popc(sm.keptw[wd] & ((1u << (id & 31)) - 1u));
+            pos[r] = r * 64 + lane < n_surv ? p : -1;
+        }
+    }
+    wave_lds_sync();  // every key is read: the storage takes the words
+    uint32_t* w = reinterpret_cast<uint32_t*>(sm.list);
+    uint32_t* tmp = w + n_surv;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < nr && pos[r] >= 0) w[pos[r]] = word[r];
+    wave_lds_sync();
+    uint16_t* tied = reinterpret_cast<uint16_t*>(tmp);
+    (void)wave_tied_order(w, tmp, n_surv, (uint32_t)kT, tied);
+    // the first n_kept - kT tied ids are kept
+    const int m_keep = n_kept - kT;
+    uint32_t tk[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) tk[r] = r * 64 + lane < m_keep ? tied[r * 64 + lane] : 0u;
+    wave_lds_sync();
+    // the list again: the kT survivors above T from the row's scores, then
+    // the kept tied ids
+    int n = 0;
+#pragma unroll 1
+    for (int j = 0; j < Q; ++j) {
+        float v[4];
+        rsc.reload4(j, lane, v, V);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const bool keep = v[c] > T;
+            const uint64_t m = __ballot(keep);
+            if (keep) sm.list[n + mbcnt64(m)] = desc_key(v[c], (uint32_t)(256 * j + 4 * lane + c));
+            n += __popcll(m);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r * 64 + lane < m_keep) sm.list[kT + r * 64 + lane] = desc_key(T, tk[r]);
+    wave_lds_sync();
+}
+
 // ------------------------------------------------------------------ kernel
 
 template <int Q, int JT>
@@ -942,6 +1064,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         if (lane == 0) {
             a.tokens[rs] = -1;
             if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
+            if (a.redo) {  // the redo pass samples the row again at full capacity
+                const int i = atomicAdd(&a.redo[0], 1);
+                if (i < a.redo_max) a.redo[2 + i] = (int32_t)rs;
+            }
         }
         if (a.probs) {
             float* prow = a.probs + rs * a.ld_probs;
@@ -1286,55 +1412,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             desc_key_value(sm.list[n_kept - 1]) == desc_key_value(sm.list[n_kept])) {
             rflags |= CBX_INFO_TOPP_TIE;
             // Equal scores straddle the cutoff: which of them the reference
-            // keeps is its std::sort's doing.  The survivors are gathered again
-            // in id order (scores reloaded; survivors are the scores > thr)
-            // and lane 0 replays that sort; its first n_kept entries are the
-            // kept ones.  The running sums, hence n_kept, do not depend on the
-            // order of equal scores.
+            // keeps is decided by its std::sort's order.  The running sums,
+            // hence n_kept, do not depend on that order; the kept ids of the
+            // tied score do, and are replayed here (wave_tied_order).
             if (!bad) {
-                __syncthreads();
-                float* qs = reinterpret_cast<float*>(sm.list);
-                uint16_t* qi = reinterpret_cast<uint16_t*>(qs + kWaveCap);
-                int base = 0;
-#pragma unroll 1
-                for (int j = 0; j < Q; ++j) {
-                    float v[4];
-                    rsc.reload4(j, lane, v, V);
-                    int c = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) c += v[e] > thr ? 1 : 0;
-                    int tot;
-                    int at = base + wave_excl_scan_i(c, tot);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (v[e] > thr && at < kWaveCap) {  // ascending ids: lane, element
-                            qs[at] = v[e];
-                            qi[at] = (uint16_t)(256 * j + 4 * lane + e);
-                            ++at;
-                        }
-                    }
-                    base += tot;
-                }
-                __syncthreads();
-                if (lane == 0 && base == n_surv)
-                    (void)stdsort_replay(SortSeq<uint16_t>{qs, qi}, n_surv);
-                __syncthreads();
-                // the kept entries back as keys (read out first: the keys'
-                // storage overlaps the arrays)
-                float kv[R];
-                uint32_t ki[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int i = r * 64 + lane;
-                    kv[r] = i < n_kept ? qs[i] : 0.0f;
-                    ki[r] = i < n_kept ? qi[i] : 0u;
-                }
-                __syncthreads();
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int i = r * 64 + lane;
-                    if (i < n_kept) sm.list[i] = desc_key(kv[r], ki[r]);
-                }
+                tie_order_wave<Q>(sm, rsc, n_surv, n_kept, V);
             }
         }
         __syncthreads();

@@ -43,13 +43,18 @@
 
 namespace cbx {
 
-// The sequence being sorted: element i is (s[i], id[i]).
-template <typename Id>
+// The sequence being sorted.  SortSeq: element i is (s[i], id[i]) with the
+// score itself as key (float: comp is a > b) or, where memory is short, the
+// score's rank among the distinct scores in descending order (uint16_t: comp
+// is a < b), which orders and ties exactly as the scores do.  PackedSeq: one
+// word per element, (rank << 16) | id.  The steps below read keys with
+// key(i) / key_of(element) and move whole elements.
+template <typename Id, typename Key = float>
 struct SortSeq {
-    float* s;
+    Key* s;
     Id* id;
     struct El {
-        float s;
+        Key s;
         Id id;
     };
     CBX_SORT_HD El get(int i) const { return {s[i], id[i]}; }
@@ -57,6 +62,8 @@ struct SortSeq {
         s[i] = e.s;
         id[i] = e.id;
     }
+    CBX_SORT_HD Key key(int i) const { return s[i]; }
+    CBX_SORT_HD static Key key_of(const El& e) { return e.s; }
     CBX_SORT_HD void swap(int i, int j) const {
         const El t = get(i);
         put(i, get(j));
@@ -64,14 +71,29 @@ struct SortSeq {
     }
 };
 
+struct PackedSeq {
+    uint32_t* w;
+    using El = uint32_t;
+    CBX_SORT_HD El get(int i) const { return w[i]; }
+    CBX_SORT_HD void put(int i, El e) const { w[i] = e; }
+    CBX_SORT_HD uint16_t key(int i) const { return (uint16_t)(w[i] >> 16); }
+    CBX_SORT_HD static uint16_t key_of(El e) { return (uint16_t)(e >> 16); }
+    CBX_SORT_HD void swap(int i, int j) const {
+        const El t = w[i];
+        w[i] = w[j];
+        w[j] = t;
+    }
+};
+
 // comp(a, b) of the reference: a.s > b.s.
 CBX_SORT_HD bool sort_comp(float a, float b) { return a > b; }
+CBX_SORT_HD bool sort_comp(uint16_t rank_a, uint16_t rank_b) { return rank_a < rank_b; }
 
-template <typename Id>
-CBX_SORT_HD void stdsort_push_heap(const SortSeq<Id>& q, int first, int hole, int top,
-                                   typename SortSeq<Id>::El v) {
+template <class Seq>
+CBX_SORT_HD void stdsort_push_heap(const Seq& q, int first, int hole, int top,
+                                   typename Seq::El v) {
     int parent = (hole - 1) / 2;
-    while (hole > top && sort_comp(q.s[first + parent], v.s)) {
+    while (hole > top && sort_comp(q.key(first + parent), Seq::key_of(v))) {
         q.put(first + hole, q.get(first + parent));
         hole = parent;
         parent = (hole - 1) / 2;
@@ -79,14 +101,14 @@ CBX_SORT_HD void stdsort_push_heap(const SortSeq<Id>& q, int first, int hole, in
     q.put(first + hole, v);
 }
 
-template <typename Id>
-CBX_SORT_HD void stdsort_adjust_heap(const SortSeq<Id>& q, int first, int hole, int len,
-                                     typename SortSeq<Id>::El v) {
+template <class Seq>
+CBX_SORT_HD void stdsort_adjust_heap(const Seq& q, int first, int hole, int len,
+                                     typename Seq::El v) {
     const int top = hole;
     int second = hole;
     while (second < (len - 1) / 2) {
         second = 2 * (second + 1);
-        if (sort_comp(q.s[first + second], q.s[first + second - 1])) second--;
+        if (sort_comp(q.key(first + second), q.key(first + second - 1))) second--;
         q.put(first + hole, q.get(first + second));
         hole = second;
     }
@@ -99,8 +121,8 @@ CBX_SORT_HD void stdsort_adjust_heap(const SortSeq<Id>& q, int first, int hole, 
 }
 
 // __partial_sort(first, last, last): __make_heap, then __sort_heap.
-template <typename Id>
-CBX_SORT_HD void stdsort_heap_sort(const SortSeq<Id>& q, int first, int last) {
+template <class Seq>
+CBX_SORT_HD void stdsort_heap_sort(const Seq& q, int first, int last) {
     const int len = last - first;
     if (len >= 2) {
         int parent = (len - 2) / 2;
@@ -112,15 +134,15 @@ CBX_SORT_HD void stdsort_heap_sort(const SortSeq<Id>& q, int first, int last) {
     }
     while (last - first > 1) {
         --last;
-        const typename SortSeq<Id>::El v = q.get(last);
+        const typename Seq::El v = q.get(last);
         q.put(last, q.get(first));
         stdsort_adjust_heap(q, first, 0, last - first, v);
     }
 }
 
-template <typename Id>
-CBX_SORT_HD void stdsort_median_to_first(const SortSeq<Id>& q, int r, int a, int b, int c) {
-    const float sa = q.s[a], sb = q.s[b], sc = q.s[c];
+template <class Seq>
+CBX_SORT_HD void stdsort_median_to_first(const Seq& q, int r, int a, int b, int c) {
+    const auto sa = q.key(a), sb = q.key(b), sc = q.key(c);
     if (sort_comp(sa, sb)) {
         if (sort_comp(sb, sc)) q.swap(r, b);
         else if (sort_comp(sa, sc)) q.swap(r, c);
@@ -136,27 +158,27 @@ CBX_SORT_HD void stdsort_median_to_first(const SortSeq<Id>& q, int r, int a, int
 
 // __unguarded_partition_pivot: the median of three moved to first, then the
 // unguarded partition of [first + 1, last) around it; returns the cut.
-template <typename Id>
-CBX_SORT_HD int stdsort_partition_pivot(const SortSeq<Id>& q, int first, int last) {
+template <class Seq>
+CBX_SORT_HD int stdsort_partition_pivot(const Seq& q, int first, int last) {
     const int mid = first + (last - first) / 2;
     stdsort_median_to_first(q, first, first + 1, mid, last - 1);
-    const float pv = q.s[first];  // the pivot stays at first throughout
+    const auto pv = q.key(first);  // the pivot stays at first throughout
     int lo = first + 1, hi = last;
     while (true) {
-        while (sort_comp(q.s[lo], pv)) ++lo;
+        while (sort_comp(q.key(lo), pv)) ++lo;
         --hi;
-        while (sort_comp(pv, q.s[hi])) --hi;
+        while (sort_comp(pv, q.key(hi))) --hi;
         if (!(lo < hi)) return lo;
         q.swap(lo, hi);
         ++lo;
     }
 }
 
-template <typename Id>
-CBX_SORT_HD void stdsort_linear_insert(const SortSeq<Id>& q, int last) {
-    const typename SortSeq<Id>::El v = q.get(last);
+template <class Seq>
+CBX_SORT_HD void stdsort_linear_insert(const Seq& q, int last) {
+    const typename Seq::El v = q.get(last);
     int next = last - 1;
-    while (sort_comp(v.s, q.s[next])) {
+    while (sort_comp(Seq::key_of(v), q.key(next))) {
         q.put(last, q.get(next));
         last = next;
         --next;
@@ -164,12 +186,12 @@ CBX_SORT_HD void stdsort_linear_insert(const SortSeq<Id>& q, int last) {
     q.put(last, v);
 }
 
-template <typename Id>
-CBX_SORT_HD void stdsort_insertion_sort(const SortSeq<Id>& q, int first, int last) {
+template <class Seq>
+CBX_SORT_HD void stdsort_insertion_sort(const Seq& q, int first, int last) {
     if (first == last) return;
     for (int i = first + 1; i != last; ++i) {
-        if (sort_comp(q.s[i], q.s[first])) {
-            const typename SortSeq<Id>::El v = q.get(i);
+        if (sort_comp(q.key(i), q.key(first))) {
+            const typename Seq::El v = q.get(i);
             for (int j = i; j > first; --j) q.put(j, q.get(j - 1));
             q.put(first, v);
         } else {
@@ -185,8 +207,8 @@ constexpr int kStdSortMaxN = 65535;   // ranges packed in 16-bit halves
 // std::sort of [0, n), n <= kStdSortMaxN.  Returns the number of ranges that
 // reached the depth limit and were heap-sorted (0 for almost every input;
 // for the tests).
-template <typename Id>
-CBX_SORT_HD int stdsort_replay(const SortSeq<Id>& q, int n) {
+template <class Seq>
+CBX_SORT_HD int stdsort_replay(const Seq& q, int n) {
     if (n <= 0 || n > kStdSortMaxN) return 0;
     int lg = 0;
     while ((n >> (lg + 1)) != 0) ++lg;  // floor(log2 n) <= 15
@@ -227,6 +249,116 @@ CBX_SORT_HD int stdsort_replay(const SortSeq<Id>& q, int n) {
         stdsort_insertion_sort(q, 0, n);
     }
     return heaped;
+}
+
+// ---------------------------------------------------------------------------
+// The same sort, reduced to what top-p needs and restated with prefix counts
+// so that a wavefront can run it in parallel.
+//
+// Elements are packed words (rank << 16) | id, rank = the score's rank among
+// the distinct scores (descending), so comp(a, b) is rank(a) < rank(b).
+//
+// 1. Only the order of the elements tied at the cutoff, rank kT, matters:
+//    __final_insertion_sort is a stable insertion sort, and after the
+//    introsort loop every element of a range it left (<= 16 elements, or
+//    heap-sorted) is no less than every element of the ranges after it, so the
+//    tied elements end in the order the introsort loop left them.  Ranges
+//    holding no element of rank kT are therefore not sorted at all.
+// 2. __unguarded_partition around pivot v (at first, moved there by
+//    __move_median_to_first) stops its left scan at the elements with
+//    !(comp(x, v)) and its right scan at those with !(comp(v, x)); nothing
+//    between the two scans has moved yet, so the k-th left stop L_k and the
+//    k-th right stop R_k (counted from the right) are swapped exactly while
+//    L_k < R_k.  With lb(p) = left stops before p and ra(p) = right stops
+//    after p: a left stop p is swapped iff ra(p) > lb(p), with partner rank
+//    lb(p); a right stop q iff lb(q) > ra(q), with partner rank ra(q).  The
+//    returned cut is the first unswapped left stop or the leftmost swapped
+//    right stop, whichever comes first (or last: the range's end).
+// Pinned against the serial restatement above and against std::sort itself
+// (tests/native/stdsort_replay.cpp).
+
+CBX_SORT_HD uint32_t pk_rank(uint32_t w) { return w >> 16; }
+
+// __unguarded_partition_pivot of [f, l) (l - f > 16) by prefix counts; tmp
+// holds l - f words.  Returns the cut.
+CBX_SORT_HD int stdsort_partition_counts(uint32_t* w, uint32_t* tmp, int f, int l) {
+    const int m = l - f, mid = f + m / 2;
+    stdsort_median_to_first(PackedSeq{w}, f, f + 1, mid, l - 1);
+    const uint32_t pv = pk_rank(w[f]);
+    const int half = (m + 1) / 2;
+    uint32_t* tl = tmp;
+    uint32_t* tr = tmp + half;
+    int n_r = 0;
+    for (int p = f + 1; p < l; ++p) n_r += !(pv < pk_rank(w[p])) ? 1 : 0;
+    int lb = 0, rb = 0, cut = l;
+    for (int p = f + 1; p < l; ++p) {
+        const uint32_t k = pk_rank(w[p]);
+        const bool is_l = !(k < pv), is_r = !(pv < k);
+        const int ra = n_r - rb - (is_r ? 1 : 0);
+        if (is_l) {
+            if (ra > lb) tl[lb] = w[p];
+            else if (p < cut) cut = p;
+        }
+        if (is_r && lb > ra) {
+            tr[ra] = w[p];
+            if (p < cut) cut = p;
+        }
+        lb += is_l ? 1 : 0;
+        rb += is_r ? 1 : 0;
+    }
+    lb = 0;
+    rb = 0;
+    for (int p = f + 1; p < l; ++p) {
+        const uint32_t k = pk_rank(w[p]);
+        const bool is_l = !(k < pv), is_r = !(pv < k);
+        const int ra = n_r - rb - (is_r ? 1 : 0);
+        const int lbp = lb;
+        lb += is_l ? 1 : 0;
+        rb += is_r ? 1 : 0;
+        if (is_l && ra > lbp) w[p] = tr[lbp];
+        else if (is_r && lbp > ra) w[p] = tl[ra];
+    }
+    return cut;
+}
+
+// The ids of the elements of rank kT in the order std::sort leaves them
+// (written to ids[0 ..]); returns their count.  w[0, n) is the sequence in
+// the reference's input order (id order); it is permuted in place; tmp
+// holds n words.  Serial form of what a wavefront does in the sampler.
+CBX_SORT_HD int stdsort_tied_order(uint32_t* w, uint32_t* tmp, int n, uint32_t kT, uint16_t* ids) {
+    if (n <= 0 || n > kStdSortMaxN) return 0;
+    int lg = 0;
+    while ((n >> (lg + 1)) != 0) ++lg;
+    uint32_t st_range[32];
+    uint8_t st_depth[32];
+    st_range[0] = (uint32_t)n << 16;
+    st_depth[0] = (uint8_t)(2 * lg);
+    int top = 1;
+    while (top > 0) {
+        --top;
+        const int f = (int)(st_range[top] & 0xffffu);
+        int l = (int)(st_range[top] >> 16);
+        int depth = st_depth[top];
+        while (l - f > kStdSortThreshold) {
+            bool has = false;
+            for (int p = f; p < l; ++p) has = has || pk_rank(w[p]) == kT;
+            if (!has) break;
+            if (depth == 0) {  // __partial_sort: rare (adversarial inputs)
+                stdsort_heap_sort(PackedSeq{w}, f, l);
+                break;
+            }
+            --depth;
+            const int cut = stdsort_partition_counts(w, tmp, f, l);
+            st_range[top] = (uint32_t)cut | ((uint32_t)l << 16);
+            st_depth[top] = (uint8_t)depth;
+            ++top;
+            l = cut;
+        }
+    }
+    int m = 0;
+    for (int p = 0; p < n; ++p)
+        if (pk_rank(w[p]) == kT) ids[m++] = (uint16_t)(w[p] & 0xffffu);
+    return m;
 }
 
 }  // namespace cbx

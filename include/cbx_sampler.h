@@ -57,11 +57,13 @@ typedef struct cbx_params {
 #define CBX_INFO_DREW      0x01u /* the uniform was consumed (reference drew from rng) */
 #define CBX_INFO_GREEDY    0x02u /* temp <= 0: first argmax of the probabilities       */
 #define CBX_INFO_EMPTY     0x04u /* every score was -inf: token 0 (main.cpp:792)       */
-#define CBX_INFO_TOPP_TIE  0x08u /* equal scores straddle the top-p cutoff: which of
-                                    them is kept depends on std::sort's tie order     */
+#define CBX_INFO_TOPP_TIE  0x08u /* equal scores straddle the top-p cutoff; the kept
+                                    ones are those the reference's std::sort puts
+                                    first (its order is replayed)                  */
 #define CBX_INFO_NONFINITE 0x10u /* NaN or +inf scores: outside the contract           */
-#define CBX_INFO_OVERFLOW  0x20u /* more survivors than the on-chip capacity:
-                                    token -1, row not sampled                         */
+#define CBX_INFO_OVERFLOW  0x20u /* more survivors than the device's on-chip
+                                    capacity (never on gfx950, whose LDS holds every
+                                    id of a 32768 vocabulary): token -1            */
 
 #define CBX_DRAW_UNIFORM 0 /* uniforms[step][row] supplied by the caller            */
 #define CBX_DRAW_PHILOX  1 /* Philox4x32-10: counter {step lo, step hi, stream lo,
@@ -91,10 +93,13 @@ typedef struct cbx_batch {
                                    but stop_token is masked                        */
     int32_t         draw_mode;  /* CBX_DRAW_UNIFORM or CBX_DRAW_PHILOX              */
     int32_t         max_survivors; /* host hint: bound on ids left by top-k (e.g. the
-                                   largest active top_k); 0 = n_vocab.  Rows that
-                                   exceed it report CBX_INFO_OVERFLOW.  At most
+                                   largest active top_k); 0 = n_vocab.  At most
                                    1024 with n_vocab <= 8448 runs one wavefront
-                                   per row (the fastest form)                      */
+                                   per row (the fastest form).  Rows with more
+                                   survivors (ties at a tiny top-k threshold, top-k
+                                   off) are sampled again on the same stream by a
+                                   second pass at the capacity of the whole
+                                   vocabulary, so every row gets its token      */
     const double*   uniforms;   /* CBX_DRAW_UNIFORM: [n_steps][n_rows] in [0,1)      */
     uint64_t        seed;       /* CBX_DRAW_PHILOX key                              */
     const uint64_t* stream_ids; /* CBX_DRAW_PHILOX: [n_rows]; NULL = row index      */

@@ -601,3 +601,75 @@ def test_topp_tie_rows(cbx, torch_cuda, case):
     tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
     assert np.count_nonzero(ir & parity.INFO_TOPP_TIE) == n  # every row is a tie row
     parity.compare(f"topp_tie_{name}", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_batch_overflow_rows_redone(cbx, torch_cuda):
+    """cbx_sample_batch at max_survivors=1000 (the one-wave kernel, 1024
+    survivors) on a batch where some rows keep far more ids: a top-k
+    threshold tied at 1e-5 (the -1e-10f nudge keeps every tie), and rows with
+    top-k off.  Those rows are sampled again at the vocabulary's capacity in
+    the same call: every token is the oracle's, no row reports overflow."""
+    V, n = 6563, 12
+    rng = np.random.default_rng(0x0F10)
+    x = (rng.standard_normal((n, V)) * 3).astype(F32)
+    plist = []
+    for r in range(n):
+        kind = r % 3
+        if kind == 0:      # 40 ids above 1e-5, 1500 tied at it: k=100 keeps 1540
+            x[r] = -1.0 - rng.random(V).astype(F32)
+            ids = rng.choice(V, size=1540, replace=False)
+            x[r, ids[:40]] = rng.uniform(1e-3, 2e-3, 40).astype(F32)
+            x[r, ids[40:]] = F32(1e-5)
+            plist.append(dict(top_k=100, top_p=0.999, temp=1.0, repeat_penalty=1.2, min_p=0.0,
+                              cfg_weight=0.0))
+        elif kind == 1:    # top-k off: every id survives
+            plist.append(dict(top_k=0, top_p=0.95, temp=0.8, repeat_penalty=1.2, min_p=0.0,
+                              cfg_weight=0.0))
+        else:              # an ordinary row
+            plist.append(dict(top_k=250, top_p=0.9, temp=0.9, repeat_penalty=1.2, min_p=0.0,
+                              cfg_weight=0.0))
+    hist = rng.integers(0, V, size=(n, 100)).astype(np.int32)
+    hl = np.full(n, 100, np.int32)
+    u = rng.random(n)
+    say("batch overflow rows redone at full capacity (one-wave launch)")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, plist, u, hist, hl, max_survivors=1000)
+    tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
+    assert np.all(tg >= 0)
+    parity.compare("batch_overflow_redo", tg, ig, tr, ir, u, pg, pr)
+
+
+@pytest.mark.parametrize("max_survivors", [0, 50])
+def test_topk_off_full_vocab_32768(cbx, torch_cuda, max_survivors):
+    """top_k = 0 at V = 32768: all 32768 ids survive top-k, so top-p sorts the
+    whole row (the workgroup kernel's score sort at capacity 32768).  With a
+    hint of 50 the first launch cannot hold them and the second pass does."""
+    V, n = 32768, 3
+    rng = np.random.default_rng(0x32768 + max_survivors)
+    x = (rng.standard_normal((n, V)) * 3).astype(F32)
+    plist = [dict(top_k=0, top_p=p, temp=0.8, repeat_penalty=1.3, min_p=0.0, cfg_weight=0.0)
+             for p in (0.95, 0.5, 0.999)]
+    hist = rng.integers(0, V, size=(n, 512)).astype(np.int32)
+    hl = np.full(n, 512, np.int32)
+    u = rng.random(n)
+    say(f"top-k off V=32768 max_survivors={max_survivors}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, plist, u, hist, hl, max_survivors=max_survivors)
+    tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
+    parity.compare(f"topk_off_32768_{max_survivors}", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_topp_tie_full_vocab_32768(cbx, torch_cuda):
+    """Equal scores across the top-p cutoff with every id of V = 32768
+    surviving: the replay of std::sort runs on 16-bit score ranks."""
+    V, n = 32768, 2
+    rng = np.random.default_rng(0x77E)
+    x = plateau_rows(rng, n, V, 5000)
+    plist = [dict(top_k=0, top_p=0.5, temp=1.0, repeat_penalty=1.3, min_p=0.0,
+                  cfg_weight=0.0)] * n
+    hist = rng.integers(0, V, size=(n, 300)).astype(np.int32)
+    hl = np.full(n, 300, np.int32)
+    u = rng.random(n)
+    say("top-p tie rows, V=32768, top-k off")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, plist, u, hist, hl)
+    tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
+    assert np.all(ir & parity.INFO_TOPP_TIE)
+    parity.compare("topp_tie_32768", tg, ig, tr, ir, u, pg, pr)
