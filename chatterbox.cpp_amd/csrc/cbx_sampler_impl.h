@@ -136,6 +136,20 @@ __device__ __forceinline__ int wave_or_i(int x) {
     return x;
 }
 
+// Bytes of the LDS region after the three bitmaps (seen, keptw, woff) for a
+// survivor capacity: the largest of its uses (radix histogram, value bins and
+// candidates, the counting sort's offsets and list, the sorted scores or F).
+__host__ __device__ inline size_t region_bytes(int32_t cap) {
+    size_t region = (size_t)kRadixBins * 4;
+    const size_t bins = (size_t)kValueBins * 4 + (size_t)kCandMax * 4;
+    if (bins > region) region = bins;
+    const size_t list = (size_t)(cap < kFastMax ? (cap < 64 ? 64 : cap) : kFastMax);
+    const size_t fast = (size_t)(kSortBins + 4) * 4 + 8 * list;
+    if (fast > region) region = fast;
+    if ((size_t)cap * 4 > region) region = (size_t)cap * 4;
+    return region;
+}
+
 struct Shared {
     int red_i[16];
     float red_f[16];
@@ -1417,39 +1431,69 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
         const bool tie = n_kept < n_surv && sh.tie[0] == sh.tie[1];
         if (tid == 0 && tie) sh.flags |= CBX_INFO_TOPP_TIE;
         if (tie && !(flags & CBX_INFO_NONFINITE)) {
-            // Equal scores straddle the cutoff: the survivors in id order
-            // (ranks from a bitmap of their ids), lane 0 replays the
-            // reference's std::sort, and its first n_kept entries are kept.
-            float* qs = reinterpret_cast<float*>(region);
-            uint16_t* qi = reinterpret_cast<uint16_t*>(qs + NR * BLOCK);
+            // Equal scores straddle the cutoff.  The survivors become words
+            // (rank << 16 | id) in id order -- rank: the first sorted position
+            // of the score, found in the sorted scores; position: from a
+            // bitmap of the ids -- and wave 0 replays the reference's
+            // std::sort over the ranges holding the tied score
+            // (wave_tied_order); of the tied ids the first n_kept - kT are kept.
+            const float T = sh.tie[0];
+            float* vals = reinterpret_cast<float*>(region);
             const int W = (a.n_vocab + 31) >> 5;
 #pragma unroll
             for (int r = 0; r < NR; ++r)
                 if (r * BLOCK + tid < n_surv) {
+                    vals[r * BLOCK + tid] = desc_key_value(x[r]);
                     const uint32_t i = (uint32_t)x[r];
                     atomicOr(&keptw[i >> 5], 1u << (i & 31));
                 }
             __syncthreads();
             (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+            // first sorted position of v: the count of scores above it
+            auto above = [&](float v) {
+                int lo = 0, hi = n_surv;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (vals[mid] > v) lo = mid + 1;
+                    else hi = mid;
+                }
+                return lo;
+            };
+            const int kT = above(T);
+            uint32_t wd[NR];
+            int at[NR];
 #pragma unroll
-            for (int r = 0; r < NR; ++r)
+            for (int r = 0; r < NR; ++r) {
+                at[r] = -1;
+                wd[r] = 0u;
                 if (r * BLOCK + tid < n_surv) {
                     const uint32_t i = (uint32_t)x[r];
-                    const int at = rank_of(keptw, woff, (int)i);
-                    qs[at] = desc_key_value(x[r]);
-                    qi[at] = (uint16_t)i;
+                    wd[r] = ((uint32_t)above(desc_key_value(x[r])) << 16) | i;
+                    at[r] = rank_of(keptw, woff, (int)i);
                 }
-            __syncthreads();
-            if (tid == 0) (void)stdsort_replay(SortSeq<uint16_t>{qs, qi}, n_surv);
+            }
+            __syncthreads();  // the scores are read: the storage takes the words
+            uint32_t* wv = reinterpret_cast<uint32_t*>(region);
+            uint32_t* tmp = wv + n_surv;
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if (at[r] >= 0) wv[at[r]] = wd[r];
             for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
             __syncthreads();
-            for (int i = tid; i < n_kept; i += BLOCK) atomicOr(&keptw[qi[i] >> 5], 1u << (qi[i] & 31));
+            uint16_t* tied = reinterpret_cast<uint16_t*>(tmp);
+            if (wid == 0) (void)wave_tied_order(wv, tmp, n_surv, (uint32_t)kT, tied);
+            __syncthreads();
+            for (int i = tid; i < n_kept - kT; i += BLOCK)
+                atomicOr(&keptw[tied[i] >> 5], 1u << (tied[i] & 31));
             __syncthreads();
             kept = 0;
 #pragma unroll
-            for (int r = 0; r < NR; ++r)
-                if (r * BLOCK + tid < n_surv && bit_of(keptw, (int)(uint32_t)x[r]))
+            for (int r = 0; r < NR; ++r) {
+                const float v = desc_key_value(x[r]);
+                if (r * BLOCK + tid < n_surv &&
+                    (v > T || (v == T && bit_of(keptw, (int)(uint32_t)x[r]))))
                     kept |= (uint64_t)1 << r;
+            }
             __syncthreads();  // finish_row clears the bitmap again
         }
     } else {
@@ -1716,12 +1760,24 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
             if (tie) sh.flags |= CBX_INFO_TOPP_TIE;
         }
         if (tie && !bad) {
-            // Equal scores straddle the cutoff.  Each survivor's key becomes
-            // its rank among the sorted scores (the first position holding its
-            // score: same order, same ties, 16 bits), the (rank, id) pairs go
-            // in id order (positions from a bitmap of the survivor ids), lane
-            // 0 replays the reference's std::sort on them, and the ids at its
-            // first n_kept positions are the kept ones.
+            // Equal scores straddle the cutoff.  Each survivor becomes a word
+            // (rank << 16 | id) -- rank: the first sorted position of its
+            // score (same order, same ties, 16 bits) -- in id order (positions
+            // from a bitmap of the survivor ids).  Wave 0 replays the
+            // reference's std::sort over the ranges holding the tied score
+            // (wave_tied_order) when the LDS holds a second array of the same
+            // size, else lane 0 replays the whole sort; the first n_kept - kT
+            // tied ids are kept.
+            const int kT = uni([&] {  // sorted positions scoring above T
+                const uint32_t key = ~okey(T);
+                int lo = 0, hi = n_surv;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (key32[mid] < key) lo = mid + 1;
+                    else hi = mid;
+                }
+                return lo;
+            }());
             uint32_t rk2[(EPT + 1) / 2];  // two 16-bit ranks per register
 #pragma unroll
             for (int q = 0; q < (EPT + 1) / 2; ++q) rk2[q] = 0u;
@@ -1738,10 +1794,9 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
                     rk2[j >> 1] |= (uint32_t)lo << (16 * (j & 1));
                 }
             }
-            uint16_t* qr = reinterpret_cast<uint16_t*>(region);
-            uint16_t* qi = qr + cap;
+            uint32_t* wv = reinterpret_cast<uint32_t*>(region);
             for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
-            __syncthreads();  // the sorted keys are read: their storage takes the pairs
+            __syncthreads();  // the sorted keys are read: their storage takes the words
 #pragma unroll
             for (int j = 0; j < EPT; ++j)
                 if (s[j] != kNegInf) {
@@ -1754,16 +1809,25 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
             for (int j = 0; j < EPT; ++j)
                 if (s[j] != kNegInf) {
                     const int i = j * BLOCK + tid;
-                    const int at = rank_of(keptw, woff, i);
-                    qr[at] = (uint16_t)(rk2[j >> 1] >> (16 * (j & 1)));
-                    qi[at] = (uint16_t)i;
+                    wv[rank_of(keptw, woff, i)] = ((rk2[j >> 1] >> (16 * (j & 1))) << 16) | (uint32_t)i;
                 }
-            __syncthreads();
-            if (tid == 0) (void)stdsort_replay(SortSeq<uint16_t, uint16_t>{qr, qi}, n_surv);
+            __syncthreads();  // every position is read from the bitmap
             for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
             __syncthreads();
-            for (int i = tid; i < n_kept; i += BLOCK)
-                atomicOr(&keptw[qi[i] >> 5], 1u << (qi[i] & 31));
+            if ((size_t)n_surv * 8 <= region_bytes(cap)) {
+                uint16_t* tied = reinterpret_cast<uint16_t*>(wv + n_surv);
+                if (wid == 0) (void)wave_tied_order(wv, wv + n_surv, n_surv, (uint32_t)kT, tied);
+                __syncthreads();
+                for (int i = tid; i < n_kept - kT; i += BLOCK)
+                    atomicOr(&keptw[tied[i] >> 5], 1u << (tied[i] & 31));
+            } else {
+                if (tid == 0) (void)stdsort_replay(PackedSeq{wv}, n_surv);
+                __syncthreads();
+                for (int i = tid; i < n_kept; i += BLOCK) {
+                    const uint32_t id = wv[i] & 0xffffu;
+                    atomicOr(&keptw[id >> 5], 1u << (id & 31));
+                }
+            }
         }
         __syncthreads();
     }
@@ -1774,7 +1838,8 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int i = j * BLOCK + tid;
-        const bool at_cut = (tie && !bad) ? bit_of(keptw, i) : s[j] >= T;
+        const bool at_cut = (tie && !bad) ? (s[j] > T || (s[j] == T && bit_of(keptw, i)))
+                                          : s[j] >= T;
         const bool k = s[j] != kNegInf && (!use_topp || at_cut);
         kept |= (uint64_t)k << j;
     }

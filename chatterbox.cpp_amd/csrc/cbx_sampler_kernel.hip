@@ -43,14 +43,7 @@ __global__ __launch_bounds__(64) void debug_seqsum_kernel(const float* t, const 
 
 size_t lds_bytes_for(int32_t cap, int32_t n_vocab) {
     const size_t Wp = (size_t)(((n_vocab + 31) / 32 + 3) & ~3);
-    size_t region = (size_t)kRadixBins * 4;                             // radix histogram
-    const size_t bins = (size_t)kValueBins * 4 + (size_t)kCandMax * 4;  // value bins + candidates
-    if (bins > region) region = bins;
-    const size_t list = (size_t)(cap < kFastMax ? (cap < 64 ? 64 : cap) : kFastMax);
-    const size_t fast = (size_t)(kSortBins + 4) * 4 + 8 * list;        // counting sort / list
-    if (fast > region) region = fast;
-    if ((size_t)cap * 4 > region) region = (size_t)cap * 4;             // sorted scores / F
-    return 3 * Wp * 4 + region;
+    return 3 * Wp * 4 + region_bytes(cap);
 }
 
 int32_t max_cap_for_lds(int32_t n_vocab, size_t lds_bytes) {

@@ -578,7 +578,9 @@ TIE_CASES = [
     ("one_wave", 6563, 1000, 200, 1024),      # one-wave kernel, list of 1000
     ("one_wave_small", 500, 100, 60, 1024),
     ("wg_fast", 6563, 1000, 300, 0),          # workgroup kernel, register list
-    ("wg_general", 8194, 0, 3000, 0),         # workgroup kernel, LDS pairs (8194 survivors)
+    ("wg_general", 8194, 0, 3000, 0),         # workgroup kernel, sorted scores (8194
+                                              # survivors): one lane replays the sort
+    ("wg_general_wave", 3000, 0, 1000, 0),    # 3000 survivors: the wavefront replay
 ]
 
 
@@ -589,7 +591,7 @@ def test_topp_tie_rows(cbx, torch_cuda, case):
     probabilities equal the oracle's (which runs std::sort itself)."""
     name, V, k, plateau, ms = case
     rng = np.random.default_rng(zlib.crc32(name.encode()))
-    n = 4 if name == "wg_general" else 32
+    n = 4 if name.startswith("wg_general") else 32
     x = plateau_rows(rng, n, V, plateau)
     plist = [dict(top_k=k, top_p=0.5, temp=1.0, repeat_penalty=1.3, min_p=0.0,
                   cfg_weight=0.0)] * n
