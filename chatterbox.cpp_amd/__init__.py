@@ -173,6 +173,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                       ctypes.POINTER(ctypes.c_uint32), vp]
     lib.cbx_sample_batch.restype = ctypes.c_int
     lib.cbx_sample_batch.argtypes = [vp, ctypes.POINTER(Batch), vp]
+    lib.cbx_sample_batch_static.restype = ctypes.c_int
+    lib.cbx_sample_batch_static.argtypes = [vp, ctypes.POINTER(Batch), vp]
     lib.cbx_debug_expf.restype = ctypes.c_int
     lib.cbx_head_logits.restype = ctypes.c_int
     lib.cbx_head_logits.argtypes = [vp, ctypes.POINTER(Head), i32, i32, i64, vp]
@@ -329,10 +331,11 @@ class Sampler:
                      logits_uncond=None, history=None, history_len=None, allowed=None,
                      force_stop=None, stop_token=0, info=None, probs=None,
                      draw_mode=None, seed=0, stream_ids=None, step0=0, max_survivors=0,
-                     n_vocab=None, stream=None, head=None):
+                     n_vocab=None, stream=None, head=None, static_scratch=False):
         """logits: device float32 [n_steps*n_rows, ld] (or [n_steps, n_rows, ld]);
         params: device uint8 tensor from params_tensor(); tokens: device int32.
-        n_vocab defaults to ld (the row stride)."""
+        n_vocab defaults to ld (the row stride).  static_scratch: call
+        cbx_sample_batch_static (the redo list in the library's device array)."""
         ld = logits.shape[-1]
         total_rows = logits.numel() // ld
         n_rows = total_rows // n_steps
@@ -366,7 +369,8 @@ class Sampler:
         b.ld_probs = 0 if probs is None else probs.shape[-1]
         st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
         if head is None:
-            _check(self.lib.cbx_sample_batch(self.handle, ctypes.byref(b), st))
+            fn = self.lib.cbx_sample_batch_static if static_scratch else self.lib.cbx_sample_batch
+            _check(fn(self.handle, ctypes.byref(b), st))
         else:
             _check(self.lib.cbx_head_sample_batch(self.handle, ctypes.byref(head), ctypes.byref(b),
                                                   st))

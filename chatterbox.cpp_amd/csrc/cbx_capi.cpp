@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "cbx_internal.h"
@@ -35,6 +36,9 @@ struct cbx_sampler {
     // the single-row calls on the handle's own stream
     int32_t* d_redo = nullptr;
     int32_t* d_redo_row = nullptr;
+    // the device's address of the file-scope redo list of
+    // cbx_sample_batch_static (shared by every handle on the device)
+    int32_t* static_redo = nullptr;
     // pinned host staging for the small per-call inputs/outputs
     struct Small {
         cbx_params params;
@@ -49,6 +53,31 @@ struct cbx_sampler {
 namespace {
 
 thread_local char g_err[512] = "";
+
+// The redo list of cbx_sample_batch_static: device memory the library never
+// allocates, one copy per GPU (a file-scope device array, zero when the
+// library is loaded; every redo pass leaves it empty again).  Host code uses
+// each device's address of it, from hipGetSymbolAddress with that device
+// current, never the array's name.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) int32_t scratch[cbx::kRedoWords];
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// The address of `scratch` on `device`, which must be current; resolved once
+// per device.
+hipError_t static_scratch(int device, int32_t** out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = static_cast<int32_t*>(p);
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
 
 int fail(int code, const char* fmt, ...) {
     va_list ap;
@@ -194,6 +223,7 @@ int cbx_sampler_create(cbx_sampler** out, int32_t device, int32_t max_vocab, int
     if (e == hipSuccess) e = hipMemset(s->d_redo, 0, sizeof(int32_t) * cbx::kRedoWords);
     if (e == hipSuccess) e = hipMemset(s->d_redo_row, 0, sizeof(int32_t) * 3);
     if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_small, sizeof(cbx_sampler::Small));
+    if (e == hipSuccess) e = static_scratch(device, &s->static_redo);
     if (e != hipSuccess) {
         release(s);
         return fail(e == hipErrorOutOfMemory ? CBX_ERR_NOMEM : CBX_ERR_HIP,
@@ -289,36 +319,39 @@ int cbx_sample_row(cbx_sampler* s, const float* logits, int32_t n_vocab, const i
                              0, u, token_out, info_out, nullptr);
 }
 
-int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
-    if (!s || !b) return fail(CBX_ERR_INVALID, "cbx_sample_batch: NULL handle or batch");
+}  // extern "C"
+
+namespace {
+// Checks a batched request and fills the kernel arguments (fn names the
+// entry point in messages).
+int batch_args(const char* fn, const cbx_sampler* s, const cbx_batch* b, cbx::KernelArgs& a) {
+    if (!s || !b) return fail(CBX_ERR_INVALID, "%s: NULL handle or batch", fn);
     if (b->n_rows < 1 || b->n_steps < 1)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: n_rows %d, n_steps %d", b->n_rows, b->n_steps);
+        return fail(CBX_ERR_INVALID, "%s: n_rows %d, n_steps %d", fn, b->n_rows, b->n_steps);
     if ((int64_t)b->n_rows * b->n_steps > 0x7fffffffLL)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: n_rows * n_steps exceeds 2^31-1");
+        return fail(CBX_ERR_INVALID, "%s: n_rows * n_steps exceeds 2^31-1", fn);
     if (b->n_vocab < 1 || b->n_vocab > cbx::kMaxVocab)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: n_vocab %d outside [1, %d]", b->n_vocab,
+        return fail(CBX_ERR_INVALID, "%s: n_vocab %d outside [1, %d]", fn, b->n_vocab,
                     cbx::kMaxVocab);
     if (!b->logits || !b->params || !b->tokens)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: NULL logits, params or tokens");
+        return fail(CBX_ERR_INVALID, "%s: NULL logits, params or tokens", fn);
     if (b->ld_logits < b->n_vocab)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: ld_logits %lld < n_vocab %d",
+        return fail(CBX_ERR_INVALID, "%s: ld_logits %lld < n_vocab %d", fn,
                     (long long)b->ld_logits, b->n_vocab);
     if (b->history && (!b->history_len || b->ld_history < 0))
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: history without history_len/ld_history");
+        return fail(CBX_ERR_INVALID, "%s: history without history_len/ld_history", fn);
     if (b->allowed && b->ld_allowed < (b->n_vocab + 31) / 32)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: ld_allowed %lld < ceil(n_vocab/32)",
+        return fail(CBX_ERR_INVALID, "%s: ld_allowed %lld < ceil(n_vocab/32)", fn,
                     (long long)b->ld_allowed);
     if (b->probs && b->ld_probs < b->n_vocab)
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: ld_probs %lld < n_vocab",
-                    (long long)b->ld_probs);
+        return fail(CBX_ERR_INVALID, "%s: ld_probs %lld < n_vocab", fn, (long long)b->ld_probs);
     if (b->draw_mode == CBX_DRAW_UNIFORM) {
-        if (!b->uniforms) return fail(CBX_ERR_INVALID, "cbx_sample_batch: uniforms is NULL");
+        if (!b->uniforms) return fail(CBX_ERR_INVALID, "%s: uniforms is NULL", fn);
     } else if (b->draw_mode != CBX_DRAW_PHILOX) {
-        return fail(CBX_ERR_INVALID, "cbx_sample_batch: unknown draw_mode %d", b->draw_mode);
+        return fail(CBX_ERR_INVALID, "%s: unknown draw_mode %d", fn, b->draw_mode);
     }
-    if (b->max_survivors < 0) return fail(CBX_ERR_INVALID, "cbx_sample_batch: max_survivors < 0");
-    DeviceGuard g(s->device);
-    cbx::KernelArgs a{};
+    if (b->max_survivors < 0) return fail(CBX_ERR_INVALID, "%s: max_survivors < 0", fn);
+    a = cbx::KernelArgs{};
     a.n_rows = b->n_rows;
     a.n_vocab = b->n_vocab;
     a.n_steps = b->n_steps;
@@ -343,7 +376,36 @@ int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
     a.info = b->info;
     a.probs = b->probs;
     a.ld_probs = b->ld_probs;
+    return CBX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
+    cbx::KernelArgs a;
+    const int rc = batch_args("cbx_sample_batch", s, b, a);
+    if (rc != CBX_OK) return rc;
+    DeviceGuard g(s->device);
     CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, (hipStream_t)stream));
+    return CBX_OK;
+}
+
+int cbx_sample_batch_static(cbx_sampler* s, const cbx_batch* b, void* stream) {
+    cbx::KernelArgs a;
+    const int rc = batch_args("cbx_sample_batch_static", s, b, a);
+    if (rc != CBX_OK) return rc;
+    const int32_t full = pick_cap(s, b->n_vocab, 0);
+    const int64_t rows = (int64_t)b->n_rows * b->n_steps;
+    if (a.cap < full && rows > cbx::kRedoMax)
+        return fail(CBX_ERR_INVALID,
+                    "cbx_sample_batch_static: %lld row-steps with max_survivors %d: its redo list "
+                    "holds %d rows (at most %d row-steps per call, or max_survivors 0)",
+                    (long long)rows, b->max_survivors, cbx::kRedoMax, cbx::kRedoMax);
+    if (!s->static_redo)
+        return fail(CBX_ERR_HIP, "cbx_sample_batch_static: no device address of the redo list");
+    DeviceGuard g(s->device);
+    CBX_HIP(launch_with_redo(full, a, s->static_redo, (hipStream_t)stream));
     return CBX_OK;
 }
 

@@ -143,6 +143,18 @@ int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_u
  * streams.  Replaces n_steps x n_rows calls of sample_next_token_ex. */
 int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream);
 
+/* cbx_sample_batch without any device memory of the handle: the rows to
+ * sample again (more survivors than max_survivors allows) go on a redo list
+ * in a file-scope device array of the library, one per GPU, whose address
+ * cbx_sampler_create resolves.  No counterpart in the reference: for callers
+ * that cannot allocate or use allocated scratch per call (code under HIP
+ * graph capture, tight serving loops).  Allocates nothing and calls no
+ * memset.  Limit: with max_survivors below the vocabulary's capacity at most
+ * 4096 row-steps (n_rows * n_steps) per call (CBX_ERR_INVALID beyond).  Every
+ * call on one GPU shares the array: calls that overlap in time on one GPU
+ * (several streams, several handles) race and must not be issued. */
+int cbx_sample_batch_static(cbx_sampler* s, const cbx_batch* b, void* stream);
+
 /* Weight formats of the speech_head projection (ggml type ids; rows of n_embd
  * weights, one per vocab id, ggml ne = [n_embd, n_vocab]). */
 #define CBX_WTYPE_F16  1 /* 2 bytes per weight                                    */
