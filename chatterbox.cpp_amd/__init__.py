@@ -175,18 +175,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_sample_batch.argtypes = [vp, ctypes.POINTER(Batch), vp]
     lib.cbx_sample_batch_static.restype = ctypes.c_int
     lib.cbx_sample_batch_static.argtypes = [vp, ctypes.POINTER(Batch), vp]
-    lib.cbx_debug_expf.restype = ctypes.c_int
     lib.cbx_head_logits.restype = ctypes.c_int
     lib.cbx_head_logits.argtypes = [vp, ctypes.POINTER(Head), i32, i32, i64, vp]
     lib.cbx_head_sample_batch.restype = ctypes.c_int
     lib.cbx_head_sample_batch.argtypes = [vp, ctypes.POINTER(Head), ctypes.POINTER(Batch), vp]
-    lib.cbx_debug_expf.argtypes = [vp, vp, vp, i64, vp]
-    lib.cbx_debug_philox.restype = ctypes.c_int
-    lib.cbx_debug_philox.argtypes = [vp, u64, vp, u64, i32, vp, vp]
-    lib.cbx_debug_seqsum.restype = ctypes.c_int
-    lib.cbx_debug_seqsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
-    lib.cbx_debug_chainsum.restype = ctypes.c_int
-    lib.cbx_debug_chainsum.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp]
     lib.cbx_gguf_read_head.restype = ctypes.c_int
     lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
     lib.cbx_gguf_load_head.restype = ctypes.c_int
@@ -403,24 +395,3 @@ class Sampler:
         """cbx_head_sample_batch: the projection into head.logits (whose
         shape gives the row stride), then sample_batch's sampling."""
         self.sample_batch(logits, params, tokens, head=head, **kw)
-
-    def debug_expf(self, x, out):
-        _check(self.lib.cbx_debug_expf(self.handle, x.data_ptr(), out.data_ptr(), x.numel(),
-                                       _stream_ptr()))
-
-    def debug_seqsum(self, terms, offsets, thr, sums, hits):
-        _check(self.lib.cbx_debug_seqsum(self.handle, terms.data_ptr(), offsets.data_ptr(),
-                                         None if thr is None else thr.data_ptr(),
-                                         offsets.numel() - 1, sums.data_ptr(), hits.data_ptr(),
-                                         _stream_ptr()))
-
-    def debug_chainsum(self, terms, offsets, thr, sums, hits):
-        _check(self.lib.cbx_debug_chainsum(self.handle, terms.data_ptr(), offsets.data_ptr(),
-                                           None if thr is None else thr.data_ptr(),
-                                           offsets.numel() - 1, sums.data_ptr(),
-                                           hits.data_ptr(), _stream_ptr()))
-
-    def debug_philox(self, seed, stream_ids, step, n, out):
-        _check(self.lib.cbx_debug_philox(self.handle, seed,
-                                         None if stream_ids is None else stream_ids.data_ptr(),
-                                         step, n, out.data_ptr(), _stream_ptr()))

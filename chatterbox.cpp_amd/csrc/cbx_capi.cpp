@@ -472,41 +472,4 @@ int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
     return cbx_sample_batch(s, &bb, stream);
 }
 
-int cbx_debug_expf(cbx_sampler* s, const float* in, float* out, int64_t n, void* stream) {
-    if (!s || !in || !out || n < 0) return fail(CBX_ERR_INVALID, "cbx_debug_expf: bad argument");
-    if (n == 0) return CBX_OK;
-    DeviceGuard g(s->device);
-    CBX_HIP(cbx::launch_debug_expf(in, out, n, (hipStream_t)stream));
-    return CBX_OK;
-}
-
-int cbx_debug_seqsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
-                     const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream) {
-    if (!s || !terms || !offsets || !sum || !hit || n_cases < 0)
-        return fail(CBX_ERR_INVALID, "cbx_debug_seqsum: bad argument");
-    if (n_cases == 0) return CBX_OK;
-    DeviceGuard g(s->device);
-    CBX_HIP(cbx::launch_debug_seqsum(terms, offsets, thr, n_cases, sum, hit, (hipStream_t)stream));
-    return CBX_OK;
-}
-
-int cbx_debug_chainsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
-                       const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream) {
-    if (!s || !terms || !offsets || !sum || !hit || n_cases < 0)
-        return fail(CBX_ERR_INVALID, "cbx_debug_chainsum: bad argument");
-    if (n_cases == 0) return CBX_OK;
-    DeviceGuard g(s->device);
-    CBX_HIP(cbx::launch_debug_chain(terms, offsets, thr, n_cases, sum, hit, (hipStream_t)stream));
-    return CBX_OK;
-}
-
-int cbx_debug_philox(cbx_sampler* s, uint64_t seed, const uint64_t* stream_ids, uint64_t step,
-                     int32_t n, double* out, void* stream) {
-    if (!s || !out || n < 0) return fail(CBX_ERR_INVALID, "cbx_debug_philox: bad argument");
-    if (n == 0) return CBX_OK;
-    DeviceGuard g(s->device);
-    CBX_HIP(cbx::launch_debug_philox(seed, stream_ids, step, n, out, (hipStream_t)stream));
-    return CBX_OK;
-}
-
 }  // extern "C"

@@ -85,14 +85,6 @@ hipError_t launch_redo_v256x32(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v1024x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v1024x32(const KernelArgs& a, hipStream_t stream);
 
-hipError_t launch_debug_expf(const float* in, float* out, int64_t n, hipStream_t stream);
-hipError_t launch_debug_seqsum(const float* terms, const int32_t* offsets, const float* thr,
-                              int32_t n_cases, float* sum, int32_t* hit, hipStream_t stream);
-hipError_t launch_debug_chain(const float* terms, const int32_t* offsets, const float* thr,
-                              int32_t n_cases, float* sum, int32_t* hit, hipStream_t stream);
-hipError_t launch_debug_philox(uint64_t seed, const uint64_t* stream_ids, uint64_t step,
-                               int32_t n, double* out, hipStream_t stream);
-
 // The speech_head projection (cbx_head.hip): out0[r][v] = W[v] . hidden0[r] + bias[v]
 // for r < n_rows, v < n_vocab, and the same from hidden1 into out1 in the same
 // launch when hidden1 is given.

@@ -192,68 +192,75 @@ __device__ __forceinline__ uint32_t lds_offset(const T* p) {
 // LDS stores and ORs made by the lanes of `mask` only (a ballot, so a subset
 // of the active lanes): the other lanes are switched off for the one
 // instruction instead of being sent to spare slots by a per-lane select.
-// This kernel runs every lane of its wave on every path (its branches are
-// wave-uniform), so exec is restored to all lanes afterwards.
+// s_and_saveexec narrows exec to the lanes of the mask that are active and
+// keeps the caller's exec, which is put back after the store, so the
+// helpers are right in divergent code too (at the cost of the two scalar
+// instructions any exec switch takes).
 //   pair: w0 at byte offset addr, w1 at addr + 4 (two data registers, so no
 //   register pair is assembled for it)
 __device__ __forceinline__ void lds_store_pair_lanes(uint32_t addr, uint32_t w0, uint32_t w1,
                                                      uint64_t mask) {
+    uint64_t save;
     asm volatile(
-        "s_mov_b64 exec, %3\n\t"
-        "ds_write2_b32 %0, %1, %2 offset1:1\n\t"
-        "s_mov_b64 exec, -1"
-        :
+        "s_and_saveexec_b64 %0, %4\n\t"
+        "ds_write2_b32 %1, %2, %3 offset1:1\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(save)
         : "v"(addr), "v"(w0), "v"(w1), "s"(mask)
-        : "memory");
+        : "memory", "scc");
 }
 __device__ __forceinline__ void lds_store_b64_lanes(uint32_t addr, uint64_t v, uint64_t mask) {
+    uint64_t save;
     asm volatile(
-        "s_mov_b64 exec, %2\n\t"
-        "ds_write_b64 %0, %1\n\t"
-        "s_mov_b64 exec, -1"
-        :
+        "s_and_saveexec_b64 %0, %3\n\t"
+        "ds_write_b64 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(save)
         : "v"(addr), "v"(v), "s"(mask)
-        : "memory");
+        : "memory", "scc");
 }
 __device__ __forceinline__ void lds_store_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
+    uint64_t save;
     asm volatile(
-        "s_mov_b64 exec, %2\n\t"
-        "ds_write_b32 %0, %1\n\t"
-        "s_mov_b64 exec, -1"
-        :
+        "s_and_saveexec_b64 %0, %3\n\t"
+        "ds_write_b32 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(save)
         : "v"(addr), "v"(v), "s"(mask)
-        : "memory");
+        : "memory", "scc");
 }
 // One step of an append: the lanes whose score v is >= b0 store (id, v) at
 // consecutive 8-byte slots from byte offset sb in lane order, and sb moves
-// past them.  v_cmpx writes the lane mask to VCC and EXEC at once; two wait
-// states separate that VALU write of VCC from its VALU reads; exec is all
-// lanes again at the end (the caller's code is wave-uniform).
+// past them.  v_cmp writes the lane mask to VCC (inactive lanes 0),
+// s_and_saveexec narrows exec to it and keeps the caller's exec, which is
+// restored after the store.
 __device__ __forceinline__ uint32_t append_ge(uint32_t sb, float b0, float v, uint32_t id) {
     uint32_t t, cnt;
+    uint64_t save;
     asm volatile(
-        "v_cmpx_le_f32 vcc, %[b0], %[v]\n\t"
-        "s_nop 1\n\t"
+        "v_cmp_le_f32 vcc, %[b0], %[v]\n\t"
+        "s_and_saveexec_b64 %[save], vcc\n\t"
         "v_mbcnt_lo_u32_b32 %[t], vcc_lo, 0\n\t"
         "v_mbcnt_hi_u32_b32 %[t], vcc_hi, %[t]\n\t"
         "v_lshl_add_u32 %[t], %[t], 3, %[sb]\n\t"
         "ds_write2_b32 %[t], %[id], %[v] offset1:1\n\t"
-        "s_mov_b64 exec, -1\n\t"
+        "s_mov_b64 exec, %[save]\n\t"
         "s_bcnt1_i32_b64 %[cnt], vcc\n\t"
         "s_lshl3_add_u32 %[sb], %[cnt], %[sb]"
-        : [t] "=&v"(t), [cnt] "=&s"(cnt), [sb] "+s"(sb)
+        : [t] "=&v"(t), [cnt] "=&s"(cnt), [sb] "+s"(sb), [save] "=&s"(save)
         : [b0] "s"(b0), [v] "v"(v), [id] "v"(id)
         : "vcc", "scc", "memory");
     return sb;
 }
 __device__ __forceinline__ void lds_or_b32_lanes(uint32_t addr, uint32_t v, uint64_t mask) {
+    uint64_t save;
     asm volatile(
-        "s_mov_b64 exec, %2\n\t"
-        "ds_or_b32 %0, %1\n\t"
-        "s_mov_b64 exec, -1"
-        :
+        "s_and_saveexec_b64 %0, %3\n\t"
+        "ds_or_b32 %1, %2\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(save)
         : "v"(addr), "v"(v), "s"(mask)
-        : "memory");
+        : "memory", "scc");
 }
 
 // An opaque copy of a uniform value: predicates built on it in one pass are

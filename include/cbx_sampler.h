@@ -193,27 +193,6 @@ int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n
  * hand-off (main.cpp:706-708) and sample_next_token_ex of one T3 step. */
 int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream);
 
-/* Diagnostics: the device exponential used by the sampler (the glibc expf
- * algorithm restated for the GPU) applied elementwise, and the device Philox
- * uniforms for (seed, stream_ids[i] or i, step).  Device memory, async. */
-int cbx_debug_expf(cbx_sampler* s, const float* in, float* out, int64_t n, void* stream);
-int cbx_debug_philox(cbx_sampler* s, uint64_t seed, const uint64_t* stream_ids,
-                     uint64_t step, int32_t n, double* out, void* stream);
-/* Diagnostics: the device's exact left-to-right binary32 running sum (the
- * evaluation the sampler uses for the reference's float accumulations,
- * main.cpp:759-768 and :786-790).  Case c sums terms[offsets[c] ..
- * offsets[c+1]) (finite, >= 0, 1 to 2048 of them) into sum[c]; when thr is given
- * and thr[c] > 0, hit[c] is the first index (from the case's start) whose
- * running sum is >= thr[c], else -1.  Device memory, async. */
-int cbx_debug_seqsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
-                     const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream);
-/* Diagnostics: the same sums and threshold indices by the one-wavefront
- * kernel's evaluation (terms in per-lane runs, DPP sweep chains or binade
- * segments); 1 to 1088 terms per case, otherwise as cbx_debug_seqsum (the
- * case's sum starts from 0).  Device memory, async. */
-int cbx_debug_chainsum(cbx_sampler* s, const float* terms, const int32_t* offsets,
-                       const float* thr, int32_t n_cases, float* sum, int32_t* hit, void* stream);
-
 /* Thread-local description of the last error on this thread ("" if none). */
 const char* cbx_last_error(void);
 

@@ -74,3 +74,21 @@ def test_python_binding_refuses_missing_library(tmp_path):
     spec.loader.exec_module(mod)
     with pytest.raises(FileNotFoundError):
         mod.load_library(str(tmp_path / "absent.so"))
+
+
+def test_diagnostics_live_in_the_test_library():
+    """The device diagnostics (tests/native/cbx_debug.h) are exported by the
+    test-only libcbx_debug.so and not by the product library."""
+    dbg = os.path.join(HERE, "native", "_build", "libcbx_debug.so")
+    if not os.path.exists(dbg):
+        subprocess.run(["make", "-s", "-C", os.path.join(HERE, "native")], check=True)
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(HERE, "native", "cbx_debug.h")).read(),
+                  flags=re.S)
+    names = set(re.findall(r"\b(cbx_debug_\w+)\s*\(", text))
+    assert len(names) == 4
+    out = subprocess.run(["nm", "-D", "--defined-only", dbg], check=True, capture_output=True,
+                         text=True).stdout
+    assert names <= {line.split()[-1] for line in out.splitlines() if " T " in line}
+    prod = subprocess.run(["nm", "-D", "--defined-only", LIB], check=True, capture_output=True,
+                          text=True).stdout
+    assert "cbx_debug_" not in prod

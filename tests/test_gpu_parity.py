@@ -11,6 +11,7 @@ import os
 import numpy as np
 import pytest
 
+import debug_lib as D
 import oracle_lib as O
 import parity
 import pkg
@@ -112,7 +113,7 @@ def test_device_expf_exhaustive(cbx, torch_cuda):
         bits = torch.arange(n, dtype=torch.int64, device="cuda") + start
         x = (bits - (1 << 32) * (bits >= 2**31).long()).to(torch.int32).view(torch.float32)
         out = torch.empty_like(x)
-        s.debug_expf(x, out)
+        D.expf(x, out)
         host = out.cpu().numpy()
         bad += O.lib().cbx_oracle_expf_mismatch(start, n, host.ctypes.data, 16)
         start += n
@@ -132,7 +133,7 @@ def test_device_running_sum_scan(cbx, torch_cuda):
     dthr = torch.from_numpy(thr).cuda()
     sums = torch.zeros(len(off) - 1, dtype=torch.float32, device="cuda")
     hits = torch.full((len(off) - 1,), -9, dtype=torch.int32, device="cuda")
-    s.debug_seqsum(dt, doff, dthr, sums, hits)
+    D.seqsum(dt, doff, dthr, sums, hits)
     torch.cuda.synchronize()
     got_sum = sums.cpu().numpy()
     got_hit = hits.cpu().numpy()
@@ -159,7 +160,7 @@ def test_device_chain_sums(cbx, torch_cuda):
     say(f"chain sums: {len(parts)} cases, {t2.size} terms")
     sums = torch.zeros(len(parts), dtype=torch.float32, device="cuda")
     hits = torch.full((len(parts),), -9, dtype=torch.int32, device="cuda")
-    s.debug_chainsum(torch.from_numpy(t2).cuda(), torch.from_numpy(off2).cuda(),
+    D.chainsum(torch.from_numpy(t2).cuda(), torch.from_numpy(off2).cuda(),
                      torch.from_numpy(thr2).cuda(), sums, hits)
     torch.cuda.synchronize()
     got_sum, got_hit = sums.cpu().numpy(), hits.cpu().numpy()
@@ -179,7 +180,7 @@ def test_device_philox_matches_oracle(cbx, torch_cuda):
     sids = np.arange(n, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15)
     for seed, step in ((0, 0), (42, 17), (0xDEADBEEFCAFEF00D, 2**40 + 3)):
         out = torch.empty(n, dtype=torch.float64, device="cuda")
-        s.debug_philox(seed, torch.from_numpy(sids.view(np.int64)).cuda(), step, n, out)
+        D.philox(seed, torch.from_numpy(sids.view(np.int64)).cuda(), step, n, out)
         got = out.cpu().numpy()
         want = np.array([O.philox_uniform(seed, int(sids[i]), step) for i in range(n)])
         assert np.array_equal(got, want)
