@@ -287,17 +287,24 @@ def config_single_stream(torch, mod, sampler, stream, dev, O):
     seed = 0x51
     u = np.array([O.philox_uniform(seed, 0, t) for t in range(n)]) if O else None
 
-    def step(i):
+    # top_k 1000 bounds the survivors by 1000 (rows with more, from ties at
+    # the k-th score, are sampled again at full capacity by the redo pass)
+    def step(i, hint=1000):
         t = i % n
         sampler.sample_batch(lg[t:t + 1], prm, tok[t:t + 1], history=hist, history_len=hl,
-                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=t)
+                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=t,
+                             max_survivors=hint)
 
+    ms_nohint = timed(torch, stream, lambda i: step(i, 0), n)
+    got_nohint = tok.cpu().numpy()
     ms_batch = timed(torch, stream, step, n)
     got = tok.cpu().numpy()
+    assert np.array_equal(got, got_nohint), "survivor hint changed tokens"
 
     def all_steps(i):
         sampler.sample_batch(lg, prm, tok, n_steps=n, history=hist, history_len=hl,
-                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=0)
+                             draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=0,
+                             max_survivors=1000)
 
     ms_all = timed(torch, stream, all_steps, 5, warm=1)
     # the row API: host logits in, token out (PCIe copies included)
@@ -309,6 +316,7 @@ def config_single_stream(torch, mod, sampler, stream, dev, O):
     out = {"workload": "B=1, V=6563, 500 steps, history 256, k 1000, p 0.95, T 0.8, pen 1.2, "
                        "min_p 0.05",
            "us_per_step_batch_api": round(ms_batch * 1e3, 2),
+           "us_per_step_batch_api_no_survivor_hint": round(ms_nohint * 1e3, 2),
            "us_per_step_one_launch_500_steps": round(ms_all * 1e3 / n, 3),
            "us_per_step_row_api_pcie": round(ms_row * 1e3, 2)}
     if O is not None:
