@@ -24,10 +24,11 @@
 //          or the libstdc++ discrete_distribution CDF (main.cpp:795-800;
 //          random.tcc:2657-2712)
 //
-// Exactness.  The binary32 running sums take the reference's values: on the
-// fast path by the exact segment scan of cbx_seqsum.h (finite terms), else by
-// one wave reading 64 terms per load and chaining dependent IEEE adds over
-// the lanes (v_readlane), so every partial sum is the reference's.
+// Exactness.  The binary32 running sums take the reference's values: one
+// wave holds a run of consecutive terms per lane and evaluates the sum by
+// binade segments (finite terms; chain_segments_x) or by sweep chains of
+// dependent IEEE adds over the lanes, so every partial sum is the
+// reference's.
 // The binary64 CDF is located in parallel with a certified margin: the
 // parallel cumulative values differ from the reference's sequential ones by
 // < 1.5e-11, so when the uniform lies more than 1e-9 from both neighbouring
@@ -42,7 +43,6 @@
 #include "cbx_expf.h"
 #include "cbx_internal.h"
 #include "cbx_philox.h"
-#include "cbx_seqsum.h"
 #include "cbx_stdsort.h"
 
 // Stage timestamps for a profiling build (CBX_STAGE_CLOCKS defined, one
@@ -70,6 +70,8 @@ constexpr int kCandMax = 512;     // scores in the selected bin
 constexpr int kRadixBins = 4096;  // 12-bit digits of the fallback radix select
 constexpr int kSortBins = 2048;   // value bins of the survivor counting sort
 constexpr int kSortBinMax = 64;   // largest bin the counting sort ranks directly
+constexpr int kKeyBins = 4096;    // value bins of the general path's key sort
+constexpr int kKeyBinMax = 255;   // largest bin it ranks directly (8-bit slots)
 constexpr double kCdfMargin = 1e-9;
 // Word 3 of a raw buffer resource on gfx9-family parts (data format 32-bit,
 // no swizzle): loads past num_records return 0.
@@ -146,7 +148,9 @@ __host__ __device__ inline size_t region_bytes(int32_t cap) {
     const size_t list = (size_t)(cap < kFastMax ? (cap < 64 ? 64 : cap) : kFastMax);
     const size_t fast = (size_t)(kSortBins + 4) * 4 + 8 * list;
     if (fast > region) region = fast;
-    if ((size_t)cap * 4 > region) region = (size_t)cap * 4;
+    // general path: the keys, then the key sort's bin offsets
+    if (cap > kFastMax && (size_t)cap * 4 + (size_t)(kKeyBins + 4) * 4 > region)
+        region = (size_t)cap * 4 + (size_t)(kKeyBins + 4) * 4;
     return region;
 }
 
@@ -599,6 +603,89 @@ __device__ __forceinline__ bool bin_sort(uint64_t (&x)[NR], int n, float blo, fl
     return true;
 }
 
+// Counting sort of the survivors' keys ~okey(s) (ascending = descending
+// score) from the registers (s[j] != -inf: a survivor, every one in [lo, hi])
+// into key32[0, n).  bin(v) = min(NB-1, int((v - lo) * scale)) does not
+// decrease with v, so the keys order first by descending bin; bin offsets come
+// from a block scan, and a key's place inside its bin is the number of smaller
+// keys there plus the equal keys in earlier slots.  Keys carry no ids: equal
+// keys are the same score, so every order among them is the sorted order.
+// Slots are kept in 8 bits, four to a register, and final places in 16 bits.
+// Returns false when the bins cannot be formed or one holds more than
+// kKeyBinMax keys (key32 then holds nothing useful); the caller sorts with the
+// bitonic network.  LDS: key32[n], start u32[kKeyBins + 4].
+template <int BLOCK, int EPT>
+__device__ __forceinline__ bool bin_sort_keys(const float (&s)[EPT], int n, float lo, float hi,
+                                              uint32_t* key32, uint32_t* start, Shared& sh) {
+    constexpr int NB = kKeyBins;
+    constexpr int BPT = NB / BLOCK;  // bins per lane in the scan
+    const int tid = threadIdx.x;
+    const float range = __fsub_rn(hi, lo);
+    const float scale = __fdiv_rn((float)NB, range);
+    if (!(range > 0.0f) || !(scale < kPosInf)) return false;
+    auto rbin = [&](float v) {  // ascending rb = descending score
+        return NB - 1 - min(NB - 1, (int)__fmul_rn(__fsub_rn(v, lo), scale));
+    };
+    for (int b = tid; b < NB + 4; b += BLOCK) start[b] = 0u;
+    __syncthreads();
+    uint32_t slot4[(EPT + 3) / 4];
+#pragma unroll
+    for (int q = 0; q < (EPT + 3) / 4; ++q) slot4[q] = 0u;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (s[j] != kNegInf) {
+            const uint32_t sl = atomicAdd(&start[rbin(s[j])], 1u);
+            slot4[j >> 2] |= min(sl, 255u) << (8 * (j & 3));
+        }
+    __syncthreads();
+    uint32_t c[BPT];
+    int local = 0;
+    uint32_t big = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        c[q] = start[tid * BPT + q];
+        local += (int)c[q];
+        big = max(big, c[q]);
+    }
+    int total;
+    int base = block_excl_scan<BLOCK>(local, sh, total);
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+        start[tid * BPT + q] = (uint32_t)base;
+        base += (int)c[q];
+    }
+    if (tid == 0) start[NB] = (uint32_t)n;
+    if (__syncthreads_or(big > (uint32_t)kKeyBinMax)) return false;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (s[j] != kNegInf)
+            key32[start[rbin(s[j])] + ((slot4[j >> 2] >> (8 * (j & 3))) & 255u)] = ~okey(s[j]);
+    __syncthreads();
+    uint32_t fin2[(EPT + 1) / 2];
+#pragma unroll
+    for (int q = 0; q < (EPT + 1) / 2; ++q) fin2[q] = 0u;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (s[j] != kNegInf) {
+            const int rb = rbin(s[j]);
+            const int s0 = (int)start[rb], s1 = (int)start[rb + 1];
+            const int me = s0 + (int)((slot4[j >> 2] >> (8 * (j & 3))) & 255u);
+            const uint32_t key = ~okey(s[j]);
+            int rank = 0;
+            for (int k = s0; k < s1; ++k) {
+                const uint32_t v = key32[k];
+                rank += (v < key || (v == key && k < me)) ? 1 : 0;
+            }
+            fin2[j >> 1] |= (uint32_t)(s0 + rank) << (16 * (j & 1));
+        }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (s[j] != kNegInf) key32[(fin2[j >> 1] >> (16 * (j & 1))) & 0xffffu] = ~okey(s[j]);
+    __syncthreads();
+    return true;
+}
+
 // Ascending bitonic sort of keys [0, n2) in LDS (n2 a power of two).
 template <int BLOCK>
 __device__ __forceinline__ void bitonic_sort_keys(uint32_t* key, int n2) {
@@ -747,6 +834,153 @@ __device__ __forceinline__ float chain_segments(const float (&t)[CM], int nl, fl
     return P;
 }
 
+// chain_segments with a threshold: the running sum acc0 + t_0 + t_1 + ... of
+// finite terms >= 0 (lane l holding terms l*C .. l*C + C - 1, nl lanes) and,
+// with THR, `hit`: the first term index of this layout whose running sum is
+// >= thr, else -1 (the value returned is then the full sum, otherwise
+// meaningless).  In every round each lane whose exact start is known -- the
+// lanes of the current binade up to and including the one that leaves it --
+// walks its own terms from that start with the reference's adds, so the
+// first lane reaching thr is found in the same pass as the sum.
+template <int C, bool THR, int CM>
+__device__ __forceinline__ float chain_segments_x(const float (&t)[CM], int nl, float acc0, float thr,
+                                                  int& hit) {
+    static_assert(C <= CM, "terms per lane");
+    const int lane = threadIdx.x & 63;
+    hit = -1;
+    float a = acc0;
+    int fa = C;
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        a = __fadd_rn(a, t[k]);
+        if constexpr (THR) fa = (fa == C && a >= thr) ? k : fa;
+    }
+    if constexpr (THR) {
+        const int f0 = __builtin_amdgcn_readlane(fa, 0);
+        if (f0 < C) {
+            hit = f0;
+            return acc0;
+        }
+    }
+    float P = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
+    int lstart = 1;
+    while (lstart < nl) {
+        if (!(P >= 0x1p-100f))  // tiny sums: one add each, from the start
+            return chain_sweeps<C, THR, CM, true>(t, nl, thr, hit, acc0);
+        const uint32_t pb = __builtin_bit_cast(uint32_t, P);
+        const uint32_t bb = pb & 0x7f800000u;  // bits of 2^b
+        const float base = __builtin_bit_cast(float, bb);
+        const float lim = __builtin_bit_cast(float, bb + 0x00800000u);  // 2^(b+1)
+        const int N0 = (int)((pb & 0x7fffffu) | 0x800000u);            // P / u
+        const int p0 = N0 & 1;
+        float A0 = base, A1 = __builtin_bit_cast(float, bb + 1u);  // N = 2^23, 2^23 + 1
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            A0 = __fadd_rn(A0, t[k]);
+            A1 = __fadd_rn(A1, t[k]);
+        }
+        int d0 = A0 < lim ? (int)(__builtin_bit_cast(uint32_t, A0) - bb) : (1 << 24);
+        int d1 = A1 < lim ? (int)(__builtin_bit_cast(uint32_t, A1) - bb) - 1 : (1 << 24);
+        d0 = lane < lstart ? 0 : d0;
+        d1 = lane < lstart ? 0 : d1;
+        auto step = [&](int a0, int a1) {
+            const int n0 = a0 + ((a0 & 1) ? d1 : d0);
+            const int n1 = a1 + ((a1 & 1) ? d0 : d1);
+            d0 = n0;
+            d1 = n1;
+        };
+        step(dpp_i<0x111, 0xf>(0, d0), dpp_i<0x111, 0xf>(0, d1));  // row_shr:1
+        step(dpp_i<0x112, 0xf>(0, d0), dpp_i<0x112, 0xf>(0, d1));  // row_shr:2
+        step(dpp_i<0x114, 0xf>(0, d0), dpp_i<0x114, 0xf>(0, d1));  // row_shr:4
+        step(dpp_i<0x118, 0xf>(0, d0), dpp_i<0x118, 0xf>(0, d1));  // row_shr:8
+        step(dpp_i<0x142, 0xa>(0, d0), dpp_i<0x142, 0xa>(0, d1));  // row_bcast:15
+        step(dpp_i<0x143, 0xc>(0, d0), dpp_i<0x143, 0xc>(0, d1));  // row_bcast:31
+        const int x0 = dpp_i<0x138, 0xf>(0, d0), x1 = dpp_i<0x138, 0xf>(0, d1);  // exclusive
+        const int din = p0 ? x1 : x0, dout = p0 ? d1 : d0;
+        const uint64_t reach = __ballot(N0 + dout >= (1 << 24));
+        const int L = reach ? (int)__builtin_ctzll(reach) : 64;
+        // lanes lstart..min(L, nl - 1) start exactly at P + din units
+        float w = __builtin_bit_cast(float, pb + (uint32_t)din);
+        int fw = C;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            w = __fadd_rn(w, t[k]);
+            if constexpr (THR) fw = (fw == C && w >= thr) ? k : fw;
+        }
+        if constexpr (THR) {
+            const uint64_t hm = __ballot(lane >= lstart && lane <= L && lane < nl && fw < C);
+            if (hm) {
+                const int l = (int)__builtin_ctzll(hm);
+                hit = l * C + __builtin_amdgcn_readlane(fw, l);
+                return P;
+            }
+        }
+        if (reach == 0)  // every remaining lane ends inside the binade
+            return __builtin_bit_cast(float, pb + (uint32_t)__builtin_amdgcn_readlane(dout, 63));
+        P = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), L));
+        lstart = L + 1;
+    }
+    return P;
+}
+
+// The running sum acc + term(0) + ... + term(n-1) (binary32, index order) by
+// one wave, in chunks of 64*C terms (lane l: terms l*C .. l*C + C - 1 of a
+// chunk; odd C reads distinct LDS banks), and with THR the first index whose
+// running sum is >= thr (`hit`, else -1).  finite: every term finite and >= 0
+// and acc finite -- binade segments for C >= 5, sweeps otherwise (and for
+// non-finite terms, exact for NaN and infinities too).  DESC: the terms do
+// not increase, so once fl(acc + term(base)) == acc at a chunk's start every
+// later add leaves acc unchanged (rounding is monotone) and the rest of the
+// sum is skipped; no threshold is crossed after that point either.  The test
+// uses 2*term(base), so that a later term up to twice as large (an exp or a
+// quotient of a slightly smaller score, off by an ulp) is covered too.
+template <int C, bool THR, bool DESC, class Term>
+__device__ __forceinline__ float wave_run(Term&& term, int n, float acc, float thr, int& hit,
+                                          bool finite) {
+    const int lane = threadIdx.x & 63;
+    hit = -1;
+    for (int base = 0; base < n; base += 64 * C) {
+        if (DESC && finite) {
+            const float t0 = unif(term(base));
+            if (__fadd_rn(acc, __fmul_rn(2.0f, t0)) == acc) return acc;
+        }
+        float t[C];
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+            const int i = base + lane * C + q;
+            t[q] = i < n ? term(i) : 0.0f;
+        }
+        const int nl = min(64, (n - base + C - 1) / C);
+        int h = -1;
+        float end;
+        if (C >= 5 && finite) end = chain_segments_x<C, THR>(t, nl, acc, thr, h);
+        else end = chain_sweeps<C, THR, C, true>(t, nl, thr, h, acc);
+        if (THR && h >= 0) {
+            hit = base + h;
+            return end;
+        }
+        acc = end;
+    }
+    return acc;
+}
+
+// wave_run with C picked from n (at most NMAX): 1, 5, 17 or 33 terms per lane.
+template <int NMAX, bool THR, bool DESC, class Term>
+__device__ __forceinline__ float wave_run_sum(Term&& term, int n, float acc, float thr, int& hit,
+                                              bool finite) {
+    n = uni(n);
+    if (NMAX <= 64 || n <= 64) return wave_run<1, THR, DESC>(term, n, acc, thr, hit, finite);
+    if constexpr (NMAX > 64) {
+        if (NMAX <= 320 || n <= 320) return wave_run<5, THR, DESC>(term, n, acc, thr, hit, finite);
+        if constexpr (NMAX > 320) {
+            if (NMAX <= 1088 || n <= 1088)
+                return wave_run<17, THR, DESC>(term, n, acc, thr, hit, finite);
+            if constexpr (NMAX > 1088) return wave_run<33, THR, DESC>(term, n, acc, thr, hit, finite);
+        }
+    }
+    return acc;  // not reached
+}
+
 // acc + v[0] + ... + v[n-1] in index order, binary32, by one wave, in chunks
 // of 64 x 17 terms (lane l holding terms l*17 .. l*17 + 16 of a chunk: odd
 // strides, distinct banks).  finite: every term finite and >= 0 and acc
@@ -817,175 +1051,6 @@ __device__ __forceinline__ int wave_chain_cross_of(Term&& term, int n, float thr
 }
 __device__ __forceinline__ int wave_chain_cross(const float* v, int n, float thr, bool finite = true) {
     return wave_chain_cross_of([&](int i) { return v[i]; }, n, thr, finite);
-}
-
-// DPP lane moves of a step table (identity where no source lane).
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ SeqTab dpp_tab(const SeqTab& x) {
-    SeqTab y;
-    y.d0 = __builtin_amdgcn_update_dpp(0, x.d0, CTRL, ROWMASK, 0xf, false);
-    y.d1 = __builtin_amdgcn_update_dpp(0, x.d1, CTRL, ROWMASK, 0xf, false);
-    y.q = __builtin_amdgcn_update_dpp(2, x.q, CTRL, ROWMASK, 0xf, false);
-    return y;
-}
-
-// Inclusive scan of step tables over the wave (lane 0 first): row shifts by
-// 1, 2, 4, 8 inside each row of 16 lanes, then row broadcasts of lanes 15 and
-// 31 into the following rows.
-__device__ __forceinline__ SeqTab wave_scan_tab(SeqTab T) {
-    T = seq_compose(dpp_tab<0x111, 0xf>(T), T);  // row_shr:1
-    T = seq_compose(dpp_tab<0x112, 0xf>(T), T);  // row_shr:2
-    T = seq_compose(dpp_tab<0x114, 0xf>(T), T);  // row_shr:4
-    T = seq_compose(dpp_tab<0x118, 0xf>(T), T);  // row_shr:8
-    T = seq_compose(dpp_tab<0x142, 0xa>(T), T);  // row_bcast:15 into rows 1, 3
-    T = seq_compose(dpp_tab<0x143, 0xc>(T), T);  // row_bcast:31 into rows 2, 3
-    return T;
-}
-
-// Left-to-right binary32 running sum P + t[i0] + t[i0+1] + ... + t[n-1] of
-// non-negative finite terms, exactly, by one wave (every lane passes the same
-// arguments; n - i0 <= 64*CMAX) with the segment scan of cbx_seqsum.h: per
-// segment each lane loads a contiguous chunk into registers and composes its
-// steps, a wave scan composes the chunks, and the one lane whose chunk holds
-// the segment's end (or the threshold) walks it.  With thr > 0 the walk also
-// stops at the first index whose running sum is >= thr, returned in `hit` (-1
-// when the sum never reaches thr; the returned sum is then the full sum,
-// otherwise meaningless).
-template <int CMAX>
-__device__ __forceinline__ float seq_sum_wave(const float* t, int n, float P, int i0, float thr,
-                                              int& hit) {
-    const int lane = threadIdx.x & 63;
-    hit = -1;
-    n = uni(n);
-    i0 = uni(i0);
-    while (i0 < n) {
-        const int e = seq_unit_exp(P);
-        const int N0 = (int)ldexpf(P, -e);  // exact integer < 2^24
-        const int p0 = N0 & 1;
-        int nthr = kSeqSat;
-        if (thr > 0.0f) nthr = (int)ceilf(fminf(ldexpf(thr, -e), kSeqClamp));
-        const int target = min(nthr, 1 << 24);
-        const int C = uni((n - i0 + 63) >> 6);  // terms per lane, <= CMAX
-        const int first = i0 + lane * C;
-        float tr[CMAX];
-#pragma unroll
-        for (int k = 0; k < CMAX; ++k) {
-            if (k < C) tr[k] = (first + k < n) ? t[first + k] : 0.0f;  // 0: no step
-        }
-        SeqTab T = seq_identity();
-#pragma unroll
-        for (int k = 0; k < CMAX; ++k)
-            if (k < C) T = seq_push(T, seq_step(tr[k], e));
-        T = wave_scan_tab(T);
-        SeqTab X = dpp_tab<0x138, 0xf>(T);  // wave_shr:1 -> exclusive
-        const int d_before = p0 ? X.d1 : X.d0;
-        const int c_before = p0 ? (X.q >> 1) & 1 : X.q & 1;
-        const int n_after = N0 + (p0 ? T.d1 : T.d0);
-        const uint64_t reach = __ballot(n_after >= target);
-        if (reach == 0) {
-            const int total = __builtin_amdgcn_readlane(n_after, 63);
-            return ldexpf((float)total, e);  // total < 2^24: exact
-        }
-        const int L = __builtin_ctzll(reach);
-        int kind = 0, idx = 0, nprev = 0;
-        if (lane == L) {
-            int d = d_before, c = c_before;
-#pragma unroll
-            for (int k = 0; k < CMAX; ++k) {
-                if (k < C && kind == 0) {
-                    const int nb = N0 + d;
-                    seq_apply(d, c, seq_step(tr[k], e));
-                    if (N0 + d >= (1 << 24)) { kind = 1; idx = first + k; nprev = nb; }
-                    else if (N0 + d >= nthr) { kind = 2; idx = first + k; }
-                }
-            }
-        }
-        kind = __builtin_amdgcn_readlane(kind, L);
-        idx = __builtin_amdgcn_readlane(idx, L);
-        nprev = __builtin_amdgcn_readlane(nprev, L);
-        if (kind == 2) {
-            hit = idx;
-            return P;
-        }
-        if (kind == 0) return P;  // unreachable for finite terms; bounds the loop
-        // the term that leaves the binade: one ordinary add of the exact sum
-        P = __fadd_rn(ldexpf((float)nprev, e), t[idx]);
-        if (thr > 0.0f && P >= thr) {
-            hit = idx;
-            return P;
-        }
-        i0 = idx + 1;
-    }
-    return P;
-}
-
-// The same running sum with the terms already in registers: lane l holds
-// terms [l*C, l*C + C) in tr[0, C) (C <= CM, zeros past n), for every
-// segment; terms before i0 count as zero (the identity step).
-template <int CM>
-__device__ __forceinline__ float seq_sum_regs(const float (&tr)[CM], int C, int n, float P, int i0,
-                                              float thr, int& hit) {
-    const int lane = threadIdx.x & 63;
-    hit = -1;
-    n = uni(n);
-    i0 = uni(i0);
-    C = uni(C);
-    const int first = lane * C;
-    while (i0 < n) {
-        const int e = seq_unit_exp(P);
-        const int N0 = (int)ldexpf(P, -e);  // exact integer < 2^24
-        const int p0 = N0 & 1;
-        int nthr = kSeqSat;
-        if (thr > 0.0f) nthr = (int)ceilf(fminf(ldexpf(thr, -e), kSeqClamp));
-        const int target = min(nthr, 1 << 24);
-        SeqTab T = seq_identity();
-#pragma unroll
-        for (int k = 0; k < CM; ++k)
-            if (k < C) T = seq_push(T, seq_step(first + k >= i0 ? tr[k] : 0.0f, e));
-        T = wave_scan_tab(T);
-        SeqTab X = dpp_tab<0x138, 0xf>(T);  // wave_shr:1 -> exclusive
-        const int d_before = p0 ? X.d1 : X.d0;
-        const int c_before = p0 ? (X.q >> 1) & 1 : X.q & 1;
-        const int n_after = N0 + (p0 ? T.d1 : T.d0);
-        const uint64_t reach = __ballot(n_after >= target);
-        if (reach == 0) {
-            const int total = __builtin_amdgcn_readlane(n_after, 63);
-            return ldexpf((float)total, e);  // total < 2^24: exact
-        }
-        const int L = __builtin_ctzll(reach);
-        int kind = 0, idx = 0, nprev = 0;
-        float tc = 0.0f;
-        if (lane == L) {
-            int d = d_before, c = c_before;
-#pragma unroll
-            for (int k = 0; k < CM; ++k) {
-                if (k < C && kind == 0) {
-                    const float t = first + k >= i0 ? tr[k] : 0.0f;
-                    const int nb = N0 + d;
-                    seq_apply(d, c, seq_step(t, e));
-                    if (N0 + d >= (1 << 24)) { kind = 1; idx = first + k; nprev = nb; tc = t; }
-                    else if (N0 + d >= nthr) { kind = 2; idx = first + k; }
-                }
-            }
-        }
-        kind = __builtin_amdgcn_readlane(kind, L);
-        idx = __builtin_amdgcn_readlane(idx, L);
-        nprev = __builtin_amdgcn_readlane(nprev, L);
-        tc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tc), L));
-        if (kind == 2) {
-            hit = idx;
-            return P;
-        }
-        if (kind == 0) return P;  // unreachable for finite terms; bounds the loop
-        // the term that leaves the binade: one ordinary add of the exact sum
-        P = __fadd_rn(ldexpf((float)nprev, e), tc);
-        if (thr > 0.0f && P >= thr) {
-            hit = idx;
-            return P;
-        }
-        i0 = idx + 1;
-    }
-    return P;
 }
 
 // --------------------------------------------------------------- bitmaps
@@ -1394,27 +1459,21 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
         if (wid == 0) {
             // psum = 0 + e_0 + e_1 + ... (e_0 = 1), then q_i = e_i / psum in place,
             // then the first i with q_0 + ... + q_i >= top_p.  Rows holding NaN or
-            // +inf take the term-by-term chains (the segment scan needs finite terms).
-            const bool scan = !(flags & CBX_INFO_NONFINITE);
+            // +inf take the term-by-term chains (the segment scan needs finite
+            // terms).  The sorted terms do not increase: the sums stop once
+            // the adds are no-ops.
+            const bool fin = !(flags & CBX_INFO_NONFINITE);
+            auto e_at = [&](int i) { return E[i]; };
             int hit;
-            const float psum = scan ? seq_sum_wave<kFastMax / 64>(E, n_surv, E[0], 1, 0.0f, hit)
-                                    : wave_chain_sum(E, n_surv, 0.0f, false);
+            const float psum =
+                wave_run_sum<NR * BLOCK, false, true>(e_at, n_surv, 0.0f, 0.0f, hit, fin);
             CBX_STAMP(6);
             for (int i = lane; i < n_surv; i += 64) E[i] = __fdiv_rn(E[i], psum);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            int last;
-            if (scan) {
-                const float q0 = E[0];
-                last = 0;
-                if (!(q0 >= P.top_p)) {
-                    (void)seq_sum_wave<kFastMax / 64>(E, n_surv, q0, 1, P.top_p, hit);
-                    last = hit < 0 ? n_surv - 1 : hit;
-                }
-            } else {
-                last = wave_chain_cross(E, n_surv, P.top_p, false);
-            }
+            (void)wave_run_sum<NR * BLOCK, true, true>(e_at, n_surv, 0.0f, P.top_p, hit, fin);
+            const int last = hit < 0 ? n_surv - 1 : hit;
             if (lane == 0) sh.n_kept = last + 1;
         }
         __syncthreads();
@@ -1551,8 +1610,11 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     //   top-k:        value histogram u32[2048] + candidates f32[512], or the
     //                 radix histogram u32[4096]
     //   fast path:    xbuf u64[2048] (list, cross-wave exchanges), then E f32
-    //   general path: key32 u32[cap] (sorted scores); for a tie at the
-    //                 top-p cutoff, rank u16[cap] | id u16[cap] in its place
+    //   general path: key32 u32[cap] (sorted scores), then the key sort's bin
+    //                 offsets u32[kKeyBins + 4], after the sort the exp terms
+    //                 f32[n_surv] right after the keys when the region holds
+    //                 them; for a tie at the top-p cutoff, words u32[n_surv]
+    //                 (rank << 16 | id) and their partition scratch in its place
     //   finish:       F f32[n_final]
     uint32_t* seen = reinterpret_cast<uint32_t*>(smem);
     uint32_t* keptw = seen + Wp;
@@ -1561,7 +1623,6 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     uint32_t* hist = reinterpret_cast<uint32_t*>(region);
     float* cand = reinterpret_cast<float*>(region + kValueBins * 4);
     uint64_t* xbuf = reinterpret_cast<uint64_t*>(region);
-    float* E = reinterpret_cast<float*>(region);
     uint32_t* key32 = reinterpret_cast<uint32_t*>(region);
     float* F = reinterpret_cast<float*>(region);
 
@@ -1574,6 +1635,9 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     // j*BLOCK stride in a scalar offset, ids >= V read 0 (masked below);
     // non-temporal (cache policy nt): each row's logits are read once.
     const float* lrow = a.logits + rs * a.ld_logits;
+    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
+    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
+    const int32_t* hrow = a.history ? a.history + (int64_t)row * a.ld_history : nullptr;
     float s[EPT];
     {
         const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
@@ -1582,6 +1646,17 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         for (int j = 0; j < EPT; ++j)
             s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                  rl, tid * 4, j * BLOCK * 4, 2));
+    }
+    // the history's first kHistPre*BLOCK ids, issued right behind the row so
+    // that one wait covers both (loads past the history read 0; masked below)
+    constexpr int kHistPre = 4;
+    int32_t hid[kHistPre];
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
+    if (use_pen) {
+#pragma unroll
+        for (int q = 0; q < kHistPre; ++q)
+            hid[q] = __builtin_amdgcn_raw_buffer_load_b32(rh, tid * 4, q * BLOCK * 4, 0);
     }
     if (a.uncond) {
         const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
@@ -1594,15 +1669,17 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         }
     }
     if (tid < 32) tab[tid] = kExp2TabDev.t[tid];
-    // history ids -> seen bitmap, overlapped with the logit loads in flight
-    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
-    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
+    // history ids -> seen bitmap
     for (int w = tid; w < W; w += BLOCK) { keptw[w] = 0u; seen[w] = 0u; }
     if (tid == 0) sh.flags = 0u;
     __syncthreads();
     if (use_pen) {
-        const int32_t* hrow = a.history + (int64_t)row * a.ld_history;
-        for (int j = tid; j < hlen; j += BLOCK) {
+#pragma unroll
+        for (int q = 0; q < kHistPre; ++q) {
+            const int32_t t = hid[q];
+            if (q * BLOCK + tid < hlen && t >= 0 && t < V) atomicOr(&seen[t >> 5], 1u << (t & 31));
+        }
+        for (int j = kHistPre * BLOCK + tid; j < hlen; j += BLOCK) {
             const int32_t t = hrow[j];
             if (t >= 0 && t < V) atomicOr(&seen[t >> 5], 1u << (t & 31));
         }
@@ -1725,31 +1802,51 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     float T = kNegInf;
     bool tie = false;
     if (use_topp) {
+        // counting sort by value bins (finite rows), else the bitonic network
+        if (bad || !bin_sort_keys<BLOCK, EPT>(s, n_surv, sblo, hi, key32, key32 + cap, sh)) {
 #pragma unroll
-        for (int j = 0; j < EPT; ++j)
-            if (s[j] != kNegInf) key32[off++] = ~okey(s[j]);
-        const int n2 = uni(max(64, pow2ceil(n_surv)));
-        for (int i = n_surv + tid; i < n2; i += BLOCK) key32[i] = 0xFFFFFFFFu;
-        __syncthreads();
-        CBX_STAMP(13);
-        bitonic_sort_keys<BLOCK>(key32, n2);
+            for (int j = 0; j < EPT; ++j)
+                if (s[j] != kNegInf) key32[off++] = ~okey(s[j]);
+            const int n2 = uni(max(64, pow2ceil(n_surv)));
+            for (int i = n_surv + tid; i < n2; i += BLOCK) key32[i] = 0xFFFFFFFFu;
+            __syncthreads();
+            CBX_STAMP(13);
+            bitonic_sort_keys<BLOCK>(key32, n2);
+        }
         CBX_STAMP(14);
         const float mx_surv = unif(okey_inv(~key32[0]));
-        // the exp terms in sorted order, formed where the sums read them
-        auto e_of = [&](int i) {
+        // The exp terms in sorted order: formed by every lane into the LDS
+        // after the keys when it holds them, else where the sums read them.
+        // The sums (wave 0) stop once their adds are no-ops.
+        float* const eg = reinterpret_cast<float*>(key32 + n_surv);
+        const bool e_lds = (size_t)n_surv * 8 <= region_bytes(cap);
+        auto e_form = [&](int i) {
             return expf_libm_branchless(__fsub_rn(okey_inv(~key32[i]), mx_surv), tab);
         };
+        if (e_lds) {
+            for (int i = tid; i < n_surv; i += BLOCK) eg[i] = e_form(i);
+            __syncthreads();
+        }
+        auto e_of = [&](int i) { return e_lds ? eg[i] : e_form(i); };
+        constexpr int NG = BLOCK * EPT;
         if (wid == 0) {
-            const float ps = wave_chain_sum_of(e_of, n_surv, 0.0f, !bad);
+            int unused;
+            const float ps = wave_run_sum<NG, false, true>(e_of, n_surv, 0.0f, 0.0f, unused, !bad);
             if (lane == 0) sh.psum = ps;
         }
         __syncthreads();
         CBX_STAMP(15);
         const float psum = unif(sh.psum);
+        if (e_lds) {
+            for (int i = tid; i < n_surv; i += BLOCK) eg[i] = __fdiv_rn(eg[i], psum);
+            __syncthreads();
+        }
         if (wid == 0) {
-            const int last = wave_chain_cross_of(
-                [&](int i) { return __fdiv_rn(e_of(i), psum); }, n_surv, P.top_p, !bad);
-            if (lane == 0) sh.n_kept = last + 1;
+            int hit;
+            (void)wave_run_sum<NG, true, true>(
+                [&](int i) { return e_lds ? eg[i] : __fdiv_rn(e_form(i), psum); }, n_surv, 0.0f,
+                P.top_p, hit, !bad);
+            if (lane == 0) sh.n_kept = (hit < 0 ? n_surv - 1 : hit) + 1;
         }
         __syncthreads();
         const int n_kept = uni(sh.n_kept);

@@ -16,8 +16,8 @@
 //          rows with NaN/+inf or degenerate ranges use an 8-bit radix select
 //   survivors -> LDS list of (descending score, ascending id) keys; counting
 //          sort by value bin, each key placed by its rank inside its bin
-//   top-p (main.cpp:750-772): the binary32 running sums psum and cum by the
-//          exact segment scan (cbx_seqsum.h); min-p [extension]; repetition
+//   top-p (main.cpp:750-772): the binary32 running sums psum and cum by
+//          binade segments or sweep chains; min-p [extension]; repetition
 //          penalty from an LDS bitmap of the history (main.cpp:774-781)
 //   softmax + draw (main.cpp:783-800): the kept exp terms in id order; the
 //          token is located on the parallel binary64 prefix of the exp terms

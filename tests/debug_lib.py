@@ -22,7 +22,7 @@ def lib():
         vp, i32, i64, u64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
         L.cbx_debug_expf.argtypes = [i32, vp, vp, i64, vp]
         L.cbx_debug_philox.argtypes = [i32, u64, vp, u64, i32, vp, vp]
-        L.cbx_debug_seqsum.argtypes = [i32, vp, vp, vp, i32, vp, vp, vp]
+        L.cbx_debug_runsum.argtypes = [i32, vp, vp, vp, vp, i32, vp, vp, vp]
         L.cbx_debug_chainsum.argtypes = [i32, vp, vp, vp, i32, vp, vp, vp]
         _lib = L
     return _lib
@@ -42,10 +42,11 @@ def expf(x, out, device=0):
     _ok(lib().cbx_debug_expf(device, x.data_ptr(), out.data_ptr(), x.numel(), _stream()), "expf")
 
 
-def seqsum(terms, offsets, thr, sums, hits, device=0):
-    _ok(lib().cbx_debug_seqsum(device, terms.data_ptr(), offsets.data_ptr(),
-                               None if thr is None else thr.data_ptr(), offsets.numel() - 1,
-                               sums.data_ptr(), hits.data_ptr(), _stream()), "seqsum")
+def runsum(terms, offsets, thr, desc, sums, hits, device=0):
+    _ok(lib().cbx_debug_runsum(device, terms.data_ptr(), offsets.data_ptr(),
+                               None if thr is None else thr.data_ptr(),
+                               None if desc is None else desc.data_ptr(), offsets.numel() - 1,
+                               sums.data_ptr(), hits.data_ptr(), _stream()), "runsum")
 
 
 def chainsum(terms, offsets, thr, sums, hits, device=0):

@@ -18,12 +18,15 @@ int cbx_debug_expf(int32_t device, const float* in, float* out, int64_t n, void*
 /* The device Philox uniforms for (seed, stream_ids[i] or i, step). */
 int cbx_debug_philox(int32_t device, uint64_t seed, const uint64_t* stream_ids, uint64_t step,
                      int32_t n, double* out, void* stream);
-/* The workgroup kernel's exact left-to-right binary32 running sum: case c sums
- * terms[offsets[c] .. offsets[c+1]) (finite, >= 0, 1 to 2048 of them) into
- * sum[c]; when thr is given and thr[c] > 0, hit[c] is the first index (from
- * the case's start) whose running sum is >= thr[c], else -1. */
-int cbx_debug_seqsum(int32_t device, const float* terms, const int32_t* offsets, const float* thr,
-                     int32_t n_cases, float* sum, int32_t* hit, void* stream);
+/* The workgroup kernel's exact left-to-right binary32 running sums: case c
+ * sums terms[offsets[c] .. offsets[c+1]) (finite, >= 0, 1 to 8192 of them)
+ * from 0 into sum[c]; when thr is given and thr[c] > 0, hit[c] is the first
+ * index (from the case's start) whose running sum is >= thr[c], else -1.
+ * desc (optional): desc[c] != 0 marks a case whose terms do not increase
+ * (the sums may then stop early). */
+int cbx_debug_runsum(int32_t device, const float* terms, const int32_t* offsets, const float* thr,
+                     const uint8_t* desc, int32_t n_cases, float* sum, int32_t* hit,
+                     void* stream);
 /* The same sums and threshold indices by the one-wavefront kernel's
  * evaluation (per-lane runs, DPP sweep chains or binade segments); 1 to 1088
  * terms per case; the case's sum starts from 0. */

@@ -24,21 +24,31 @@ __global__ void debug_philox_kernel(uint64_t seed, const uint64_t* sid, uint64_t
     if (i < n) out[i] = philox_uniform(seed, sid ? sid[i] : (uint64_t)i, step);
 }
 
-// One wave per case: the exact left-to-right binary32 sum of the case's terms
-// (starting from its first term; at most 2048 terms are read) and, for thr > 0, the first index whose
-// running sum reaches thr.
-__global__ __launch_bounds__(64) void debug_seqsum_kernel(const float* t, const int32_t* off,
-                                                          const float* thr, float* sum,
-                                                          int32_t* hit) {
+// One wave per case: the workgroup kernel's running sums (wave_run_sum over
+// up to 8192 terms read from memory, the per-lane run length picked from n):
+// sum[c] = 0 + t_0 + t_1 + ... and, for thr[c] > 0, hit[c] = the first index
+// whose running sum is >= thr[c] (else -1).  desc[c] != 0: the terms do not
+// increase, and the sums may stop once their adds are no-ops.
+__global__ __launch_bounds__(64) void debug_runsum_kernel(const float* t, const int32_t* off,
+                                                          const float* thr, const uint8_t* desc,
+                                                          float* sum, int32_t* hit) {
     const int c = blockIdx.x;
     const int b = off[c], n = off[c + 1] - b;
-    if (n <= 0) return;
-    int h;
+    if (n <= 0 || n > 8192) return;
     const float th = thr ? thr[c] : 0.0f;
-    const float s = seq_sum_wave<kFastMax / 64>(t + b, min(n, kFastMax), t[b], 1, th, h);
+    auto term = [&](int i) { return t[b + i]; };
+    int h = -1, unused;
+    float s;
+    if (desc && desc[c]) {
+        s = wave_run_sum<8192, false, true>(term, n, 0.0f, 0.0f, unused, true);
+        if (th > 0.0f) (void)wave_run_sum<8192, true, true>(term, n, 0.0f, th, h, true);
+    } else {
+        s = wave_run_sum<8192, false, false>(term, n, 0.0f, 0.0f, unused, true);
+        if (th > 0.0f) (void)wave_run_sum<8192, true, false>(term, n, 0.0f, th, h, true);
+    }
     if (threadIdx.x == 0) {
         sum[c] = s;
-        hit[c] = (th > 0.0f && t[b] >= th) ? 0 : h;
+        hit[c] = h;
     }
 }
 
@@ -121,13 +131,14 @@ int cbx_debug_philox(int32_t device, uint64_t seed, const uint64_t* stream_ids, 
     return launch_done(device, hipGetLastError());
 }
 
-int cbx_debug_seqsum(int32_t device, const float* terms, const int32_t* offsets, const float* thr,
-                     int32_t n_cases, float* sum, int32_t* hit, void* stream) {
+int cbx_debug_runsum(int32_t device, const float* terms, const int32_t* offsets, const float* thr,
+                     const uint8_t* desc, int32_t n_cases, float* sum, int32_t* hit,
+                     void* stream) {
     if (!terms || !offsets || !sum || !hit || n_cases < 0) return CBX_ERR_INVALID;
     if (n_cases == 0) return CBX_OK;
     DevGuard g(device);
-    hipLaunchKernelGGL(cbx::debug_seqsum_kernel, dim3(n_cases), dim3(64), 0, (hipStream_t)stream,
-                       terms, offsets, thr, sum, hit);
+    hipLaunchKernelGGL(cbx::debug_runsum_kernel, dim3(n_cases), dim3(64), 0, (hipStream_t)stream,
+                       terms, offsets, thr, desc, sum, hit);
     return launch_done(device, hipGetLastError());
 }
 

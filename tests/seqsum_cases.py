@@ -4,11 +4,13 @@ plain left-to-right binary32 results they must reproduce."""
 import numpy as np
 
 
-def make_cases(n_cases, seed):
+def make_cases(n_cases, seed, max_n=2048, with_order=False):
+    """with_order: also return, per case, whether its terms do not increase
+    (the cases left sorted)."""
     rng = np.random.default_rng(seed)
-    terms, offs, thr, exp_sum, exp_hit = [], [0], [], [], []
+    terms, offs, thr, exp_sum, exp_hit, desc = [], [0], [], [], [], []
     for c in range(n_cases):
-        n = int(rng.integers(1, 2049))
+        n = int(rng.integers(1, max_n + 1))
         mode = c % 7
         sig = 0.5 + 6 * rng.random()
         if mode == 0:
@@ -29,6 +31,7 @@ def make_cases(n_cases, seed):
         t = np.exp((s - s[0]).astype(np.float32)).astype(np.float32)
         if c % 3 == 0:
             t = rng.permutation(t)
+        desc.append(c % 3 != 0)
         if c % 5 == 4:
             # normalised terms: the top-p cumulative search
             total = np.add.accumulate(t, dtype=np.float32)[-1]
@@ -46,6 +49,7 @@ def make_cases(n_cases, seed):
             exp_hit.append(int(idx[0]) if idx.size else -1)
         else:
             exp_hit.append(-1)
-    return (np.concatenate(terms).astype(np.float32), np.array(offs, np.int32),
-            np.array(thr, np.float32), np.array(exp_sum, np.float32),
-            np.array(exp_hit, np.int32))
+    out = (np.concatenate(terms).astype(np.float32), np.array(offs, np.int32),
+           np.array(thr, np.float32), np.array(exp_sum, np.float32),
+           np.array(exp_hit, np.int32))
+    return out + (np.array(desc, np.uint8),) if with_order else out

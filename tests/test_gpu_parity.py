@@ -121,25 +121,32 @@ def test_device_expf_exhaustive(cbx, torch_cuda):
 
 
 def test_device_running_sum_scan(cbx, torch_cuda):
-    # The device's exact segment scan against numpy's left-to-right float32
-    # accumulation, bit for bit, and the threshold index of the top-p search.
+    # The workgroup kernel's running sums (wave_run_sum: binade segments with
+    # the threshold search in the same pass, sweep chains for short runs, the
+    # early stop on sorted terms) against numpy's left-to-right float32
+    # accumulation, bit for bit, and the threshold index of the top-p search;
+    # 1 to 8192 terms per case.
     import seqsum_cases
     torch = torch_cuda
     mod, s = cbx
-    t, off, thr, want_sum, want_hit = seqsum_cases.make_cases(6000, 11)
-    say(f"running-sum scan: {len(off) - 1} cases, {t.size} terms")
-    dt = torch.from_numpy(t).cuda()
-    doff = torch.from_numpy(off).cuda()
-    dthr = torch.from_numpy(thr).cuda()
+    t, off, thr, want_sum, want_hit, desc = seqsum_cases.make_cases(4000, 11, max_n=8192,
+                                                                    with_order=True)
+    say(f"running sums: {len(off) - 1} cases, {t.size} terms")
     sums = torch.zeros(len(off) - 1, dtype=torch.float32, device="cuda")
     hits = torch.full((len(off) - 1,), -9, dtype=torch.int32, device="cuda")
-    D.seqsum(dt, doff, dthr, sums, hits)
+    D.runsum(torch.from_numpy(t).cuda(), torch.from_numpy(off).cuda(),
+             torch.from_numpy(thr).cuda(), torch.from_numpy(desc).cuda(), sums, hits)
     torch.cuda.synchronize()
     got_sum = sums.cpu().numpy()
     got_hit = hits.cpu().numpy()
+    bad = np.nonzero(got_sum.view(np.uint32) != want_sum.view(np.uint32))[0]
+    assert bad.size == 0, (bad[:5], got_sum[bad[:5]], want_sum[bad[:5]])
     has_thr = thr > 0
-    assert np.array_equal(got_sum[~has_thr].view(np.uint32), want_sum[~has_thr].view(np.uint32))
     assert np.array_equal(got_hit[has_thr], want_hit[has_thr])
+    assert np.array_equal(got_hit[~has_thr], np.full((~has_thr).sum(), -1, np.int32))
+    # every run length, both orders and long lists were exercised
+    n = np.diff(off)
+    assert (n <= 64).sum() > 10 and ((n > 1088) & (desc == 1)).sum() > 100
 
 
 def test_device_chain_sums(cbx, torch_cuda):

@@ -115,30 +115,6 @@ def test_philox_uniform_construction():
     assert abs(np.mean(us) - 0.5) < 0.02
 
 
-# ---------------------------------------------------------------- segment scan
-
-@pytest.fixture(scope="module")
-def seqsum_bin(tmp_path_factory):
-    out = str(tmp_path_factory.mktemp("native") / "seqsum_rules")
-    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-o", out,
-                    os.path.join(NATIVE, "seqsum_rules.cpp")], check=True)
-    return out
-
-
-@pytest.mark.parametrize("seed", [1, 2])
-def test_segment_scan_rules_match_sequential_float_sums(seqsum_bin, seed):
-    # The parity-table rules of cbx_seqsum.h, run as the device runs them over
-    # 64 lanes, against the plain left-to-right binary32 loop: sums of sorted
-    # and shuffled exp terms (many ties, near-equal, wide, tiny), and the first
-    # index whose running sum of normalised terms reaches a threshold.
-    r = subprocess.run([seqsum_bin, "20000", str(seed)], check=True, capture_output=True,
-                       text=True)
-    bad_sum, bad_hit, cases, segments = (int(v) for v in r.stdout.split()[-4:])
-    assert cases == 20000
-    assert segments > 2 * cases  # binade changes are exercised, not only one segment
-    assert bad_sum == 0 and bad_hit == 0, r.stdout
-
-
 def test_stdsort_replay_matches_libstdcxx(tmp_path):
     """The one-lane restatement of libstdc++'s std::sort (csrc/cbx_stdsort.h)
     orders (id, score) pairs exactly as std::sort does with the reference's
