@@ -164,6 +164,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_sampler_create.argtypes = [ctypes.POINTER(vp), i32, i32, i32]
     lib.cbx_sampler_destroy.restype = ctypes.c_int
     lib.cbx_sampler_destroy.argtypes = [vp]
+    lib.cbx_sampler_set_latency_rows.restype = ctypes.c_int
+    lib.cbx_sampler_set_latency_rows.argtypes = [vp, ctypes.c_int64]
     lib.cbx_sample_row.restype = ctypes.c_int
     lib.cbx_sample_row.argtypes = [vp, vp, i32, vp, i32, ctypes.POINTER(Params), ctypes.c_double,
                                    ctypes.POINTER(i32), ctypes.POINTER(ctypes.c_uint32)]
@@ -297,6 +299,11 @@ class Sampler:
             self.close()
         except Exception:
             pass
+
+    def set_latency_rows(self, rows: int):
+        """Calls of at most `rows` row-steps run at full survivor capacity on
+        the workgroup kernel (default 512; 0: never)."""
+        _check(self.lib.cbx_sampler_set_latency_rows(self.handle, rows))
 
     # -- single row, host memory (the reference call shape) -------------------
     def sample_row(self, logits, history, params, u, logits_uncond=None, allowed=None,

@@ -39,6 +39,8 @@ struct cbx_sampler {
     // the device's address of the file-scope redo list of
     // cbx_sample_batch_static (shared by every handle on the device)
     int32_t* static_redo = nullptr;
+    // launches of at most this many row-steps run at full capacity
+    int64_t latency_rows = cbx::kLatencyRows;
     // pinned host staging for the small per-call inputs/outputs
     struct Small {
         cbx_params params;
@@ -143,8 +145,14 @@ int32_t pick_cap(const cbx_sampler* s, int32_t n_vocab, int32_t hint) {
 // go on the redo list `redo` and are sampled again, on the same stream, at
 // the largest capacity the device's LDS allows -- the whole vocabulary for
 // every n_vocab <= 32768 on gfx950.
-hipError_t launch_with_redo(int32_t full, cbx::KernelArgs a, int32_t* redo, hipStream_t st) {
+//
+// A launch of at most `latency_rows` rows is bound by one row's latency, not
+// by throughput: it runs at full capacity whatever the hint (the workgroup
+// kernel, a row spread over several waves, with nothing to redo).
+hipError_t launch_with_redo(int32_t full, cbx::KernelArgs a, int32_t* redo, int64_t latency_rows,
+                            hipStream_t st) {
     const int64_t rows = (int64_t)a.n_steps * a.n_rows;
+    if (rows <= latency_rows) a.cap = full;
     a.redo = a.cap < full ? redo : nullptr;
     a.redo_max = (int32_t)(rows < cbx::kRedoMax ? rows : cbx::kRedoMax);
     hipError_t e = cbx::launch_sample(a, st);
@@ -233,6 +241,13 @@ int cbx_sampler_create(cbx_sampler** out, int32_t device, int32_t max_vocab, int
     return CBX_OK;
 }
 
+int cbx_sampler_set_latency_rows(cbx_sampler* s, int64_t rows) {
+    if (!s) return fail(CBX_ERR_INVALID, "cbx_sampler_set_latency_rows: NULL handle");
+    if (rows < 0) return fail(CBX_ERR_INVALID, "cbx_sampler_set_latency_rows: rows < 0");
+    s->latency_rows = rows;
+    return CBX_OK;
+}
+
 int cbx_sampler_destroy(cbx_sampler* s) {
     if (!s) return CBX_OK;
     release(s);
@@ -298,7 +313,7 @@ int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_u
     a.info = s->d_info;
     a.probs = probs_out ? s->d_probs : nullptr;
     a.ld_probs = n_vocab;
-    CBX_HIP(launch_with_redo(pick_cap(s, n_vocab, 0), a, s->d_redo_row, st));
+    CBX_HIP(launch_with_redo(pick_cap(s, n_vocab, 0), a, s->d_redo_row, s->latency_rows, st));
     CBX_HIP(hipMemcpyAsync(&hs->token, s->d_token, sizeof(int32_t), hipMemcpyDeviceToHost, st));
     CBX_HIP(hipMemcpyAsync(&hs->info, s->d_info, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     if (probs_out)
@@ -387,7 +402,8 @@ int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
     const int rc = batch_args("cbx_sample_batch", s, b, a);
     if (rc != CBX_OK) return rc;
     DeviceGuard g(s->device);
-    CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, (hipStream_t)stream));
+    CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, s->latency_rows,
+                             (hipStream_t)stream));
     return CBX_OK;
 }
 
@@ -405,7 +421,7 @@ int cbx_sample_batch_static(cbx_sampler* s, const cbx_batch* b, void* stream) {
     if (!s->static_redo)
         return fail(CBX_ERR_HIP, "cbx_sample_batch_static: no device address of the redo list");
     DeviceGuard g(s->device);
-    CBX_HIP(launch_with_redo(full, a, s->static_redo, (hipStream_t)stream));
+    CBX_HIP(launch_with_redo(full, a, s->static_redo, s->latency_rows, (hipStream_t)stream));
     return CBX_OK;
 }
 

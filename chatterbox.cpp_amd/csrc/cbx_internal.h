@@ -50,6 +50,9 @@ constexpr int32_t kMaxVocab = 32768;
 // Survivors after top-k that the one-wave kernel holds; launches whose
 // capacity is at most this (and V <= kWaveMaxVocab) use it.
 constexpr int32_t kWaveCap = 1024;
+// Launches of at most this many rows (two per CU) run the workgroup kernel at
+// full survivor capacity: one row's latency, not throughput, sets their time.
+constexpr int64_t kLatencyRows = 512;
 constexpr int32_t kWaveMaxVocab = 256 * 33;
 
 // Largest survivor capacity whose lists fit `lds_bytes` of LDS for n_vocab.
@@ -70,18 +73,18 @@ hipError_t launch_w33(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w16t(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w26t(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w33t(const KernelArgs& a, hipStream_t stream);
-hipError_t launch_v256x16(const KernelArgs& a, hipStream_t stream);
-hipError_t launch_v256x26(const KernelArgs& a, hipStream_t stream);
-hipError_t launch_v256x32(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v512x8(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v512x13(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_v512x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v1024x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v1024x32(const KernelArgs& a, hipStream_t stream);
 // After a launch at capacity below the vocabulary's: sample again, at a.cap,
 // the rows it put on its redo list, on the same stream (one workgroup per
 // listed row; the last workgroup clears the list for the next launch).
 hipError_t launch_redo(const KernelArgs& a, hipStream_t stream);
-hipError_t launch_redo_v256x16(const KernelArgs& a, hipStream_t stream);
-hipError_t launch_redo_v256x26(const KernelArgs& a, hipStream_t stream);
-hipError_t launch_redo_v256x32(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v512x8(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v512x13(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_redo_v512x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v1024x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v1024x32(const KernelArgs& a, hipStream_t stream);
 

@@ -2057,23 +2057,22 @@ hipError_t launch_redo_cfg(const KernelArgs& a, hipStream_t stream) {
 // The redo pass at capacity a.cap (every row of the vocabulary, on gfx950).
 template <int BLOCK, int EPT>
 hipError_t launch_redo_for(const KernelArgs& a, hipStream_t stream) {
-    if constexpr (4 * BLOCK <= kFastMax) return launch_redo_cfg<BLOCK, EPT, 8>(a, stream);
-    else return launch_redo_cfg<BLOCK, EPT, kFastMax / BLOCK>(a, stream);
+    return launch_redo_cfg<BLOCK, EPT, kFastMax / BLOCK>(a, stream);
 }
 
 // Variant by survivor capacity: the smallest register list that holds `cap`
-// survivors, or the full kernel when cap exceeds the register lists.
+// survivors, or the full kernel when cap exceeds the register lists (the
+// lists hold at most kFastMax survivors: kFastMax / BLOCK rows per lane).
 template <int BLOCK, int EPT>
 hipError_t launch_for(const KernelArgs& a, hipStream_t stream) {
+    constexpr int NRMAX = kFastMax / BLOCK;
+    static_assert(NRMAX >= 1 && NRMAX * BLOCK == kFastMax, "register list rows");
     if (a.cap <= BLOCK) return launch_cfg<BLOCK, EPT, 1, false>(a, stream);
-    if constexpr (4 * BLOCK <= kFastMax) {
+    if constexpr (NRMAX > 4) {
         if (a.cap <= 4 * BLOCK) return launch_cfg<BLOCK, EPT, 4, false>(a, stream);
-        if (a.cap <= kFastMax) return launch_cfg<BLOCK, EPT, 8, false>(a, stream);
-        return launch_cfg<BLOCK, EPT, 8, true>(a, stream);
-    } else {
-        if (a.cap <= kFastMax) return launch_cfg<BLOCK, EPT, kFastMax / BLOCK, false>(a, stream);
-        return launch_cfg<BLOCK, EPT, kFastMax / BLOCK, true>(a, stream);
     }
+    if (a.cap <= kFastMax) return launch_cfg<BLOCK, EPT, NRMAX, false>(a, stream);
+    return launch_cfg<BLOCK, EPT, NRMAX, true>(a, stream);
 }
 
 }  // namespace

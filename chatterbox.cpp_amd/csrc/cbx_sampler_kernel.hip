@@ -29,18 +29,18 @@ hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
         if (a.n_vocab <= kWaveMaxVocab)
             return a.n_vocab > 256 * 32 ? launch_w33t(a, stream) : launch_w33(a, stream);
     }
-    // registers per lane sized to the vocabulary (6563 -> 26 per lane)
-    if (a.n_vocab <= 256 * 16) return launch_v256x16(a, stream);
-    if (a.n_vocab <= 256 * 26) return launch_v256x26(a, stream);
-    if (a.n_vocab <= 256 * 32) return launch_v256x32(a, stream);
+    // registers per lane sized to the vocabulary (6563 -> 13 per lane)
+    if (a.n_vocab <= 512 * 8) return launch_v512x8(a, stream);
+    if (a.n_vocab <= 512 * 13) return launch_v512x13(a, stream);
+    if (a.n_vocab <= 512 * 16) return launch_v512x16(a, stream);
     if (a.n_vocab <= 1024 * 16) return launch_v1024x16(a, stream);
     return launch_v1024x32(a, stream);
 }
 
 hipError_t launch_redo(const KernelArgs& a, hipStream_t stream) {
-    if (a.n_vocab <= 256 * 16) return launch_redo_v256x16(a, stream);
-    if (a.n_vocab <= 256 * 26) return launch_redo_v256x26(a, stream);
-    if (a.n_vocab <= 256 * 32) return launch_redo_v256x32(a, stream);
+    if (a.n_vocab <= 512 * 8) return launch_redo_v512x8(a, stream);
+    if (a.n_vocab <= 512 * 13) return launch_redo_v512x13(a, stream);
+    if (a.n_vocab <= 512 * 16) return launch_redo_v512x16(a, stream);
     if (a.n_vocab <= 1024 * 16) return launch_redo_v1024x16(a, stream);
     return launch_redo_v1024x32(a, stream);
 }

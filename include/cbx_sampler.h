@@ -95,7 +95,9 @@ typedef struct cbx_batch {
     int32_t         max_survivors; /* host hint: bound on ids left by top-k (e.g. the
                                    largest active top_k); 0 = n_vocab.  At most
                                    1024 with n_vocab <= 8448 runs one wavefront
-                                   per row (the fastest form).  Rows with more
+                                   per row (the fastest form for large calls;
+                                   small calls: cbx_sampler_set_latency_rows).
+                                   Rows with more
                                    survivors (ties at a tiny top-k threshold, top-k
                                    off) are sampled again on the same stream by a
                                    second pass at the capacity of the whole
@@ -120,6 +122,15 @@ int32_t cbx_max_vocab(void);
 int cbx_sampler_create(cbx_sampler** out, int32_t device, int32_t max_vocab,
                        int32_t max_history);
 int cbx_sampler_destroy(cbx_sampler* s);
+
+/* Launch policy (no counterpart in the reference, which samples one row on
+ * the CPU): a call of at most `rows` row-steps (n_rows * n_steps; default
+ * 512, two per CU on MI355X) is bound by one row's latency and runs at full
+ * survivor capacity, ignoring max_survivors -- a row spread over the waves of
+ * a workgroup, and no redo pass.  Larger calls keep max_survivors (one wave
+ * per row while the survivors fit).  0 turns the rule off.  Results are the
+ * same either way. */
+int cbx_sampler_set_latency_rows(cbx_sampler* s, int64_t rows);
 
 /* Single row, host memory in and out, synchronous: the reference call shape
  * (logits, history, params in; token out).  Replaces the body of

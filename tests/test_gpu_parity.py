@@ -34,6 +34,18 @@ def torch_cuda():
 
 @pytest.fixture(scope="module")
 def cbx(torch_cuda):
+    # The small-launch rule (calls of at most 512 row-steps run the workgroup
+    # kernel at full capacity) is off here, so that each test's launch takes
+    # the kernel its survivor bound names; test_latency_rule_* cover the rule.
+    mod = pkg.load()
+    s = mod.Sampler(device=0, max_vocab=32768, max_history=4096)
+    s.set_latency_rows(0)
+    yield mod, s
+    s.close()
+
+
+@pytest.fixture(scope="module")
+def cbx_default(torch_cuda):
     mod = pkg.load()
     s = mod.Sampler(device=0, max_vocab=32768, max_history=4096)
     yield mod, s
@@ -683,3 +695,75 @@ def test_topp_tie_full_vocab_32768(cbx, torch_cuda):
     tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
     assert np.all(ir & parity.INFO_TOPP_TIE)
     parity.compare("topp_tie_32768", tg, ig, tr, ir, u, pg, pr)
+
+
+# ---------------------------------------------- the small-launch rule (default)
+
+def test_latency_rule_batched_streams(cbx_default, torch_cuda):
+    """Default handle: B=256 streams x 2 steps (512 row-steps) with the
+    survivor bound 1000 run on the workgroup kernel at full capacity; Philox
+    draws; every token, flag and probability the oracle's."""
+    w = pkg.workloads()
+    d = w.batched_streams(B=256, steps=2, seed=0x5EED35)
+    n = d["logits"].shape[0]
+    seed, step0 = 0xFACE, 3
+    u = np.array([O.philox_uniform(seed, r % 256, step0 + r // 256) for r in range(n)])
+    say("latency rule: batched streams 256 x 2, max_survivors=1000")
+    tg, ig, pg = gpu_batch(cbx_default, torch_cuda, d["logits"], d["params"], None, d["history"],
+                           d["hist_len"], n_steps=2, draw_mode=1, seed=seed, step0=step0,
+                           max_survivors=1000)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
+    parity.compare("latency_rule_batched", tg, ig, tr, ir, u, pg, pr)
+
+
+@pytest.mark.parametrize("V", [6563, 8194, 3000])
+def test_latency_rule_masked(cbx_default, torch_cuda, V):
+    """Default handle: masked rows with forced stops, min-p and penalty, 256
+    rows at survivor bound 1024 (full capacity under the rule)."""
+    w = pkg.workloads()
+    d = w.masked_stress(B=256, V=V, seed=0x5EED7 + V)
+    u = O.mt_canonical(13 + V, d["B"])
+    say(f"latency rule: masked B=256 V={V}")
+    tg, ig, pg = gpu_batch(cbx_default, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], allowed=d["allowed"], force_stop=d["force_stop"],
+                           stop=d["stop"], max_survivors=1024)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"],
+                             allowed=d["allowed"], force_stop=d["force_stop"], stop=d["stop"])
+    parity.compare(f"latency_rule_masked_{V}", tg, ig, tr, ir, u, pg, pr)
+
+
+def test_latency_rule_same_results_either_way(cbx_default, torch_cuda):
+    """The rule changes the kernel, not the result: a CFG batch of 128 rows
+    with top-p ties and tiny top-k ties sampled with the rule on and off is
+    identical bit for bit (tokens, flags, probabilities) and the oracle's."""
+    torch = torch_cuda
+    mod, s = cbx_default
+    rng = np.random.default_rng(0x1A7E)
+    V, n = 6563, 128
+    x = (rng.standard_normal((n, V)) * 3).astype(np.float32)
+    un = (x + rng.standard_normal((n, V))).astype(np.float32)
+    plist = []
+    for r in range(n):
+        if r % 3 == 0:  # equal scores across the top-p cutoff
+            ids = rng.choice(V, size=120, replace=False)
+            x[r, ids[:2]] = [14.0, 13.0]
+            x[r, ids[2:]] = 11.0
+            un[r, ids] = x[r, ids]
+        plist.append(dict(top_k=1000 if r % 3 == 0 else [50, 250][r % 2],
+                          top_p=0.6 if r % 3 == 0 else 0.95,
+                          temp=0.8, repeat_penalty=1.2, min_p=0.02, cfg_weight=0.5))
+    hist = rng.integers(0, V, size=(n, 300)).astype(np.int32)
+    hl = rng.integers(0, 301, size=n).astype(np.int32)
+    u = rng.random(n)
+    say("latency rule on/off: CFG 128 rows")
+    on = gpu_batch(cbx_default, torch, x, plist, u, hist, hl, uncond=un, max_survivors=1000)
+    s.set_latency_rows(0)
+    try:
+        off = gpu_batch(cbx_default, torch, x, plist, u, hist, hl, uncond=un, max_survivors=1000)
+    finally:
+        s.set_latency_rows(512)
+    assert np.array_equal(on[0], off[0]) and np.array_equal(on[1], off[1])
+    assert np.array_equal(on[2].view(np.uint32), off[2].view(np.uint32))
+    tr, ir, pr = oracle_rows(x, plist, u, hist, hl, uncond=un)
+    parity.compare("latency_rule_on_off", on[0], on[1], tr, ir, u, on[2], pr)
+    assert np.count_nonzero(on[1] & parity.INFO_TOPP_TIE) > 10
