@@ -72,7 +72,10 @@ constexpr int kSortBins = 2048;   // value bins of the survivor counting sort
 constexpr int kSortBinMax = 64;   // largest bin the counting sort ranks directly
 constexpr int kKeyBins = 4096;    // value bins of the general path's key sort
 constexpr int kKeyBinMax = 255;   // largest bin it ranks directly (8-bit slots)
-constexpr double kCdfMargin = 1e-9;
+// Relative distance from u to a located CDF boundary beyond which the draw
+// on the binary64 prefix of the exp terms is certain (the reference's values
+// are within 2^-23 relative of it).
+constexpr double kDrawMargin = 3e-7;
 // Word 3 of a raw buffer resource on gfx9-family parts (data format 32-bit,
 // no swizzle): loads past num_records return 0.
 constexpr int kBufferWord3 = 0x00020000;
@@ -158,17 +161,15 @@ struct Shared {
     int red_i[16];
     float red_f[16];
     float red_f2[16];
-    double red_d[16];
     uint32_t sel_digit, sel_above;
     int bin, above_bins, n_cand, above;
     float thr;
     float psum;        // broadcast of a running sum
     float mx;          // broadcast of the top survivor score
     int n_kept;        // survivors after top-p
-    int token;
-    double cdf_lo, cdf_hi;
     float tie[2];      // scores at the top-p cutoff and just after it
     uint32_t flags;
+    uint32_t mxk;      // okey of the largest kept score (an LDS maximum)
 };
 
 // Exclusive block scan of one int per lane; `total` receives the block sum.
@@ -198,26 +199,6 @@ __device__ __forceinline__ int block_sum(int v, Shared& sh) {
     return total;
 }
 
-// Exclusive block scan of one double per lane (approximate: any order).
-template <int BLOCK>
-__device__ __forceinline__ double block_excl_scan_f64(double v, Shared& sh, double& total) {
-    constexpr int NW = BLOCK / 64;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const double incl = wave_incl_scan_f64(v, lane);
-    if (lane == 63) sh.red_d[wid] = incl;
-    __syncthreads();
-    double before = 0.0, tot = 0.0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        const double t = sh.red_d[w];
-        if (w < wid) before = __dadd_rn(before, t);
-        tot = __dadd_rn(tot, t);
-    }
-    __syncthreads();
-    total = tot;
-    return __dsub_rn(__dadd_rn(before, incl), v);
-}
-
 template <int BLOCK>
 __device__ __forceinline__ float block_max(float v, Shared& sh) {
     constexpr int NW = BLOCK / 64;
@@ -232,19 +213,6 @@ __device__ __forceinline__ float block_max(float v, Shared& sh) {
     return unif(m);
 }
 
-template <int BLOCK>
-__device__ __forceinline__ int block_min_i(int v, Shared& sh) {
-    constexpr int NW = BLOCK / 64;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    v = wave_min_i(v);
-    if (lane == 0) sh.red_i[wid] = v;
-    __syncthreads();
-    int m = sh.red_i[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) m = min(m, sh.red_i[w]);
-    __syncthreads();
-    return uni(m);
-}
 
 // min and max of the finite scores and whether any score is NaN / +inf.
 template <int BLOCK>
@@ -718,6 +686,88 @@ __device__ __forceinline__ float dpp_f(float old, float x) {
                                                                  RM, 0xf, false));
 }
 
+// Reductions and scans over the wave by DPP: row shifts 1, 2, 4, 8 inside
+// rows of 16 lanes, then row broadcasts of lanes 15 and 31.  Lane 63 ends
+// with the total (inclusive scans: every lane its prefix).
+__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
+    x += dpp_i<0x111, 0xf>(0, x);
+    x += dpp_i<0x112, 0xf>(0, x);
+    x += dpp_i<0x114, 0xf>(0, x);
+    x += dpp_i<0x118, 0xf>(0, x);
+    x += dpp_i<0x142, 0xa>(0, x);
+    x += dpp_i<0x143, 0xc>(0, x);
+    return x;
+}
+__device__ __forceinline__ int wave_excl_scan_i(int v, int& total) {
+    const int incl = wave_incl_scan_dpp(v);
+    total = __builtin_amdgcn_readlane(incl, 63);
+    return incl - v;
+}
+__device__ __forceinline__ int wave_sum_dpp(int x) {
+    return __builtin_amdgcn_readlane(wave_incl_scan_dpp(x), 63);
+}
+__device__ __forceinline__ float wave_max_dpp(float x) {
+    x = fmaxf(x, dpp_f<0x111, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x112, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x114, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x118, 0xf>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x142, 0xa>(kNegInf, x));
+    x = fmaxf(x, dpp_f<0x143, 0xc>(kNegInf, x));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+__device__ __forceinline__ float wave_sum_f_dpp(float x) {
+    x += dpp_f<0x111, 0xf>(0.0f, x);
+    x += dpp_f<0x112, 0xf>(0.0f, x);
+    x += dpp_f<0x114, 0xf>(0.0f, x);
+    x += dpp_f<0x118, 0xf>(0.0f, x);
+    x += dpp_f<0x142, 0xa>(0.0f, x);
+    x += dpp_f<0x143, 0xc>(0.0f, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+__device__ __forceinline__ float wave_min_dpp(float x) {
+    x = fminf(x, dpp_f<0x111, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x112, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x114, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x118, 0xf>(kPosInf, x));
+    x = fminf(x, dpp_f<0x142, 0xa>(kPosInf, x));
+    x = fminf(x, dpp_f<0x143, 0xc>(kPosInf, x));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+__device__ __forceinline__ int wave_min_i_dpp(int x) {
+    x = min(x, dpp_i<0x111, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x112, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x114, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x118, 0xf>(0x7fffffff, x));
+    x = min(x, dpp_i<0x142, 0xa>(0x7fffffff, x));
+    x = min(x, dpp_i<0x143, 0xc>(0x7fffffff, x));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
+template <int CTRL, int RM>
+__device__ __forceinline__ double dpp_d(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)dpp_i<CTRL, RM>(0, (int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)dpp_i<CTRL, RM>(0, (int)(uint32_t)(b >> 32));
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// Inclusive scan of doubles over the wave (lanes without a source add +0).
+__device__ __forceinline__ double wave_incl_scan_f64_dpp(double x) {
+    x = __dadd_rn(x, dpp_d<0x111, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x112, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x114, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x118, 0xf>(x));
+    x = __dadd_rn(x, dpp_d<0x142, 0xa>(x));
+    x = __dadd_rn(x, dpp_d<0x143, 0xc>(x));
+    return x;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
 // The binary32 running sum acc0 + t_0 + t_1 + ... in order, where lane l holds
 // terms l*C .. l*C + C - 1 in t[0, C) (zeros past the last term), by sweeps
 // of the wave: a sweep adds each lane's terms, one after the other, to the
@@ -981,6 +1031,92 @@ __device__ __forceinline__ float wave_run_sum(Term&& term, int n, float acc, flo
     return acc;  // not reached
 }
 
+// Largest per-lane run (64*C terms per chunk) the one-wave sums and draws of
+// a BLOCK-lane kernel are compiled for: 1024-lane kernels (128 registers per
+// lane) stop at 17 terms per lane and take longer lists in more chunks.
+template <int BLOCK>
+constexpr int run_bound(int n) {
+    return BLOCK >= 1024 && n > 1088 ? 1088 : n;
+}
+
+// The top-p cutoff without forming the q's, when it is certain: the first
+// index i whose running sum cum_i = q_0 + ... + q_i (q_j = fl(e_j / psum),
+// binary32 adds in order) is >= top_p, for sorted finite terms e_j >= 0 and
+// the exact binary32 psum.  With Y_i = (e_0 + ... + e_i) / psum in binary64,
+// |cum_i - Y_i| <= i half-ulps of cum_i (one rounding per add) + 2^-24 Y_i
+// (the rounding of each q_j); each lane bounds this for its run of C terms by
+// its last index and the binade of its last Y (raised by 2^-12), doubled on
+// the second term, plus 1e-12 for the binary64 arithmetic.  Where Y -/+ that
+// bound puts the first crossing at one index the answer is certain (`last`,
+// n - 1 when the sum never reaches top_p); otherwise returns false and the
+// caller sums the q's.  One wave, chunks of 64*C terms.
+template <int C, class Term>
+__device__ __forceinline__ bool certified_cut_c(Term&& term, int n, float psum, float top_p,
+                                                int& last) {
+    const int lane = threadIdx.x & 63;
+    const double p = (double)top_p;
+    const double inv = __ddiv_rn(1.0, (double)psum);
+    double xb = 0.0;  // the terms before the chunk
+    for (int base = 0; base < n; base += 64 * C) {
+        float ev[C];
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+            const int i = base + lane * C + q;
+            ev[q] = i < n ? term(i) : 0.0f;
+        }
+        double part = 0.0;
+#pragma unroll
+        for (int q = 0; q < C; ++q) part = __dadd_rn(part, (double)ev[q]);
+        const double incl = wave_incl_scan_f64_dpp(part);
+        const double x0 = __dadd_rn(xb, __dsub_rn(incl, part));
+        const double yl = __dmul_rn(__dadd_rn(x0, part), inv);
+        const double cm = __dmul_rn(yl, 1.0 + 0x1p-12);
+        const int b = __builtin_amdgcn_frexp_exp(cm) - 1;  // cm in [2^b, 2^(b+1))
+        const double err = __dadd_rn(
+            __dadd_rn(__dmul_rn((double)(base + lane * C + C - 1), ldexp(1.0, max(b, -126) - 24)),
+                      __dmul_rn(yl, 0x1p-23)),
+            1e-12);
+        const double lo_thr = __dsub_rn(p, err), hi_thr = __dadd_rn(p, err);
+        // y does not decrease: the first index meeting a bound is the count
+        // of the lane's terms before it
+        int n_hi = 0, n_lo = 0;
+        double x = x0;
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+            x = __dadd_rn(x, (double)ev[q]);
+            const double y = __dmul_rn(x, inv);
+            n_hi += y < lo_thr ? 1 : 0;
+            n_lo += y < hi_thr ? 1 : 0;
+        }
+        const int c_hi = min(wave_min_i_dpp(n_hi < C ? base + lane * C + n_hi : 0x7fffffff), n);
+        const int c_lo = min(wave_min_i_dpp(n_lo < C ? base + lane * C + n_lo : 0x7fffffff), n);
+        if (c_hi < n) {  // the earliest possible crossing is here
+            if (c_lo != c_hi) return false;
+            last = c_hi;
+            return true;
+        }
+        xb = __dadd_rn(xb, readlane_f64(incl, 63));
+    }
+    last = n - 1;  // Y stays below top_p - err: the sum never reaches top_p
+    return true;
+}
+
+// certified_cut_c with C picked from n (at most NMAX): 1, 5, 17 or 33.
+template <int NMAX, class Term>
+__device__ __forceinline__ bool certified_cut(Term&& term, int n, float psum, float top_p,
+                                              int& last) {
+    n = uni(n);
+    if (NMAX <= 64 || n <= 64) return certified_cut_c<1>(term, n, psum, top_p, last);
+    if constexpr (NMAX > 64) {
+        if (NMAX <= 320 || n <= 320) return certified_cut_c<5>(term, n, psum, top_p, last);
+        if constexpr (NMAX > 320) {
+            if (NMAX <= 1088 || n <= 1088) return certified_cut_c<17>(term, n, psum, top_p, last);
+            if constexpr (NMAX > 1088) return certified_cut_c<33>(term, n, psum, top_p, last);
+        }
+    }
+    return false;  // not reached
+}
+
 // acc + v[0] + ... + v[n-1] in index order, binary32, by one wave, in chunks
 // of 64 x 17 terms (lane l holding terms l*17 .. l*17 + 16 of a chunk: odd
 // strides, distinct banks).  finite: every term finite and >= 0 and acc
@@ -1070,17 +1206,6 @@ __device__ __forceinline__ int rank_of(const uint32_t* keptw, const uint32_t* wo
     return (int)woff[i >> 5] + __popc(wb & ((1u << (i & 31)) - 1u));
 }
 
-// Id of the rank-th set bit of the kept bitmap (ranks from the word offsets).
-__device__ __forceinline__ int id_of_rank(const uint32_t* keptw, const uint32_t* woff, int W, int rank) {
-    int lo = 0, hi = W - 1;  // last word w with woff[w] <= rank
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if ((int)woff[mid] <= rank) lo = mid; else hi = mid - 1;
-    }
-    uint32_t bits = keptw[lo];
-    for (int k = rank - (int)woff[lo]; k > 0; --k) bits &= bits - 1u;
-    return lo * 32 + __ffs(bits) - 1;
-}
 
 // Exclusive prefix counts of the kept bitmap's words; returns the count.
 template <int BLOCK>
@@ -1251,166 +1376,253 @@ __device__ __forceinline__ int wave_tied_order(uint32_t* w, uint32_t* tmp, int n
 
 // ----------------------------------------------------------------- the draw
 
-// Token for uniform u from the id-ordered probabilities F[0, n) (the kept ids
-// of the bitmap): random.tcc:2665-2676 builds double weights summed from 0.0
-// in id order, divides each by the sum, takes running partial sums and
-// forces the last entry (id V-1) to 1.0; :2708-2712 returns the first id whose
-// cumulative value is >= u.  Ids before the first kept one have cumulative
-// value 0, so u == 0 gives id 0.
-template <int BLOCK>
-__device__ __forceinline__ int draw_token(const float* F, int n, const uint32_t* keptw, const uint32_t* woff,
-                          int W, int V, double u, Shared& sh) {
-    const int tid = threadIdx.x;
-    const bool last_kept = bit_of(keptw, V - 1);
-    // parallel pass over contiguous chunks: unnormalised prefix sums
-    const int C = (n + BLOCK - 1) / BLOCK;
-    const int r0 = min(tid * C, n), r1 = min(r0 + C, n);
-    double part = 0.0;
-    for (int r = r0; r < r1; ++r) part = __dadd_rn(part, (double)F[r]);
-    double total;
-    double cp = block_excl_scan_f64<BLOCK>(part, sh, total);
-    const double target = __dmul_rn(u, total);  // cumulative >= u  <=>  prefix >= u*total
-    int found = 0x7fffffff;
-    double lo = 0.0, hi = 0.0;
-    for (int r = r0; r < r1; ++r) {
-        const double before = cp;
-        cp = __dadd_rn(cp, (double)F[r]);
-        const bool forced = (r == n - 1 && last_kept);
-        if (forced || cp >= target) { found = r; lo = before; hi = forced ? total : cp; break; }
-    }
-    const int rank = block_min_i<BLOCK>(found, sh);
-    if (found == rank && found != 0x7fffffff) { sh.cdf_lo = lo; sh.cdf_hi = hi; }
-    __syncthreads();
-    if (tid == 0) {
-        const double inv = __ddiv_rn(1.0, total);
-        int tok;
-        bool certain;
-        if (!(u > 0.0)) {
-            tok = 0;
-            certain = true;
-        } else if (rank == 0x7fffffff) {
-            tok = V - 1;  // past every computed value: the forced last entry
-            certain = u - __dmul_rn(total, inv) > kCdfMargin;
-        } else {
-            tok = id_of_rank(keptw, woff, W, rank);
-            const bool exact_hi = (rank == n - 1 && last_kept);
-            certain = (rank == 0 || u - __dmul_rn(sh.cdf_lo, inv) > kCdfMargin) &&
-                      (exact_hi || __dmul_rn(sh.cdf_hi, inv) - u >= kCdfMargin);
-        }
-        if (!certain) {
-            // the reference's sequential CDF, exactly (rare)
-            double sum = 0.0;
-            for (int r = 0; r < n; ++r) sum = __dadd_rn(sum, (double)F[r]);
-            double acc = 0.0;
-            int rk = -1;
-            for (int r = 0; r < n; ++r) {
-                acc = __dadd_rn(acc, __ddiv_rn((double)F[r], sum));
-                const double c = (r == n - 1 && last_kept) ? 1.0 : acc;
-                if (c >= u) { rk = r; break; }
+// The draw by one wave (main.cpp:795-800; random.tcc:2665-2676, :2708-2712):
+// the reference builds double weights from the float probabilities in id
+// order, divides each by their double sum, takes running partial sums, forces
+// the last entry (id V-1) to 1.0 and returns the first id whose cumulative
+// value is >= u (ids before the first kept one have cumulative 0: u == 0
+// gives id 0).  Here the cumulative values are located on the binary64
+// prefix of the unnormalised exp terms F[0, n) (kept ids in id order; lane l
+// holds the runs [base + l*C, base + l*C + C), odd C in distinct banks): the
+// ratio differs from the reference's value by less than 2^-23 relative
+// whatever its float normaliser, so a rank whose neighbouring boundaries are
+// more than kDrawMargin (relative) from u is certain.  Returns the rank, or -1
+// when it is not certain (the caller replays the reference's arithmetic).
+template <int C>
+__device__ __forceinline__ int draw_rank_c(const float* F, int n, double u, bool last_kept) {
+    const int lane = threadIdx.x & 63;
+    const bool one = n <= 64 * C;  // one chunk: the total comes with the prefix
+    double total = 0.0;
+    if (!one) {
+        for (int base = 0; base < n; base += 64 * C) {
+            double part = 0.0;
+#pragma unroll
+            for (int q = 0; q < C; ++q) {
+                const int i = base + lane * C + q;
+                part = __dadd_rn(part, (double)(i < n ? F[i] : 0.0f));
             }
-            tok = rk < 0 ? V - 1 : id_of_rank(keptw, woff, W, rk);
+            total = __dadd_rn(total, readlane_f64(wave_incl_scan_f64_dpp(part), 63));
         }
-        sh.token = tok;
     }
-    __syncthreads();
-    return uni(sh.token);
+    double xb = 0.0;
+    for (int base = 0; base < n; base += 64 * C) {
+        float f[C];
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+            const int i = base + lane * C + q;
+            f[q] = i < n ? F[i] : 0.0f;
+        }
+        double part = 0.0;
+#pragma unroll
+        for (int q = 0; q < C; ++q) part = __dadd_rn(part, (double)f[q]);
+        const double incl = wave_incl_scan_f64_dpp(part);
+        if (one) total = readlane_f64(incl, 63);
+        const double target = __dmul_rn(u, total);
+        double cp = __dadd_rn(xb, __dsub_rn(incl, part));  // exclusive
+        double blo = 0.0, bhi = 0.0;
+        int found = 0x7fffffff;
+        bool got = false;
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+            const double before = cp;
+            cp = __dadd_rn(cp, (double)f[q]);
+            const bool hit = !got && cp >= target && base + lane * C + q < n;
+            blo = hit ? before : blo;
+            bhi = hit ? cp : bhi;
+            found = hit ? base + lane * C + q : found;
+            got = got || hit;
+        }
+        const int rank = wave_min_i_dpp(found);
+        if (rank != 0x7fffffff) {
+            const int L = __builtin_ctzll(__ballot(found == rank));
+            const double inv = __ddiv_rn(1.0, total);
+            const double clo = __dmul_rn(readlane_f64(blo, L), inv);
+            const double chi = __dmul_rn(readlane_f64(bhi, L), inv);
+            const bool lo_ok = rank == 0 || __dsub_rn(u, clo) > kDrawMargin * clo + 1e-30;
+            const bool hi_ok = (rank == n - 1 && last_kept) ||
+                               __dsub_rn(chi, u) > kDrawMargin * chi + 1e-30;
+            return (lo_ok && hi_ok) ? rank : -1;
+        }
+        xb = __dadd_rn(xb, readlane_f64(incl, 63));
+    }
+    return -1;
+}
+
+// draw_rank_c with C picked from n (at most NMAX).
+template <int NMAX>
+__device__ __forceinline__ int draw_rank(const float* F, int n, double u, bool last_kept) {
+    n = uni(n);
+    if (NMAX <= 64 || n <= 64) return draw_rank_c<1>(F, n, u, last_kept);
+    if constexpr (NMAX > 64) {
+        if (NMAX <= 320 || n <= 320) return draw_rank_c<5>(F, n, u, last_kept);
+        if constexpr (NMAX > 320) {
+            if (NMAX <= 1088 || n <= 1088) return draw_rank_c<17>(F, n, u, last_kept);
+            if constexpr (NMAX > 1088) return draw_rank_c<33>(F, n, u, last_kept);
+        }
+    }
+    return -1;  // not reached
 }
 
 // Softmax over the kept entries (val[q], id[q] for bit q of `kept`), then
-// greedy or draw; writes token, info and, if asked, the probability row
-// (element owners read the id-ordered F through the bitmap).  Shared by both
-// paths.
+// greedy or draw; writes token, info and, if asked, the probability row.
+// Shared by both paths.  Every wave takes part in three steps -- the kept
+// bitmap and the maximum kept score (each wave's maximum into an LDS
+// maximum), then (wave 0) the bitmap's word offsets, then the exp terms F in
+// id order -- after which wave 0 alone forms the id-order binary32 sum
+// (main.cpp:786-790) and the token, with no workgroup barrier; the other
+// waves are done, or wait once for the sum when probabilities are written.
 template <int BLOCK, int EPT, int N>
 __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], uint64_t kept,
                            const KernelArgs& a, const cbx_params& P, int64_t rs, int row, int step,
                            uint32_t flags, uint32_t* keptw, uint32_t* woff, float* F,
                            const uint64_t* tab, Shared& sh) {
+    constexpr int WMAX = (BLOCK * EPT + 31) / 32;  // bitmap words of the largest vocabulary
+    constexpr int WPL = (WMAX + 63) / 64;          // of them per lane of wave 0
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int V = a.n_vocab;
     const int W = (V + 31) >> 5;
-    // final kept bitmap and id-order ranks
     for (int w = tid; w < W; w += BLOCK) keptw[w] = 0u;
+    if (tid == 0) sh.mxk = 0u;
     __syncthreads();
-#pragma unroll
-    for (int q = 0; q < N; ++q)
-        if ((kept >> q) & 1u) atomicOr(&keptw[id[q] >> 5], 1u << (id[q] & 31));
-    __syncthreads();
-    const int n_final = bitmap_offsets<BLOCK>(keptw, woff, W, sh);
-    CBX_STAMP(9);
-
-    // softmax (main.cpp:783-793)
     float m = kNegInf;
 #pragma unroll
-    for (int q = 0; q < N; ++q) m = ((kept >> q) & 1u) ? fmaxf(m, val[q]) : m;
-    const float mx2 = block_max<BLOCK>(m, sh);
-#pragma unroll
-    for (int q = 0; q < N; ++q) {
+    for (int q = 0; q < N; ++q)
         if ((kept >> q) & 1u) {
-            val[q] = expf_libm_branchless(__fsub_rn(val[q], mx2), tab);
-            F[rank_of(keptw, woff, id[q])] = val[q];
+            atomicOr(&keptw[id[q] >> 5], 1u << (id[q] & 31));
+            m = fmaxf(m, val[q]);
+        }
+    m = wave_max_dpp(m);
+    if (lane == 0) atomicMax(&sh.mxk, okey(m));
+    __syncthreads();
+    // wave 0: word offsets; each lane keeps its words' counts for id lookups
+    int cw[WPL];
+    int loc = 0, wbase = 0, n_final = 0;
+    if (wid == 0) {
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) {
+            const int w = lane * WPL + q;
+            cw[q] = (w < W) ? __popc(keptw[w]) : 0;
+            loc += cw[q];
+        }
+        wbase = wave_excl_scan_i(loc, n_final);
+        int run = wbase;
+#pragma unroll
+        for (int q = 0; q < WPL; ++q) {
+            const int w = lane * WPL + q;
+            if (w < W) woff[w] = (uint32_t)run;
+            run += cw[q];
         }
     }
+    __syncthreads();
+    CBX_STAMP(9);
+    // softmax terms (main.cpp:783-785) in id order
+    const float mx2 = okey_inv(uni((int)sh.mxk));
+#pragma unroll
+    for (int q = 0; q < N; ++q)
+        if ((kept >> q) & 1u)
+            F[rank_of(keptw, woff, id[q])] = expf_libm_branchless(__fsub_rn(val[q], mx2), tab);
     __syncthreads();
     if (wid == 0) {
-        const float ps = wave_chain_sum(F, n_final, 0.0f, !(flags & CBX_INFO_NONFINITE));
-        if (lane == 0) sh.psum = ps;
-    }
-    __syncthreads();
-    const float psum2 = unif(sh.psum);
-    CBX_STAMP(10);
-    const bool empty = (psum2 == 0.0f);
-    if (!empty) {
+        // the id of id-order rank `rank` (0 <= rank < n_final): the lane whose
+        // words hold it finds the word; lanes 0..31 then count the word's set
+        // bits below their own bit
+        auto id_of_rank_w = [&](int rank) -> int {
+            const int L = __builtin_ctzll(__ballot(wbase <= rank && rank < wbase + loc));
+            int run = wbase, wq = 0, kq = 0;
+            bool got = false;
 #pragma unroll
-        for (int q = 0; q < N; ++q) {
-            if ((kept >> q) & 1u) {
-                val[q] = __fdiv_rn(val[q], psum2);
-                F[rank_of(keptw, woff, id[q])] = val[q];
+            for (int q = 0; q < WPL; ++q) {
+                const bool in = !got && rank < run + cw[q];
+                wq = in ? lane * WPL + q : wq;
+                kq = in ? rank - run : kq;
+                got = got || in;
+                run += cw[q];
             }
+            const int w = __builtin_amdgcn_readlane(wq, L);
+            const int kb = __builtin_amdgcn_readlane(kq, L);
+            const uint32_t bits = keptw[w];
+            const bool hit = lane < 32 && ((bits >> (lane & 31)) & 1u) &&
+                             (int)__builtin_amdgcn_mbcnt_lo(bits, 0u) == kb;
+            return w * 32 + __builtin_ctzll(__ballot(hit));
+        };
+        const bool fin = !(flags & CBX_INFO_NONFINITE);
+        int unused;
+        const float psum2 = n_final > 0 ? wave_run_sum<run_bound<BLOCK>(BLOCK * EPT), false, false>(
+                                              [&](int i) { return F[i]; }, n_final, 0.0f, 0.0f,
+                                              unused, fin)
+                                        : 0.0f;
+        CBX_STAMP(10);
+        const bool empty = (psum2 == 0.0f);
+        int token = 0;
+        if (empty) {
+            flags |= CBX_INFO_EMPTY;
+        } else if (P.temp <= 0.0f) {
+            // first argmax of p_i = e_i / psum over ids (zeros elsewhere);
+            // only NaN probabilities: no maximum, id 0
+            float best = -1.0f;
+            int first = 0x7fffffff;
+            for (int i = lane; i < n_final; i += 64) {
+                const float p = __fdiv_rn(F[i], psum2);
+                if (p > best) { best = p; first = i; }  // ascending i: keeps the first
+            }
+            const float b = wave_max_dpp(best);
+            const int rk = wave_min_i_dpp(best == b ? first : 0x7fffffff);
+            token = rk == 0x7fffffff ? 0 : id_of_rank_w(rk);
+            flags |= CBX_INFO_GREEDY;
+        } else if (V >= 2) {
+            flags |= CBX_INFO_DREW;
+            double u;
+            if (a.draw_mode == CBX_DRAW_PHILOX) {
+                const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
+                u = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
+            } else {
+                u = a.uniforms[rs];
+            }
+            const bool last_kept = bit_of(keptw, V - 1);
+            int rank = -1;
+            if (!(u > 0.0)) {
+                token = 0;  // lower_bound of 0 is the first entry
+            } else {
+                rank = draw_rank<run_bound<BLOCK>(BLOCK * EPT)>(F, n_final, u, last_kept);
+                if (rank < 0) {
+                    // the reference's arithmetic: float probabilities, double
+                    // CDF, on one lane (rare)
+                    int rk = -1;
+                    if (lane == 0) {
+                        double sum = 0.0;
+                        for (int r = 0; r < n_final; ++r)
+                            sum = __dadd_rn(sum, (double)__fdiv_rn(F[r], psum2));
+                        double acc = 0.0;
+                        for (int r = 0; r < n_final; ++r) {
+                            acc = __dadd_rn(acc, __ddiv_rn((double)__fdiv_rn(F[r], psum2), sum));
+                            const double c = (r == n_final - 1 && last_kept) ? 1.0 : acc;
+                            if (c >= u) { rk = r; break; }
+                        }
+                    }
+                    rank = __builtin_amdgcn_readlane(rk, 0);
+                    if (rank < 0) token = V - 1;
+                }
+                if (rank >= 0) token = id_of_rank_w(rank);
+            }
+            CBX_STAMP(11);
         }
-    }
-    __syncthreads();
-
-    // greedy or draw (main.cpp:795-800)
-    int token = 0;
-    if (empty) {
-        flags |= CBX_INFO_EMPTY;
-    } else if (P.temp <= 0.0f) {
-        // first argmax over the full probability vector (zeros elsewhere)
-        float best = -1.0f;
-#pragma unroll
-        for (int q = 0; q < N; ++q) best = ((kept >> q) & 1u) ? fmaxf(best, val[q]) : best;
-        best = block_max<BLOCK>(best, sh);
-        int first = 0x7fffffff;
-#pragma unroll
-        for (int q = 0; q < N; ++q)
-            first = (((kept >> q) & 1u) && val[q] == best) ? min(first, id[q]) : first;
-        token = block_min_i<BLOCK>(first, sh);
-        if (token == 0x7fffffff) token = 0;  // only NaN probabilities: no maximum
-        flags |= CBX_INFO_GREEDY;
-    } else if (V >= 2) {
-        flags |= CBX_INFO_DREW;
-        double u;
-        if (a.draw_mode == CBX_DRAW_PHILOX) {
-            const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
-            u = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
-        } else {
-            u = a.uniforms[rs];
+        CBX_STAMP(12);
+        if (lane == 0) {
+            a.tokens[rs] = token;
+            if (a.info) a.info[rs] = flags | sh.flags;
+            sh.psum = empty ? 0.0f : psum2;
         }
-        token = draw_token<BLOCK>(F, n_final, keptw, woff, W, V, u, sh);
-        CBX_STAMP(11);
-    }
-
-    CBX_STAMP(12);
-    if (tid == 0) {
-        a.tokens[rs] = token;
-        if (a.info) a.info[rs] = flags | sh.flags;
     }
     if (a.probs) {
+        __syncthreads();
+        const float ps = unif(sh.psum);
         float* prow = a.probs + rs * a.ld_probs;
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             const int i = j * BLOCK + tid;
-            if (i < V) prow[i] = (!empty && bit_of(keptw, i)) ? F[rank_of(keptw, woff, i)] : 0.0f;
+            if (i < V)
+                prow[i] = (ps != 0.0f && bit_of(keptw, i)) ? __fdiv_rn(F[rank_of(keptw, woff, i)], ps)
+                                                          : 0.0f;
         }
     }
 }
@@ -1466,14 +1678,17 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
             auto e_at = [&](int i) { return E[i]; };
             int hit;
             const float psum =
-                wave_run_sum<NR * BLOCK, false, true>(e_at, n_surv, 0.0f, 0.0f, hit, fin);
+                wave_run_sum<run_bound<BLOCK>(NR * BLOCK), false, true>(e_at, n_surv, 0.0f, 0.0f, hit, fin);
             CBX_STAMP(6);
-            for (int i = lane; i < n_surv; i += 64) E[i] = __fdiv_rn(E[i], psum);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            (void)wave_run_sum<NR * BLOCK, true, true>(e_at, n_surv, 0.0f, P.top_p, hit, fin);
-            const int last = hit < 0 ? n_surv - 1 : hit;
+            int last;
+            if (!(fin && certified_cut<run_bound<BLOCK>(NR * BLOCK)>(e_at, n_surv, psum, P.top_p, last))) {
+                for (int i = lane; i < n_surv; i += 64) E[i] = __fdiv_rn(E[i], psum);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                (void)wave_run_sum<run_bound<BLOCK>(NR * BLOCK), true, true>(e_at, n_surv, 0.0f, P.top_p, hit, fin);
+                last = hit < 0 ? n_surv - 1 : hit;
+            }
             if (lane == 0) sh.n_kept = last + 1;
         }
         __syncthreads();
@@ -1828,7 +2043,7 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
             __syncthreads();
         }
         auto e_of = [&](int i) { return e_lds ? eg[i] : e_form(i); };
-        constexpr int NG = BLOCK * EPT;
+        constexpr int NG = run_bound<BLOCK>(BLOCK * EPT);
         if (wid == 0) {
             int unused;
             const float ps = wave_run_sum<NG, false, true>(e_of, n_surv, 0.0f, 0.0f, unused, !bad);
@@ -1837,18 +2052,25 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         __syncthreads();
         CBX_STAMP(15);
         const float psum = unif(sh.psum);
-        if (e_lds) {
-            for (int i = tid; i < n_surv; i += BLOCK) eg[i] = __fdiv_rn(eg[i], psum);
+        // the cutoff: certified in binary64 where it can be, else the q's summed
+        int last = -1;
+        if (wid == 0 && !bad && !certified_cut<NG>(e_of, n_surv, psum, P.top_p, last)) last = -1;
+        if (wid == 0 && lane == 0) sh.n_kept = last + 1;
+        __syncthreads();
+        if (uni(sh.n_kept) == 0) {  // not certain (or NaN / +inf rows)
+            if (e_lds) {
+                for (int i = tid; i < n_surv; i += BLOCK) eg[i] = __fdiv_rn(eg[i], psum);
+                __syncthreads();
+            }
+            if (wid == 0) {
+                int hit;
+                (void)wave_run_sum<NG, true, true>(
+                    [&](int i) { return e_lds ? eg[i] : __fdiv_rn(e_form(i), psum); }, n_surv,
+                    0.0f, P.top_p, hit, !bad);
+                if (lane == 0) sh.n_kept = (hit < 0 ? n_surv - 1 : hit) + 1;
+            }
             __syncthreads();
         }
-        if (wid == 0) {
-            int hit;
-            (void)wave_run_sum<NG, true, true>(
-                [&](int i) { return e_lds ? eg[i] : __fdiv_rn(e_form(i), psum); }, n_surv, 0.0f,
-                P.top_p, hit, !bad);
-            if (lane == 0) sh.n_kept = (hit < 0 ? n_surv - 1 : hit) + 1;
-        }
-        __syncthreads();
         const int n_kept = uni(sh.n_kept);
         T = unif(okey_inv(~key32[n_kept - 1]));
         tie = n_kept < n_surv && unif(okey_inv(~key32[n_kept])) == T;

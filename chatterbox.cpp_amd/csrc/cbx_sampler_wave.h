@@ -44,7 +44,6 @@ constexpr int kWaveBins = 1024;   // value bins: top-k select, survivor sort
 constexpr int kWaveCand = 256;    // scores in the selected top-k bin
 constexpr int kWaveSortMax = 64;  // largest bin the counting sort ranks directly
 constexpr int kWaveRows = kWaveCap / 64;
-constexpr double kDrawMargin = 3e-7;
 
 // Waves per SIMD the register allocation aims for (the row's scores take
 // 4*Q registers; the rest of the kernel is kept within the same budget).
@@ -83,88 +82,6 @@ struct WaveSmem {
 
 // ------------------------------------------------------------ wave helpers
 
-
-// Reductions and scans over the wave by DPP: row shifts 1, 2, 4, 8 inside
-// rows of 16 lanes, then row broadcasts of lanes 15 and 31.  Lane 63 ends
-// with the total (inclusive scans: every lane its prefix).
-__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
-    x += dpp_i<0x111, 0xf>(0, x);
-    x += dpp_i<0x112, 0xf>(0, x);
-    x += dpp_i<0x114, 0xf>(0, x);
-    x += dpp_i<0x118, 0xf>(0, x);
-    x += dpp_i<0x142, 0xa>(0, x);
-    x += dpp_i<0x143, 0xc>(0, x);
-    return x;
-}
-__device__ __forceinline__ int wave_excl_scan_i(int v, int& total) {
-    const int incl = wave_incl_scan_dpp(v);
-    total = __builtin_amdgcn_readlane(incl, 63);
-    return incl - v;
-}
-__device__ __forceinline__ int wave_sum_dpp(int x) {
-    return __builtin_amdgcn_readlane(wave_incl_scan_dpp(x), 63);
-}
-__device__ __forceinline__ float wave_max_dpp(float x) {
-    x = fmaxf(x, dpp_f<0x111, 0xf>(kNegInf, x));
-    x = fmaxf(x, dpp_f<0x112, 0xf>(kNegInf, x));
-    x = fmaxf(x, dpp_f<0x114, 0xf>(kNegInf, x));
-    x = fmaxf(x, dpp_f<0x118, 0xf>(kNegInf, x));
-    x = fmaxf(x, dpp_f<0x142, 0xa>(kNegInf, x));
-    x = fmaxf(x, dpp_f<0x143, 0xc>(kNegInf, x));
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-__device__ __forceinline__ float wave_sum_f_dpp(float x) {
-    x += dpp_f<0x111, 0xf>(0.0f, x);
-    x += dpp_f<0x112, 0xf>(0.0f, x);
-    x += dpp_f<0x114, 0xf>(0.0f, x);
-    x += dpp_f<0x118, 0xf>(0.0f, x);
-    x += dpp_f<0x142, 0xa>(0.0f, x);
-    x += dpp_f<0x143, 0xc>(0.0f, x);
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-__device__ __forceinline__ float wave_min_dpp(float x) {
-    x = fminf(x, dpp_f<0x111, 0xf>(kPosInf, x));
-    x = fminf(x, dpp_f<0x112, 0xf>(kPosInf, x));
-    x = fminf(x, dpp_f<0x114, 0xf>(kPosInf, x));
-    x = fminf(x, dpp_f<0x118, 0xf>(kPosInf, x));
-    x = fminf(x, dpp_f<0x142, 0xa>(kPosInf, x));
-    x = fminf(x, dpp_f<0x143, 0xc>(kPosInf, x));
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-__device__ __forceinline__ int wave_min_i_dpp(int x) {
-    x = min(x, dpp_i<0x111, 0xf>(0x7fffffff, x));
-    x = min(x, dpp_i<0x112, 0xf>(0x7fffffff, x));
-    x = min(x, dpp_i<0x114, 0xf>(0x7fffffff, x));
-    x = min(x, dpp_i<0x118, 0xf>(0x7fffffff, x));
-    x = min(x, dpp_i<0x142, 0xa>(0x7fffffff, x));
-    x = min(x, dpp_i<0x143, 0xc>(0x7fffffff, x));
-    return __builtin_amdgcn_readlane(x, 63);
-}
-
-template <int CTRL, int RM>
-__device__ __forceinline__ double dpp_d(double x) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, x);
-    const uint32_t lo = (uint32_t)dpp_i<CTRL, RM>(0, (int)(uint32_t)b);
-    const uint32_t hi = (uint32_t)dpp_i<CTRL, RM>(0, (int)(uint32_t)(b >> 32));
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-// Inclusive scan of doubles over the wave (lanes without a source add +0).
-__device__ __forceinline__ double wave_incl_scan_f64_dpp(double x) {
-    x = __dadd_rn(x, dpp_d<0x111, 0xf>(x));
-    x = __dadd_rn(x, dpp_d<0x112, 0xf>(x));
-    x = __dadd_rn(x, dpp_d<0x114, 0xf>(x));
-    x = __dadd_rn(x, dpp_d<0x118, 0xf>(x));
-    x = __dadd_rn(x, dpp_d<0x142, 0xa>(x));
-    x = __dadd_rn(x, dpp_d<0x143, 0xc>(x));
-    return x;
-}
-
-__device__ __forceinline__ double readlane_f64(double v, int l) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
 
 // Four consecutive words of a raw buffer (one 16-byte load).  The vector is
 // copied out as bytes: subscripting the builtin's vector result directly
