@@ -271,12 +271,205 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     }
 }
 
+// ----------------------------------------------------------------- mat-vec
+// Fewer than 16 projected rows (a CFG pair is 2): no row tile to fill, so
+// the weights are read once by plain FMAs.  The R rows of activations are
+// staged in LDS with each 32-element block padded to 33 words; 16 lanes take
+// one vocab row, lane s owning blocks s, s + 16, ... of it, and the 16 lanes'
+// reads of one block offset then fall in distinct banks (the four vocab rows
+// of a wave share the addresses: broadcasts).  Each lane's weights come
+// straight from memory (the 16 lanes of a vocab row read its contiguous
+// blocks), dequantized to the format's exact fp32 values; each lane sums its
+// blocks' products in element order, then the 16 lanes add by a fixed DPP
+// tree, so results do not depend on scheduling.
+constexpr int kGemvLanes = 16;       // lanes per vocab row
+constexpr int kGemvRowsPerWave = 4;  // vocab rows per wave and pass
+constexpr int kGemvWaves = 4;
+
+// Words of one staged activation row: 33 per 32-element block.
+__host__ __device__ inline int gemv_row_words(int n_embd) { return n_embd / 32 * 33; }
+
+// The 32 weights of block b of vocab row v (zeros past the table).
+template <int WT>
+__device__ __forceinline__ void gemv_block(const __amdgpu_buffer_rsrc_t& rw, int v, int nball, int b,
+                                           float* w) {
+    if constexpr (WT == CBX_WTYPE_F16) {
+        const uint32_t off = (uint32_t)(((int64_t)v * nball + b) * 64);
+        uint32_t t[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16u * i, 0, 0);
+            uint32_t y[4];
+            __builtin_memcpy(y, &x, 16);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) t[4 * i + c] = y[c];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            w[2 * i] = half_bits_to_float(t[i] & 0xffffu);
+            w[2 * i + 1] = half_bits_to_float(t[i] >> 16);
+        }
+    } else {
+        constexpr int BB = WT == CBX_WTYPE_Q4_0 ? 18 : 34;
+        constexpr int ND = WT == CBX_WTYPE_Q4_0 ? 5 : 9;  // dwords covering the block
+        const uint32_t off = (uint32_t)(((int64_t)v * nball + b) * BB);  // even
+        const uint32_t a0 = off & ~3u, sh = 8u * (off & 3u);               // sh: 0 or 16
+        uint32_t t[ND];
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+            t[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, a0 + 4u * i, 0, 0);
+        const float d = half_bits_to_float((t[0] >> sh) & 0xffffu);
+        // the block's bytes after the scale, as dwords: byte 2 of the block first
+        uint32_t q[ND - 1];
+#pragma unroll
+        for (int i = 0; i < ND - 1; ++i)
+            q[i] = sh ? t[i + 1] : __builtin_amdgcn_alignbit(t[i + 1], t[i], 16);
+        if constexpr (WT == CBX_WTYPE_Q4_0) {
+            // element j < 16: low nibble of byte j; element 16 + j: its high nibble
+            const float o = __fmul_rn(d, -8.0f);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t by = (q[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                w[j] = __fmaf_rn((float)(by & 15u), d, o);
+                w[16 + j] = __fmaf_rn((float)(by >> 4), d, o);
+            }
+        } else {
+            const float o = __fmul_rn(d, -128.0f);
+#pragma unroll
+            for (int j = 0; j < 32; ++j)
+                w[j] = __fmaf_rn(ubyte(q[j >> 2] ^ 0x80808080u, j & 3), d, o);
+        }
+    }
+}
+
+template <int WT, int RMAX>
+__global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
+    const void* W, const float* bias, const float* hidden0, const float* hidden1,
+    int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int n_rows, int n_vocab,
+    int n_embd) {
+    extern __shared__ float hs[];  // [R][gemv_row_words(n_embd)]
+    const int R = hidden1 ? 2 * n_rows : n_rows;  // <= RMAX
+    const int nball = n_embd / 32, rw_words = gemv_row_words(n_embd);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int s = lane & (kGemvLanes - 1), grp = lane / kGemvLanes;
+    for (int i = tid; i < R * n_embd; i += 64 * kGemvWaves) {
+        const int r = i / n_embd, k = i - r * n_embd;
+        const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
+                                      : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
+        hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
+    }
+    constexpr int64_t kBB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
+    const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
+    __syncthreads();
+    constexpr int kRowsPerPass = kGemvRowsPerWave * kGemvWaves;
+    for (int vb = blockIdx.x * kRowsPerPass; vb < n_vocab; vb += gridDim.x * kRowsPerPass) {
+        const int v = vb + wave * kGemvRowsPerWave + grp;
+        const int vc = v < n_vocab ? v : n_vocab;  // past the table: zeros
+        float acc[RMAX];
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) acc[r] = 0.0f;
+        for (int b = s; b < nball; b += kGemvLanes) {
+            float w[32];
+            gemv_block<WT>(rw, vc, nball, b, w);
+            const float* hb = hs + b * 33;
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (r < R) {
+                    const float* h = hb + r * rw_words;
+                    float a = acc[r];
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) a = __fmaf_rn(w[j], h[j], a);
+                    acc[r] = a;
+                }
+            }
+        }
+        // the 16 lanes' sums: lane 15 of each 16-lane row ends with the total
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            float a = acc[r];
+            a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                           0, __builtin_bit_cast(int, a), 0x111, 0xf, 0xf, false)));
+            a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                           0, __builtin_bit_cast(int, a), 0x112, 0xf, 0xf, false)));
+            a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                           0, __builtin_bit_cast(int, a), 0x114, 0xf, 0xf, false)));
+            a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                           0, __builtin_bit_cast(int, a), 0x118, 0xf, 0xf, false)));
+            acc[r] = a;
+        }
+        if (s == kGemvLanes - 1 && v < n_vocab) {
+            const float bv = bias ? bias[v] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (r < R) {
+                    float* o = r < n_rows ? out0 + (int64_t)r * ld_out
+                                          : out1 + (int64_t)(r - n_rows) * ld_out;
+                    o[v] = __fadd_rn(acc[r], bv);
+                }
+            }
+        }
+    }
+}
+
+template <int WT, int RMAX>
+hipError_t launch_gemv(const void* W, const float* bias, const float* hidden0, const float* hidden1,
+                       int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int32_t n_rows,
+                       int32_t n_vocab, int32_t n_embd, hipStream_t stream) {
+    const int R = hidden1 ? 2 * n_rows : n_rows;
+    const size_t lds = (size_t)R * gemv_row_words(n_embd) * 4;
+    constexpr int kRowsPerPass = kGemvRowsPerWave * kGemvWaves;
+    const unsigned grid = (unsigned)((n_vocab + kRowsPerPass - 1) / kRowsPerPass);
+    hipLaunchKernelGGL((head_gemv<WT, RMAX>), dim3(grid), dim3(64 * kGemvWaves), lds, stream, W,
+                       bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
+                       n_embd);
+    return hipGetLastError();
+}
+
+template <int WT>
+hipError_t launch_gemv_r(const void* W, const float* bias, const float* hidden0,
+                         const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                         int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                         hipStream_t stream) {
+    const int R = hidden1 ? 2 * n_rows : n_rows;
+    if (R <= 2)
+        return launch_gemv<WT, 2>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
+                                  n_vocab, n_embd, stream);
+    if (R <= 4)
+        return launch_gemv<WT, 4>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
+                                  n_vocab, n_embd, stream);
+    if (R <= 8)
+        return launch_gemv<WT, 8>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
+                                  n_vocab, n_embd, stream);
+    return launch_gemv<WT, 16>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
+                               n_vocab, n_embd, stream);
+}
+
 }  // namespace
 
 hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
                        hipStream_t stream) {
+    // fewer than 16 projected rows: the mat-vec (activations staged in LDS,
+    // at most 64 KiB of them), else the 16-row matrix-core tiles
+    const int R = hidden1 ? 2 * n_rows : n_rows;
+    if (R < 16 && (size_t)R * gemv_row_words(n_embd) * 4 <= 65536) {
+        switch (wtype) {
+            case CBX_WTYPE_F16:
+                return launch_gemv_r<CBX_WTYPE_F16>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                    out1, ld_out, n_rows, n_vocab, n_embd, stream);
+            case CBX_WTYPE_Q4_0:
+                return launch_gemv_r<CBX_WTYPE_Q4_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
+            case CBX_WTYPE_Q8_0:
+                return launch_gemv_r<CBX_WTYPE_Q8_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
+            default:
+                return hipErrorInvalidValue;
+        }
+    }
     const int n_tiles = ((n_rows + 15) / 16) * (hidden1 ? 2 : 1);
     const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT), 1u);
     switch (wtype) {

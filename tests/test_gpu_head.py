@@ -75,6 +75,15 @@ CASES = [
     (O.WTYPE_Q4_0, 8194, 1024, 2, 8194),     # one CFG pair, the Llama vocab
     (O.WTYPE_Q8_0, 300, 64, 17, 301),        # ragged tiles on both axes
     (O.WTYPE_F16, 33, 32, 1, 40),
+    # fewer than 16 rows: the mat-vec kernel
+    (O.WTYPE_Q4_0, 6563, 1024, 1, 6563),     # one stream of the Turbo vocab
+    (O.WTYPE_Q8_0, 6563, 1024, 2, 6570),
+    (O.WTYPE_F16, 6563, 1024, 2, 6563),
+    (O.WTYPE_Q4_0, 6563, 1024, 15, 6563),    # the largest mat-vec batch
+    (O.WTYPE_Q8_0, 1000, 4096, 3, 1000),
+    (O.WTYPE_Q4_0, 300, 64, 5, 301),
+    (O.WTYPE_F16, 500, 8192, 1, 500),
+    (O.WTYPE_Q4_0, 700, 512, 16, 700),       # 16 rows: the matrix-core tiles again
 ]
 
 
@@ -133,14 +142,17 @@ def test_head_without_bias(cbx, torch_cuda):
     assert np.all(np.abs(got - ref) <= tol)
 
 
+@pytest.mark.parametrize("B,S", [(64, 2), (1, 1), (7, 1)])
 @pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
-def test_fused_head_sample_cfg(cbx, torch_cuda, wtype):
-    """B=64 CFG streams, two steps: projection of cond and uncond hidden rows
+def test_fused_head_sample_cfg(cbx, torch_cuda, wtype, B, S):
+    """B CFG streams, S steps: projection of cond and uncond hidden rows
     (weights from N(0, 0.02), hidden rows N(0, 1)), then the sampler (k 1000,
-    p 0.95, T 0.8, pen 1.2, w 0.5) in one call."""
+    p 0.95, T 0.8, pen 1.2, w 0.5) in one call.  B=64 x 2 projects 256 rows
+    on the matrix cores; one CFG pair (2 rows) and 7 pairs (14 rows) take the
+    mat-vec kernel."""
     torch = torch_cuda
     mod, s = cbx
-    V, K, B, S = 6563, 1024, 64, 2
+    V, K = 6563, 1024
     rng = np.random.default_rng(77 + wtype)
     blocks, bias, h = _problem(rng, V, K, B * S, wtype, scale=0.02)
     hu = (h + 0.5 * rng.standard_normal(h.shape)).astype(np.float32)
