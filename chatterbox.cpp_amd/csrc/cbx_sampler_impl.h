@@ -1884,8 +1884,15 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         }
     }
     if (tid < 32) tab[tid] = kExp2TabDev.t[tid];
-    // history ids -> seen bitmap
-    for (int w = tid; w < W; w += BLOCK) { keptw[w] = 0u; seen[w] = 0u; }
+    // the allowed row, staged in the region (free until the top-k pass) so
+    // the mask pass reads its words from LDS; history ids -> seen bitmap
+    const uint32_t* arow = a.allowed ? a.allowed + (int64_t)row * a.ld_allowed : nullptr;
+    uint32_t* const mrow = reinterpret_cast<uint32_t*>(region);
+    for (int w = tid; w < W; w += BLOCK) {
+        keptw[w] = 0u;
+        seen[w] = 0u;
+        if (arow) mrow[w] = arow[w];
+    }
     if (tid == 0) sh.flags = 0u;
     __syncthreads();
     if (use_pen) {
@@ -1899,7 +1906,6 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
             if (t >= 0 && t < V) atomicOr(&seen[t >> 5], 1u << (t & 31));
         }
     }
-    const uint32_t* arow = a.allowed ? a.allowed + (int64_t)row * a.ld_allowed : nullptr;
     const bool fstop = a.force_stop && a.force_stop[rs];
     const bool scale = P.temp > 0.0f && P.temp != 1.0f;
     const float inv_t = __fdiv_rn(1.0f, P.temp);
@@ -1908,17 +1914,14 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     // element j of this lane is id j*BLOCK + tid: valid for j < n_mine; its
     // allowed bit is bit (tid & 31) of word j*BLOCK/32 + tid/32
     const int n_mine = (V - tid + BLOCK - 1) / BLOCK;
-    __amdgpu_buffer_rsrc_t ra_mask;
-    if (arow)
-        ra_mask = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(arow), (short)0, W * 4,
-                                                    kBufferWord3);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         float v = s[j];
         bool masked = j >= n_mine;
         if (arow) {
-            const uint32_t word = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                ra_mask, (tid >> 5) * 4, j * (BLOCK / 32) * 4, 0);
+            // word j*BLOCK/32 + tid/32 (words past the row: the element is past V)
+            const int w = j * (BLOCK / 32) + (tid >> 5);
+            const uint32_t word = w < W ? mrow[w] : 0u;
             masked = masked || !((word >> (tid & 31)) & 1u);
         }
         if (fstop) masked = masked || (j * BLOCK + tid) != a.stop_token;
@@ -1940,8 +1943,17 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     if (use_topk) {
         float thr;
         int above;
-        if (bad || !(hi > lo) ||
-            !topk_value_bins<BLOCK, EPT>(s, P.top_k, lo, hi, hist, cand, sh, thr, above)) {
+        if (!bad && !(hi > lo)) {
+            // every finite score equal (or none): the (k+1)-th largest is that
+            // score when more than k are finite, else -inf; none is above it
+            int mine_f = 0;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) mine_f += (s[j] != kNegInf) ? 1 : 0;
+            const int n_fin = block_sum<BLOCK>(mine_f, sh);
+            thr = n_fin > P.top_k ? lo : kNegInf;
+            above = n_fin > P.top_k ? 0 : n_fin;
+        } else if (bad ||
+                   !topk_value_bins<BLOCK, EPT>(s, P.top_k, lo, hi, hist, cand, sh, thr, above)) {
             thr = okey_inv(radix_select_desc<BLOCK, EPT>(s, V, P.top_k, hist, sh));
             int n_above = 0;
 #pragma unroll

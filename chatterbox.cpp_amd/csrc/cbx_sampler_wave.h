@@ -949,8 +949,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 if (above < k) thr = __fsub_rn(thr, 1e-10f);
             }
         }
+        if (!done && !bad && !(range > 0.0f)) {
+            // every finite score equal (or none; forced-stop rows): the
+            // (k+1)-th largest is that score when more than k are finite,
+            // else -inf, and no score is above it
+            int nf = 0;
+            each_score([&](float v, int) { nf += (v != kNegInf) ? 1 : 0; });
+            const int n_fin = wave_sum_dpp(nf);
+            thr = n_fin > k ? lo : kNegInf;
+            above = n_fin > k ? 0 : n_fin;
+            if (above < k) thr = __fsub_rn(thr, 1e-10f);
+            done = true;
+        }
         if (!done) {
-            // 8-bit radix select over all ids (NaN / inf / degenerate rows)
+            // 8-bit radix select over all ids (NaN / inf rows)
             uint32_t prefix = 0, pmask = 0, rem = (uint32_t)k;
             wave_radix_pass<Q>(rsc, 24, prefix, pmask, rem, sm.khist());
             wave_radix_pass<Q>(rsc, 16, prefix, pmask, rem, sm.khist());

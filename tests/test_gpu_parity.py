@@ -465,6 +465,20 @@ EDGE_CASES = [
     ("topk_rank_below_mean_bins", 6563, dict(top_k=200, top_p=0.9, temp=1.0, repeat_penalty=1.2),
      lambda V, r: np.concatenate([np.full(10, 100.0), np.zeros(246), np.full(300, 3.85),
                                   -5.0 - r.random(V - 556)]).astype(F32), 0.7),
+    # every finite score equal (the top-k threshold in closed form): more than
+    # k of them at 4.0 (the nudge is a no-op: nothing survives), more than k
+    # at 1e-4 (the nudge keeps them all), one finite id (a forced-stop row),
+    # fewer than k finite ids, more than k finite ids among -inf
+    ("all_equal_topk_large", 500, dict(top_k=10, top_p=0.9, temp=1.0, repeat_penalty=1.2),
+     lambda V, r: np.full(V, 4.0, F32), 0.5),
+    ("all_equal_topk_small", 500, dict(top_k=10, top_p=0.9, temp=1.0, repeat_penalty=1.2),
+     lambda V, r: np.full(V, 1e-4, F32), 0.5),
+    ("one_finite_topk", 6563, dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.3),
+     lambda V, r: np.where(np.arange(V) == 6562, F32(3.0), F32(-np.inf)).astype(F32), 0.5),
+    ("few_finite_equal", 6563, dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.3),
+     lambda V, r: np.where(np.arange(V) % 219 == 5, F32(2.0), F32(-np.inf)).astype(F32), 0.5),
+    ("many_finite_equal", 6563, dict(top_k=50, top_p=0.9, temp=0.8, repeat_penalty=1.3),
+     lambda V, r: np.where(np.arange(V) % 64 == 5, F32(2.0), F32(-np.inf)).astype(F32), 0.5),
     # 150 equal survivors in one value bin: the sort falls back to the bitonic network
     ("crowded_bin", 600, dict(top_k=500, top_p=0.9, temp=1.0, repeat_penalty=1.2),
      lambda V, r: np.concatenate([np.full(150, 3.0), np.full(200, 2.0), [10.0],
