@@ -1545,24 +1545,35 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
                              (int)__builtin_amdgcn_mbcnt_lo(bits, 0u) == kb;
             return w * 32 + __builtin_ctzll(__ballot(hit));
         };
+        // The id-order binary32 sum (main.cpp:786-790) is formed only where it
+        // is read: greedy rows, a draw that is not certain, probabilities.
+        // A kept row is never empty: the largest kept score's term is
+        // expf(0) = 1, or NaN when the row holds NaN or +inf.
         const bool fin = !(flags & CBX_INFO_NONFINITE);
-        int unused;
-        const float psum2 = n_final > 0 ? wave_run_sum<run_bound<BLOCK>(BLOCK * EPT), false, false>(
-                                              [&](int i) { return F[i]; }, n_final, 0.0f, 0.0f,
-                                              unused, fin)
-                                        : 0.0f;
+        const bool empty = n_final == 0;
+        float psum2 = 0.0f;
+        bool have_psum2 = false;
+        auto exact_psum2 = [&]() {
+            if (!have_psum2) {
+                int unused;
+                psum2 = wave_run_sum<run_bound<BLOCK>(BLOCK * EPT), false, false>(
+                    [&](int i) { return F[i]; }, n_final, 0.0f, 0.0f, unused, fin);
+                have_psum2 = true;
+            }
+            return psum2;
+        };
         CBX_STAMP(10);
-        const bool empty = (psum2 == 0.0f);
         int token = 0;
         if (empty) {
             flags |= CBX_INFO_EMPTY;
         } else if (P.temp <= 0.0f) {
             // first argmax of p_i = e_i / psum over ids (zeros elsewhere);
             // only NaN probabilities: no maximum, id 0
+            const float ps = exact_psum2();
             float best = -1.0f;
             int first = 0x7fffffff;
             for (int i = lane; i < n_final; i += 64) {
-                const float p = __fdiv_rn(F[i], psum2);
+                const float p = __fdiv_rn(F[i], ps);
                 if (p > best) { best = p; first = i; }  // ascending i: keeps the first
             }
             const float b = wave_max_dpp(best);
@@ -1587,14 +1598,15 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
                 if (rank < 0) {
                     // the reference's arithmetic: float probabilities, double
                     // CDF, on one lane (rare)
+                    const float ps = exact_psum2();
                     int rk = -1;
                     if (lane == 0) {
                         double sum = 0.0;
                         for (int r = 0; r < n_final; ++r)
-                            sum = __dadd_rn(sum, (double)__fdiv_rn(F[r], psum2));
+                            sum = __dadd_rn(sum, (double)__fdiv_rn(F[r], ps));
                         double acc = 0.0;
                         for (int r = 0; r < n_final; ++r) {
-                            acc = __dadd_rn(acc, __ddiv_rn((double)__fdiv_rn(F[r], psum2), sum));
+                            acc = __dadd_rn(acc, __ddiv_rn((double)__fdiv_rn(F[r], ps), sum));
                             const double c = (r == n_final - 1 && last_kept) ? 1.0 : acc;
                             if (c >= u) { rk = r; break; }
                         }
@@ -1607,10 +1619,11 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
             CBX_STAMP(11);
         }
         CBX_STAMP(12);
+        const float ps_out = (a.probs && !empty) ? exact_psum2() : 0.0f;
         if (lane == 0) {
             a.tokens[rs] = token;
             if (a.info) a.info[rs] = flags | sh.flags;
-            sh.psum = empty ? 0.0f : psum2;
+            sh.psum = ps_out;
         }
     }
     if (a.probs) {
