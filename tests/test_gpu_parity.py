@@ -746,6 +746,22 @@ def test_latency_rule_masked(cbx_default, torch_cuda, V):
     parity.compare(f"latency_rule_masked_{V}", tg, ig, tr, ir, u, pg, pr)
 
 
+@pytest.mark.parametrize("V", [1000, 4096, 6656, 8192, 12000, 16384, 20000, 32768])
+def test_latency_rule_vocab_classes(cbx_default, torch_cuda, V):
+    """Default handle: 64 streams x 2 steps with the survivor bound 1000 at
+    every vocabulary class of the workgroup kernel (512 lanes x 8, 13, 16;
+    1024 lanes x 16, 32), at and past each class's end."""
+    w = pkg.workloads()
+    d = w.batched_streams(B=64, steps=2, seed=0x5EED50 + V, V=V)
+    n = d["logits"].shape[0]
+    u = O.mt_canonical(51 + V, n)
+    say(f"latency rule: batched streams 64 x 2, V={V}")
+    tg, ig, pg = gpu_batch(cbx_default, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], n_steps=2, max_survivors=1000)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"])
+    parity.compare(f"latency_rule_V{V}", tg, ig, tr, ir, u, pg, pr)
+
+
 def test_latency_rule_same_results_either_way(cbx_default, torch_cuda):
     """The rule changes the kernel, not the result: a CFG batch of 128 rows
     with top-p ties and tiny top-k ties sampled with the rule on and off is
