@@ -1338,7 +1338,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
                 for (int q = 0; q < CC; ++q) ev[q] = __fdiv_rn(ev[q], psum);  // 0 stays 0
                 int hit;
-                (void)chain_sweeps<CC, true>(ev, nl, P.top_p, hit);
+                if constexpr (CC >= 7) {
+                    if (!bad) (void)chain_segments_x<CC, true>(ev, nl, 0.0f, P.top_p, hit);
+                    else (void)chain_sweeps<CC, true>(ev, nl, P.top_p, hit);
+                } else {
+                    (void)chain_sweeps<CC, true>(ev, nl, P.top_p, hit);
+                }
                 last = hit < 0 ? n_surv - 1 : hit;
             }
         });
