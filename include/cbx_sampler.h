@@ -61,9 +61,11 @@ typedef struct cbx_params {
                                     ones are those the reference's std::sort puts
                                     first (its order is replayed)                  */
 #define CBX_INFO_NONFINITE 0x10u /* NaN or +inf scores: outside the contract           */
-#define CBX_INFO_OVERFLOW  0x20u /* more survivors than the device's on-chip
-                                    capacity (never on gfx950, whose LDS holds every
-                                    id of a 32768 vocabulary): token -1            */
+#define CBX_INFO_OVERFLOW  0x20u /* more survivors than the launch's capacity:
+                                    token -1.  Only past the 4096 row-steps of a
+                                    call's redo list (max_survivors set too low);
+                                    at full capacity never on gfx950, whose LDS
+                                    holds every id of a 32768 vocabulary           */
 
 #define CBX_DRAW_UNIFORM 0 /* uniforms[step][row] supplied by the caller            */
 #define CBX_DRAW_PHILOX  1 /* Philox4x32-10: counter {step lo, step hi, stream lo,
@@ -101,7 +103,10 @@ typedef struct cbx_batch {
                                    survivors (ties at a tiny top-k threshold, top-k
                                    off) are sampled again on the same stream by a
                                    second pass at the capacity of the whole
-                                   vocabulary, so every row gets its token      */
+                                   vocabulary: up to 4096 such row-steps per call;
+                                   any beyond keep token -1 and CBX_INFO_OVERFLOW
+                                   (a call whose rows may all exceed the bound,
+                                   e.g. top-k off, passes 0)                    */
     const double*   uniforms;   /* CBX_DRAW_UNIFORM: [n_steps][n_rows] in [0,1)      */
     uint64_t        seed;       /* CBX_DRAW_PHILOX key                              */
     const uint64_t* stream_ids; /* CBX_DRAW_PHILOX: [n_rows]; NULL = row index      */

@@ -674,6 +674,31 @@ def test_batch_overflow_rows_redone(cbx, torch_cuda):
     parity.compare("batch_overflow_redo", tg, ig, tr, ir, u, pg, pr)
 
 
+def test_batch_overflow_past_redo_list(cbx, torch_cuda):
+    """More overflowing row-steps in one call than the redo list holds (4096):
+    4200 rows with top-k off at max_survivors=64.  Exactly 4096 of them are
+    sampled again (which ones depends on the order the rows finish), each the
+    oracle's token; the other 104 keep token -1 and CBX_INFO_OVERFLOW."""
+    V, n, redo_len = 600, 4200, 4096
+    rng = np.random.default_rng(0x4200)
+    x = (rng.standard_normal((n, V)) * 2).astype(F32)
+    plist = [dict(top_k=0, top_p=0.9, temp=0.9, repeat_penalty=1.2, min_p=0.0,
+                  cfg_weight=0.0)] * n
+    hist = rng.integers(0, V, size=(n, 32)).astype(np.int32)
+    hl = np.full(n, 32, np.int32)
+    u = rng.random(n)
+    say(f"batch overflow past the redo list: n={n} V={V} max_survivors=64")
+    tg, ig, _ = gpu_batch(cbx, torch_cuda, x, plist, u, hist, hl, max_survivors=64,
+                          want_probs=False)
+    done = tg >= 0
+    assert np.count_nonzero(done) == redo_len
+    assert np.all(tg[~done] == -1)
+    assert np.all(ig[~done] & parity.INFO_OVERFLOW)
+    assert not np.any(ig[done] & parity.INFO_OVERFLOW)
+    tr, ir, _ = oracle_rows(x, plist, u, hist, hl, want_probs=False)
+    parity.compare("batch_overflow_past_redo", tg[done], ig[done], tr[done], ir[done], u[done])
+
+
 @pytest.mark.parametrize("max_survivors", [0, 50])
 def test_topk_off_full_vocab_32768(cbx, torch_cuda, max_survivors):
     """top_k = 0 at V = 32768: all 32768 ids survive top-k, so top-p sorts the
