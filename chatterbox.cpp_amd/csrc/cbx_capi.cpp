@@ -41,6 +41,9 @@ struct cbx_sampler {
     int32_t* static_redo = nullptr;
     // launches of at most this many row-steps run at full capacity
     int64_t latency_rows = cbx::kLatencyRows;
+    // the head's activation split (matrix-core projections), grown on demand
+    void* d_head = nullptr;
+    size_t head_bytes = 0;
     // pinned host staging for the small per-call inputs/outputs
     struct Small {
         cbx_params params;
@@ -124,6 +127,7 @@ void release(cbx_sampler* s) {
     (void)hipFree(s->d_probs);
     (void)hipFree(s->d_redo);
     (void)hipFree(s->d_redo_row);
+    (void)hipFree(s->d_head);
     if (s->h_small) (void)hipHostFree(s->h_small);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
@@ -446,16 +450,29 @@ int check_head(const char* fn, const cbx_head* h, int32_t n_rows, int32_t n_voca
     // the kernel's buffer descriptors address the weights and rows in 32 bits
     const int64_t bpb = h->wtype == CBX_WTYPE_F16 ? 64 : (h->wtype == CBX_WTYPE_Q4_0 ? 18 : 34);
     if ((int64_t)n_vocab * (h->n_embd / 32) * bpb > 0x7fffffffLL ||
-        ((int64_t)n_rows * h->ld_hidden + h->n_embd) * 4 > 0x7fffffffLL)
+        ((int64_t)n_rows * h->ld_hidden + h->n_embd) * 4 > 0x7fffffffLL ||
+        (int64_t)(h->hidden_uncond ? 2 : 1) * (n_rows + 15) * h->n_embd * 4 > 0x7fffffffLL)
         return fail(CBX_ERR_UNSUPPORTED, "%s: weights or hidden rows past 2 GiB", fn);
     return CBX_OK;
 }
 
-int run_head(const cbx_head* h, int32_t n_rows, int32_t n_vocab, int64_t ld_logits,
-             hipStream_t st) {
+// The handle's split buffer holds one call's activations at a time: head calls
+// on one handle are ordered on one stream (a larger call than any before
+// waits for the device while the buffer is replaced).
+int run_head(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n_vocab,
+             int64_t ld_logits, hipStream_t st) {
+    const size_t need = cbx::head_scratch_bytes(n_rows, h->hidden_uncond != nullptr, h->n_embd);
+    if (need > s->head_bytes) {
+        CBX_HIP(hipDeviceSynchronize());
+        CBX_HIP(hipFree(s->d_head));
+        s->d_head = nullptr;
+        s->head_bytes = 0;
+        CBX_HIP(hipMalloc(&s->d_head, need));
+        s->head_bytes = need;
+    }
     CBX_HIP(cbx::launch_head(h->weights, h->wtype, h->bias, h->hidden, h->hidden_uncond,
                              h->ld_hidden, h->logits, h->logits_uncond, ld_logits, n_rows,
-                             n_vocab, h->n_embd, st));
+                             n_vocab, h->n_embd, s->d_head, st));
     return CBX_OK;
 }
 }  // namespace
@@ -466,7 +483,7 @@ int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n
     const int rc = check_head("cbx_head_logits", h, n_rows, n_vocab, ld_logits);
     if (rc != CBX_OK) return rc;
     DeviceGuard g(s->device);
-    return run_head(h, n_rows, n_vocab, ld_logits, (hipStream_t)stream);
+    return run_head(s, h, n_rows, n_vocab, ld_logits, (hipStream_t)stream);
 }
 
 int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream) {
@@ -482,7 +499,7 @@ int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
     if (h->hidden_uncond) bb.logits_uncond = h->logits_uncond;
     {
         DeviceGuard g(s->device);
-        const int rh = run_head(h, rows, b->n_vocab, b->ld_logits, (hipStream_t)stream);
+        const int rh = run_head(s, h, rows, b->n_vocab, b->ld_logits, (hipStream_t)stream);
         if (rh != CBX_OK) return rh;
     }
     return cbx_sample_batch(s, &bb, stream);

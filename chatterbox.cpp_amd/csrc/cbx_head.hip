@@ -1,4 +1,4 @@
-// cbx_head.hip -- the T3 speech_head projection on the matrix cores:
+// cbx_head.hip -- the T3 speech_head projection:
 // logits[r][v] = sum_k W[v][k] * h[r][k] + b[v]   (src/main.cpp:577; the weights
 // and bias are chatterbox/speech_head(_bias), main.cpp:394-395), for F16, Q4_0
 // and Q8_0 weights in ggml's layout (ne = [n_embd, n_vocab]: row v holds the
@@ -6,23 +6,29 @@
 // of nibbles, element j < 16 in the low nibble of byte j and element j + 16
 // in its high nibble, w = (q - 8) d; Q8_0 blocks are d and 32 int8, w = q d).
 //
-// A workgroup of KS wavefronts computes 32 vocab ids x NT row tiles of 16
-// rows with v_mfma_f32_16x16x4_f32 (two 16x16 accumulators per tile per
-// wave); the row tiles run over the tiles of the first (cond) row set, then
-// those of the second (uncond), so one workgroup can serve both.  Wave w
-// takes the w-th of KS runs of 32-weight blocks along n_embd, and the KS
-// partial tiles are added in wave order through LDS (a fixed order: results
-// do not depend on scheduling).  Lane l feeds A[l%16][l/16]
-// and B[l/16][l%16] and holds D[4(l/16)+i][l%16] in accumulator register i.
-// Inside a 32-weight block, step s (0..7) and lane group g = l/16 carry
-// k = 8g + s, so each lane dequantizes 8 consecutive weights of one block per
-// vocab row (one fp16 scale, 8 bytes of nibbles or int8) and reads 8
-// consecutive activations: the same k assignment on both operands makes the
-// tile's dot products exact sums over every k.  Weights are dequantized in
-// registers to the fp32 value the format defines (exactly representable);
-// products and sums are the matrix core's fp32.  Rows v >= n_vocab and
-// r >= n_rows read zeros through the buffer descriptors' ranges and store
-// nothing.
+// 16 rows and more run on the fp16 matrix cores in two launches:
+//  * head_split: each activation row r is scaled by a power of two 2^s_r (its
+//    largest magnitude to [2^14, 2^15)) and written as two fp16 parts,
+//    x 2^s = hi + lo + e with |e| <= 2^-23 |x 2^s| + 2^-25 (hi and lo rounded
+//    to nearest; the 2^-25 is lo's subnormal step, 2^-39 of the row's largest
+//    value), together with 2^-s_r, in the matrix-core operand order: for
+//    each 16-row tile and 32-weight block, the 64 lanes' 16 bytes of hi parts,
+//    then their 16 bytes of lo parts, so each operand load reads 1 KB
+//    contiguous (loads of 64-byte pieces of 16 rows were the kernel's limit).
+//  * head_mfma: a workgroup of KS waves computes 32 vocab ids x NT row tiles
+//    of 16 rows with v_mfma_f32_16x16x32_f16, A = the activation parts, B =
+//    the weights: F16 weights as they are, Q4_0 / Q8_0 as their integers
+//    (n - 8 or q, exact in fp16) with each block's product scaled by its d
+//    in fp32.  Products of fp16 values are exact in fp32; sums are the
+//    matrix core's fp32.  Wave w takes the w-th of KS runs of 32-weight
+//    blocks along n_embd, and the KS partial tiles are added in wave order
+//    through LDS (a fixed order: results do not depend on scheduling); the
+//    sum is scaled back by 2^-s_r (exact) and the bias added.
+// Lane l feeds A[l%16][8(l/16) ..] and B[8(l/16) ..][l%16] (the same k on
+// both operands, so a tile's products are sums over every k) and holds
+// D[4(l/16)+i][l%16]: hidden row 4(l/16)+i of the tile, vocab id l%16.
+// Rows v >= n_vocab and r >= n_rows read zeros through the buffer
+// descriptors' ranges and store nothing.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,12 +38,99 @@ namespace cbx {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 constexpr int32_t kBufWord3 = 0x00020000;  // raw buffer: 32-bit data format
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t hb) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
 }
 
+__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+// ------------------------------------------------------------ activation split
+constexpr int kSplitThreads = 256;
+// Bytes of head_split's output for R rows (a multiple of 16) of n_embd: the
+// parts (4 bytes per activation), then R scales from the next 256-byte
+// boundary.
+size_t split_bytes(int R, int n_embd) {
+    return ((size_t)R * n_embd * 4 + 255) / 256 * 256 + (size_t)R * 4;
+}
+
+// One workgroup per padded row p = 16 T + m of the row tiles T (the tiles of
+// hidden0's n_rows rows, then those of hidden1's); rows past a set's n_rows
+// are written as zeros.  The row is read once into registers (thread t holds
+// the groups t, t + 256, ...: at most kSplitGroups of them, n_embd <= 16384).
+// Group j (activations 8j .. 8j + 7) of the row is lane 16 (j % 4) + m's
+// operand of block j / 4: dwords ((T nball + j/4) 512 + 4 lane) .. + 3 hold
+// its hi parts and the same + 256 its lo parts; inv[p] = 2^-s_p.
+constexpr int kSplitGroups = 16384 / 8 / kSplitThreads;
+__global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0,
+                                                            const float* hidden1, int64_t ld_hidden,
+                                                            int n_rows, int n_embd,
+                                                            uint32_t* parts, float* inv) {
+    __shared__ float wmax[kSplitThreads / 64];
+    const int p = blockIdx.x, tid = threadIdx.x;
+    const int tps = (n_rows + 15) / 16, T = p / 16, m = p % 16;
+    const int rr = (T % tps) * 16 + m;
+    const bool real = rr < n_rows;
+    const float* src = (T < tps ? hidden0 : hidden1) + (int64_t)(real ? rr : 0) * ld_hidden;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(src), (short)0, real ? n_embd * 4 : 0, kBufWord3);
+    const int ng = n_embd / 8, nball = n_embd / 32;
+    f4 a[kSplitGroups], b[kSplitGroups];
+    float mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kSplitGroups; ++q) {
+        const int j = tid + q * kSplitThreads;
+        if (q == 0 || j < ng) {  // past the row (or a padding row): zeros
+            a[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j, 0, 0));
+            b[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16, 0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fmaxf(fabsf(a[q][i]), fabsf(b[q][i])));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kSplitThreads / 64; ++w) mx = fmaxf(mx, wmax[w]);
+    // largest magnitude in [2^E, 2^(E+1)): s = 14 - E, clamped so 2^s and
+    // 2^-s are normal floats (a zero row: s = 0)
+    const int E = (int)(fbits(mx) >> 23) - 127;
+    const int s = mx > 0.0f ? min(max(14 - E, -100), 100) : 0;
+    const float sc = __builtin_bit_cast(float, (uint32_t)(127 + s) << 23);
+    if (tid == 0) inv[p] = __builtin_bit_cast(float, (uint32_t)(127 - s) << 23);
+    uint32_t* const dst = parts + (int64_t)T * nball * 512 + 4 * m;
+#pragma unroll
+    for (int q = 0; q < kSplitGroups; ++q) {
+        const int j = tid + q * kSplitThreads;
+        if (j < ng) {
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                y[i] = __fmul_rn(a[q][i], sc);
+                y[4 + i] = __fmul_rn(b[q][i], sc);
+            }
+            u4v hi, lo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 h0 = (_Float16)y[2 * i], h1 = (_Float16)y[2 * i + 1];
+                const _Float16 l0 = (_Float16)__fsub_rn(y[2 * i], (float)h0);
+                const _Float16 l1 = (_Float16)__fsub_rn(y[2 * i + 1], (float)h1);
+                hi[i] = __builtin_bit_cast(uint32_t, h2{h0, h1});
+                lo[i] = __builtin_bit_cast(uint32_t, h2{l0, l1});
+            }
+            uint32_t* const o = dst + (j >> 2) * 512 + 64 * (j & 3);
+            *reinterpret_cast<u4v*>(o) = hi;
+            *reinterpret_cast<u4v*>(o + 256) = lo;
+        }
+    }
+}
+
+// --------------------------------------------------------------- matrix cores
 // Raw bytes of the 8 weights k = 8g .. 8g + 7 of one block of a vocab row,
 // from the row's chunk staged in LDS: F16 four dwords; Q4_0 / Q8_0 the fp16
 // scale in q[4] and the 8 bytes of nibbles or int8 in q[0..1].  Blocks are
@@ -67,51 +160,60 @@ __device__ __forceinline__ void lds_w(const uint32_t* srow, int off, int g, uint
 
 __device__ __forceinline__ float ubyte(uint32_t x, int i) { return (float)((x >> (8 * i)) & 0xffu); }
 
-// The fp32 weights the format defines, from lds_w's bytes.  Q4_0: nibble
-// n = q + 8 and w = (n - 8) d = fma(n, d, -8d), exact (n d and -8d are exact
-// and their sum is representable); Q8_0: u = q + 128 (sign bit flipped) and
-// w = fma(u, d, -128d), exact for the same reason.
+// Two bytes b0, b1 of x (bytes sel0, sel1) as fp16 (b - off): the byte under
+// the high byte 0x64 is the fp16 1024 + b, exactly, and the packed fp16
+// subtraction of 1024 + off leaves b - off (an integer of at most 8 bits:
+// exact).
+__device__ __forceinline__ uint32_t bytes_f16(uint32_t x, uint32_t sel, _Float16 off) {
+    const uint32_t v = __builtin_amdgcn_perm(0x64646464u, x, sel);
+    const h2 r = __builtin_bit_cast(h2, v) - h2{off, off};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// The 8 integer weights of lds_w's bytes as fp16: Q4_0 n - 8, Q8_0 q; and the
+// block's scale d.
 template <int WT>
-__device__ __forceinline__ void dequant(const uint32_t* q, int g, float* w) {
-    if constexpr (WT == CBX_WTYPE_F16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w[2 * i] = half_bits_to_float(q[i] & 0xffffu);
-            w[2 * i + 1] = half_bits_to_float(q[i] >> 16);
-        }
+__device__ __forceinline__ u4v int_weights(const uint32_t* q, int g, float& d) {
+    d = half_bits_to_float(q[4]);
+    uint32_t x0, x1;
+    _Float16 off;
+    if constexpr (WT == CBX_WTYPE_Q4_0) {
+        const int sh = g < 2 ? 0 : 4;
+        x0 = (q[0] >> sh) & 0x0f0f0f0fu;
+        x1 = (q[1] >> sh) & 0x0f0f0f0fu;
+        off = (_Float16)1032.0f;
     } else {
-        const float d = half_bits_to_float(q[4]);
-        uint32_t x0, x1;
-        float off;
-        if constexpr (WT == CBX_WTYPE_Q4_0) {
-            const int sh = g < 2 ? 0 : 4;
-            x0 = (q[0] >> sh) & 0x0f0f0f0fu;
-            x1 = (q[1] >> sh) & 0x0f0f0f0fu;
-            off = __fmul_rn(d, -8.0f);
-        } else {
-            x0 = q[0] ^ 0x80808080u;
-            x1 = q[1] ^ 0x80808080u;
-            off = __fmul_rn(d, -128.0f);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w[i] = __fmaf_rn(ubyte(x0, i), d, off);
-            w[4 + i] = __fmaf_rn(ubyte(x1, i), d, off);
-        }
+        x0 = q[0] ^ 0x80808080u;
+        x1 = q[1] ^ 0x80808080u;
+        off = (_Float16)1152.0f;
     }
+    // selector bytes: 0-3 the bytes of x, 4 the constant's 0x64
+    return u4v{bytes_f16(x0, 0x04010400u, off), bytes_f16(x0, 0x04030402u, off),
+               bytes_f16(x1, 0x04010400u, off), bytes_f16(x1, 0x04030402u, off)};
+}
+
+__device__ __forceinline__ f4 mfma_f16(const u4v& a, const u4v& b, const f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a),
+                                                  __builtin_bit_cast(h8, b), c, 0, 0, 0);
 }
 
 constexpr int KS = 4;  // waves per workgroup (runs of blocks along n_embd)
-// Row tiles of 16 per workgroup: each dequantized weight feeds the products
-// of NT tiles, so weight loads and dequantization are shared by 16*NT rows
-// (NT = 4: 37.2 -> 31.7 us at 128 rows, V = 6563; NT = 8 leaves one wave
-// per SIMD and ran slower).
-constexpr int NT = 4;
+// NT row tiles of 16 per workgroup (a template argument): each weight block
+// feeds the products of NT tiles, so weight loads and conversions are shared
+// by 16 NT rows.  Measured at 128 rows, V = 6563, n_embd = 1024 (us, 4 / 2
+// tiles): Q4_0 15.3 / 13.9, Q8_0 15.6 / 17.7, F16 17.6 / 23.7; at 16 rows 2
+// tiles is faster for all three (one workgroup per CU either way).
+// Register sets for the activation parts of RING consecutive blocks: the
+// loads of block kb + RING - 1 are issued as block kb's products start (4
+// sets measured no faster than 2).
+constexpr int RING = 2;
 
-template <int WT>
+// parts, inv: head_split's output for the n_tiles row tiles (those of
+// hidden0, then those of hidden1).
+template <int WT, int NT>
 __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float* bias,
-                                                     const float* hidden0, const float* hidden1,
-                                                     int64_t ld_hidden, float* out0, float* out1,
+                                                     const uint32_t* parts, const float* inv,
+                                                     int n_tiles, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
                                                      int n_embd) {
     constexpr int BB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
@@ -122,36 +224,31 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     // texture-address path was the measured limit).  RSW dwords per staged
     // row: the bytes from the dword holding the first, plus one.
     constexpr int CB = WT == CBX_WTYPE_F16 ? 4 : 8;
+    static_assert(CB % RING == 0, "a chunk holds whole rings of blocks");
     constexpr int RSW = (CB * BB + 6) / 4 + 1;
     __shared__ uint32_t stage[KS][32 * RSW];
     __shared__ f4 part[KS - 1][2 * NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = lane & 15, g = lane >> 4;
     const int v0 = blockIdx.x * 32;
-    constexpr int64_t kBlockBytes = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
-    const int64_t wbytes = (int64_t)n_vocab * (n_embd / 32) * kBlockBytes;
+    const int64_t wbytes = (int64_t)n_vocab * (n_embd / 32) * BB;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
-    const int hbytes = (int)(((int64_t)(n_rows - 1) * ld_hidden + n_embd) * 4);
-    const __amdgpu_buffer_rsrc_t rh0 =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(hidden0), (short)0, hbytes, kBufWord3);
-    const __amdgpu_buffer_rsrc_t rh1 = hidden1 ? __builtin_amdgcn_make_buffer_rsrc(
-                                                     const_cast<float*>(hidden1), (short)0, hbytes,
-                                                     kBufWord3)
-                                               : rh0;
+    const int pbytes = n_tiles * 16 * n_embd * 4;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(parts), (short)0, pbytes, kBufWord3);
     const int va = v0 + m, vb = v0 + 16 + m;
     // rows past the table read zeros (byte offsets past the range)
     const int va_c = va < n_vocab ? va : n_vocab, vb_c = vb < n_vocab ? vb : n_vocab;
     // Row tile T = blockIdx.y * NT + t of the tiles of both row sets (those
     // of hidden0, then those of hidden1): set T / tps, rows 16 (T % tps) ...
-    const int tps = (n_rows + 15) / 16, n_tiles = hidden1 ? 2 * tps : tps;
-    int64_t hrow[NT];
+    const int tps = (n_rows + 15) / 16;
+    const int nball = n_embd / 32;
+    uint32_t hoff[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int T = blockIdx.y * NT + t;
-        const int rr = (T % tps) * 16 + m;
-        hrow[t] = (T < n_tiles && rr < n_rows) ? (int64_t)rr * ld_hidden
-                                                : ((int64_t)n_rows * ld_hidden + n_embd);
+        hoff[t] = T < n_tiles ? (uint32_t)(T * nball * 512 + 4 * lane) * 4u : (uint32_t)pbytes;
     }
     f4 acc0[NT], acc1[NT];
 #pragma unroll
@@ -159,79 +256,103 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
         acc0[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
         acc1[t] = acc0[t];
     }
-    const int nball = n_embd / 32;
     const int kb0 = nball * wave / KS, kb1 = nball * (wave + 1) / KS;
-    // block kb + 1's loads are in flight while block kb's products run
-    // (more blocks in flight measured slower: the loads' throughput, not
-    // their latency, is what the products wait for)
-    uint32_t qa[5], qb[5];
-    f4 h0[NT], h1[NT];
-    auto load = [&](int kb) {
+    // The activation parts of RING consecutive blocks are in flight in RING
+    // register sets (block kb in set (kb - kb0) % RING).  The loads are
+    // unconditional (past a wave's run they read the next run's parts, or
+    // zeros past the buffer) and the block loop is unrolled by RING, so no
+    // register copies (and no waits for the loads just issued) join the sets.
+    u4v ph[RING][NT], pl[RING][NT];
+    auto load = [&](int kb, int r) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int T = blockIdx.y * NT + t;
-            const __amdgpu_buffer_rsrc_t rh = T >= tps ? rh1 : rh0;
-            const uint32_t hoff = (uint32_t)((hrow[t] + kb * 32 + 8 * g) * 4);
-            h0[t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rh, hoff, 0, 0));
-            h1[t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rh, hoff + 16, 0, 0));
+            const uint32_t o = hoff[t] + (uint32_t)kb * 2048u;
+            ph[r][t] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 0));
+            pl[r][t] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 1024, 0, 0));
         }
     };
-    if (kb0 < kb1) load(kb0);
+#pragma unroll
+    for (int r = 0; r + 1 < RING; ++r) load(kb0 + r, r);
     uint32_t* const sw = stage[wave];
+    // one block: its weights from the staged chunk, the next block's parts
+    // requested, then the products
+    auto block = [&](int kb, int kbc, int sha, int shb, int r) {
+        const u4v* const ch = ph[r];
+        const u4v* const cl = pl[r];
+        uint32_t qa[5], qb[5];
+        lds_w<WT>(sw + m * RSW, sha + (kb - kbc) * BB, g, qa);
+        lds_w<WT>(sw + (16 + m) * RSW, shb + (kb - kbc) * BB, g, qb);
+        load(kb + RING - 1, (r + RING - 1) % RING);
+        if constexpr (WT == CBX_WTYPE_F16) {
+            const u4v wa = u4v{qa[0], qa[1], qa[2], qa[3]}, wb = u4v{qb[0], qb[1], qb[2], qb[3]};
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc0[t] = mfma_f16(cl[t], wa, acc0[t]);
+                acc1[t] = mfma_f16(cl[t], wb, acc1[t]);
+                acc0[t] = mfma_f16(ch[t], wa, acc0[t]);
+                acc1[t] = mfma_f16(ch[t], wb, acc1[t]);
+            }
+        } else {
+            float da, db;
+            const u4v ia = int_weights<WT>(qa, g, da), ib = int_weights<WT>(qb, g, db);
+            f4 pa[NT], pb[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const f4 z = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                pa[t] = mfma_f16(cl[t], ia, z);
+                pb[t] = mfma_f16(cl[t], ib, z);
+                pa[t] = mfma_f16(ch[t], ia, pa[t]);
+                pb[t] = mfma_f16(ch[t], ib, pb[t]);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc0[t][i] = __fmaf_rn(pa[t][i], da, acc0[t][i]);
+                    acc1[t][i] = __fmaf_rn(pb[t][i], db, acc1[t][i]);
+                }
+            }
+        }
+    };
 #pragma unroll 1
     for (int kbc = kb0; kbc < kb1; kbc += CB) {
         const int nb = min(CB, kb1 - kbc);
-        // stage rows v0 .. v0 + 31 (rows past the table read zeros): the
-        // dwords from the one holding the chunk's first byte
-        const int ndw = (3 + nb * BB + 3) >> 2;  // <= RSW - 1
+        // stage rows v0 .. v0 + 31 (rows past the table read zeros): the NDW
+        // dwords from the one holding the chunk's first byte (a shorter last
+        // chunk stages as many, the rest unused).  Lane 2 rr + h takes
+        // dwords [h H, h H + H) of row rr: one row address per lane, and
+        // every load and store at a constant offset from it (computing each
+        // dword's row and column was a fifth of the kernel's VALU work).
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         {
-            int rr = lane / ndw, d = lane % ndw;
-            const int q64 = 64 / ndw, r64 = 64 % ndw;
-            for (int i = lane; i < 32 * ndw; i += 64) {
-                const int v = v0 + rr < n_vocab ? v0 + rr : n_vocab;
-                const uint32_t a0 = (uint32_t)(((int64_t)v * nball + kbc) * BB) & ~3u;
-                sw[rr * RSW + d] =
-                    (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, a0 + 4u * (uint32_t)d, 0, 0);
-                d += r64;
-                rr += q64;
-                if (d >= ndw) {
-                    d -= ndw;
-                    ++rr;
-                }
-            }
+            constexpr int NDW = RSW - 1, H = (NDW + 1) / 2;
+            const int rr = lane >> 1, hh = lane & 1;
+            const int vrow = v0 + rr;
+            const uint32_t rb =
+                vrow < n_vocab
+                    ? (((uint32_t)(vrow * nball + kbc) * (uint32_t)BB) & ~3u) + 4u * H * hh
+                    : 0x80000000u;
+            uint32_t tv[H];
+#pragma unroll
+            for (int q = 0; q < H; ++q)
+                tv[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, rb + 4u * q, 0, 0);
+            uint32_t* const dst = sw + rr * RSW + H * hh;
+#pragma unroll
+            for (int q = 0; q < H; ++q) dst[q] = tv[q];
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
         const int sha = (int)((((int64_t)va_c * nball + kbc) * BB) & 3);
         const int shb = (int)((((int64_t)vb_c * nball + kbc) * BB) & 3);
+        // chunks start a multiple of RING blocks after kb0 (CB is one), and
+        // only a wave's last chunk can hold fewer
 #pragma unroll 1
-    for (int kb = kbc; kb < kbc + nb; ++kb) {
-        lds_w<WT>(sw + m * RSW, sha + (kb - kbc) * BB, g, qa);
-        lds_w<WT>(sw + (16 + m) * RSW, shb + (kb - kbc) * BB, g, qb);
-        float wa[8], wb[8];
-        dequant<WT>(qa, g, wa);
-        dequant<WT>(qb, g, wb);
-        float hv[NT][8];
+        for (int kb = kbc; kb < kbc + nb; kb += RING) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[t][e] = h0[t][e];
-                hv[t][4 + e] = h1[t][e];
-            }
+            for (int u = 0; u < RING; ++u)
+                if (kb + u < kbc + nb) block(kb + u, kbc, sha, shb, u);
         }
-        if (kb + 1 < kb1) load(kb + 1);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                acc0[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], hv[t][s], acc0[t], 0, 0, 0);
-                acc1[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb[s], hv[t][s], acc1[t], 0, 0, 0);
-            }
-        }
-    }
     }
     // the partial tiles of waves 1 .. KS-1 join wave 0's in wave order
     if (wave > 0) {
@@ -255,17 +376,23 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
             }
         }
     }
+    // D[4g + i][m]: hidden row 4g + i of the tile, vocab ids va and vb; the
+    // scale 2^-s is exact
+    const float ba = bias && va < n_vocab ? bias[va] : 0.0f;
+    const float bb = bias && vb < n_vocab ? bias[vb] : 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int T = blockIdx.y * NT + t;
-        const int rr = (T % tps) * 16 + m;
-        if (T < n_tiles && rr < n_rows) {
-            float* orow = (T >= tps ? out1 : out0) + (int64_t)rr * ld_out;
+        if (T >= n_tiles) continue;
+        float* const o = T >= tps ? out1 : out0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int v = v0 + 4 * g + i, v2 = v + 16;
-                if (v < n_vocab) orow[v] = __fadd_rn(acc0[t][i], bias ? bias[v] : 0.0f);
-                if (v2 < n_vocab) orow[v2] = __fadd_rn(acc1[t][i], bias ? bias[v2] : 0.0f);
+        for (int i = 0; i < 4; ++i) {
+            const int rr = (T % tps) * 16 + 4 * g + i;
+            if (rr < n_rows) {
+                const float sinv = inv[T * 16 + 4 * g + i];
+                float* orow = o + (int64_t)rr * ld_out;
+                if (va < n_vocab) orow[va] = __fadd_rn(__fmul_rn(acc0[t][i], sinv), ba);
+                if (vb < n_vocab) orow[vb] = __fadd_rn(__fmul_rn(acc1[t][i], sinv), bb);
             }
         }
     }
@@ -446,16 +573,36 @@ hipError_t launch_gemv_r(const void* W, const float* bias, const float* hidden0,
                                n_vocab, n_embd, stream);
 }
 
+template <int WT, int NT>
+hipError_t launch_mfma(const void* W, const float* bias, const uint32_t* parts, const float* inv,
+                       int n_tiles, float* out0, float* out1, int64_t ld_out, int n_rows,
+                       int n_vocab, int n_embd, hipStream_t stream) {
+    const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT), 1u);
+    hipLaunchKernelGGL((head_mfma<WT, NT>), grid, dim3(64 * KS), 0, stream, W, bias, parts, inv,
+                       n_tiles, out0, out1, ld_out, n_rows, n_vocab, n_embd);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd) {
+    const int R = cfg ? 2 * n_rows : n_rows;
+    return R < 16 && (size_t)R * gemv_row_words(n_embd) * 4 <= 65536;
+}
+
+size_t head_scratch_bytes(int32_t n_rows, bool cfg, int32_t n_embd) {
+    const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1);
+    return head_uses_gemv(n_rows, cfg, n_embd) ? 0 : split_bytes(16 * n_tiles, n_embd);
+}
 
 hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                       hipStream_t stream) {
+                       void* scratch, hipStream_t stream) {
     // fewer than 16 projected rows: the mat-vec (activations staged in LDS,
-    // at most 64 KiB of them), else the 16-row matrix-core tiles
-    const int R = hidden1 ? 2 * n_rows : n_rows;
-    if (R < 16 && (size_t)R * gemv_row_words(n_embd) * 4 <= 65536) {
+    // at most 64 KiB of them), else the split and the 16-row matrix-core tiles
+    const bool cfg = hidden1 != nullptr;
+    if (head_uses_gemv(n_rows, cfg, n_embd)) {
         switch (wtype) {
             case CBX_WTYPE_F16:
                 return launch_gemv_r<CBX_WTYPE_F16>(W, bias, hidden0, hidden1, ld_hidden, out0,
@@ -470,28 +617,34 @@ hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const fl
                 return hipErrorInvalidValue;
         }
     }
-    const int n_tiles = ((n_rows + 15) / 16) * (hidden1 ? 2 : 1);
-    const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT), 1u);
+    if (!scratch) return hipErrorInvalidValue;
+    const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1), R = 16 * n_tiles;
+    uint32_t* parts = static_cast<uint32_t*>(scratch);
+    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) +
+                                          ((size_t)R * n_embd * 4 + 255) / 256 * 256);
+    hipLaunchKernelGGL(head_split, dim3((unsigned)R), dim3(kSplitThreads), 0, stream, hidden0,
+                       hidden1, ld_hidden, n_rows, n_embd, parts, inv);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // two row tiles per workgroup for Q4_0 and for at most two tiles
+    const bool two = wtype == CBX_WTYPE_Q4_0 || n_tiles <= 2;
     switch (wtype) {
         case CBX_WTYPE_F16:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_F16>, grid, dim3(64 * KS), 0, stream, W, bias,
-                               hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
-                               n_embd);
-            break;
+            return two ? launch_mfma<CBX_WTYPE_F16, 2>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                       ld_out, n_rows, n_vocab, n_embd, stream)
+                       : launch_mfma<CBX_WTYPE_F16, 4>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                       ld_out, n_rows, n_vocab, n_embd, stream);
         case CBX_WTYPE_Q4_0:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q4_0>, grid, dim3(64 * KS), 0, stream, W, bias,
-                               hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
-                               n_embd);
-            break;
+            return launch_mfma<CBX_WTYPE_Q4_0, 2>(W, bias, parts, inv, n_tiles, out0, out1, ld_out,
+                                                  n_rows, n_vocab, n_embd, stream);
         case CBX_WTYPE_Q8_0:
-            hipLaunchKernelGGL(head_mfma<CBX_WTYPE_Q8_0>, grid, dim3(64 * KS), 0, stream, W, bias,
-                               hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
-                               n_embd);
-            break;
+            return two ? launch_mfma<CBX_WTYPE_Q8_0, 2>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                        ld_out, n_rows, n_vocab, n_embd, stream)
+                       : launch_mfma<CBX_WTYPE_Q8_0, 4>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                        ld_out, n_rows, n_vocab, n_embd, stream);
         default:
             return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace cbx

@@ -90,10 +90,13 @@ hipError_t launch_redo_v1024x32(const KernelArgs& a, hipStream_t stream);
 
 // The speech_head projection (cbx_head.hip): out0[r][v] = W[v] . hidden0[r] + bias[v]
 // for r < n_rows, v < n_vocab, and the same from hidden1 into out1 in the same
-// launch when hidden1 is given.
+// launches when hidden1 is given.  `scratch` is device memory of at least
+// head_scratch_bytes(n_rows, hidden1 != NULL, n_embd) bytes (the activations
+// split for the matrix cores; 0 bytes, and NULL allowed, below 16 rows).
+size_t head_scratch_bytes(int32_t n_rows, bool cfg, int32_t n_embd);
 hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                       hipStream_t stream);
+                       void* scratch, hipStream_t stream);
 
 }  // namespace cbx

@@ -154,9 +154,11 @@ int cbx_sample_row_ex(cbx_sampler* s, const float* logits, const float* logits_u
                       int32_t force_stop, int32_t stop_token, double u,
                       int32_t* token_out, uint32_t* info_out, float* probs_out);
 
-/* Batched, device memory, asynchronous on `stream`.  The handle only supplies
- * the device; no handle state is written, so one handle may serve several
- * streams.  Replaces n_steps x n_rows calls of sample_next_token_ex. */
+/* Batched, device memory, asynchronous on `stream`.  The handle supplies the
+ * device and the redo list of a launch with max_survivors set (the rows it
+ * samples again): calls on one handle that overlap in time on several
+ * streams race on that list, so each stream takes its own handle.
+ * Replaces n_steps x n_rows calls of sample_next_token_ex. */
 int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream);
 
 /* cbx_sample_batch without any device memory of the handle: the rows to
@@ -195,8 +197,12 @@ typedef struct cbx_head {
 } cbx_head;
 
 /* The projection alone for n_rows rows of hidden (and hidden_uncond) into
- * logits (and logits_uncond), row stride ld_logits >= n_vocab; fp32 weights
- * as the format defines them, fp32 matrix-core products and sums.
+ * logits (and logits_uncond), row stride ld_logits >= n_vocab; weights as
+ * the format defines them, exact products, fp32 sums.  From 16 projected rows
+ * on, the fp16 matrix cores take each activation row scaled by a power of
+ * two as two fp16 parts (2^-23 relative), held in a device buffer of the
+ * handle that a call larger than any before it replaces (waiting for the
+ * device): head calls on one handle are ordered on one stream.
  * Replaces the speech_head mul_mat of the T3 step (main.cpp:577).  Async. */
 int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n_vocab,
                     int64_t ld_logits, void* stream);
