@@ -148,14 +148,16 @@ __device__ __forceinline__ void lds_store_b32_lanes(uint32_t addr, uint32_t v, u
 }
 // One step of an append: the lanes whose score v is >= b0 store (id, v) at
 // consecutive 8-byte slots from byte offset sb in lane order, and sb moves
-// past them.  v_cmp writes the lane mask to VCC (inactive lanes 0),
-// s_and_saveexec narrows exec to it and keeps the caller's exec, which is
-// restored after the store.
+// past them.  v_cmp writes the lane mask to VCC (inactive lanes 0); when no
+// lane passes, the rest is branched over (most vectors of a row with a small
+// top_k hold no survivor); else s_and_saveexec narrows exec to it and keeps
+// the caller's exec, which is restored after the store.
 __device__ __forceinline__ uint32_t append_ge(uint32_t sb, float b0, float v, uint32_t id) {
     uint32_t t, cnt;
     uint64_t save;
     asm volatile(
         "v_cmp_le_f32 vcc, %[b0], %[v]\n\t"
+        "s_cbranch_vccz 1f\n\t"
         "s_and_saveexec_b64 %[save], vcc\n\t"
         "v_mbcnt_lo_u32_b32 %[t], vcc_lo, 0\n\t"
         "v_mbcnt_hi_u32_b32 %[t], vcc_hi, %[t]\n\t"
@@ -163,7 +165,8 @@ __device__ __forceinline__ uint32_t append_ge(uint32_t sb, float b0, float v, ui
         "ds_write2_b32 %[t], %[id], %[v] offset1:1\n\t"
         "s_mov_b64 exec, %[save]\n\t"
         "s_bcnt1_i32_b64 %[cnt], vcc\n\t"
-        "s_lshl3_add_u32 %[sb], %[cnt], %[sb]"
+        "s_lshl3_add_u32 %[sb], %[cnt], %[sb]\n"
+        "1:"
         : [t] "=&v"(t), [cnt] "=&s"(cnt), [sb] "+s"(sb), [save] "=&s"(save)
         : [b0] "s"(b0), [v] "v"(v), [id] "v"(id)
         : "vcc", "scc", "memory");
