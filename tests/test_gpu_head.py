@@ -133,6 +133,29 @@ def test_head_from_gguf(cbx, torch_cuda, tmp_path, wtype):
     assert np.all(np.abs(got.astype(np.float64) - ref) <= tol)
 
 
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+def test_head_row_magnitudes(cbx, torch_cuda, wtype):
+    """The matrix-core path scales each activation row by its own power of two
+    before splitting it into two fp16 parts: rows of magnitude 1e6 (past the
+    fp16 range), 1e-6 (below its normal range), all zeros, and mixed rows
+    (one 1e5 entry among ordinary ones) all project as the binary64 head
+    does, within the same bound."""
+    V, K, R = 900, 512, 32
+    rng = np.random.default_rng(77 + wtype)
+    blocks, bias, h = _problem(rng, V, K, R, wtype)
+    h[0:8] *= 1e6
+    h[8:16] *= 1e-6
+    h[16:20] = 0.0
+    h[20:24, 7] = 1e5
+    say(f"head row magnitudes wtype={wtype} V={V} K={K} R={R}")
+    got = _gpu_head(cbx, torch_cuda, blocks, wtype, bias, h, V, K, V)
+    ref = O.head_f64(blocks, wtype, bias, h, V, K)
+    tol = 1e-5 * _bound(blocks, wtype, h, K) + 1e-6
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= tol), f"max err {err.max():.3g}, worst ratio {(err / tol).max():.3g}"
+    assert np.array_equal(got[16:20], np.broadcast_to(bias, (4, V)))  # zero rows: the bias
+
+
 def test_head_without_bias(cbx, torch_cuda):
     rng = np.random.default_rng(5)
     blocks, _, h = _problem(rng, 500, 256, 20, O.WTYPE_Q4_0)
