@@ -97,10 +97,13 @@ __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < kSplitThreads / 64; ++w) mx = fmaxf(mx, wmax[w]);
-    // largest magnitude in [2^E, 2^(E+1)): s = 14 - E, clamped so 2^s and
-    // 2^-s are normal floats (a zero row: s = 0)
+    // largest magnitude in [2^E, 2^(E+1)): s = 14 - E, clamped to [-126, 126]
+    // so 2^s and 2^-s are normal floats (a zero row: s = 0).  A finite row has
+    // E <= 127, so the lower clamp never binds and no part overflows; the upper
+    // one binds only for rows below 2^-112, whose split error (2^-25 scaled
+    // back by 2^-126) is below the smallest fp32 subnormal.
     const int E = (int)(fbits(mx) >> 23) - 127;
-    const int s = mx > 0.0f ? min(max(14 - E, -100), 100) : 0;
+    const int s = mx > 0.0f ? min(max(14 - E, -126), 126) : 0;
     const float sc = __builtin_bit_cast(float, (uint32_t)(127 + s) << 23);
     if (tid == 0) inv[p] = __builtin_bit_cast(float, (uint32_t)(127 - s) << 23);
     uint32_t* const dst = parts + (int64_t)T * nball * 512 + 4 * m;

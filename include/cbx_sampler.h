@@ -200,7 +200,8 @@ typedef struct cbx_head {
  * logits (and logits_uncond), row stride ld_logits >= n_vocab; weights as
  * the format defines them, exact products, fp32 sums.  From 16 projected rows
  * on, the fp16 matrix cores take each activation row scaled by a power of
- * two as two fp16 parts (2^-23 relative), held in a device buffer of the
+ * two as two fp16 parts (each activation to 2^-23 relative plus 2^-39 of
+ * its row's largest magnitude), held in a device buffer of the
  * handle that a call larger than any before it replaces (waiting for the
  * device): head calls on one handle are ordered on one stream.
  * Replaces the speech_head mul_mat of the T3 step (main.cpp:577).  Async. */

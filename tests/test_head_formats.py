@@ -86,3 +86,66 @@ def test_head_f64_matches_direct_product():
         deq = O.dequantize(b, wtype, K).astype(np.float64)
         want = h.astype(np.float64) @ deq.T + bias.astype(np.float64)
         assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
+
+
+def _split_rows(x):
+    """The matrix-core head's activation split, restated in numpy: each row
+    scaled by 2^s (s = 14 - E for a largest magnitude in [2^E, 2^(E+1)),
+    clamped to [-126, 126]; 0 for a zero row), then hi = fp16(y) and
+    lo = fp16(y - hi) with y = x * 2^s, each rounded to nearest."""
+    x = np.asarray(x, np.float32)
+    mx = np.max(np.abs(x), axis=1)
+    e = np.frexp(np.where(mx > 0, mx, 1.0))[1].astype(np.int64) - 1
+    s = np.where(mx > 0, np.clip(14 - e, -126, 126), 0)
+    sc = np.ldexp(np.float32(1.0), s).astype(np.float32)[:, None]
+    y = (x * sc).astype(np.float32)
+    hi = y.astype(np.float16)
+    lo = (y - hi.astype(np.float32)).astype(np.float16)
+    return y, hi, lo
+
+
+def test_fp16_split_bound():
+    """|x 2^s - hi - lo| <= 2^-23 |x 2^s| + 2^-25 on rows of every magnitude
+    fp32 holds (subnormal 1e-40 .. 3e38, far past the fp16 range either way),
+    and no part overflows: the bound the head's error budget rests on.  Rows
+    above 2^-112 land in [2^14, 2^15); smaller ones take the largest scale."""
+    rng = np.random.default_rng(11)
+    rows = []
+    for mag in (1e-40, 1e-30, 1e-8, 1e-3, 1.0, 3e4, 1e6, 1e30, 1e35):
+        r = (rng.standard_normal((4, 1024)) * mag).astype(np.float32)
+        r[0, ::7] = 0.0
+        r[1, 5] = np.float32(mag * 1e3)  # one entry far above the rest
+        rows.append(r)
+    top = np.full((2, 1024), 1.0, np.float32)
+    top[:, 3] = np.finfo(np.float32).max  # the largest finite float
+    top[1, 4] = -np.finfo(np.float32).max
+    rows.append(top)
+    x = np.concatenate(rows)
+    assert np.all(np.isfinite(x))
+    y, hi, lo = _split_rows(x)
+    assert np.all(np.isfinite(hi)) and np.all(np.isfinite(lo))
+    err = np.abs(y.astype(np.float64) - hi.astype(np.float64) - lo.astype(np.float64))
+    bound = 2.0 ** -23 * np.abs(y.astype(np.float64)) + 2.0 ** -25
+    assert np.all(err <= bound)
+    mx = np.max(np.abs(x), axis=1)
+    m = np.max(np.abs(y), axis=1)
+    big = mx >= 2.0 ** -112
+    assert np.all((m[big] >= 2.0 ** 14) & (m[big] < 2.0 ** 15))
+    assert np.array_equal(y[~big], (x[~big] * np.float32(2.0 ** 126)).astype(np.float32))
+    assert big.sum() >= 30 and (~big).sum() >= 4
+
+
+def test_fp16_integer_weights():
+    """The head's integer weights in fp16: a byte b placed under the exponent
+    of 1024 is 1024 + b exactly, and one fp16 subtraction leaves the Q4_0
+    value n - 8 (b = n <= 15) or the Q8_0 value q (b = q ^ 0x80), exactly."""
+    b = np.arange(256, dtype=np.uint16)
+    f = (np.uint16(0x6400) | b).view(np.float16)
+    assert np.array_equal(f.astype(np.float64), 1024.0 + b)
+    n = b[:16]
+    q4 = (f[:16] - np.float16(1032.0)).astype(np.float64)
+    assert np.array_equal(q4, n.astype(np.float64) - 8)
+    q = np.arange(-128, 128)
+    u = (q.astype(np.int64) & 0xFF) ^ 0x80
+    q8 = (f[u] - np.float16(1152.0)).astype(np.float64)
+    assert np.array_equal(q8, q.astype(np.float64))
