@@ -31,8 +31,15 @@ CBX_INFO_TOPP_TIE = 0x08
 CBX_INFO_NONFINITE = 0x10
 CBX_INFO_OVERFLOW = 0x20
 
+CBX_INFO_ENDED = 0x40
+
 CBX_DRAW_UNIFORM = 0
 CBX_DRAW_PHILOX = 1
+
+CBX_DECODE_RUNNING = 0
+CBX_DECODE_STOP = 1
+CBX_DECODE_LIMIT = 2
+CBX_DECODE_FAILED = 3
 
 
 class Params(ctypes.Structure):
@@ -99,6 +106,19 @@ class Head(ctypes.Structure):
         ("ld_hidden", ctypes.c_int64),
         ("logits", ctypes.c_void_p),
         ("logits_uncond", ctypes.c_void_p),
+    ]
+
+
+class Decode(ctypes.Structure):
+    """cbx_decode (include/cbx_sampler.h): device-resident decode state."""
+
+    _fields_ = [
+        ("state", ctypes.c_void_p),
+        ("history", ctypes.c_void_p),
+        ("history_len", ctypes.c_void_p),
+        ("ld_history", ctypes.c_int64),
+        ("max_len", ctypes.c_void_p),
+        ("next_token", ctypes.c_void_p),
     ]
 
 
@@ -181,6 +201,11 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_head_logits.argtypes = [vp, ctypes.POINTER(Head), i32, i32, i64, vp]
     lib.cbx_head_sample_batch.restype = ctypes.c_int
     lib.cbx_head_sample_batch.argtypes = [vp, ctypes.POINTER(Head), ctypes.POINTER(Batch), vp]
+    lib.cbx_decode_step.restype = ctypes.c_int
+    lib.cbx_decode_step.argtypes = [vp, ctypes.POINTER(Batch), ctypes.POINTER(Decode), vp]
+    lib.cbx_head_decode_step.restype = ctypes.c_int
+    lib.cbx_head_decode_step.argtypes = [vp, ctypes.POINTER(Head), ctypes.POINTER(Batch),
+                                         ctypes.POINTER(Decode), vp]
     lib.cbx_gguf_read_head.restype = ctypes.c_int
     lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
     lib.cbx_gguf_load_head.restype = ctypes.c_int
@@ -330,11 +355,14 @@ class Sampler:
                      logits_uncond=None, history=None, history_len=None, allowed=None,
                      force_stop=None, stop_token=0, info=None, probs=None,
                      draw_mode=None, seed=0, stream_ids=None, step0=0, max_survivors=0,
-                     n_vocab=None, stream=None, head=None, static_scratch=False):
+                     n_vocab=None, stream=None, head=None, static_scratch=False, decode=None):
         """logits: device float32 [n_steps*n_rows, ld] (or [n_steps, n_rows, ld]);
         params: device uint8 tensor from params_tensor(); tokens: device int32.
         n_vocab defaults to ld (the row stride).  static_scratch: call
-        cbx_sample_batch_static (the redo list in the library's device array)."""
+        cbx_sample_batch_static (the redo list in the library's device array).
+        decode: a Decode from decode_state(): one decode step
+        (cbx_decode_step / cbx_head_decode_step), its history in place of
+        history/history_len."""
         ld = logits.shape[-1]
         total_rows = logits.numel() // ld
         n_rows = total_rows // n_steps
@@ -367,12 +395,38 @@ class Sampler:
         b.probs = None if probs is None else probs.data_ptr()
         b.ld_probs = 0 if probs is None else probs.shape[-1]
         st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
-        if head is None:
+        if decode is not None:
+            if head is None:
+                _check(self.lib.cbx_decode_step(self.handle, ctypes.byref(b), ctypes.byref(decode),
+                                                st))
+            else:
+                _check(self.lib.cbx_head_decode_step(self.handle, ctypes.byref(head),
+                                                     ctypes.byref(b), ctypes.byref(decode), st))
+        elif head is None:
             fn = self.lib.cbx_sample_batch_static if static_scratch else self.lib.cbx_sample_batch
             _check(fn(self.handle, ctypes.byref(b), st))
         else:
             _check(self.lib.cbx_head_sample_batch(self.handle, ctypes.byref(head), ctypes.byref(b),
                                                   st))
+
+    @staticmethod
+    def decode_state(state, history, history_len, *, max_len=None, next_token=None):
+        """A cbx_decode over device int32 tensors: state [n_rows], history
+        [n_rows, ld_history], history_len [n_rows], optional max_len and
+        next_token [n_rows]."""
+        d = Decode()
+        d.state = state.data_ptr()
+        d.history = history.data_ptr()
+        d.history_len = history_len.data_ptr()
+        d.ld_history = history.shape[-1]
+        d.max_len = None if max_len is None else max_len.data_ptr()
+        d.next_token = None if next_token is None else next_token.data_ptr()
+        d._tensors = (state, history, history_len, max_len, next_token)
+        return d
+
+    def decode_step(self, logits, params, tokens, decode, **kw):
+        """cbx_decode_step (head=...: cbx_head_decode_step) of one step."""
+        self.sample_batch(logits, params, tokens, decode=decode, **kw)
 
     @staticmethod
     def head(weights, wtype, n_embd, hidden, logits, *, bias=None, hidden_uncond=None,

@@ -397,18 +397,54 @@ int batch_args(const char* fn, const cbx_sampler* s, const cbx_batch* b, cbx::Ke
     a.ld_probs = b->ld_probs;
     return CBX_OK;
 }
+
+// A decode step's batch: b with d's history (one step only).
+int decode_batch(const char* fn, const cbx_batch* b, const cbx_decode* d, cbx_batch& bb) {
+    if (!b || !d) return fail(CBX_ERR_INVALID, "%s: NULL batch or decode state", fn);
+    if (b->n_steps != 1)
+        return fail(CBX_ERR_INVALID, "%s: n_steps %d (a decode step samples one step)", fn,
+                    b->n_steps);
+    if (!d->state || !d->history || !d->history_len || d->ld_history < 1)
+        return fail(CBX_ERR_INVALID, "%s: NULL state, history or history_len, or ld_history < 1",
+                    fn);
+    bb = *b;
+    bb.history = d->history;
+    bb.history_len = d->history_len;
+    bb.ld_history = d->ld_history;
+    return CBX_OK;
+}
+
+// The batched sampler (with a decode step's state update when d is set) on
+// the handle's redo list.
+int sample(const char* fn, cbx_sampler* s, const cbx_batch* b, const cbx_decode* d,
+           hipStream_t st) {
+    cbx::KernelArgs a;
+    const int rc = batch_args(fn, s, b, a);
+    if (rc != CBX_OK) return rc;
+    if (d) {
+        a.dec_state = d->state;
+        a.dec_history = d->history;
+        a.dec_len = d->history_len;
+        a.dec_max = d->max_len;
+        a.dec_next = d->next_token;
+    }
+    DeviceGuard g(s->device);
+    CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, s->latency_rows, st));
+    return CBX_OK;
+}
 }  // namespace
 
 extern "C" {
 
 int cbx_sample_batch(cbx_sampler* s, const cbx_batch* b, void* stream) {
-    cbx::KernelArgs a;
-    const int rc = batch_args("cbx_sample_batch", s, b, a);
+    return sample("cbx_sample_batch", s, b, nullptr, (hipStream_t)stream);
+}
+
+int cbx_decode_step(cbx_sampler* s, const cbx_batch* b, const cbx_decode* d, void* stream) {
+    cbx_batch bb;
+    const int rc = decode_batch("cbx_decode_step", b, d, bb);
     if (rc != CBX_OK) return rc;
-    DeviceGuard g(s->device);
-    CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, s->latency_rows,
-                             (hipStream_t)stream));
-    return CBX_OK;
+    return sample("cbx_decode_step", s, &bb, d, (hipStream_t)stream);
 }
 
 int cbx_sample_batch_static(cbx_sampler* s, const cbx_batch* b, void* stream) {
@@ -486,23 +522,44 @@ int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n
     return run_head(s, h, n_rows, n_vocab, ld_logits, (hipStream_t)stream);
 }
 
-int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream) {
-    if (!s || !b) return fail(CBX_ERR_INVALID, "cbx_head_sample_batch: NULL handle or batch");
+}  // extern "C"
+
+namespace {
+// The projection into h->logits, then the sampler over them (fn names the
+// entry point in messages; d set: a decode step).
+int head_then_sample(const char* fn, cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
+                     const cbx_decode* d, hipStream_t st) {
+    if (!s || !b) return fail(CBX_ERR_INVALID, "%s: NULL handle or batch", fn);
     if (b->n_rows < 1 || b->n_steps < 1 || (int64_t)b->n_rows * b->n_steps > 0x7fffffffLL)
-        return fail(CBX_ERR_INVALID, "cbx_head_sample_batch: n_rows %d, n_steps %d", b->n_rows,
-                    b->n_steps);
+        return fail(CBX_ERR_INVALID, "%s: n_rows %d, n_steps %d", fn, b->n_rows, b->n_steps);
     const int32_t rows = b->n_rows * b->n_steps;
-    const int rc = check_head("cbx_head_sample_batch", h, rows, b->n_vocab, b->ld_logits);
+    const int rc = check_head(fn, h, rows, b->n_vocab, b->ld_logits);
     if (rc != CBX_OK) return rc;
     cbx_batch bb = *b;
+    if (d) {
+        const int rd = decode_batch(fn, b, d, bb);
+        if (rd != CBX_OK) return rd;
+    }
     bb.logits = h->logits;
     if (h->hidden_uncond) bb.logits_uncond = h->logits_uncond;
     {
         DeviceGuard g(s->device);
-        const int rh = run_head(s, h, rows, b->n_vocab, b->ld_logits, (hipStream_t)stream);
+        const int rh = run_head(s, h, rows, b->n_vocab, b->ld_logits, st);
         if (rh != CBX_OK) return rh;
     }
-    return cbx_sample_batch(s, &bb, stream);
+    return sample(fn, s, &bb, d, st);
+}
+}  // namespace
+
+extern "C" {
+
+int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream) {
+    return head_then_sample("cbx_head_sample_batch", s, h, b, nullptr, (hipStream_t)stream);
+}
+
+int cbx_head_decode_step(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
+                         const cbx_decode* d, void* stream) {
+    return head_then_sample("cbx_head_decode_step", s, h, b, d, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -39,6 +39,15 @@ struct KernelArgs {
     // redo_max).  NULL when no redo pass follows the launch.
     int32_t* redo;
     int32_t redo_max;
+    // A decode step's stream state (n_steps == 1, so a row-step is its row;
+    // dec_state NULL for every other call): the writable history and length
+    // (the same memory as history and history_len), the optional length
+    // limits and next-step input ids.
+    int32_t* dec_state;
+    int32_t* dec_history;
+    int32_t* dec_len;
+    const int32_t* dec_max;
+    int32_t* dec_next;
 };
 
 // Rows one redo pass takes at most (one workgroup each).

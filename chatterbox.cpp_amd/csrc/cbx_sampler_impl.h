@@ -1374,6 +1374,51 @@ __device__ __forceinline__ int wave_tied_order(uint32_t* w, uint32_t* tmp, int n
     return m;
 }
 
+// --------------------------------------------------------- decode state
+
+// A decode step's update of stream `row` once its token is final, by one
+// lane: the engine loop's stop test, its push onto `generated` and its length
+// limit (chatterbox_engine.cpp:345-353).  The row read history[0, len) for its
+// penalty before this appends at len; no other row touches the stream.
+__device__ inline void decode_apply(const KernelArgs& a, int row, int32_t token) {
+    if (token < 0) {
+        a.dec_state[row] = CBX_DECODE_FAILED;
+        return;
+    }
+    if (token == a.stop_token) {
+        a.dec_state[row] = CBX_DECODE_STOP;
+        return;
+    }
+    const int64_t lim = a.dec_max ? min((int64_t)a.dec_max[row], a.ld_history) : a.ld_history;
+    int32_t len = max(a.dec_len[row], 0);
+    if (len < lim) {
+        a.dec_history[(int64_t)row * a.ld_history + len] = token;
+        a.dec_len[row] = ++len;
+    }
+    if (a.dec_next) a.dec_next[row] = token;
+    if (len >= lim) a.dec_state[row] = CBX_DECODE_LIMIT;
+}
+
+// A decode step does not sample a stream that has ended (uniform per row).
+__device__ inline bool decode_ended(const KernelArgs& a, int row) {
+    return a.dec_state && a.dec_state[row] != CBX_DECODE_RUNNING;
+}
+
+// A row that overflowed its launch's capacity: onto the redo list when there
+// is one with room (by one lane); a decode step's stream fails when the row
+// keeps token -1.
+__device__ inline void queue_redo(const KernelArgs& a, int64_t rs, int row) {
+    bool queued = false;
+    if (a.redo) {  // the redo pass samples the row again at full capacity
+        const int i = atomicAdd(&a.redo[0], 1);
+        if (i < a.redo_max) {
+            a.redo[2 + i] = (int32_t)rs;
+            queued = true;
+        }
+    }
+    if (a.dec_state && !queued) a.dec_state[row] = CBX_DECODE_FAILED;
+}
+
 // ----------------------------------------------------------------- the draw
 
 // The draw by one wave (main.cpp:795-800; random.tcc:2665-2676, :2708-2712):
@@ -1624,6 +1669,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
             a.tokens[rs] = token;
             if (a.info) a.info[rs] = flags | sh.flags;
             sh.psum = ps_out;
+            if (a.dec_state) decode_apply(a, row, token);
         }
     }
     if (a.probs) {
@@ -1854,8 +1900,15 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     uint32_t* key32 = reinterpret_cast<uint32_t*>(region);
     float* F = reinterpret_cast<float*>(region);
 
-    const cbx_params P = a.params[row];
     const int64_t rs = (int64_t)step * a.n_rows + row;  // row-step linear id
+    if (decode_ended(a, row)) {
+        if (tid == 0) {
+            a.tokens[rs] = a.stop_token;
+            if (a.info) a.info[rs] = CBX_INFO_ENDED;
+        }
+        return;
+    }
+    const cbx_params P = a.params[row];
     CBX_STAMP(0);
 
     // ---- load (all loads first), combine, mask, temperature (main.cpp:733-738) ----
@@ -1990,10 +2043,7 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         if (tid == 0) {
             a.tokens[rs] = -1;
             if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
-            if (a.redo) {  // the redo pass samples the row again at full capacity
-                const int i = atomicAdd(&a.redo[0], 1);
-                if (i < a.redo_max) a.redo[2 + i] = (int32_t)rs;
-            }
+            queue_redo(a, rs, row);
         }
         if (a.probs) {
             float* prow = a.probs + rs * a.ld_probs;

@@ -216,6 +216,54 @@ int cbx_head_logits(cbx_sampler* s, const cbx_head* h, int32_t n_rows, int32_t n
  * hand-off (main.cpp:706-708) and sample_next_token_ex of one T3 step. */
 int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b, void* stream);
 
+/* Decode state of n_rows streams, kept on the device.  The engine's T3 loop
+ * (src/chatterbox_engine.cpp:337-356) pushes each sampled id onto
+ * `generated` (the penalty history of the next call), feeds it to the next
+ * step graph as its "speech_token" input (main.cpp:697), ends a stream at
+ * its stop token (dropped from the result) or after n_predict + 1 ids (or
+ * n_ctx), and copies the logits to the host and waits for them every token
+ * (main.cpp:706-708).  A decode step updates this state on the device
+ * instead, so a loop of steps copies nothing to the host until the caller
+ * reads `state`; `history[r][0, history_len[r])` is then stream r's result. */
+#define CBX_DECODE_RUNNING 0 /* sampled next step                                  */
+#define CBX_DECODE_STOP    1 /* sampled stop_token (not appended): ended           */
+#define CBX_DECODE_LIMIT   2 /* history holds max_len ids: ended                   */
+#define CBX_DECODE_FAILED  3 /* token -1 (CBX_INFO_OVERFLOW past the redo list)    */
+
+#define CBX_INFO_ENDED 0x40u /* decode step: the stream had ended; not sampled, its
+                                token is stop_token                                */
+
+typedef struct cbx_decode {
+    int32_t*       state;       /* [n_rows] CBX_DECODE_*; streams start RUNNING    */
+    int32_t*       history;     /* [n_rows][ld_history] ids sampled so far        */
+    int32_t*       history_len; /* [n_rows]                                       */
+    int64_t        ld_history;  /* >= 1                                           */
+    const int32_t* max_len;     /* optional [n_rows] id limit per stream
+                                   (min(n_predict, n_ctx - prompt_len) + 1 for
+                                   the engine loop); NULL or above ld_history:
+                                   ld_history                                     */
+    int32_t*       next_token;  /* optional [n_rows] out: each id appended, for the
+                                   next step's input                              */
+} cbx_decode;
+
+/* One decode step of b->n_rows streams (b->n_steps must be 1; b's history,
+ * history_len and ld_history are ignored: d's are used): each running stream
+ * is sampled as cbx_sample_batch does, with b->stop_token as its stop id;
+ * then the stop token ends it (CBX_DECODE_STOP), any other id is appended
+ * to its history and written to next_token, and a history of max_len ids
+ * ends it (CBX_DECODE_LIMIT).  Streams already ended are not sampled: their
+ * token is stop_token, info CBX_INFO_ENDED, their probs row is not written.
+ * Asynchronous on `stream`, on the device alone.  Replaces one iteration of
+ * the engine's decode loop after its step graph (chatterbox_engine.cpp:
+ * 345-353) with the logits left on the device. */
+int cbx_decode_step(cbx_sampler* s, const cbx_batch* b, const cbx_decode* d, void* stream);
+
+/* cbx_decode_step on logits projected by the speech_head first, as in
+ * cbx_head_sample_batch: the step graph's ln_f rows in, the next step's input
+ * ids out. */
+int cbx_head_decode_step(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
+                         const cbx_decode* d, void* stream);
+
 /* Thread-local description of the last error on this thread ("" if none). */
 const char* cbx_last_error(void);
 
