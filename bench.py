@@ -20,6 +20,8 @@ kernel (algorithmic bytes / measured launch time vs 8 TB/s), the CPU baseline
 measured shapes:
   launch_shapes           the same kernel at 16 and 64 steps per launch
   single_launch_per_step  B=256, one launch per step (the decode-loop shape)
+  decode_loop             B=256, cbx_decode_step per step with the streams'
+                          state on the device, and with a per-token host sync
   configs                 single stream (B=1, V=6563, 500 steps), CFG pair
                           (B=1, V=8194, history growing to 1000), masked
                           stress (B=1024, V=32768, 20% allowed ids)
@@ -208,6 +210,55 @@ def timed(torch, stream, fn, n, warm=3):
     b.record(stream)
     torch.cuda.synchronize()
     return a.elapsed_time(b) / n
+
+
+def decode_loop_bench(torch, mod, sampler, dev, slabs, S, d_par, hist, hist_len, steps, seed):
+    """B=256 streams of the engine's decode loop, one cbx_decode_step per step
+    on logits taken from the slabs (the step graph's output left on the
+    device): each stream's history grows on the device and nothing is copied
+    to the host between steps.  Beside it, the same loop with the reference's
+    per-token host round trip: the step's tokens copied to the host and waited
+    for before the next step is issued.  The stop id lies outside the
+    vocabulary so every stream is sampled at every step.  Wall clock over the
+    timed steps."""
+    ld = int(hist_len.max()) + steps + 64
+    h0 = np.zeros((B, ld), np.int32)
+    h0[:, :hist.shape[1]] = hist
+    warm, res, grew = 10, {}, True
+    for mode in ("device", "host_sync"):
+        dh = torch.from_numpy(h0).to(dev)
+        dl = torch.from_numpy(hist_len).to(dev)
+        st = torch.zeros(B, dtype=torch.int32, device=dev)
+        nxt = torch.zeros(B, dtype=torch.int32, device=dev)
+        tok = torch.empty(B, dtype=torch.int32, device=dev)
+        host = torch.empty(B, dtype=torch.int32, pin_memory=True)
+        dec = mod.Sampler.decode_state(st, dh, dl, next_token=nxt)
+        cur = torch.cuda.current_stream()
+
+        def step(i):
+            sampler.decode_step(slabs[i % len(slabs)][(i % S) * B:(i % S + 1) * B], d_par, tok,
+                                dec, draw_mode=mod.CBX_DRAW_PHILOX, seed=seed, step0=i,
+                                stop_token=-1)
+            if mode == "host_sync":
+                host.copy_(tok, non_blocking=True)
+                cur.synchronize()
+        for i in range(warm):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(warm + i)
+        torch.cuda.synchronize()
+        res[mode] = (time.perf_counter() - t0) * 1e3 / steps
+        grew = grew and bool(np.array_equal(dl.cpu().numpy(), hist_len + warm + steps)) and \
+            int(st.abs().sum().item()) == 0
+    return {"workload": "decode loop, B=256 streams, V=6563, one cbx_decode_step per step "
+                        "(history grows on the device)",
+            "steps": steps,
+            "ms_per_step_device": round(res["device"], 5),
+            "ms_per_step_host_sync": round(res["host_sync"], 5),
+            "tokens_per_s_device": round(B / (res["device"] / 1e3), 1),
+            "histories_grew_by_steps": grew}
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
@@ -441,6 +492,9 @@ def parse_args(argv=None):
     ap.add_argument("--slabs", type=int, default=2)
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
+    ap.add_argument("--decode-steps", type=int, default=200,
+                    help="timed steps of the device decode loop and its host-synced twin "
+                         "(0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="wall seconds of the single-thread CPU baseline")
     ap.add_argument("--cpu-mt-seconds", type=float, default=2.0,
@@ -552,6 +606,12 @@ def main():
         ms = timed(torch, stream, one, args.single_launch_steps, warm=10)
         single = {"ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1)}
 
+    # the decode loop with its state on the device, beside a per-token host sync
+    decode = None
+    if args.decode_steps > 0:
+        decode = decode_loop_bench(torch, mod, sampler, dev, slabs, S, d_par, hist, hist_len,
+                                   args.decode_steps, philox_seed)
+
     O = None
     if not args.no_cpu:
         import oracle_lib as O
@@ -633,6 +693,7 @@ def main():
         "parity_vs_oracle": parity,
         "launch_shapes": shapes,
         "single_launch_per_step": single,
+        "decode_loop": decode,
         "configs": configs,
         "fused_head": fused,
         "wall_s": round(time.perf_counter() - t_start, 1),

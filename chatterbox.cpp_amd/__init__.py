@@ -39,7 +39,6 @@ CBX_DRAW_PHILOX = 1
 CBX_DECODE_RUNNING = 0
 CBX_DECODE_STOP = 1
 CBX_DECODE_LIMIT = 2
-CBX_DECODE_FAILED = 3
 
 
 class Params(ctypes.Structure):

@@ -414,22 +414,30 @@ int decode_batch(const char* fn, const cbx_batch* b, const cbx_decode* d, cbx_ba
     return CBX_OK;
 }
 
-// The batched sampler (with a decode step's state update when d is set) on
-// the handle's redo list.
+// The batched sampler on the handle's redo list, or with d set a decode step:
+// its own kernel at the capacity of the whole vocabulary (no row overflows,
+// so no redo pass), max_survivors ignored.
 int sample(const char* fn, cbx_sampler* s, const cbx_batch* b, const cbx_decode* d,
            hipStream_t st) {
     cbx::KernelArgs a;
     const int rc = batch_args(fn, s, b, a);
     if (rc != CBX_OK) return rc;
+    const int32_t full = pick_cap(s, b->n_vocab, 0);
+    DeviceGuard g(s->device);
     if (d) {
+        if (full < b->n_vocab)
+            return fail(CBX_ERR_UNSUPPORTED, "%s: this device's LDS holds %d of %d survivors", fn,
+                        full, b->n_vocab);
+        a.cap = full;
         a.dec_state = d->state;
         a.dec_history = d->history;
         a.dec_len = d->history_len;
         a.dec_max = d->max_len;
         a.dec_next = d->next_token;
+        CBX_HIP(cbx::launch_decode(a, st));
+        return CBX_OK;
     }
-    DeviceGuard g(s->device);
-    CBX_HIP(launch_with_redo(pick_cap(s, b->n_vocab, 0), a, s->d_redo, s->latency_rows, st));
+    CBX_HIP(launch_with_redo(full, a, s->d_redo, s->latency_rows, st));
     return CBX_OK;
 }
 }  // namespace

@@ -40,9 +40,9 @@ struct KernelArgs {
     int32_t* redo;
     int32_t redo_max;
     // A decode step's stream state (n_steps == 1, so a row-step is its row;
-    // dec_state NULL for every other call): the writable history and length
-    // (the same memory as history and history_len), the optional length
-    // limits and next-step input ids.
+    // dec_state NULL for every other call; only the decode kernel reads
+    // these): the writable history and length (the same memory as history
+    // and history_len), the optional length limits and next-step input ids.
     int32_t* dec_state;
     int32_t* dec_history;
     int32_t* dec_len;
@@ -96,6 +96,14 @@ hipError_t launch_redo_v512x13(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v512x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v1024x16(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_redo_v1024x32(const KernelArgs& a, hipStream_t stream);
+// A decode step (a.dec_state set, one step, a.cap the full capacity): one
+// workgroup per stream of the vocabulary class's workgroup kernel.
+hipError_t launch_decode(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_decode_v512x8(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_decode_v512x13(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_decode_v512x16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_decode_v1024x16(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_decode_v1024x32(const KernelArgs& a, hipStream_t stream);
 
 // The speech_head projection (cbx_head.hip): out0[r][v] = W[v] . hidden0[r] + bias[v]
 // for r < n_rows, v < n_vocab, and the same from hidden1 into out1 in the same

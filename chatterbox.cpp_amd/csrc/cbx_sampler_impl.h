@@ -1374,51 +1374,6 @@ __device__ __forceinline__ int wave_tied_order(uint32_t* w, uint32_t* tmp, int n
     return m;
 }
 
-// --------------------------------------------------------- decode state
-
-// A decode step's update of stream `row` once its token is final, by one
-// lane: the engine loop's stop test, its push onto `generated` and its length
-// limit (chatterbox_engine.cpp:345-353).  The row read history[0, len) for its
-// penalty before this appends at len; no other row touches the stream.
-__device__ inline void decode_apply(const KernelArgs& a, int row, int32_t token) {
-    if (token < 0) {
-        a.dec_state[row] = CBX_DECODE_FAILED;
-        return;
-    }
-    if (token == a.stop_token) {
-        a.dec_state[row] = CBX_DECODE_STOP;
-        return;
-    }
-    const int64_t lim = a.dec_max ? min((int64_t)a.dec_max[row], a.ld_history) : a.ld_history;
-    int32_t len = max(a.dec_len[row], 0);
-    if (len < lim) {
-        a.dec_history[(int64_t)row * a.ld_history + len] = token;
-        a.dec_len[row] = ++len;
-    }
-    if (a.dec_next) a.dec_next[row] = token;
-    if (len >= lim) a.dec_state[row] = CBX_DECODE_LIMIT;
-}
-
-// A decode step does not sample a stream that has ended (uniform per row).
-__device__ inline bool decode_ended(const KernelArgs& a, int row) {
-    return a.dec_state && a.dec_state[row] != CBX_DECODE_RUNNING;
-}
-
-// A row that overflowed its launch's capacity: onto the redo list when there
-// is one with room (by one lane); a decode step's stream fails when the row
-// keeps token -1.
-__device__ inline void queue_redo(const KernelArgs& a, int64_t rs, int row) {
-    bool queued = false;
-    if (a.redo) {  // the redo pass samples the row again at full capacity
-        const int i = atomicAdd(&a.redo[0], 1);
-        if (i < a.redo_max) {
-            a.redo[2 + i] = (int32_t)rs;
-            queued = true;
-        }
-    }
-    if (a.dec_state && !queued) a.dec_state[row] = CBX_DECODE_FAILED;
-}
-
 // ----------------------------------------------------------------- the draw
 
 // The draw by one wave (main.cpp:795-800; random.tcc:2665-2676, :2708-2712):
@@ -1669,7 +1624,6 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
             a.tokens[rs] = token;
             if (a.info) a.info[rs] = flags | sh.flags;
             sh.psum = ps_out;
-            if (a.dec_state) decode_apply(a, row, token);
         }
     }
     if (a.probs) {
@@ -1900,15 +1854,8 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     uint32_t* key32 = reinterpret_cast<uint32_t*>(region);
     float* F = reinterpret_cast<float*>(region);
 
-    const int64_t rs = (int64_t)step * a.n_rows + row;  // row-step linear id
-    if (decode_ended(a, row)) {
-        if (tid == 0) {
-            a.tokens[rs] = a.stop_token;
-            if (a.info) a.info[rs] = CBX_INFO_ENDED;
-        }
-        return;
-    }
     const cbx_params P = a.params[row];
+    const int64_t rs = (int64_t)step * a.n_rows + row;  // row-step linear id
     CBX_STAMP(0);
 
     // ---- load (all loads first), combine, mask, temperature (main.cpp:733-738) ----
@@ -2043,7 +1990,10 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         if (tid == 0) {
             a.tokens[rs] = -1;
             if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
-            queue_redo(a, rs, row);
+            if (a.redo) {  // the redo pass samples the row again at full capacity
+                const int i = atomicAdd(&a.redo[0], 1);
+                if (i < a.redo_max) a.redo[2 + i] = (int32_t)rs;
+            }
         }
         if (a.probs) {
             float* prow = a.probs + rs * a.ld_probs;
@@ -2312,6 +2262,47 @@ __global__ __launch_bounds__(BLOCK) void redo_rows_kernel(KernelArgs a) {
     }
 }
 
+// One decode step (cbx_decode_step): workgroup r takes stream r (one step, so
+// the row-step is the row) at full capacity, where no row overflows.  A
+// stream that has ended is not sampled; a running one is sampled by the
+// plain row code, after which thread 0 -- the thread that stored the row's
+// token -- reads its own store back and applies the engine loop's update
+// (chatterbox_engine.cpp:345-353): the stop token ends the stream, any other
+// id is pushed onto its history (which the row read, [0, len), for its
+// penalty), written as the next step's input, and ends the stream at its
+// length limit.  The other kernels carry none of this.
+template <int BLOCK, int EPT, int MAXNR>
+__global__ __launch_bounds__(BLOCK) void decode_rows_kernel(KernelArgs a) {
+    __shared__ Shared sh;
+    __shared__ uint64_t tab[32];
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int row = blockIdx.x;
+    if (a.dec_state[row] != CBX_DECODE_RUNNING) {
+        if (threadIdx.x == 0) {
+            a.tokens[row] = a.stop_token;
+            if (a.info) a.info[row] = CBX_INFO_ENDED;
+        }
+        return;
+    }
+    sample_row_wg<BLOCK, EPT, MAXNR, true>(a, row, sh, tab, smem);
+    if (threadIdx.x == 0) {
+        const int32_t token = a.tokens[row];
+        if (token == a.stop_token) {
+            a.dec_state[row] = CBX_DECODE_STOP;
+            return;
+        }
+        const int64_t lim =
+            a.dec_max ? min((int64_t)a.dec_max[row], a.ld_history) : a.ld_history;
+        int32_t len = max(a.dec_len[row], 0);
+        if (len < lim) {
+            a.dec_history[(int64_t)row * a.ld_history + len] = token;
+            a.dec_len[row] = ++len;
+        }
+        if (a.dec_next) a.dec_next[row] = token;
+        if (len >= lim) a.dec_state[row] = CBX_DECODE_LIMIT;
+    }
+}
+
 // LDS a workgroup kernel declares besides its dynamic share (the redo
 // kernel's row list included).
 constexpr size_t kStaticLds = sizeof(Shared) + 32 * 8 + 64;
@@ -2347,6 +2338,24 @@ hipError_t launch_redo_cfg(const KernelArgs& a, hipStream_t stream) {
         granted = lds;
     }
     hipLaunchKernelGGL((redo_rows_kernel<BLOCK, EPT, MAXNR>), dim3((unsigned)a.redo_max),
+                       dim3(BLOCK), lds, stream, a);
+    return hipGetLastError();
+}
+
+// A decode step at capacity a.cap (every row of the vocabulary).
+template <int BLOCK, int EPT>
+hipError_t launch_decode_for(const KernelArgs& a, hipStream_t stream) {
+    constexpr int NRMAX = kFastMax / BLOCK;
+    const size_t lds = lds_bytes_for(a.cap, a.n_vocab);
+    static size_t granted = 64 * 1024 - kStaticLds;
+    if (lds > granted) {
+        hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&decode_rows_kernel<BLOCK, EPT, NRMAX>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        granted = lds;
+    }
+    hipLaunchKernelGGL((decode_rows_kernel<BLOCK, EPT, NRMAX>), dim3((unsigned)a.n_rows),
                        dim3(BLOCK), lds, stream, a);
     return hipGetLastError();
 }

@@ -37,6 +37,14 @@ hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
     return launch_v1024x32(a, stream);
 }
 
+hipError_t launch_decode(const KernelArgs& a, hipStream_t stream) {
+    if (a.n_vocab <= 512 * 8) return launch_decode_v512x8(a, stream);
+    if (a.n_vocab <= 512 * 13) return launch_decode_v512x13(a, stream);
+    if (a.n_vocab <= 512 * 16) return launch_decode_v512x16(a, stream);
+    if (a.n_vocab <= 1024 * 16) return launch_decode_v1024x16(a, stream);
+    return launch_decode_v1024x32(a, stream);
+}
+
 hipError_t launch_redo(const KernelArgs& a, hipStream_t stream) {
     if (a.n_vocab <= 512 * 8) return launch_redo_v512x8(a, stream);
     if (a.n_vocab <= 512 * 13) return launch_redo_v512x13(a, stream);

@@ -8,4 +8,7 @@ hipError_t launch_v512x8(const KernelArgs& a, hipStream_t stream) {
 hipError_t launch_redo_v512x8(const KernelArgs& a, hipStream_t stream) {
     return launch_redo_for<512, 8>(a, stream);
 }
+hipError_t launch_decode_v512x8(const KernelArgs& a, hipStream_t stream) {
+    return launch_decode_for<512, 8>(a, stream);
+}
 }  // namespace cbx

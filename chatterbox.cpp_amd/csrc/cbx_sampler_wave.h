@@ -471,15 +471,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     const int V = a.n_vocab;
     const int W = (V + 31) >> 5;
     const int cap = min(a.cap, kWaveCap);
-    const int64_t rs = (int64_t)step * a.n_rows + row;
-    if (decode_ended(a, row)) {
-        if (lane == 0) {
-            a.tokens[rs] = a.stop_token;
-            if (a.info) a.info[rs] = CBX_INFO_ENDED;
-        }
-        return;
-    }
     const cbx_params P = a.params[row];
+    const int64_t rs = (int64_t)step * a.n_rows + row;
     CBX_STAMP(0);
 
     // ---- load: 16-byte buffer loads bounded at V floats (main.cpp:733) ----
@@ -1010,7 +1003,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         if (lane == 0) {
             a.tokens[rs] = -1;
             if (a.info) a.info[rs] = flags | CBX_INFO_OVERFLOW;
-            queue_redo(a, rs, row);
+            if (a.redo) {  // the redo pass samples the row again at full capacity
+                const int i = atomicAdd(&a.redo[0], 1);
+                if (i < a.redo_max) a.redo[2 + i] = (int32_t)rs;
+            }
         }
         if (a.probs) {
             float* prow = a.probs + rs * a.ld_probs;
@@ -1595,7 +1591,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     if (lane == 0) {
         a.tokens[rs] = token;
         if (a.info) a.info[rs] = oflags;
-        if (a.dec_state) decode_apply(a, row, token);
     }
     if (a.probs) {
         const float ps = empty ? 0.0f : exact_psum2();

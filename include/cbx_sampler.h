@@ -228,7 +228,6 @@ int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
 #define CBX_DECODE_RUNNING 0 /* sampled next step                                  */
 #define CBX_DECODE_STOP    1 /* sampled stop_token (not appended): ended           */
 #define CBX_DECODE_LIMIT   2 /* history holds max_len ids: ended                   */
-#define CBX_DECODE_FAILED  3 /* token -1 (CBX_INFO_OVERFLOW past the redo list)    */
 
 #define CBX_INFO_ENDED 0x40u /* decode step: the stream had ended; not sampled, its
                                 token is stop_token                                */
@@ -248,14 +247,15 @@ typedef struct cbx_decode {
 
 /* One decode step of b->n_rows streams (b->n_steps must be 1; b's history,
  * history_len and ld_history are ignored: d's are used): each running stream
- * is sampled as cbx_sample_batch does, with b->stop_token as its stop id;
- * then the stop token ends it (CBX_DECODE_STOP), any other id is appended
- * to its history and written to next_token, and a history of max_len ids
- * ends it (CBX_DECODE_LIMIT).  Streams already ended are not sampled: their
- * token is stop_token, info CBX_INFO_ENDED, their probs row is not written.
- * Asynchronous on `stream`, on the device alone.  Replaces one iteration of
- * the engine's decode loop after its step graph (chatterbox_engine.cpp:
- * 345-353) with the logits left on the device. */
+ * is sampled as cbx_sample_batch does, with b->stop_token as its stop id, at
+ * the capacity of the whole vocabulary (max_survivors is ignored: no row
+ * overflows); then the stop token ends it (CBX_DECODE_STOP), any other id is
+ * appended to its history and written to next_token, and a history of
+ * max_len ids ends it (CBX_DECODE_LIMIT).  Streams already ended are not
+ * sampled: their token is stop_token, info CBX_INFO_ENDED, their probs row is
+ * not written.  One launch, asynchronous on `stream`, on the device alone.
+ * Replaces one iteration of the engine's decode loop after its step graph
+ * (chatterbox_engine.cpp:345-353) with the logits left on the device. */
 int cbx_decode_step(cbx_sampler* s, const cbx_batch* b, const cbx_decode* d, void* stream);
 
 /* cbx_decode_step on logits projected by the speech_head first, as in
