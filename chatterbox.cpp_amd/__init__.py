@@ -121,6 +121,39 @@ class Decode(ctypes.Structure):
     ]
 
 
+class T3Layer(ctypes.Structure):
+    """cbx_t3_layer (include/cbx_t3.h)."""
+
+    _fields_ = [(f, ctypes.c_void_p) for f in (
+        "ln_1_g", "ln_1_b", "attn_w", "attn_b", "attn_proj_w", "attn_proj_b", "ln_2_g", "ln_2_b",
+        "fc_w", "fc_b", "fc_proj_w", "fc_proj_b")]
+
+
+class T3Model(ctypes.Structure):
+    """cbx_t3_model (include/cbx_t3.h)."""
+
+    _fields_ = [
+        ("n_layer", ctypes.c_int32),
+        ("n_embd", ctypes.c_int32),
+        ("n_head", ctypes.c_int32),
+        ("n_pos", ctypes.c_int32),
+        ("n_speech_vocab", ctypes.c_int32),
+        ("wtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("wpe", ctypes.c_void_p),
+        ("speech_emb", ctypes.c_void_p),
+        ("layers", ctypes.POINTER(T3Layer)),
+        ("ln_f_g", ctypes.c_void_p),
+        ("ln_f_b", ctypes.c_void_p),
+    ]
+
+
+class T3Cache(ctypes.Structure):
+    """cbx_t3_cache (include/cbx_t3.h)."""
+
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("n_ctx", ctypes.c_int32)]
+
+
 class HeadFile(ctypes.Structure):
     """cbx_head_file (include/cbx_gguf.h): the speech_head of a T3 GGUF."""
 
@@ -205,6 +238,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_head_decode_step.restype = ctypes.c_int
     lib.cbx_head_decode_step.argtypes = [vp, ctypes.POINTER(Head), ctypes.POINTER(Batch),
                                          ctypes.POINTER(Decode), vp]
+    lib.cbx_t3_step.restype = ctypes.c_int
+    lib.cbx_t3_step.argtypes = [vp, ctypes.POINTER(T3Model), i32, vp, vp, vp, vp,
+                                ctypes.POINTER(T3Cache), vp, vp]
     lib.cbx_gguf_read_head.restype = ctypes.c_int
     lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
     lib.cbx_gguf_load_head.restype = ctypes.c_int
@@ -422,6 +458,46 @@ class Sampler:
         d.next_token = None if next_token is None else next_token.data_ptr()
         d._tensors = (state, history, history_len, max_len, next_token)
         return d
+
+    @staticmethod
+    def t3_model(layers, wpe, speech_emb, ln_f_g, ln_f_b, *, wtype, n_head, eps=1e-5):
+        """A cbx_t3_model over device tensors: layers a list of dicts with
+        the cbx_t3_layer field names (matrices as uint8 bytes of the wtype
+        layout, the rest float32), wpe [n_pos, n_embd], speech_emb
+        [V, n_embd]."""
+        arr = (T3Layer * len(layers))()
+        for i, L in enumerate(layers):
+            for f, _ in T3Layer._fields_:
+                setattr(arr[i], f, L[f].data_ptr())
+        m = T3Model()
+        m.n_layer = len(layers)
+        m.n_embd = wpe.shape[1]
+        m.n_head = n_head
+        m.n_pos = wpe.shape[0]
+        m.n_speech_vocab = speech_emb.shape[0]
+        m.wtype = wtype
+        m.eps = eps
+        m.wpe = wpe.data_ptr()
+        m.speech_emb = speech_emb.data_ptr()
+        m.layers = arr
+        m.ln_f_g = ln_f_g.data_ptr()
+        m.ln_f_b = ln_f_b.data_ptr()
+        m._keep = (arr, layers, wpe, speech_emb, ln_f_g, ln_f_b)
+        return m
+
+    def t3_step(self, model, positions, k_cache, v_cache, hidden, *, tokens=None, inputs=None,
+                state=None, stream=None):
+        """cbx_t3_step: one decode step of positions.numel() streams; caches
+        [n_rows, n_layer, n_head, n_ctx, 64] float32, hidden [n_rows, n_embd]
+        out; positions (int32) advance by one for the streams that step."""
+        c = T3Cache()
+        c.k = k_cache.data_ptr()
+        c.v = v_cache.data_ptr()
+        c.n_ctx = k_cache.shape[-2]
+        st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
+        _check(self.lib.cbx_t3_step(self.handle, ctypes.byref(model), positions.numel(),
+                                    _ptr(tokens), _ptr(inputs), _ptr(positions), _ptr(state),
+                                    ctypes.byref(c), _ptr(hidden), st))
 
     def decode_step(self, logits, params, tokens, decode, **kw):
         """cbx_decode_step (head=...: cbx_head_decode_step) of one step."""

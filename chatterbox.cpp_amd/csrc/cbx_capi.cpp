@@ -44,6 +44,9 @@ struct cbx_sampler {
     // the head's activation split (matrix-core projections), grown on demand
     void* d_head = nullptr;
     size_t head_bytes = 0;
+    // the T3 decode step's workspace, grown on demand
+    void* d_t3 = nullptr;
+    size_t t3_bytes = 0;
     // pinned host staging for the small per-call inputs/outputs
     struct Small {
         cbx_params params;
@@ -128,6 +131,7 @@ void release(cbx_sampler* s) {
     (void)hipFree(s->d_redo);
     (void)hipFree(s->d_redo_row);
     (void)hipFree(s->d_head);
+    (void)hipFree(s->d_t3);
     if (s->h_small) (void)hipHostFree(s->h_small);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
@@ -568,6 +572,55 @@ int cbx_head_sample_batch(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
 int cbx_head_decode_step(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
                          const cbx_decode* d, void* stream) {
     return head_then_sample("cbx_head_decode_step", s, h, b, d, (hipStream_t)stream);
+}
+
+int cbx_t3_step(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows, const int32_t* tokens,
+                const float* inputs, int32_t* positions, const int32_t* state,
+                const cbx_t3_cache* cache, float* hidden, void* stream) {
+    const char* fn = "cbx_t3_step";
+    if (!s || !m || !cache) return fail(CBX_ERR_INVALID, "%s: NULL handle, model or cache", fn);
+    if (n_rows < 1) return fail(CBX_ERR_INVALID, "%s: n_rows %d", fn, n_rows);
+    if (m->n_layer < 1 || m->n_layer > 256 || !m->layers)
+        return fail(CBX_ERR_INVALID, "%s: n_layer %d or NULL layers", fn, m->n_layer);
+    if (m->n_embd < 1 || m->n_embd > 4096 || !cbx::t3_shape_ok(m->n_embd, m->n_head))
+        return fail(CBX_ERR_UNSUPPORTED,
+                    "%s: n_embd %d, n_head %d (heads of 64, n_embd in {256..1024 by 256, 1536, "
+                    "2048, 3072, 4096})", fn, m->n_embd, m->n_head);
+    if (m->wtype != CBX_WTYPE_F16 && m->wtype != CBX_WTYPE_Q4_0 && m->wtype != CBX_WTYPE_Q8_0)
+        return fail(CBX_ERR_INVALID, "%s: unknown wtype %d", fn, m->wtype);
+    if (!(m->eps >= 0.0f) || !m->wpe || !m->ln_f_g || !m->ln_f_b || m->n_pos < 1 ||
+        (!inputs && (!tokens || !m->speech_emb || m->n_speech_vocab < 1)))
+        return fail(CBX_ERR_INVALID, "%s: eps, wpe, ln_f, n_pos or the embedding missing", fn);
+    for (int l = 0; l < m->n_layer; ++l) {
+        const cbx_t3_layer& L = m->layers[l];
+        if (!L.ln_1_g || !L.ln_1_b || !L.attn_w || !L.attn_b || !L.attn_proj_w ||
+            !L.attn_proj_b || !L.ln_2_g || !L.ln_2_b || !L.fc_w || !L.fc_b || !L.fc_proj_w ||
+            !L.fc_proj_b)
+            return fail(CBX_ERR_INVALID, "%s: layer %d has a NULL tensor", fn, l);
+    }
+    if (!cache->k || !cache->v || cache->n_ctx < 1 || cache->n_ctx > m->n_pos)
+        return fail(CBX_ERR_INVALID, "%s: cache k/v NULL or n_ctx %d outside [1, n_pos]", fn,
+                    cache->n_ctx);
+    if (cbx::t3_attn_lds(cache->n_ctx) + 256 > s->lds_limit)
+        return fail(CBX_ERR_UNSUPPORTED, "%s: n_ctx %d: the attention's LDS exceeds the device's",
+                    fn, cache->n_ctx);
+    if (!positions || !hidden) return fail(CBX_ERR_INVALID, "%s: NULL positions or hidden", fn);
+    // the matrix kernels' buffer descriptors address rows in 32 bits
+    if ((int64_t)n_rows * 4 * m->n_embd * 4 > 0x7fffffffLL)
+        return fail(CBX_ERR_UNSUPPORTED, "%s: %d rows past 2 GiB of activations", fn, n_rows);
+    DeviceGuard g(s->device);
+    const size_t need = cbx::t3_workspace_bytes(n_rows, m->n_embd);
+    if (need > s->t3_bytes) {
+        CBX_HIP(hipDeviceSynchronize());
+        CBX_HIP(hipFree(s->d_t3));
+        s->d_t3 = nullptr;
+        s->t3_bytes = 0;
+        CBX_HIP(hipMalloc(&s->d_t3, need));
+        s->t3_bytes = need;
+    }
+    CBX_HIP(cbx::launch_t3_step(*m, n_rows, tokens, inputs, positions, state, *cache, hidden,
+                                s->d_t3, (hipStream_t)stream));
+    return CBX_OK;
 }
 
 }  // extern "C"

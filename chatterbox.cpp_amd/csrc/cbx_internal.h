@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/cbx_sampler.h"
+#include "../../include/cbx_t3.h"
 
 namespace cbx {
 
@@ -115,5 +116,16 @@ hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const fl
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
                        void* scratch, hipStream_t stream);
+
+// The T3 decode step (cbx_t3.hip).  t3_shape_ok: the widths the kernels take
+// (heads of 64, n_embd a supported multiple of 256); t3_attn_lds: the
+// attention kernel's LDS for a cache of n_ctx positions; t3_workspace_bytes:
+// the step's device workspace for n_rows streams.
+bool t3_shape_ok(int32_t n_embd, int32_t n_head);
+size_t t3_attn_lds(int32_t n_ctx);
+size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd);
+hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* tokens,
+                          const float* inputs, int32_t* positions, const int32_t* state,
+                          const cbx_t3_cache& c, float* hidden, void* ws, hipStream_t st);
 
 }  // namespace cbx

@@ -1,0 +1,367 @@
+// cbx_t3.hip -- one decode step of the T3 transformer (GPT-2) for n streams,
+// each at its own position with its own KV cache: the step graph of
+// src/main.cpp:617-633 through build_transformer_core (main.cpp:469-575),
+// up to ln_f's output.
+//
+// Per step, for every stream row:
+//   x  = speech_emb[token] + wpe[pos]                       (main.cpp:628-630)
+//   per layer l:
+//     u   = LN(x) * ln_1_g + ln_1_b                          (:522-523)
+//     qkv = c_attn u + b                                     (:524)
+//     k, v of this position appended to the stream's cache   (:517-531)
+//     a   = softmax(q . K^T / sqrt(64)) V over [0, pos]      (:542-548, N = 1)
+//     x  += c_proj a + b                                     (:551)
+//     u   = LN(x) * ln_2_g + ln_2_b                          (:554-555)
+//     x  += mlp_proj gelu(mlp_fc u + b) + b                  (:556-559)
+//   hidden = LN(x) * ln_f_g + ln_f_b                         (:562-563)
+// LN(x) = (x - mean) / sqrt(var + eps), var the mean square of x - mean
+// (ggml_norm); gelu the tanh form 0.5 x (1 + tanh(sqrt(2/pi) x (1 +
+// 0.044715 x^2))) (Hendrycks and Gimpel's approximation, ggml_gelu's).
+//
+// The four matrix products of a layer have the speech_head's shape (rows of
+// n_in weights per output, F16 / Q4_0 / Q8_0): they run on the head's
+// kernels (launch_head: fp16 matrix cores on split activations from 16 rows,
+// a mat-vec below).  The kernels here are the row-wise rest: the embedding,
+// the residual add fused with the next layer norm, the attention with its
+// cache append (one wave per stream and head), and gelu.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "cbx_internal.h"
+#include "../../include/cbx_t3.h"
+
+namespace cbx {
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kHeadDim = 64;
+
+struct NormArgs {
+    int32_t n_embd;
+    float eps;
+    float* x;              // residual rows [n_rows][n_embd], in/out
+    const float* y;        // added to x first when set
+    // embedding mode (emb set): x = emb[token] + wpe[pos], or x = inputs[r]
+    const float* emb;
+    const float* wpe;
+    const float* inputs;
+    const int32_t* tokens;
+    int32_t* positions;
+    const int32_t* state;
+    int32_t n_vocab, n_pos, n_ctx;
+    int32_t* act;          // per row: 1 when the stream takes this step
+    const float* g;
+    const float* b;
+    float* out;            // LN(x) * g + b
+    int32_t advance;       // last norm of the step: positions[r] += 1
+};
+
+// Sum of one value per thread over the workgroup (256 threads): butterfly in
+// each wave, then the four waves' sums in a fixed order, so every thread
+// returns the same value.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+    __syncthreads();  // red[] is reused by consecutive calls
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
+}
+
+// One row per workgroup: the embedding or the residual add, then the layer
+// norm.  Inactive rows (streams that take no step) keep x and write zeros.
+template <int EPT>
+__global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const int n = a.n_embd;
+    float* xr = a.x + (int64_t)r * n;
+    float* orow = a.out + (int64_t)r * n;
+    bool active;
+    float xv[EPT];
+    if (a.emb || a.inputs) {
+        const int pos = a.positions[r];
+        const int tok = a.tokens ? a.tokens[r] : 0;
+        active = (!a.state || a.state[r] == CBX_DECODE_RUNNING) && pos >= 0 && pos < a.n_ctx &&
+                 pos < a.n_pos && (a.inputs || (tok >= 0 && tok < a.n_vocab));
+        if (tid == 0) a.act[r] = active ? 1 : 0;
+        if (!active) {
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                xr[j * kNormThreads + tid] = 0.0f;
+                orow[j * kNormThreads + tid] = 0.0f;
+            }
+            return;
+        }
+        if (a.inputs) {
+            const float* in = a.inputs + (int64_t)r * n;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) xv[j] = in[j * kNormThreads + tid];
+        } else {
+            const float* e = a.emb + (int64_t)tok * n;
+            const float* p = a.wpe + (int64_t)pos * n;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j)
+                xv[j] = __fadd_rn(e[j * kNormThreads + tid], p[j * kNormThreads + tid]);
+        }
+    } else {
+        active = a.act[r] != 0;
+        if (!active) {
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) orow[j * kNormThreads + tid] = 0.0f;
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            xv[j] = xr[j * kNormThreads + tid];
+            if (a.y) xv[j] = __fadd_rn(xv[j], a.y[(int64_t)r * n + j * kNormThreads + tid]);
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) s = __fadd_rn(s, xv[j]);
+    const float mean = __fdiv_rn(block_sum(s, red), (float)n);
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const float d = __fsub_rn(xv[j], mean);
+        q = __fadd_rn(q, __fmul_rn(d, d));
+    }
+    const float var = __fdiv_rn(block_sum(q, red), (float)n);
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, a.eps)));
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int i = j * kNormThreads + tid;
+        xr[i] = xv[j];
+        orow[i] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), a.g[i]), a.b[i]);
+    }
+    if (a.advance && tid == 0) a.positions[r] += 1;
+}
+
+struct AttnArgs {
+    const float* qkv;      // [n_rows][3 n_embd]: q | k | v, head h at h*64
+    float* kc;             // this layer's caches: stream r, head h at
+    float* vc;             //   ((r * n_layer + layer) * n_head + h) * n_ctx * 64
+    int32_t n_layer, layer, n_head, n_ctx;
+    const int32_t* positions;
+    const int32_t* act;
+    float* out;            // [n_rows][n_embd]
+    float scale;           // 1 / sqrt(64)
+};
+
+// One wave per (stream, head).  The new k and v are stored at the stream's
+// position; the scores of positions [0, pos] (lane j takes positions j,
+// j + 64, ...; the new position's k from LDS, not read back from memory) go
+// to LDS, their softmax (max, then expf and the sum), and the output lane d
+// sums p_j v_j[d] over the positions in order.
+__global__ __launch_bounds__(kHeadDim) void t3_attn(AttnArgs a) {
+    extern __shared__ float p[];  // [n_ctx] scores, then weights
+    __shared__ float kn_s[kHeadDim];
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int n = a.n_head * kHeadDim;
+    float* orow = a.out + (int64_t)r * n + h * kHeadDim;
+    if (!a.act[r]) {
+        orow[lane] = 0.0f;
+        return;
+    }
+    const int pos = a.positions[r];
+    const float* qr = a.qkv + (int64_t)r * 3 * n + h * kHeadDim;
+    const float kn = qr[n + lane], vn = qr[2 * n + lane];
+    const int64_t base = (((int64_t)r * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim;
+    float* kc = a.kc + base;
+    float* vc = a.vc + base;
+    kc[(int64_t)pos * kHeadDim + lane] = kn;
+    vc[(int64_t)pos * kHeadDim + lane] = vn;
+    kn_s[lane] = kn;
+    float q[kHeadDim];
+#pragma unroll
+    for (int d = 0; d < kHeadDim; ++d) q[d] = qr[d];  // the same address in every lane
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = lane; j <= pos; j += kHeadDim) {
+        float dot = 0.0f;
+        if (j == pos) {
+#pragma unroll
+            for (int d = 0; d < kHeadDim; ++d) dot = __fadd_rn(dot, __fmul_rn(q[d], kn_s[d]));
+        } else {
+            const float4* kr = reinterpret_cast<const float4*>(kc + (int64_t)j * kHeadDim);
+#pragma unroll
+            for (int c = 0; c < kHeadDim / 4; ++c) {
+                const float4 k4 = kr[c];
+                dot = __fadd_rn(dot, __fmul_rn(q[4 * c], k4.x));
+                dot = __fadd_rn(dot, __fmul_rn(q[4 * c + 1], k4.y));
+                dot = __fadd_rn(dot, __fmul_rn(q[4 * c + 2], k4.z));
+                dot = __fadd_rn(dot, __fmul_rn(q[4 * c + 3], k4.w));
+            }
+        }
+        const float sc = __fmul_rn(dot, a.scale);
+        p[j] = sc;
+        mx = fmaxf(mx, sc);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.0f;
+    for (int j = lane; j <= pos; j += kHeadDim) {
+        const float e = expf(__fsub_rn(p[j], mx));
+        p[j] = e;
+        sum = __fadd_rn(sum, e);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o));
+    sum = __shfl(sum, 0);
+    __syncthreads();
+    float acc = 0.0f;
+    for (int j = 0; j < pos; ++j)
+        acc = __fadd_rn(acc, __fmul_rn(p[j], vc[(int64_t)j * kHeadDim + lane]));
+    acc = __fadd_rn(acc, __fmul_rn(p[pos], vn));
+    orow[lane] = __fdiv_rn(acc, sum);
+}
+
+// gelu in place over n values (the fc output, bias included).
+__global__ __launch_bounds__(256) void t3_gelu(float* h, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float x = h[i];
+    const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+    const float inner = __fmul_rn(__fmul_rn(c, x), __fadd_rn(1.0f, __fmul_rn(__fmul_rn(0.044715f, x), x)));
+    h[i] = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+
+template <int EPT>
+hipError_t launch_norm_ept(const NormArgs& a, int n_rows, hipStream_t st) {
+    hipLaunchKernelGGL(t3_norm<EPT>, dim3((unsigned)n_rows), dim3(kNormThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm(const NormArgs& a, int n_rows, hipStream_t st) {
+    switch (a.n_embd / kNormThreads) {
+        case 1: return launch_norm_ept<1>(a, n_rows, st);
+        case 2: return launch_norm_ept<2>(a, n_rows, st);
+        case 3: return launch_norm_ept<3>(a, n_rows, st);
+        case 4: return launch_norm_ept<4>(a, n_rows, st);
+        case 6: return launch_norm_ept<6>(a, n_rows, st);
+        case 8: return launch_norm_ept<8>(a, n_rows, st);
+        case 12: return launch_norm_ept<12>(a, n_rows, st);
+        case 16: return launch_norm_ept<16>(a, n_rows, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool t3_shape_ok(int32_t n_embd, int32_t n_head) {
+    const int e = n_embd / kNormThreads;
+    return n_head >= 1 && n_embd == n_head * kHeadDim && n_embd % kNormThreads == 0 &&
+           (e == 1 || e == 2 || e == 3 || e == 4 || e == 6 || e == 8 || e == 12 || e == 16);
+}
+
+size_t t3_attn_lds(int32_t n_ctx) { return (size_t)n_ctx * 4; }
+
+// Workspace of a step: x, u, a, y [n_rows][n_embd], qkv [n_rows][3 n_embd],
+// f [n_rows][4 n_embd], act [n_rows], then the matrix products' split
+// activations (the widest input, 4 n_embd).
+size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd) {
+    const size_t row = (size_t)n_rows * n_embd * 4;
+    const size_t body = 4 * row + 3 * row + 4 * row + ((size_t)n_rows * 4 + 255) / 256 * 256;
+    return body + head_scratch_bytes(n_rows, false, 4 * n_embd);
+}
+
+hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* tokens,
+                          const float* inputs, int32_t* positions, const int32_t* state,
+                          const cbx_t3_cache& c, float* hidden, void* ws, hipStream_t st) {
+    const int n = m.n_embd;
+    const size_t row = (size_t)n_rows * n;
+    float* x = static_cast<float*>(ws);
+    float* u = x + row;
+    float* att = u + row;
+    float* y = att + row;
+    float* qkv = y + row;
+    float* f = qkv + 3 * row;
+    int32_t* act = reinterpret_cast<int32_t*>(f + 4 * row);
+    void* split = reinterpret_cast<char*>(act) + ((size_t)n_rows * 4 + 255) / 256 * 256;
+
+    NormArgs na{};
+    na.n_embd = n;
+    na.eps = m.eps;
+    na.x = x;
+    na.emb = inputs ? nullptr : m.speech_emb;
+    na.wpe = m.wpe;
+    na.inputs = inputs;
+    na.tokens = inputs ? nullptr : tokens;
+    na.positions = positions;
+    na.state = state;
+    na.n_vocab = m.n_speech_vocab;
+    na.n_pos = m.n_pos;
+    na.n_ctx = c.n_ctx;
+    na.act = act;
+    na.g = m.layers[0].ln_1_g;
+    na.b = m.layers[0].ln_1_b;
+    na.out = u;
+    hipError_t e = launch_norm(na, n_rows, st);
+    if (e != hipSuccess) return e;
+
+    AttnArgs aa{};
+    aa.qkv = qkv;
+    aa.kc = c.k;
+    aa.vc = c.v;
+    aa.n_layer = m.n_layer;
+    aa.n_head = m.n_head;
+    aa.n_ctx = c.n_ctx;
+    aa.positions = positions;
+    aa.act = act;
+    aa.out = att;
+    aa.scale = 0.125f;  // 1 / sqrt(64)
+    const size_t lds = t3_attn_lds(c.n_ctx);
+    if (lds > 64 * 1024 - kHeadDim * 4) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&t3_attn),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+
+    for (int l = 0; l < m.n_layer; ++l) {
+        const cbx_t3_layer& L = m.layers[l];
+        e = launch_head(L.attn_w, m.wtype, L.attn_b, u, nullptr, n, qkv, nullptr, 3 * n, n_rows,
+                        3 * n, n, split, st);
+        if (e != hipSuccess) return e;
+        aa.layer = l;
+        hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head), dim3(kHeadDim),
+                           lds, st, aa);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        e = launch_head(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
+                        n_rows, n, n, split, st);
+        if (e != hipSuccess) return e;
+        NormArgs nb{};
+        nb.n_embd = n;
+        nb.eps = m.eps;
+        nb.x = x;
+        nb.y = y;
+        nb.act = act;
+        nb.g = L.ln_2_g;
+        nb.b = L.ln_2_b;
+        nb.out = u;
+        if ((e = launch_norm(nb, n_rows, st)) != hipSuccess) return e;
+        e = launch_head(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows, 4 * n,
+                        n, split, st);
+        if (e != hipSuccess) return e;
+        const int64_t nf = (int64_t)4 * row;
+        hipLaunchKernelGGL(t3_gelu, dim3((unsigned)((nf + 255) / 256)), dim3(256), 0, st, f, nf);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        e = launch_head(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
+                        n_rows, n, 4 * n, split, st);
+        if (e != hipSuccess) return e;
+        // the residual, then the next layer's ln_1 or, after the last, ln_f
+        // into `hidden` and the positions advanced
+        NormArgs nc = nb;
+        const bool last = l + 1 == m.n_layer;
+        nc.g = last ? m.ln_f_g : m.layers[l + 1].ln_1_g;
+        nc.b = last ? m.ln_f_b : m.layers[l + 1].ln_1_b;
+        nc.out = last ? hidden : u;
+        nc.positions = positions;
+        nc.advance = last ? 1 : 0;
+        if ((e = launch_norm(nc, n_rows, st)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace cbx

@@ -1,0 +1,247 @@
+"""GPU parity of the T3 transformer's decode step (cbx_t3_step,
+chatterbox.cpp_amd/csrc/cbx_t3.hip) against the binary64 oracle
+(oracle/cbx_t3_oracle.py), on the Turbo shape (24 layers, n_embd 1024, 16
+heads of 64) with random weights in each matrix format, and the whole
+batched decode loop on the device: T3 step, fused head, sampler, ids fed
+back.
+
+Tolerance on ln_f's output rows: |gpu - ref| <= 5e-5 + 5e-5 |ref|.  The GPU
+computes in binary32 (the reference's own dtype: fp32 activations, fp32 KV
+cache, main.cpp:419-424) through 24 layers of products over 1024 to 4096
+terms, each layer's residual re-normalized; the oracle in binary64 with the
+same dequantized weights.  Values are O(1) after ln_f; the largest error
+measured over every case here is 3.2e-6 (about 50 binary32 ulps of 1), and
+the bound allows 15 times that.  A wrong head offset, a missing residual or
+a cache row written at the wrong position moves rows by O(1).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import pkg
+from oracle import cbx_t3_oracle as T3
+
+pytestmark = pytest.mark.gpu
+
+N_LAYER, N, H, N_POS, V = 24, 1024, 16, 64, 6563
+TOL_ABS, TOL_REL = 5e-5, 5e-5
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def cbx(torch_cuda):
+    mod = pkg.load()
+    s = mod.Sampler(device=0, max_vocab=32768, max_history=4096)
+    yield mod, s
+    s.close()
+
+
+_MODELS = {}
+
+
+def model(torch, mod, wtype):
+    """Random Turbo-shaped weights in `wtype` (matrices N(0, 0.02)): the
+    device model and the oracle's binary64 copy of the same values."""
+    if wtype in _MODELS:
+        return _MODELS[wtype]
+    rng = np.random.default_rng(0x7300 + wtype)
+    vec = lambda k, base=0.0, sd=0.1: (base + rng.standard_normal(k) * sd).astype(np.float32)
+    dev_layers, ref_layers = [], []
+    for _ in range(N_LAYER):
+        d, r = {}, {}
+        for key, (o, i) in (("attn_w", (3 * N, N)), ("attn_proj_w", (N, N)), ("fc_w", (4 * N, N)),
+                            ("fc_proj_w", (N, 4 * N))):
+            w = (rng.standard_normal((o, i)) * 0.02).astype(np.float32)
+            blocks = O.quantize(w, wtype)
+            d[key] = torch.from_numpy(blocks.reshape(-1)).cuda()
+            r[key] = O.dequantize(blocks, wtype, i)
+        for key, k, base, sd in (("ln_1_g", N, 1.0, 0.1), ("ln_1_b", N, 0.0, 0.1),
+                                 ("attn_b", 3 * N, 0.0, 0.02), ("attn_proj_b", N, 0.0, 0.02),
+                                 ("ln_2_g", N, 1.0, 0.1), ("ln_2_b", N, 0.0, 0.1),
+                                 ("fc_b", 4 * N, 0.0, 0.02), ("fc_proj_b", N, 0.0, 0.02)):
+            a = vec(k, base, sd)
+            d[key] = torch.from_numpy(a).cuda()
+            r[key] = a
+        dev_layers.append(d)
+        ref_layers.append(r)
+    wpe = (rng.standard_normal((N_POS, N)) * 0.1).astype(np.float32)
+    emb = (rng.standard_normal((V, N)) * 0.5).astype(np.float32)
+    gf, bf = vec(N, 1.0), vec(N)
+    t = lambda a: torch.from_numpy(a).cuda()
+    dm = mod.Sampler.t3_model(dev_layers, t(wpe), t(emb), t(gf), t(bf), wtype=wtype, n_head=H)
+    rm = T3.Model(ref_layers, wpe, emb, gf, bf, 1e-5, H)
+    _MODELS[wtype] = (dm, rm)
+    return dm, rm
+
+
+def close(got, want):
+    err = np.abs(got.astype(np.float64) - want)
+    return np.all(err <= TOL_ABS + TOL_REL * np.abs(want)), float(err.max())
+
+
+@pytest.mark.parametrize("B", [20, 5])
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+def test_t3_step_matches_oracle(cbx, torch_cuda, wtype, B):
+    """B streams, 4 steps with per-stream ids; in step 2 every third stream
+    sits out (state not running), so positions differ afterwards.  Each step's
+    ln_f rows, every stream's position and the skipped rows' zeros match the
+    oracle.  B = 20 runs the products on the matrix cores, B = 5 on the
+    mat-vec (fc_proj's 4096-wide rows on the matrix cores)."""
+    torch = torch_cuda
+    mod, s = cbx
+    dm, rm = model(torch, mod, wtype)
+    rng = np.random.default_rng(0x7310 + B)
+    kd = torch.zeros((B, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
+    vd = torch.zeros_like(kd)
+    kr, vr = T3.new_cache(B, N_LAYER, H, N_POS)
+    pos_d = torch.zeros(B, dtype=torch.int32, device="cuda")
+    pos_r = np.zeros(B, np.int64)
+    hid = torch.zeros((B, N), dtype=torch.float32, device="cuda")
+    worst = 0.0
+    for t in range(4):
+        toks = rng.integers(0, V, B).astype(np.int32)
+        state = np.zeros(B, np.int32)
+        if t == 2:
+            state[::3] = 1
+        say(f"t3 step wtype={wtype} B={B} t={t}")
+        s.t3_step(dm, pos_d, kd, vd, hid, tokens=torch.from_numpy(toks).cuda(),
+                  state=torch.from_numpy(state).cuda())
+        torch.cuda.synchronize()
+        want = T3.step(rm, toks, pos_r, kr, vr, active=state == 0)
+        got = hid.cpu().numpy()
+        ok, err = close(got, want)
+        worst = max(worst, err)
+        assert ok, f"step {t}: max err {err:.3g}"
+        assert np.all(got[state != 0] == 0.0)
+        assert np.array_equal(pos_d.cpu().numpy(), pos_r)
+    say(f"  max |err| {worst:.3g}")
+
+
+def test_t3_inputs_then_tokens(cbx, torch_cuda):
+    """Prompt rows fed as embedded inputs (one position per call), then ids:
+    the same ln_f rows as the oracle fed the same rows."""
+    torch = torch_cuda
+    mod, s = cbx
+    dm, rm = model(torch, mod, O.WTYPE_Q4_0)
+    B = 16
+    rng = np.random.default_rng(0x7320)
+    kd = torch.zeros((B, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
+    vd = torch.zeros_like(kd)
+    kr, vr = T3.new_cache(B, N_LAYER, H, N_POS)
+    pos_d = torch.zeros(B, dtype=torch.int32, device="cuda")
+    pos_r = np.zeros(B, np.int64)
+    hid = torch.zeros((B, N), dtype=torch.float32, device="cuda")
+    for t in range(5):
+        say(f"t3 inputs/tokens t={t}")
+        if t < 3:
+            rows = (rng.standard_normal((B, N)) * 0.5).astype(np.float32)
+            s.t3_step(dm, pos_d, kd, vd, hid, inputs=torch.from_numpy(rows).cuda())
+            want = T3.step(rm, None, pos_r, kr, vr, inputs=rows)
+        else:
+            toks = rng.integers(0, V, B).astype(np.int32)
+            s.t3_step(dm, pos_d, kd, vd, hid, tokens=torch.from_numpy(toks).cuda())
+            want = T3.step(rm, toks, pos_r, kr, vr)
+        torch.cuda.synchronize()
+        ok, err = close(hid.cpu().numpy(), want)
+        assert ok, f"step {t}: max err {err:.3g}"
+
+
+def test_t3_head_decode_loop(cbx, torch_cuda):
+    """The whole decode loop on the device for 16 streams, 8 steps: T3 step
+    on the fed-back ids, the fused Q4_0 speech_head and the sampler
+    (cbx_head_decode_step), no host copy between steps.  Afterwards, step by
+    step: the T3 rows match the oracle fed the same ids, the logits the head
+    of those rows, and every id is the oracle sampler's on the GPU's logits
+    with the history so far."""
+    torch = torch_cuda
+    mod, s = cbx
+    dm, rm = model(torch, mod, O.WTYPE_Q4_0)
+    B, T, LD = 16, 8, 16
+    stop, start = -1, V - 2  # no id stops a stream: all 16 run the 8 steps
+    rng = np.random.default_rng(0x7330)
+    hw = (rng.standard_normal((V, N)) * 0.02).astype(np.float32)
+    hblocks = O.quantize(hw, O.WTYPE_Q4_0)
+    hbias = (rng.standard_normal(V) * 0.1).astype(np.float32)
+    plist = [dict(top_k=1000, top_p=0.95, temp=0.8, repeat_penalty=1.2, min_p=0.0,
+                  cfg_weight=0.0)] * B
+    w = pkg.workloads()
+    prm = torch.from_numpy(w.pack_params(plist)).cuda()
+    dW = torch.from_numpy(hblocks.reshape(-1)).cuda()
+    db = torch.from_numpy(hbias).cuda()
+    kd = torch.zeros((B, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
+    vd = torch.zeros_like(kd)
+    pos_d = torch.zeros(B, dtype=torch.int32, device="cuda")
+    state = torch.zeros(B, dtype=torch.int32, device="cuda")
+    hist = torch.full((B, LD), -9, dtype=torch.int32, device="cuda")
+    hlen = torch.zeros(B, dtype=torch.int32, device="cuda")
+    nxt = torch.full((B,), start, dtype=torch.int32, device="cuda")
+    hids = torch.zeros((T, B, N), dtype=torch.float32, device="cuda")
+    logits = torch.zeros((T, B, V), dtype=torch.float32, device="cuda")
+    toks = torch.full((T, B), -5, dtype=torch.int32, device="cuda")
+    ins = torch.zeros((T, B), dtype=torch.int32, device="cuda")
+    dec = mod.Sampler.decode_state(state, hist, hlen, next_token=nxt)
+    say(f"t3 + head decode loop B={B} T={T}")
+    for t in range(T):
+        ins[t] = nxt
+        s.t3_step(dm, pos_d, kd, vd, hids[t], tokens=nxt, state=state)
+        head = mod.Sampler.head(dW, O.WTYPE_Q4_0, N, hids[t], logits[t], bias=db)
+        s.decode_step(logits[t], prm, toks[t], dec, head=head, seed=0x7331, step0=t,
+                      stop_token=stop)
+    torch.cuda.synchronize()
+    hid_g, lg_g = hids.cpu().numpy(), logits.cpu().numpy()
+    tok_g, in_g = toks.cpu().numpy(), ins.cpu().numpy()
+    kr, vr = T3.new_cache(B, N_LAYER, H, N_POS)
+    pos_r = np.zeros(B, np.int64)
+    gen = [[] for _ in range(B)]
+    op = O.params(**plist[0])
+    hdeq = np.abs(O.dequantize(hblocks, O.WTYPE_Q4_0, N)).astype(np.float64)
+    for t in range(T):
+        # the ids each stream fed back: its previous token (start at step 0)
+        want_in = np.array([gen[r][-1] if gen[r] else start for r in range(B)])
+        assert np.array_equal(in_g[t], want_in), t
+        want = T3.step(rm, want_in, pos_r, kr, vr)
+        ok, err = close(hid_g[t], want)
+        assert ok, f"step {t}: T3 rows max err {err:.3g}"
+        # the head's bound (tests/test_gpu_head.py): fp32 sums plus the split floor
+        ref = O.head_f64(hblocks, O.WTYPE_Q4_0, hbias, hid_g[t], V, N)
+        ah = np.abs(hid_g[t]).astype(np.float64)
+        tol = 1e-5 * (ah @ hdeq.T) + 2.0 ** -39 * ah.max(1)[:, None] * hdeq.sum(1) + 1e-6
+        assert np.all(np.abs(lg_g[t] - ref) <= tol), t
+        for r in range(B):
+            u = O.philox_uniform(0x7331, r, t)
+            tk = O.sample_row(lg_g[t, r], np.array(gen[r], np.int32), op, u)[0]
+            assert tok_g[t, r] == tk, (t, r)
+            gen[r].append(tk)
+    assert np.array_equal(pos_d.cpu().numpy(), np.full(B, T))
+    assert np.array_equal(hlen.cpu().numpy(), np.full(B, T))
+
+
+def test_t3_rejects_bad_arguments(cbx, torch_cuda):
+    torch = torch_cuda
+    mod, s = cbx
+    dm, _ = model(torch, mod, O.WTYPE_Q4_0)
+    pos = torch.zeros(2, dtype=torch.int32, device="cuda")
+    toks = torch.zeros(2, dtype=torch.int32, device="cuda")
+    hid = torch.zeros((2, N), dtype=torch.float32, device="cuda")
+    kd = torch.zeros((2, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
+    big = torch.zeros((1, 1, 1, N_POS + 1, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(mod.CbxError):  # n_ctx above the model's positions
+        s.t3_step(dm, pos, big, big, hid, tokens=toks)
+    n_head = dm.n_head
+    dm.n_head = 8  # 128-wide heads
+    with pytest.raises(mod.CbxError):
+        s.t3_step(dm, pos, kd, kd, hid, tokens=toks)
+    dm.n_head = n_head
+    with pytest.raises(mod.CbxError):  # neither ids nor input rows
+        s.t3_step(dm, pos, kd, kd, hid)
+    torch.cuda.synchronize()
