@@ -26,6 +26,9 @@ measured shapes:
                           (B=1, V=8194, history growing to 1000), masked
                           stress (B=1024, V=32768, 20% allowed ids)
   fused_head              Q4_0 speech_head + sampler, B=64 CFG pairs
+  t3_decode               the T3 transformer's decode step (24 layers, Q4_0)
+                          for 64 streams and for 1, alone and with the head and
+                          the sampler
 """
 import argparse
 import json
@@ -261,6 +264,93 @@ def decode_loop_bench(torch, mod, sampler, dev, slabs, S, d_par, hist, hist_len,
             "histories_grew_by_steps": grew}
 
 
+T3_LAYER, T3_EMBD, T3_HEAD = 24, 1024, 16  # GPT-2 medium, the Turbo T3
+
+
+def q4_0_rows(torch, rows, n_in, dev, g):
+    """Random Q4_0 matrix bytes [rows][n_in/32 blocks of 18]: fp16 scales in
+    [0.001, 0.004] (weights of about N(0, 0.02)), random nibbles."""
+    nb = n_in // 32
+    b = torch.randint(0, 256, (rows, nb, 18), generator=g, device=dev, dtype=torch.uint8)
+    d = (torch.rand((rows, nb), generator=g, device=dev) * 0.003 + 0.001).half()
+    b[:, :, :2] = d.contiguous().view(torch.uint8).view(rows, nb, 2)
+    return b.reshape(-1)
+
+
+def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps):
+    """The T3 decode step (cbx_t3_step) of B streams on the Turbo shape with
+    random Q4_0 matrices, every stream at position pos0 (caches of n_ctx
+    positions), alone and followed by the fused Q4_0 speech_head and the
+    sampler (cbx_head_decode_step): the whole device decode step.  Bytes per
+    step: the layer matrices once, every stream's K and V read over its
+    positions and the new row written."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x7333)
+    n = T3_EMBD
+    vec = lambda k, base=0.0, sd=0.1: (base + torch.randn(k, generator=g, device=dev) * sd)
+    layers = [dict(ln_1_g=vec(n, 1.0), ln_1_b=vec(n), attn_w=q4_0_rows(torch, 3 * n, n, dev, g),
+                   attn_b=vec(3 * n, 0.0, 0.02), attn_proj_w=q4_0_rows(torch, n, n, dev, g),
+                   attn_proj_b=vec(n, 0.0, 0.02), ln_2_g=vec(n, 1.0), ln_2_b=vec(n),
+                   fc_w=q4_0_rows(torch, 4 * n, n, dev, g), fc_b=vec(4 * n, 0.0, 0.02),
+                   fc_proj_w=q4_0_rows(torch, n, 4 * n, dev, g), fc_proj_b=vec(n, 0.0, 0.02))
+              for _ in range(T3_LAYER)]
+    wpe = vec(n_ctx * n, 0.0, 0.1).view(n_ctx, n)
+    emb = vec(V * n, 0.0, 0.5).view(V, n)
+    model = mod.Sampler.t3_model(layers, wpe, emb, vec(n, 1.0), vec(n), wtype=mod.CBX_WTYPE_Q4_0,
+                                 n_head=T3_HEAD)
+    kc = torch.randn((B, T3_LAYER, T3_HEAD, n_ctx, 64), generator=g, device=dev) * 0.5
+    vc = torch.randn((B, T3_LAYER, T3_HEAD, n_ctx, 64), generator=g, device=dev) * 0.5
+    hid = torch.empty((B, n), dtype=torch.float32, device=dev)
+    pos = torch.full((B,), pos0, dtype=torch.int32, device=dev)
+    toks = torch.randint(0, V, (B,), generator=g, device=dev, dtype=torch.int32)
+    head_w = q4_0_rows(torch, V, n, dev, g)
+    head_b = vec(V, 0.0, 0.1)
+    logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+    head = mod.Sampler.head(head_w, mod.CBX_WTYPE_Q4_0, n, hid, logits, bias=head_b)
+    w = pkg_workloads()
+    prm = torch.from_numpy(w.pack_params([dict(top_k=1000, top_p=0.95, temp=0.8,
+                                                repeat_penalty=1.2, min_p=0.0,
+                                                cfg_weight=0.0)] * B)).to(dev)
+    state = torch.zeros(B, dtype=torch.int32, device=dev)
+    hist = torch.zeros((B, steps + 16), dtype=torch.int32, device=dev)
+    hlen = torch.zeros(B, dtype=torch.int32, device=dev)
+    tok_out = torch.empty(B, dtype=torch.int32, device=dev)
+    dec = mod.Sampler.decode_state(state, hist, hlen, next_token=toks)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name in ("t3", "t3_head_sampler"):
+        def one(i, name=name):
+            if i == 0:
+                pos.fill_(pos0)
+                hlen.zero_()
+            sampler.t3_step(model, pos, kc, vc, hid, tokens=toks, state=state)
+            if name != "t3":
+                sampler.decode_step(logits, prm, tok_out, dec, head=head, seed=7, step0=i,
+                                    stop_token=-1)
+        res[name] = timed(torch, stream, one, steps, warm=1)
+    mat_bytes = T3_LAYER * 12 * n * n * 18 // 32
+    # per step and stream: K and V read over positions [0, pos] (pos0 .. pos0
+    # + steps - 1 over the timed steps) and written at pos, every layer
+    mean_pos = pos0 + (steps - 1) / 2.0
+    kv_bytes = B * T3_LAYER * 2 * n * 4 * (mean_pos + 2)
+    bytes_step = mat_bytes + kv_bytes
+    ms = res["t3"]
+    return {"workload": "T3 decode step, GPT-2 medium (24 layers, 1024, 16 heads), Q4_0 "
+                        "matrices, %d streams at positions %d-%d, fp32 KV caches" % (
+                            B, pos0, pos0 + steps),
+            "streams": B, "steps": steps,
+            "ms_per_step_t3": round(ms, 5),
+            "ms_per_step_with_head_and_sampler": round(res["t3_head_sampler"], 5),
+            "tokens_per_s": round(B / (res["t3_head_sampler"] / 1e3), 1),
+            "algorithmic_bytes_per_step": int(bytes_step),
+            "hbm_frac_t3": round(bytes_step / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 5)}
+
+
+def pkg_workloads():
+    import pkg
+    return pkg.workloads()
+
+
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 HEAD_EMBD, HEAD_B = 1024, 64
 
@@ -492,6 +582,8 @@ def parse_args(argv=None):
     ap.add_argument("--slabs", type=int, default=2)
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
+    ap.add_argument("--t3-steps", type=int, default=20,
+                    help="timed steps of the T3 decode step, B=64 and B=1 (0: skip)")
     ap.add_argument("--decode-steps", type=int, default=200,
                     help="timed steps of the device decode loop and its host-synced twin "
                          "(0: skip)")
@@ -612,6 +704,12 @@ def main():
         decode = decode_loop_bench(torch, mod, sampler, dev, slabs, S, d_par, hist, hist_len,
                                    args.decode_steps, philox_seed)
 
+    # the T3 transformer's decode step feeding the head and the sampler
+    t3 = None
+    if args.t3_steps > 0:
+        t3 = {"b64": t3_bench(torch, mod, sampler, dev, 64, 256, 512, args.t3_steps),
+              "b1": t3_bench(torch, mod, sampler, dev, 1, 256, 512, args.t3_steps)}
+
     O = None
     if not args.no_cpu:
         import oracle_lib as O
@@ -694,6 +792,7 @@ def main():
         "launch_shapes": shapes,
         "single_launch_per_step": single,
         "decode_loop": decode,
+        "t3_decode": t3,
         "configs": configs,
         "fused_head": fused,
         "wall_s": round(time.perf_counter() - t_start, 1),

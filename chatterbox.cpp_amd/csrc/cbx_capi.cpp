@@ -601,7 +601,7 @@ int cbx_t3_step(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows, const int
     if (!cache->k || !cache->v || cache->n_ctx < 1 || cache->n_ctx > m->n_pos)
         return fail(CBX_ERR_INVALID, "%s: cache k/v NULL or n_ctx %d outside [1, n_pos]", fn,
                     cache->n_ctx);
-    if (cbx::t3_attn_lds(cache->n_ctx) + 256 > s->lds_limit)
+    if (cbx::t3_attn_lds(cache->n_ctx) + 2048 > s->lds_limit)
         return fail(CBX_ERR_UNSUPPORTED, "%s: n_ctx %d: the attention's LDS exceeds the device's",
                     fn, cache->n_ctx);
     if (!positions || !hidden) return fail(CBX_ERR_INVALID, "%s: NULL positions or hidden", fn);

@@ -629,7 +629,24 @@ hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const fl
                        hidden1, ld_hidden, n_rows, n_embd, parts, inv);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // two row tiles per workgroup for Q4_0 and for at most two tiles
+    // one row tile per workgroup where two would leave fewer than 512
+    // workgroups (narrow outputs, few rows: the T3 layer products); else two
+    // row tiles per workgroup for Q4_0 and for at most two tiles
+    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512) {
+        switch (wtype) {
+            case CBX_WTYPE_F16:
+                return launch_mfma<CBX_WTYPE_F16, 1>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                     ld_out, n_rows, n_vocab, n_embd, stream);
+            case CBX_WTYPE_Q4_0:
+                return launch_mfma<CBX_WTYPE_Q4_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                      ld_out, n_rows, n_vocab, n_embd, stream);
+            case CBX_WTYPE_Q8_0:
+                return launch_mfma<CBX_WTYPE_Q8_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                      ld_out, n_rows, n_vocab, n_embd, stream);
+            default:
+                return hipErrorInvalidValue;
+        }
+    }
     const bool two = wtype == CBX_WTYPE_Q4_0 || n_tiles <= 2;
     switch (wtype) {
         case CBX_WTYPE_F16:

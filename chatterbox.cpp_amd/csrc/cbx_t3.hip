@@ -23,7 +23,7 @@
 // kernels (launch_head: fp16 matrix cores on split activations from 16 rows,
 // a mat-vec below).  The kernels here are the row-wise rest: the embedding,
 // the residual add fused with the next layer norm, the attention with its
-// cache append (one wave per stream and head), and gelu.
+// cache append (a workgroup of 4 waves per stream and head), and gelu.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -150,72 +150,113 @@ struct AttnArgs {
     float scale;           // 1 / sqrt(64)
 };
 
-// One wave per (stream, head).  The new k and v are stored at the stream's
-// position; the scores of positions [0, pos] (lane j takes positions j,
-// j + 64, ...; the new position's k from LDS, not read back from memory) go
-// to LDS, their softmax (max, then expf and the sum), and the output lane d
-// sums p_j v_j[d] over the positions in order.
-__global__ __launch_bounds__(kHeadDim) void t3_attn(AttnArgs a) {
+// One workgroup of 4 waves per (stream, head).  Wave 0 stores the new k and
+// v at the stream's position (and keeps them in LDS: that position is never
+// read back from memory).  The positions [0, pos] are cut into 4 runs, one
+// per wave: its lanes score their run's positions (lane j takes positions
+// j, j + 64, ... of the run) into LDS, the maxima and then the sums of
+// expf(score - max) are combined over the 4 waves in a fixed order, and each
+// wave sums p_j v_j over its run (four interleaved partial sums, added in a
+// fixed order); the 4 waves' outputs are added in wave order and divided by
+// the sum.
+constexpr int kAttnWaves = 4;
+
+__global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     extern __shared__ float p[];  // [n_ctx] scores, then weights
-    __shared__ float kn_s[kHeadDim];
-    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    __shared__ __align__(16) float kn_s[kHeadDim];
+    __shared__ __align__(16) float vn_s[kHeadDim];
+    __shared__ float red[2 * kAttnWaves];
+    __shared__ __align__(16) float part[kAttnWaves][kHeadDim];
+    const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
     const int n = a.n_head * kHeadDim;
     float* orow = a.out + (int64_t)r * n + h * kHeadDim;
     if (!a.act[r]) {
-        orow[lane] = 0.0f;
+        if (tid < kHeadDim) orow[tid] = 0.0f;
         return;
     }
     const int pos = a.positions[r];
     const float* qr = a.qkv + (int64_t)r * 3 * n + h * kHeadDim;
-    const float kn = qr[n + lane], vn = qr[2 * n + lane];
     const int64_t base = (((int64_t)r * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim;
     float* kc = a.kc + base;
     float* vc = a.vc + base;
-    kc[(int64_t)pos * kHeadDim + lane] = kn;
-    vc[(int64_t)pos * kHeadDim + lane] = vn;
-    kn_s[lane] = kn;
-    float q[kHeadDim];
-#pragma unroll
-    for (int d = 0; d < kHeadDim; ++d) q[d] = qr[d];  // the same address in every lane
+    if (w == 0) {
+        const float kn = qr[n + lane], vn = qr[2 * n + lane];
+        kc[(int64_t)pos * kHeadDim + lane] = kn;
+        vc[(int64_t)pos * kHeadDim + lane] = vn;
+        kn_s[lane] = kn;
+        vn_s[lane] = vn;
+    }
+    // lane = 16 sub + e holds q[4e .. 4e + 3] and takes position c0 + sub + 4i,
+    // dimensions 4e .. 4e + 3: a wave reads 4 rows of k per instruction
+    const int sub = lane >> 4, e4 = 4 * (lane & 15);
+    const float4 q4 = *reinterpret_cast<const float4*>(qr + e4);
+    const int L = pos + 1, run = (L + kAttnWaves - 1) / kAttnWaves;
+    const int c0 = min(w * run, L), c1 = min(c0 + run, L);
     __syncthreads();
     float mx = -INFINITY;
-    for (int j = lane; j <= pos; j += kHeadDim) {
+    for (int j0 = c0; j0 < c1; j0 += 4) {
+        const int j = j0 + sub;
         float dot = 0.0f;
-        if (j == pos) {
-#pragma unroll
-            for (int d = 0; d < kHeadDim; ++d) dot = __fadd_rn(dot, __fmul_rn(q[d], kn_s[d]));
-        } else {
-            const float4* kr = reinterpret_cast<const float4*>(kc + (int64_t)j * kHeadDim);
-#pragma unroll
-            for (int c = 0; c < kHeadDim / 4; ++c) {
-                const float4 k4 = kr[c];
-                dot = __fadd_rn(dot, __fmul_rn(q[4 * c], k4.x));
-                dot = __fadd_rn(dot, __fmul_rn(q[4 * c + 1], k4.y));
-                dot = __fadd_rn(dot, __fmul_rn(q[4 * c + 2], k4.z));
-                dot = __fadd_rn(dot, __fmul_rn(q[4 * c + 3], k4.w));
-            }
+        if (j < c1) {
+            const float4 k4 = j == pos ? *reinterpret_cast<const float4*>(kn_s + e4)
+                                       : *reinterpret_cast<const float4*>(kc + (int64_t)j * kHeadDim + e4);
+            dot = __fadd_rn(__fadd_rn(__fmul_rn(q4.x, k4.x), __fmul_rn(q4.y, k4.y)),
+                            __fadd_rn(__fmul_rn(q4.z, k4.z), __fmul_rn(q4.w, k4.w)));
         }
-        const float sc = __fmul_rn(dot, a.scale);
-        p[j] = sc;
-        mx = fmaxf(mx, sc);
+        // the 16 lanes of a row: butterfly over e (the same sum in each)
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) dot = __fadd_rn(dot, __shfl_xor(dot, o));
+        if (j < c1) {
+            const float sc = __fmul_rn(dot, a.scale);
+            if ((lane & 15) == 0) p[j] = sc;
+            mx = fmaxf(mx, sc);
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float sum = 0.0f;
-    for (int j = lane; j <= pos; j += kHeadDim) {
+    for (int j = c0 + lane; j < c1; j += kHeadDim) {
         const float e = expf(__fsub_rn(p[j], mx));
         p[j] = e;
         sum = __fadd_rn(sum, e);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o));
-    sum = __shfl(sum, 0);
+    if (lane == 0) red[kAttnWaves + w] = __shfl(sum, 0);
     __syncthreads();
-    float acc = 0.0f;
-    for (int j = 0; j < pos; ++j)
-        acc = __fadd_rn(acc, __fmul_rn(p[j], vc[(int64_t)j * kHeadDim + lane]));
-    acc = __fadd_rn(acc, __fmul_rn(p[pos], vn));
-    orow[lane] = __fdiv_rn(acc, sum);
+    sum = __fadd_rn(__fadd_rn(red[4], red[5]), __fadd_rn(red[6], red[7]));
+    // the same lanes for v: position c0 + sub + 4i, dimensions 4e .. 4e + 3;
+    // then the 4 subs' sums (sub 0 + sub 1) + (sub 2 + sub 3), the same in
+    // every lane
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+    for (int j = c0 + sub; j < c1; j += 4) {
+        const float pj = p[j];
+        const float4 v4 = j == pos ? *reinterpret_cast<const float4*>(vn_s + e4)
+                                   : *reinterpret_cast<const float4*>(vc + (int64_t)j * kHeadDim + e4);
+        acc.x = __fadd_rn(acc.x, __fmul_rn(pj, v4.x));
+        acc.y = __fadd_rn(acc.y, __fmul_rn(pj, v4.y));
+        acc.z = __fadd_rn(acc.z, __fmul_rn(pj, v4.z));
+        acc.w = __fadd_rn(acc.w, __fmul_rn(pj, v4.w));
+    }
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
+        acc.x = __fadd_rn(acc.x, __shfl_xor(acc.x, o));
+        acc.y = __fadd_rn(acc.y, __shfl_xor(acc.y, o));
+        acc.z = __fadd_rn(acc.z, __shfl_xor(acc.z, o));
+        acc.w = __fadd_rn(acc.w, __shfl_xor(acc.w, o));
+    }
+    if (sub == 0) *reinterpret_cast<float4*>(&part[w][e4]) = acc;
+    __syncthreads();
+    if (w == 0)
+        orow[lane] = __fdiv_rn(
+            __fadd_rn(__fadd_rn(__fadd_rn(part[0][lane], part[1][lane]), part[2][lane]),
+                      part[3][lane]),
+            sum);
 }
 
 // gelu in place over n values (the fc output, bias included).
@@ -313,7 +354,7 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     aa.out = att;
     aa.scale = 0.125f;  // 1 / sqrt(64)
     const size_t lds = t3_attn_lds(c.n_ctx);
-    if (lds > 64 * 1024 - kHeadDim * 4) {
+    if (lds > 64 * 1024 - 2048) {  // beyond the default share (static LDS ~1.6 KB)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(&t3_attn),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
@@ -325,8 +366,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
                         3 * n, n, split, st);
         if (e != hipSuccess) return e;
         aa.layer = l;
-        hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head), dim3(kHeadDim),
-                           lds, st, aa);
+        hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head),
+                           dim3(kAttnWaves * kHeadDim), lds, st, aa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         e = launch_head(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
                         n_rows, n, n, split, st);
