@@ -404,16 +404,16 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
 // ----------------------------------------------------------------- mat-vec
 // Fewer than 16 projected rows (a CFG pair is 2): no row tile to fill, so
 // the weights are read once by plain FMAs.  The R rows of activations are
-// staged in LDS with each 32-element block padded to 33 words; 16 lanes take
-// one vocab row, lane s owning blocks s, s + 16, ... of it, and the 16 lanes'
-// reads of one block offset then fall in distinct banks (the four vocab rows
-// of a wave share the addresses: broadcasts).  Each lane's weights come
-// straight from memory (the 16 lanes of a vocab row read its contiguous
-// blocks), dequantized to the format's exact fp32 values; each lane sums its
-// blocks' products in element order, then the 16 lanes add by a fixed DPP
-// tree, so results do not depend on scheduling.
-constexpr int kGemvLanes = 16;       // lanes per vocab row
-constexpr int kGemvRowsPerWave = 4;  // vocab rows per wave and pass
+// staged in LDS with each 32-element block padded to 33 words; LANES lanes
+// (16, or 32 / 64 for narrow outputs with long rows) take one vocab row, lane
+// s owning blocks s, s + LANES, ... of it, and 32 lanes' reads of one block
+// offset then fall in distinct banks (the vocab rows of a wave share the
+// addresses: broadcasts).  Each lane's weights come straight from memory
+// (the lanes of a vocab row read its contiguous blocks), dequantized to the
+// format's exact fp32 values; each lane sums its blocks' products in element
+// order, then the lanes add by a fixed tree (16-lane DPP, then exchanges
+// across 16 and 32 lanes, each a commutative pair sum), so results do not
+// depend on scheduling.
 constexpr int kGemvWaves = 4;
 
 // Words of one staged activation row: 33 per 32-element block.
@@ -472,7 +472,7 @@ __device__ __forceinline__ void gemv_block(const __amdgpu_buffer_rsrc_t& rw, int
     }
 }
 
-template <int WT, int RMAX>
+template <int WT, int RMAX, int LANES>
 __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const void* W, const float* bias, const float* hidden0, const float* hidden1,
     int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int n_rows, int n_vocab,
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const int R = hidden1 ? 2 * n_rows : n_rows;  // <= RMAX
     const int nball = n_embd / 32, rw_words = gemv_row_words(n_embd);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int s = lane & (kGemvLanes - 1), grp = lane / kGemvLanes;
+    const int s = lane & (LANES - 1), grp = lane / LANES;
     for (int i = tid; i < R * n_embd; i += 64 * kGemvWaves) {
         const int r = i / n_embd, k = i - r * n_embd;
         const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
@@ -493,14 +493,15 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
     __syncthreads();
-    constexpr int kRowsPerPass = kGemvRowsPerWave * kGemvWaves;
+    constexpr int kRowsPerWave = 64 / LANES;
+    constexpr int kRowsPerPass = kRowsPerWave * kGemvWaves;
     for (int vb = blockIdx.x * kRowsPerPass; vb < n_vocab; vb += gridDim.x * kRowsPerPass) {
-        const int v = vb + wave * kGemvRowsPerWave + grp;
+        const int v = vb + wave * kRowsPerWave + grp;
         const int vc = v < n_vocab ? v : n_vocab;  // past the table: zeros
         float acc[RMAX];
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) acc[r] = 0.0f;
-        for (int b = s; b < nball; b += kGemvLanes) {
+        for (int b = s; b < nball; b += LANES) {
             float w[32];
             gemv_block<WT>(rw, vc, nball, b, w);
             const float* hb = hs + b * 33;
@@ -515,7 +516,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
                 }
             }
         }
-        // the 16 lanes' sums: lane 15 of each 16-lane row ends with the total
+        // the lanes' sums: lane 15 of each 16-lane row ends with its total,
+        // then lanes 16 and 32 apart add theirs, so lane LANES - 1 of each
+        // group ends with the total
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
             float a = acc[r];
@@ -527,9 +530,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
                                                            0, __builtin_bit_cast(int, a), 0x114, 0xf, 0xf, false)));
             a = __fadd_rn(a, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                                                            0, __builtin_bit_cast(int, a), 0x118, 0xf, 0xf, false)));
+            if constexpr (LANES >= 32) a = __fadd_rn(a, __shfl_xor(a, 16));
+            if constexpr (LANES >= 64) a = __fadd_rn(a, __shfl_xor(a, 32));
             acc[r] = a;
         }
-        if (s == kGemvLanes - 1 && v < n_vocab) {
+        if (s == LANES - 1 && v < n_vocab) {
             const float bv = bias ? bias[v] : 0.0f;
 #pragma unroll
             for (int r = 0; r < RMAX; ++r) {
@@ -543,18 +548,41 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     }
 }
 
+template <int WT, int RMAX, int LANES>
+hipError_t launch_gemv_l(const void* W, const float* bias, const float* hidden0,
+                         const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                         int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                         hipStream_t stream) {
+    const int R = hidden1 ? 2 * n_rows : n_rows;
+    const size_t lds = (size_t)R * gemv_row_words(n_embd) * 4;
+    constexpr int kRowsPerPass = 64 / LANES * kGemvWaves;
+    const unsigned grid = (unsigned)((n_vocab + kRowsPerPass - 1) / kRowsPerPass);
+    hipLaunchKernelGGL((head_gemv<WT, RMAX, LANES>), dim3(grid), dim3(64 * kGemvWaves), lds,
+                       stream, W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
+                       n_vocab, n_embd);
+    return hipGetLastError();
+}
+
+// Lanes per vocab row: 16, doubled (to 64 at most) while the grid would hold
+// fewer than 256 workgroups and every lane keeps a block (narrow outputs: the
+// T3 layers' products at one stream).
 template <int WT, int RMAX>
 hipError_t launch_gemv(const void* W, const float* bias, const float* hidden0, const float* hidden1,
                        int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int32_t n_rows,
                        int32_t n_vocab, int32_t n_embd, hipStream_t stream) {
-    const int R = hidden1 ? 2 * n_rows : n_rows;
-    const size_t lds = (size_t)R * gemv_row_words(n_embd) * 4;
-    constexpr int kRowsPerPass = kGemvRowsPerWave * kGemvWaves;
-    const unsigned grid = (unsigned)((n_vocab + kRowsPerPass - 1) / kRowsPerPass);
-    hipLaunchKernelGGL((head_gemv<WT, RMAX>), dim3(grid), dim3(64 * kGemvWaves), lds, stream, W,
-                       bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows, n_vocab,
-                       n_embd);
-    return hipGetLastError();
+    const int nball = n_embd / 32;
+    int lanes = 16;
+    while (lanes < 64 && (n_vocab + 64 / lanes * kGemvWaves - 1) / (64 / lanes * kGemvWaves) < 256 &&
+           nball >= 2 * lanes)
+        lanes *= 2;
+    if (lanes == 64)
+        return launch_gemv_l<WT, RMAX, 64>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
+                                           n_rows, n_vocab, n_embd, stream);
+    if (lanes == 32)
+        return launch_gemv_l<WT, RMAX, 32>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
+                                           n_rows, n_vocab, n_embd, stream);
+    return launch_gemv_l<WT, RMAX, 16>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
+                                       n_rows, n_vocab, n_embd, stream);
 }
 
 template <int WT>
