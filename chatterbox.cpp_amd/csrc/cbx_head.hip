@@ -33,6 +33,7 @@
 #include <stdint.h>
 
 #include "cbx_internal.h"
+#include "cbx_split.h"
 
 namespace cbx {
 namespace {
@@ -66,6 +67,8 @@ size_t split_bytes(int R, int n_embd) {
 // operand of block j / 4: dwords ((T nball + j/4) 512 + 4 lane) .. + 3 hold
 // its hi parts and the same + 256 its lo parts; inv[p] = 2^-s_p.
 constexpr int kSplitGroups = 16384 / 8 / kSplitThreads;
+// GELU: the T3 MLP's gelu (t3_gelu_f) applied to each value as it is read.
+template <bool GELU>
 __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0,
                                                             const float* hidden1, int64_t ld_hidden,
                                                             int n_rows, int n_embd,
@@ -79,16 +82,21 @@ __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(src), (short)0, real ? n_embd * 4 : 0, kBufWord3);
     const int ng = n_embd / 8, nball = n_embd / 32;
-    f4 a[kSplitGroups], b[kSplitGroups];
+    float x[kSplitGroups][8];
     float mx = 0.0f;
 #pragma unroll
     for (int q = 0; q < kSplitGroups; ++q) {
         const int j = tid + q * kSplitThreads;
         if (q == 0 || j < ng) {  // past the row (or a padding row): zeros
-            a[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j, 0, 0));
-            b[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16, 0, 0));
+            const f4 a = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j, 0, 0));
+            const f4 b = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16, 0, 0));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fmaxf(fabsf(a[q][i]), fabsf(b[q][i])));
+            for (int i = 0; i < 4; ++i) {
+                x[q][i] = GELU ? t3_gelu_f(a[i]) : a[i];
+                x[q][4 + i] = GELU ? t3_gelu_f(b[i]) : b[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(x[q][i]));
         }
     }
 #pragma unroll
@@ -97,39 +105,13 @@ __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < kSplitThreads / 64; ++w) mx = fmaxf(mx, wmax[w]);
-    // largest magnitude in [2^E, 2^(E+1)): s = 14 - E, clamped to [-126, 126]
-    // so 2^s and 2^-s are normal floats (a zero row: s = 0).  A finite row has
-    // E <= 127, so the lower clamp never binds and no part overflows; the upper
-    // one binds only for rows below 2^-112, whose split error (2^-25 scaled
-    // back by 2^-126) is below the smallest fp32 subnormal.
-    const int E = (int)(fbits(mx) >> 23) - 127;
-    const int s = mx > 0.0f ? min(max(14 - E, -126), 126) : 0;
-    const float sc = __builtin_bit_cast(float, (uint32_t)(127 + s) << 23);
-    if (tid == 0) inv[p] = __builtin_bit_cast(float, (uint32_t)(127 - s) << 23);
-    uint32_t* const dst = parts + (int64_t)T * nball * 512 + 4 * m;
+    float sc, sinv;
+    split_scale(mx, sc, sinv);
+    if (tid == 0) inv[p] = sinv;
 #pragma unroll
     for (int q = 0; q < kSplitGroups; ++q) {
         const int j = tid + q * kSplitThreads;
-        if (j < ng) {
-            float y[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                y[i] = __fmul_rn(a[q][i], sc);
-                y[4 + i] = __fmul_rn(b[q][i], sc);
-            }
-            u4v hi, lo;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const _Float16 h0 = (_Float16)y[2 * i], h1 = (_Float16)y[2 * i + 1];
-                const _Float16 l0 = (_Float16)__fsub_rn(y[2 * i], (float)h0);
-                const _Float16 l1 = (_Float16)__fsub_rn(y[2 * i + 1], (float)h1);
-                hi[i] = __builtin_bit_cast(uint32_t, h2{h0, h1});
-                lo[i] = __builtin_bit_cast(uint32_t, h2{l0, l1});
-            }
-            uint32_t* const o = dst + (j >> 2) * 512 + 64 * (j & 3);
-            *reinterpret_cast<u4v*>(o) = hi;
-            *reinterpret_cast<u4v*>(o + 256) = lo;
-        }
+        if (j < ng) split_store(parts, T, m, nball, j, x[q], sc);
     }
 }
 
@@ -213,12 +195,15 @@ constexpr int RING = 2;
 
 // parts, inv: head_split's output for the n_tiles row tiles (those of
 // hidden0, then those of hidden1).
+// K split over workgroups (gridDim.z > 1): workgroup z takes blocks
+// [nball z / Z, nball (z + 1) / Z) and writes its partial products to
+// out0 + z * zstride (the bias in slab 0 only); the caller adds the slabs.
 template <int WT, int NT>
 __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float* bias,
                                                      const uint32_t* parts, const float* inv,
                                                      int n_tiles, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
-                                                     int n_embd) {
+                                                     int n_embd, int64_t zstride) {
     constexpr int BB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
     // Weights are staged per wave in chunks of CB blocks: for each of the 32
     // vocab rows the chunk's CB * BB bytes are contiguous, so whole-row dword
@@ -259,7 +244,9 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
         acc0[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
         acc1[t] = acc0[t];
     }
-    const int kb0 = nball * wave / KS, kb1 = nball * (wave + 1) / KS;
+    const int z0 = nball * (int)blockIdx.z / (int)gridDim.z;
+    const int zn = nball * ((int)blockIdx.z + 1) / (int)gridDim.z - z0;
+    const int kb0 = z0 + zn * wave / KS, kb1 = z0 + zn * (wave + 1) / KS;
     // The activation parts of RING consecutive blocks are in flight in RING
     // register sets (block kb in set (kb - kb0) % RING).  The loads are
     // unconditional (past a wave's run they read the next run's parts, or
@@ -381,13 +368,14 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     }
     // D[4g + i][m]: hidden row 4g + i of the tile, vocab ids va and vb; the
     // scale 2^-s is exact
-    const float ba = bias && va < n_vocab ? bias[va] : 0.0f;
-    const float bb = bias && vb < n_vocab ? bias[vb] : 0.0f;
+    const bool with_bias = bias && blockIdx.z == 0;
+    const float ba = with_bias && va < n_vocab ? bias[va] : 0.0f;
+    const float bb = with_bias && vb < n_vocab ? bias[vb] : 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int T = blockIdx.y * NT + t;
         if (T >= n_tiles) continue;
-        float* const o = T >= tps ? out1 : out0;
+        float* const o = (T >= tps ? out1 : out0) + (int64_t)blockIdx.z * zstride;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rr = (T % tps) * 16 + 4 * g + i;
@@ -607,70 +595,34 @@ hipError_t launch_gemv_r(const void* W, const float* bias, const float* hidden0,
 template <int WT, int NT>
 hipError_t launch_mfma(const void* W, const float* bias, const uint32_t* parts, const float* inv,
                        int n_tiles, float* out0, float* out1, int64_t ld_out, int n_rows,
-                       int n_vocab, int n_embd, hipStream_t stream) {
-    const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT), 1u);
+                       int n_vocab, int n_embd, hipStream_t stream, int kz = 1) {
+    const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT),
+                    (unsigned)kz);
     hipLaunchKernelGGL((head_mfma<WT, NT>), grid, dim3(64 * KS), 0, stream, W, bias, parts, inv,
-                       n_tiles, out0, out1, ld_out, n_rows, n_vocab, n_embd);
+                       n_tiles, out0, out1, ld_out, n_rows, n_vocab, n_embd,
+                       (int64_t)n_rows * ld_out);
     return hipGetLastError();
 }
 
-}  // namespace
-
-bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd) {
-    const int R = cfg ? 2 * n_rows : n_rows;
-    return R < 16 && (size_t)R * gemv_row_words(n_embd) * 4 <= 65536;
-}
-
-size_t head_scratch_bytes(int32_t n_rows, bool cfg, int32_t n_embd) {
-    const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1);
-    return head_uses_gemv(n_rows, cfg, n_embd) ? 0 : split_bytes(16 * n_tiles, n_embd);
-}
-
-hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
-                       const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
-                       int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                       void* scratch, hipStream_t stream) {
-    // fewer than 16 projected rows: the mat-vec (activations staged in LDS,
-    // at most 64 KiB of them), else the split and the 16-row matrix-core tiles
-    const bool cfg = hidden1 != nullptr;
-    if (head_uses_gemv(n_rows, cfg, n_embd)) {
-        switch (wtype) {
-            case CBX_WTYPE_F16:
-                return launch_gemv_r<CBX_WTYPE_F16>(W, bias, hidden0, hidden1, ld_hidden, out0,
-                                                    out1, ld_out, n_rows, n_vocab, n_embd, stream);
-            case CBX_WTYPE_Q4_0:
-                return launch_gemv_r<CBX_WTYPE_Q4_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
-                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
-            case CBX_WTYPE_Q8_0:
-                return launch_gemv_r<CBX_WTYPE_Q8_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
-                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
-            default:
-                return hipErrorInvalidValue;
-        }
-    }
-    if (!scratch) return hipErrorInvalidValue;
-    const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1), R = 16 * n_tiles;
-    uint32_t* parts = static_cast<uint32_t*>(scratch);
-    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) +
-                                          ((size_t)R * n_embd * 4 + 255) / 256 * 256);
-    hipLaunchKernelGGL(head_split, dim3((unsigned)R), dim3(kSplitThreads), 0, stream, hidden0,
-                       hidden1, ld_hidden, n_rows, n_embd, parts, inv);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    // one row tile per workgroup where two would leave fewer than 512
-    // workgroups (narrow outputs, few rows: the T3 layer products); else two
-    // row tiles per workgroup for Q4_0 and for at most two tiles
-    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512) {
+// The matrix-core products on split activations: one row tile per workgroup
+// where two would leave fewer than 512 workgroups (narrow outputs, few rows:
+// the T3 layer products) or the K is split; else two row tiles per
+// workgroup for Q4_0 and for at most two tiles.
+hipError_t mfma_dispatch(const void* W, int32_t wtype, const float* bias, const uint32_t* parts,
+                         const float* inv, int n_tiles, float* out0, float* out1, int64_t ld_out,
+                         int32_t n_rows, int32_t n_vocab, int32_t n_embd, hipStream_t stream,
+                         int kz) {
+    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512 || kz > 1) {
         switch (wtype) {
             case CBX_WTYPE_F16:
                 return launch_mfma<CBX_WTYPE_F16, 1>(W, bias, parts, inv, n_tiles, out0, out1,
-                                                     ld_out, n_rows, n_vocab, n_embd, stream);
+                                                     ld_out, n_rows, n_vocab, n_embd, stream, kz);
             case CBX_WTYPE_Q4_0:
                 return launch_mfma<CBX_WTYPE_Q4_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
-                                                      ld_out, n_rows, n_vocab, n_embd, stream);
+                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz);
             case CBX_WTYPE_Q8_0:
                 return launch_mfma<CBX_WTYPE_Q8_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
-                                                      ld_out, n_rows, n_vocab, n_embd, stream);
+                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz);
             default:
                 return hipErrorInvalidValue;
         }
@@ -693,6 +645,87 @@ hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const fl
         default:
             return hipErrorInvalidValue;
     }
+}
+
+}  // namespace
+
+bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd) {
+    const int R = cfg ? 2 * n_rows : n_rows;
+    return R < 16 && (size_t)R * gemv_row_words(n_embd) * 4 <= 65536;
+}
+
+size_t head_scratch_bytes(int32_t n_rows, bool cfg, int32_t n_embd) {
+    const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1);
+    return head_uses_gemv(n_rows, cfg, n_embd) ? 0 : split_bytes(16 * n_tiles, n_embd);
+}
+
+hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
+                       const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                       int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                       void* scratch, hipStream_t stream) {
+    return launch_head_k(W, wtype, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
+                         n_vocab, n_embd, scratch, stream, 1, false);
+}
+
+int head_k_split(int32_t n_rows, int32_t n_vocab, int32_t n_embd) {
+    if (head_uses_gemv(n_rows, false, n_embd)) return 1;
+    const int64_t wg = (int64_t)((n_vocab + 31) / 32) * ((n_rows + 15) / 16);  // one tile each
+    const int nball = n_embd / 32;
+    int kz = 1;
+    while (kz < 8 && wg * kz < 512 && nball / (2 * kz * KS) >= 4) kz *= 2;
+    return kz;
+}
+
+hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const float* hidden0,
+                         const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                         int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                         void* scratch, hipStream_t stream, int kz, bool gelu_in) {
+    // fewer than 16 projected rows: the mat-vec (activations staged in LDS,
+    // at most 64 KiB of them), else the split and the 16-row matrix-core tiles
+    const bool cfg = hidden1 != nullptr;
+    if (kz < 1 || ((kz > 1 || gelu_in) && (cfg || head_uses_gemv(n_rows, cfg, n_embd))))
+        return hipErrorInvalidValue;  // K split and gelu: one row set on the matrix cores
+    if (head_uses_gemv(n_rows, cfg, n_embd)) {
+        switch (wtype) {
+            case CBX_WTYPE_F16:
+                return launch_gemv_r<CBX_WTYPE_F16>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                    out1, ld_out, n_rows, n_vocab, n_embd, stream);
+            case CBX_WTYPE_Q4_0:
+                return launch_gemv_r<CBX_WTYPE_Q4_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
+            case CBX_WTYPE_Q8_0:
+                return launch_gemv_r<CBX_WTYPE_Q8_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
+            default:
+                return hipErrorInvalidValue;
+        }
+    }
+    if (!scratch) return hipErrorInvalidValue;
+    const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1), R = 16 * n_tiles;
+    uint32_t* parts = static_cast<uint32_t*>(scratch);
+    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + split_inv_offset(R, n_embd));
+    if (gelu_in)
+        hipLaunchKernelGGL(head_split<true>, dim3((unsigned)R), dim3(kSplitThreads), 0, stream,
+                           hidden0, hidden1, ld_hidden, n_rows, n_embd, parts, inv);
+    else
+        hipLaunchKernelGGL(head_split<false>, dim3((unsigned)R), dim3(kSplitThreads), 0, stream,
+                           hidden0, hidden1, ld_hidden, n_rows, n_embd, parts, inv);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, out1, ld_out, n_rows, n_vocab,
+                         n_embd, stream, kz);
+}
+
+hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias, float* out0,
+                                int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                                const void* scratch, hipStream_t stream, int kz) {
+    if (!scratch || kz < 1 || head_uses_gemv(n_rows, false, n_embd)) return hipErrorInvalidValue;
+    const int n_tiles = (n_rows + 15) / 16, R = 16 * n_tiles;
+    const uint32_t* parts = static_cast<const uint32_t*>(scratch);
+    const float* inv =
+        reinterpret_cast<const float*>(static_cast<const char*>(scratch) + split_inv_offset(R, n_embd));
+    return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, nullptr, ld_out, n_rows,
+                         n_vocab, n_embd, stream, kz);
 }
 
 }  // namespace cbx

@@ -112,6 +112,28 @@ hipError_t launch_decode_v1024x32(const KernelArgs& a, hipStream_t stream);
 // head_scratch_bytes(n_rows, hidden1 != NULL, n_embd) bytes (the activations
 // split for the matrix cores; 0 bytes, and NULL allowed, below 16 rows).
 size_t head_scratch_bytes(int32_t n_rows, bool cfg, int32_t n_embd);
+// Whether launch_head takes the mat-vec (fewer than 16 projected rows whose
+// activations fit its LDS) rather than the split and the matrix cores.
+bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd);
+// launch_head with the products' K split over kz workgroups (one row set, the
+// matrix-core path): slab z of out0 (out0 + z * n_rows * ld_out) holds the
+// partial products of the z-th run of blocks, the bias in slab 0 only; the
+// caller adds the kz slabs.  head_k_split: the kz that launch would use
+// (1 for the mat-vec, else doubled up to 8 while the grid holds fewer than
+// 512 workgroups and each wave keeps 4 blocks).
+// gelu_in: the T3 MLP's gelu (t3_gelu_f) applied to the hidden rows as they
+// are split (the matrix-core path only).
+int head_k_split(int32_t n_rows, int32_t n_vocab, int32_t n_embd);
+hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const float* hidden0,
+                         const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
+                         int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                         void* scratch, hipStream_t stream, int kz, bool gelu_in);
+// The matrix-core products of n_rows rows already split into `scratch` by
+// their producer (cbx_split.h's layout, n_rows padded to whole 16-row tiles):
+// launch_head_k without its split launch (one row set; 16 rows and more).
+hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias, float* out0,
+                                int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
+                                const void* scratch, hipStream_t stream, int kz);
 hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,

@@ -1,0 +1,65 @@
+// cbx_split.h -- the matrix-core products' activation split, shared by its
+// producers (head_split in cbx_head.hip, the T3 layer norm in cbx_t3.hip).
+//
+// A row is scaled by 2^s (its largest magnitude to [2^14, 2^15)) and each
+// value written as two fp16 parts, y = x 2^s = hi + lo + e with
+// |e| <= 2^-23 |y| + 2^-25 (hi and lo rounded to nearest), next to 2^-s.
+// Layout for padded row p = 16 T + m (row tile T): group j (values 8j ..
+// 8j + 7) is lane 16 (j % 4) + m's operand of block j / 4, its hi parts in
+// dwords ((T nball + j/4) 512 + 4 lane) .. + 3 and its lo parts 256 dwords on;
+// the scales follow the parts from the next 256-byte boundary.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cbx {
+
+typedef uint32_t split_u4 __attribute__((ext_vector_type(4)));
+typedef _Float16 split_h2 __attribute__((ext_vector_type(2)));
+
+// 2^s and 2^-s for a row whose largest magnitude is mx: s = 14 - E for mx in
+// [2^E, 2^(E+1)), clamped to [-126, 126] so both are normal floats (a finite
+// row never meets the lower clamp, so no part overflows; the upper one binds
+// only below 2^-112, where the split's error, 2^-25 scaled back by 2^-126, is
+// below the smallest fp32 subnormal); s = 0 for a zero row.
+__device__ __forceinline__ void split_scale(float mx, float& sc, float& inv) {
+    const int E = (int)(__builtin_bit_cast(uint32_t, mx) >> 23) - 127;
+    const int s = mx > 0.0f ? min(max(14 - E, -126), 126) : 0;
+    sc = __builtin_bit_cast(float, (uint32_t)(127 + s) << 23);
+    inv = __builtin_bit_cast(float, (uint32_t)(127 - s) << 23);
+}
+
+// Group j of row (T, m) from its 8 values x, scaled by sc, stored in place.
+__device__ __forceinline__ void split_store(uint32_t* parts, int T, int m, int nball, int j,
+                                            const float (&x)[8], float sc) {
+    split_u4 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float y0 = __fmul_rn(x[2 * i], sc), y1 = __fmul_rn(x[2 * i + 1], sc);
+        const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+        const _Float16 l0 = (_Float16)__fsub_rn(y0, (float)h0);
+        const _Float16 l1 = (_Float16)__fsub_rn(y1, (float)h1);
+        hi[i] = __builtin_bit_cast(uint32_t, split_h2{h0, h1});
+        lo[i] = __builtin_bit_cast(uint32_t, split_h2{l0, l1});
+    }
+    uint32_t* const o = parts + (int64_t)T * nball * 512 + 4 * m + (j >> 2) * 512 + 64 * (j & 3);
+    *reinterpret_cast<split_u4*>(o) = hi;
+    *reinterpret_cast<split_u4*>(o + 256) = lo;
+}
+
+// The T3 MLP's gelu, tanh form (Hendrycks and Gimpel; ggml_gelu's):
+// 0.5 x (1 + tanh(sqrt(2/pi) x (1 + 0.044715 x^2))), each operation rounded.
+__device__ __forceinline__ float t3_gelu_f(float x) {
+    const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+    const float inner =
+        __fmul_rn(__fmul_rn(c, x), __fadd_rn(1.0f, __fmul_rn(__fmul_rn(0.044715f, x), x)));
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+
+// Byte offset of the scales in a split buffer of R padded rows of n_embd.
+__host__ __device__ inline size_t split_inv_offset(int R, int n_embd) {
+    return ((size_t)R * n_embd * 4 + 255) / 256 * 256;
+}
+
+}  // namespace cbx

@@ -20,8 +20,12 @@
 //
 // The four matrix products of a layer have the speech_head's shape (rows of
 // n_in weights per output, F16 / Q4_0 / Q8_0): they run on the head's
-// kernels (launch_head: fp16 matrix cores on split activations from 16 rows,
-// a mat-vec below).  The kernels here are the row-wise rest: the embedding,
+// kernels (fp16 matrix cores on split activations from 16 rows, a mat-vec
+// below).  From 16 rows the layer norms write the split activations of the
+// products they feed themselves, gelu is applied as the mlp output is split,
+// and the two products the residual adds take a K split over workgroups
+// when their grid is narrow, their slabs added by the norm that follows.
+// The kernels here are the row-wise rest: the embedding,
 // the residual add fused with the next layer norm, the attention with its
 // cache append (a workgroup of 4 waves per stream and head), and gelu.
 #include <hip/hip_runtime.h>
@@ -29,6 +33,7 @@
 #include <stdint.h>
 
 #include "cbx_internal.h"
+#include "cbx_split.h"
 #include "../../include/cbx_t3.h"
 
 namespace cbx {
@@ -36,12 +41,16 @@ namespace {
 
 constexpr int kNormThreads = 256;
 constexpr int kHeadDim = 64;
+// Products split over K write up to this many slabs.
+constexpr int kMaxKSplit = 8;
 
 struct NormArgs {
     int32_t n_embd;
     float eps;
     float* x;              // residual rows [n_rows][n_embd], in/out
-    const float* y;        // added to x first when set
+    const float* y;        // when set, the ny slabs y + z * ystride (a product
+    int32_t ny;            //   split over K, in slab order) are added to x
+    int64_t ystride;
     // embedding mode (emb set): x = emb[token] + wpe[pos], or x = inputs[r]
     const float* emb;
     const float* wpe;
@@ -54,6 +63,8 @@ struct NormArgs {
     const float* g;
     const float* b;
     float* out;            // LN(x) * g + b
+    uint32_t* parts;       // when set, LN(x) * g + b goes there instead, split
+    float* inv;            //   for the next product (cbx_split.h), and 2^-s here
     int32_t advance;       // last norm of the step: positions[r] += 1
 };
 
@@ -71,9 +82,26 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 // One row per workgroup: the embedding or the residual add, then the layer
 // norm.  Inactive rows (streams that take no step) keep x and write zeros.
+// The next product's split activations for row r from its values in LDS:
+// the row's scale from its largest magnitude mx, then 8 consecutive values
+// per group, groups tid, tid + 256, ...
+__device__ __forceinline__ void norm_split(const NormArgs& a, int r, const float* row_s, float mx) {
+    const int n = a.n_embd, tid = threadIdx.x;
+    float sc, sinv;
+    split_scale(mx, sc, sinv);
+    if (tid == 0) a.inv[r] = sinv;
+    for (int j = tid; j < n / 8; j += kNormThreads) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = row_s[8 * j + i];
+        split_store(a.parts, r >> 4, r & 15, n / 32, j, v, sc);
+    }
+}
+
 template <int EPT>
 __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
     __shared__ float red[4];
+    __shared__ float row_s[EPT * kNormThreads];
     const int r = blockIdx.x, tid = threadIdx.x;
     const int n = a.n_embd;
     float* xr = a.x + (int64_t)r * n;
@@ -90,7 +118,12 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
 #pragma unroll
             for (int j = 0; j < EPT; ++j) {
                 xr[j * kNormThreads + tid] = 0.0f;
-                orow[j * kNormThreads + tid] = 0.0f;
+                row_s[j * kNormThreads + tid] = 0.0f;
+                if (!a.parts) orow[j * kNormThreads + tid] = 0.0f;
+            }
+            if (a.parts) {
+                __syncthreads();
+                norm_split(a, r, row_s, 0.0f);
             }
             return;
         }
@@ -109,13 +142,36 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
         active = a.act[r] != 0;
         if (!active) {
 #pragma unroll
-            for (int j = 0; j < EPT; ++j) orow[j * kNormThreads + tid] = 0.0f;
+            for (int j = 0; j < EPT; ++j) {
+                row_s[j * kNormThreads + tid] = 0.0f;
+                if (!a.parts) orow[j * kNormThreads + tid] = 0.0f;
+            }
+            if (a.parts) {
+                __syncthreads();
+                norm_split(a, r, row_s, 0.0f);
+            }
             return;
         }
+        // the product's slabs (all loads issued first), added in slab order,
+        // then the residual (main.cpp:551, :559)
+        float ys[kMaxKSplit][EPT];
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-            xv[j] = xr[j * kNormThreads + tid];
-            if (a.y) xv[j] = __fadd_rn(xv[j], a.y[(int64_t)r * n + j * kNormThreads + tid]);
+        for (int j = 0; j < EPT; ++j) xv[j] = xr[j * kNormThreads + tid];
+        if (a.y) {
+            const float* yr = a.y + (int64_t)r * n + tid;
+#pragma unroll
+            for (int z = 0; z < kMaxKSplit; ++z)
+#pragma unroll
+                for (int j = 0; j < EPT; ++j)
+                    ys[z][j] = z < a.ny ? yr[z * a.ystride + j * kNormThreads] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                float c = ys[0][j];
+#pragma unroll
+                for (int z = 1; z < kMaxKSplit; ++z)
+                    if (z < a.ny) c = __fadd_rn(c, ys[z][j]);
+                xv[j] = __fadd_rn(c, xv[j]);
+            }
         }
     }
     float s = 0.0f;
@@ -130,11 +186,28 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
     }
     const float var = __fdiv_rn(block_sum(q, red), (float)n);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, a.eps)));
+    float mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int i = j * kNormThreads + tid;
         xr[i] = xv[j];
-        orow[i] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), a.g[i]), a.b[i]);
+        const float o =
+            __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), a.g[i]), a.b[i]);
+        if (a.parts) {
+            row_s[i] = o;
+            mx = fmaxf(mx, fabsf(o));
+        } else {
+            orow[i] = o;
+        }
+    }
+    if (a.parts) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        __syncthreads();  // red[] was read by the sums; row_s complete
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        norm_split(a, r, row_s, mx);
     }
     if (a.advance && tid == 0) a.positions[r] += 1;
 }
@@ -259,14 +332,12 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
             sum);
 }
 
-// gelu in place over n values (the fc output, bias included).
+// gelu in place over n values (the fc output, bias included), for the
+// mat-vec path (the matrix-core path applies it in the split).
 __global__ __launch_bounds__(256) void t3_gelu(float* h, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float x = h[i];
-    const float c = 0.7978845608028654f;  // sqrt(2 / pi)
-    const float inner = __fmul_rn(__fmul_rn(c, x), __fadd_rn(1.0f, __fmul_rn(__fmul_rn(0.044715f, x), x)));
-    h[i] = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+    h[i] = t3_gelu_f(h[i]);
 }
 
 template <int EPT>
@@ -299,12 +370,13 @@ bool t3_shape_ok(int32_t n_embd, int32_t n_head) {
 
 size_t t3_attn_lds(int32_t n_ctx) { return (size_t)n_ctx * 4; }
 
-// Workspace of a step: x, u, a, y [n_rows][n_embd], qkv [n_rows][3 n_embd],
-// f [n_rows][4 n_embd], act [n_rows], then the matrix products' split
-// activations (the widest input, 4 n_embd).
+// Workspace of a step: x, u, a [n_rows][n_embd], y [kMaxKSplit][n_rows][n_embd],
+// qkv [n_rows][3 n_embd], f [n_rows][4 n_embd], act [n_rows], then the matrix
+// products' split activations (the widest input, 4 n_embd).
 size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd) {
     const size_t row = (size_t)n_rows * n_embd * 4;
-    const size_t body = 4 * row + 3 * row + 4 * row + ((size_t)n_rows * 4 + 255) / 256 * 256;
+    const size_t body = (3 + kMaxKSplit) * row + 3 * row + 4 * row +
+                        ((size_t)n_rows * 4 + 255) / 256 * 256;
     return body + head_scratch_bytes(n_rows, false, 4 * n_embd);
 }
 
@@ -317,7 +389,7 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     float* u = x + row;
     float* att = u + row;
     float* y = att + row;
-    float* qkv = y + row;
+    float* qkv = y + kMaxKSplit * row;
     float* f = qkv + 3 * row;
     int32_t* act = reinterpret_cast<int32_t*>(f + 4 * row);
     void* split = reinterpret_cast<char*>(act) + ((size_t)n_rows * 4 + 255) / 256 * 256;
@@ -339,6 +411,15 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     na.g = m.layers[0].ln_1_g;
     na.b = m.layers[0].ln_1_b;
     na.out = u;
+    // 16 streams and more (the matrix-core path): the norms write the next
+    // product's split activations themselves, and gelu is applied as the mlp
+    // output is split; below, plain rows for the mat-vec
+    const bool mc = !head_uses_gemv(n_rows, false, n);
+    uint32_t* const sparts = static_cast<uint32_t*>(split);
+    float* const sinv = reinterpret_cast<float*>(static_cast<char*>(split) +
+                                                 split_inv_offset(16 * ((n_rows + 15) / 16), n));
+    na.parts = mc ? sparts : nullptr;
+    na.inv = sinv;
     hipError_t e = launch_norm(na, n_rows, st);
     if (e != hipSuccess) return e;
 
@@ -360,44 +441,61 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         if (e != hipSuccess) return e;
     }
 
+    const int kz_a = min(head_k_split(n_rows, n, n), kMaxKSplit);
+    const int kz_f = min(head_k_split(n_rows, n, 4 * n), kMaxKSplit);
     for (int l = 0; l < m.n_layer; ++l) {
         const cbx_t3_layer& L = m.layers[l];
-        e = launch_head(L.attn_w, m.wtype, L.attn_b, u, nullptr, n, qkv, nullptr, 3 * n, n_rows,
-                        3 * n, n, split, st);
+        e = mc ? launch_head_presplit(L.attn_w, m.wtype, L.attn_b, qkv, 3 * n, n_rows, 3 * n, n,
+                                      split, st, 1)
+               : launch_head(L.attn_w, m.wtype, L.attn_b, u, nullptr, n, qkv, nullptr, 3 * n,
+                             n_rows, 3 * n, n, split, st);
         if (e != hipSuccess) return e;
         aa.layer = l;
         hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head),
                            dim3(kAttnWaves * kHeadDim), lds, st, aa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        e = launch_head(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
-                        n_rows, n, n, split, st);
+        // the two products the residual adds take a K split when their grid
+        // is narrow (the norm adds the slabs)
+        e = launch_head_k(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
+                          n_rows, n, n, split, st, kz_a, false);
         if (e != hipSuccess) return e;
         NormArgs nb{};
         nb.n_embd = n;
         nb.eps = m.eps;
         nb.x = x;
         nb.y = y;
+        nb.ny = kz_a;
+        nb.ystride = (int64_t)row;
         nb.act = act;
         nb.g = L.ln_2_g;
         nb.b = L.ln_2_b;
         nb.out = u;
+        nb.parts = mc ? sparts : nullptr;
+        nb.inv = sinv;
         if ((e = launch_norm(nb, n_rows, st)) != hipSuccess) return e;
-        e = launch_head(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows, 4 * n,
-                        n, split, st);
+        e = mc ? launch_head_presplit(L.fc_w, m.wtype, L.fc_b, f, 4 * n, n_rows, 4 * n, n, split,
+                                      st, 1)
+               : launch_head(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows,
+                             4 * n, n, split, st);
         if (e != hipSuccess) return e;
-        const int64_t nf = (int64_t)4 * row;
-        hipLaunchKernelGGL(t3_gelu, dim3((unsigned)((nf + 255) / 256)), dim3(256), 0, st, f, nf);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        e = launch_head(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
-                        n_rows, n, 4 * n, split, st);
+        if (!mc) {
+            const int64_t nf = (int64_t)4 * row;
+            hipLaunchKernelGGL(t3_gelu, dim3((unsigned)((nf + 255) / 256)), dim3(256), 0, st, f,
+                               nf);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        e = launch_head_k(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
+                          n_rows, n, 4 * n, split, st, kz_f, mc);
         if (e != hipSuccess) return e;
         // the residual, then the next layer's ln_1 or, after the last, ln_f
         // into `hidden` and the positions advanced
         NormArgs nc = nb;
+        nc.ny = kz_f;
         const bool last = l + 1 == m.n_layer;
         nc.g = last ? m.ln_f_g : m.layers[l + 1].ln_1_g;
         nc.b = last ? m.ln_f_b : m.layers[l + 1].ln_1_b;
         nc.out = last ? hidden : u;
+        nc.parts = mc && !last ? sparts : nullptr;
         nc.positions = positions;
         nc.advance = last ? 1 : 0;
         if ((e = launch_norm(nc, n_rows, st)) != hipSuccess) return e;
