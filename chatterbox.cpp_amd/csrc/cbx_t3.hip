@@ -233,6 +233,7 @@ struct AttnArgs {
 // fixed order); the 4 waves' outputs are added in wave order and divided by
 // the sum.
 constexpr int kAttnWaves = 4;
+constexpr int kAttnBatch = 8;  // cache rows per lane in flight
 
 __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     extern __shared__ float p[];  // [n_ctx] scores, then weights
@@ -267,23 +268,33 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     const int L = pos + 1, run = (L + kAttnWaves - 1) / kAttnWaves;
     const int c0 = min(w * run, L), c1 = min(c0 + run, L);
     __syncthreads();
+    // rows in batches of kAttnBatch per lane, every load issued before the
+    // products (a row past the run reads the run's last row, unused); the
+    // new position's row is taken from LDS after its load (its store above
+    // need not be visible to this load)
+    const float4 kn4 = *reinterpret_cast<const float4*>(kn_s + e4);
     float mx = -INFINITY;
-    for (int j0 = c0; j0 < c1; j0 += 4) {
-        const int j = j0 + sub;
-        float dot = 0.0f;
-        if (j < c1) {
-            const float4 k4 = j == pos ? *reinterpret_cast<const float4*>(kn_s + e4)
-                                       : *reinterpret_cast<const float4*>(kc + (int64_t)j * kHeadDim + e4);
-            dot = __fadd_rn(__fadd_rn(__fmul_rn(q4.x, k4.x), __fmul_rn(q4.y, k4.y)),
-                            __fadd_rn(__fmul_rn(q4.z, k4.z), __fmul_rn(q4.w, k4.w)));
-        }
-        // the 16 lanes of a row: butterfly over e (the same sum in each)
+    for (int j0 = c0; j0 < c1; j0 += 4 * kAttnBatch) {
+        float4 kk[kAttnBatch];
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) dot = __fadd_rn(dot, __shfl_xor(dot, o));
-        if (j < c1) {
-            const float sc = __fmul_rn(dot, a.scale);
-            if ((lane & 15) == 0) p[j] = sc;
-            mx = fmaxf(mx, sc);
+        for (int u = 0; u < kAttnBatch; ++u) {
+            const int jc = min(j0 + 4 * u + sub, c1 - 1);
+            kk[u] = *reinterpret_cast<const float4*>(kc + (int64_t)jc * kHeadDim + e4);
+        }
+#pragma unroll
+        for (int u = 0; u < kAttnBatch; ++u) {
+            const int j = j0 + 4 * u + sub;
+            const float4 k4 = j == pos ? kn4 : kk[u];
+            float dot = __fadd_rn(__fadd_rn(__fmul_rn(q4.x, k4.x), __fmul_rn(q4.y, k4.y)),
+                                  __fadd_rn(__fmul_rn(q4.z, k4.z), __fmul_rn(q4.w, k4.w)));
+            // the 16 lanes of a row: butterfly over e (the same sum in each)
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) dot = __fadd_rn(dot, __shfl_xor(dot, o));
+            if (j < c1) {
+                const float sc = __fmul_rn(dot, a.scale);
+                if ((lane & 15) == 0) p[j] = sc;
+                mx = fmaxf(mx, sc);
+            }
         }
     }
 #pragma unroll
@@ -305,16 +316,27 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     // the same lanes for v: position c0 + sub + 4i, dimensions 4e .. 4e + 3;
     // then the 4 subs' sums (sub 0 + sub 1) + (sub 2 + sub 3), the same in
     // every lane
+    const float4 vn4 = *reinterpret_cast<const float4*>(vn_s + e4);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-    for (int j = c0 + sub; j < c1; j += 4) {
-        const float pj = p[j];
-        const float4 v4 = j == pos ? *reinterpret_cast<const float4*>(vn_s + e4)
-                                   : *reinterpret_cast<const float4*>(vc + (int64_t)j * kHeadDim + e4);
-        acc.x = __fadd_rn(acc.x, __fmul_rn(pj, v4.x));
-        acc.y = __fadd_rn(acc.y, __fmul_rn(pj, v4.y));
-        acc.z = __fadd_rn(acc.z, __fmul_rn(pj, v4.z));
-        acc.w = __fadd_rn(acc.w, __fmul_rn(pj, v4.w));
+    for (int j0 = c0 + sub; j0 < c1; j0 += 4 * kAttnBatch) {
+        float4 vv[kAttnBatch];
+#pragma unroll
+        for (int u = 0; u < kAttnBatch; ++u) {
+            const int jc = min(j0 + 4 * u, c1 - 1);
+            vv[u] = *reinterpret_cast<const float4*>(vc + (int64_t)jc * kHeadDim + e4);
+        }
+#pragma unroll
+        for (int u = 0; u < kAttnBatch; ++u) {
+            const int j = j0 + 4 * u;
+            if (j < c1) {
+                const float pj = p[j];
+                const float4 v4 = j == pos ? vn4 : vv[u];
+                acc.x = __fadd_rn(acc.x, __fmul_rn(pj, v4.x));
+                acc.y = __fadd_rn(acc.y, __fmul_rn(pj, v4.y));
+                acc.z = __fadd_rn(acc.z, __fmul_rn(pj, v4.z));
+                acc.w = __fadd_rn(acc.w, __fmul_rn(pj, v4.w));
+            }
+        }
     }
 #pragma unroll
     for (int o = 16; o <= 32; o <<= 1) {
