@@ -176,6 +176,27 @@ class HeadFile(ctypes.Structure):
         return {f: getattr(self, f) for f, _ in self._fields_}
 
 
+class T3File(ctypes.Structure):
+    """cbx_t3_file (include/cbx_gguf.h): the T3 transformer of a T3 GGUF."""
+
+    _fields_ = [
+        ("n_layer", ctypes.c_int32),
+        ("n_embd", ctypes.c_int32),
+        ("n_head", ctypes.c_int32),
+        ("n_pos", ctypes.c_int32),
+        ("n_speech_vocab", ctypes.c_int32),
+        ("wtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("start_speech_token", ctypes.c_int32),
+        ("stop_speech_token", ctypes.c_int32),
+        ("gguf_version", ctypes.c_int32),
+        ("device_bytes", ctypes.c_uint64),
+    ]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 class Retry(ctypes.Structure):
     """cbx_retry (include/cbx_retry.h): the early-stop retry policy of one segment."""
 
@@ -245,6 +266,11 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
     lib.cbx_gguf_load_head.restype = ctypes.c_int
     lib.cbx_gguf_load_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile), vp, vp]
+    lib.cbx_gguf_read_t3.restype = ctypes.c_int
+    lib.cbx_gguf_read_t3.argtypes = [ctypes.c_char_p, ctypes.POINTER(T3File)]
+    lib.cbx_gguf_load_t3.restype = ctypes.c_int
+    lib.cbx_gguf_load_t3.argtypes = [ctypes.c_char_p, ctypes.POINTER(T3File), vp,
+                                     ctypes.POINTER(T3Layer), ctypes.POINTER(T3Model)]
     lib.cbx_retry_init.restype = ctypes.c_int
     lib.cbx_retry_init.argtypes = [ctypes.POINTER(Retry), i32]
     lib.cbx_retry_stream_id.restype = u64
@@ -292,6 +318,29 @@ def load_head_gguf(path, device="cuda"):
     _check(_lib.cbx_gguf_load_head(os.fsencode(path), ctypes.byref(info),
                                    ctypes.c_void_p(w.data_ptr()), _ptr(b)))
     return info, w, b
+
+
+def read_t3_gguf(path) -> T3File:
+    """cbx_gguf_read_t3: the T3 transformer's shape in the GGUF at `path`."""
+    load_library()
+    info = T3File()
+    _check(_lib.cbx_gguf_read_t3(os.fsencode(path), ctypes.byref(info)))
+    return info
+
+
+def load_t3_gguf(path, device="cuda"):
+    """cbx_gguf_load_t3 into one new device buffer: returns (info, model),
+    the T3Model ready for Sampler.t3_step (it keeps the buffer alive)."""
+    import torch
+    info = read_t3_gguf(path)
+    buf = torch.empty(int(info.device_bytes), dtype=torch.uint8, device=device)
+    layers = (T3Layer * info.n_layer)()
+    m = T3Model()
+    _check(_lib.cbx_gguf_load_t3(os.fsencode(path), ctypes.byref(info),
+                                 ctypes.c_void_p(buf.data_ptr()), layers, ctypes.byref(m)))
+    m.layers = layers
+    m._keep = (buf, layers)
+    return info, m
 
 
 def retry_start(n_text_tokens) -> Retry:

@@ -1,4 +1,5 @@
-/* cbx_gguf.h -- the speech_head and sampling metadata of a chatterbox T3 GGUF.
+/* cbx_gguf.h -- the speech_head, sampling metadata and T3 transformer of a
+ * chatterbox T3 GGUF.
  *
  * The reference loads the T3 model with ggml's gguf reader
  * (src/main.cpp:356-399): the speech vocabulary size and the stop token from
@@ -22,6 +23,7 @@
 #include <stdint.h>
 
 #include "cbx_sampler.h"
+#include "cbx_t3.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -57,6 +59,44 @@ int cbx_gguf_read_head(const char* path, cbx_head_file* out);
  * file again against it.  Synchronous. */
 int cbx_gguf_load_head(const char* path, const cbx_head_file* info, void* d_weights,
                        float* d_bias);
+
+/* The T3 transformer of the same file, for cbx_t3_step: the keys
+ * chatterbox.n_embd, n_head, n_layer, n_ctx and layer_norm_eps (required, as
+ * the reference's loader requires them, main.cpp:356-367) and the tensors of
+ * main.cpp:400-416 as the converter names them (scripts/convert-t3-turbo-to-
+ * gguf.py:150-189): model/wpe (F32 [n_embd, n_ctx]), chatterbox/speech_emb
+ * (F16 or F32 [n_embd, n_speech_vocab]), model/ln_f/{g,b} and per layer i
+ * model/h<i>/ln_1/{g,b}, ln_2/{g,b}, attn/c_attn/{w,b}, attn/c_proj/{w,b},
+ * mlp/c_fc/{w,b}, mlp/c_proj/{w,b}: the four matrices F16, Q4_0 or Q8_0 (one
+ * type for all), the rest F32. */
+typedef struct cbx_t3_file {
+    int32_t  n_layer;
+    int32_t  n_embd;
+    int32_t  n_head;
+    int32_t  n_pos;              /* model/wpe rows (chatterbox.n_ctx)               */
+    int32_t  n_speech_vocab;     /* chatterbox/speech_emb rows                      */
+    int32_t  wtype;              /* CBX_WTYPE_* of the layer matrices               */
+    float    eps;                /* chatterbox.layer_norm_eps                       */
+    int32_t  start_speech_token; /* -1 if absent                                    */
+    int32_t  stop_speech_token;  /* -1 if absent                                    */
+    int32_t  gguf_version;
+    uint64_t device_bytes;       /* one device buffer of this size holds the model  */
+} cbx_t3_file;
+
+/* Parse the T3 tensors and keys of the GGUF at `path` (host only): their
+ * names, types, shapes and data ranges are checked, and *out gets the model's
+ * shape and the device bytes its tensors take (each at a 256-byte boundary,
+ * speech_emb widened to F32). */
+int cbx_gguf_read_t3(const char* path, cbx_t3_file* out);
+
+/* Copy every T3 tensor of the file into d_buffer (info->device_bytes of
+ * device memory of the current HIP device, allocated by the caller), fill
+ * layers[0 .. n_layer) (host memory) with their device addresses and *model
+ * with the rest (model->layers = layers), ready for cbx_t3_step.  `info` is
+ * what cbx_gguf_read_t3 returned for the same file; the load checks the file
+ * again against it.  Synchronous. */
+int cbx_gguf_load_t3(const char* path, const cbx_t3_file* info, void* d_buffer,
+                     cbx_t3_layer* layers, cbx_t3_model* model);
 
 #ifdef __cplusplus
 }

@@ -245,3 +245,35 @@ def test_t3_rejects_bad_arguments(cbx, torch_cuda):
     with pytest.raises(mod.CbxError):  # neither ids nor input rows
         s.t3_step(dm, pos, kd, kd, hid)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("B", [18, 3])
+def test_t3_from_gguf(cbx, torch_cuda, tmp_path, B):
+    """A T3 GGUF (2 layers, n_embd 256, Q8_0 matrices, speech_emb F16 as the
+    converter writes it) loaded by cbx_gguf_load_t3 into one device buffer:
+    3 steps of cbx_t3_step match the oracle built from the file's values."""
+    import test_gguf_t3 as GT
+    torch = torch_cuda
+    mod, s = cbx
+    rng = np.random.default_rng(0x7340 + B)
+    data, vals = GT.make_t3(rng)
+    path = tmp_path / "t3.gguf"
+    path.write_bytes(data)
+    say(f"t3 from gguf B={B}")
+    info, dm = mod.load_t3_gguf(str(path))
+    assert (info.n_layer, info.n_embd, info.wtype) == (2, 256, O.WTYPE_Q8_0)
+    rm = T3.Model(vals["layers"], vals["wpe"], vals["speech_emb"], vals["ln_f_g"],
+                  vals["ln_f_b"], 1e-5, 4)
+    kd = torch.zeros((B, 2, 4, 32, 64), dtype=torch.float32, device="cuda")
+    vd = torch.zeros_like(kd)
+    kr, vr = T3.new_cache(B, 2, 4, 32)
+    pos_d = torch.zeros(B, dtype=torch.int32, device="cuda")
+    pos_r = np.zeros(B, np.int64)
+    hid = torch.zeros((B, 256), dtype=torch.float32, device="cuda")
+    for t in range(3):
+        toks = rng.integers(0, 300, B).astype(np.int32)
+        s.t3_step(dm, pos_d, kd, vd, hid, tokens=torch.from_numpy(toks).cuda())
+        torch.cuda.synchronize()
+        want = T3.step(rm, toks, pos_r, kr, vr)
+        ok, err = close(hid.cpu().numpy(), want)
+        assert ok, f"step {t}: max err {err:.3g}"
