@@ -10,8 +10,8 @@ device Philox keyed (seed, stream, step).  Inputs are synthetic and resident
 in HBM before timing.  Steps are issued `--steps-per-launch` at a time (one
 launch samples that many independent batches; 256 by default, so that the
 fill at a launch's start and the drain at its end stay small); `--steps` and
-`--warmup` are minimums, rounded up to whole launches (at least 16 timed and
-4 untimed), and the line reports the steps actually timed.  Logits rotate over slabs totalling > 2x the 256 MB
+`--warmup` are minimums, rounded up to whole launches (at least 64 timed and
+32 untimed), and the line reports the steps actually timed.  Logits rotate over slabs totalling > 2x the 256 MB
 Infinity Cache so every step reads its logits from HBM.
 
 Prints one JSON line with the headline value, the roofline of the sampling
@@ -51,11 +51,11 @@ SEED = 0x5EED3
 CPU_SHARE = 16
 
 
-# Fewest launches timed (and run before timing): one cold launch of 256
-# steps reads about 7% slow, 16 (half a millisecond each) agree with 64 to
-# within the run-to-run spread.
-MIN_TIMED_LAUNCHES = 16
-MIN_WARMUP_LAUNCHES = 4
+# Fewest launches timed (and run before timing): 16 timed after 4 untimed
+# (10 ms of work) read 7% below 64 after 32 (the GPU's clocks still
+# ramping); 64 after 32 take about 50 ms.
+MIN_TIMED_LAUNCHES = 64
+MIN_WARMUP_LAUNCHES = 32
 
 
 def launches_for(steps, warmup, steps_per_launch):

@@ -15,7 +15,9 @@ def test_default_counts():
     a = bench.parse_args([])
     n, nw = bench.launches_for(a.steps, a.warmup, a.steps_per_launch)
     assert a.gpus == 1
-    assert (n * a.steps_per_launch, nw * a.steps_per_launch) == (16384, 1024)
+    S = a.steps_per_launch
+    assert (n * S, nw * S) == (max(16384, bench.MIN_TIMED_LAUNCHES * S),
+                               max(1024, bench.MIN_WARMUP_LAUNCHES * S))
 
 
 def test_counts_are_minimums():
