@@ -328,6 +328,14 @@ def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps):
                 sampler.decode_step(logits, prm, tok_out, dec, head=head, seed=7, step0=i,
                                     stop_token=-1)
         res[name] = timed(torch, stream, one, steps, warm=1)
+    # the prompt pass: every stream's first pos0 positions in one call
+    P = min(pos0, n_ctx)
+    slots = torch.arange(B, device=dev, dtype=torch.int32).repeat_interleave(P)
+    ppos = torch.arange(P, device=dev, dtype=torch.int32).repeat(B)
+    prow = torch.randn((B * P, n), generator=g, device=dev) * 0.5
+    phid = torch.empty((B * P, n), dtype=torch.float32, device=dev)
+    res["prefill"] = timed(torch, stream, lambda i: sampler.t3_prefill(
+        model, slots, ppos, kc, vc, phid, inputs=prow), 3, warm=1)
     mat_bytes = T3_LAYER * 12 * n * n * 18 // 32
     # per step and stream: K and V read over positions [0, pos] (pos0 .. pos0
     # + steps - 1 over the timed steps) and written at pos, every layer
@@ -343,7 +351,10 @@ def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps):
             "ms_per_step_with_head_and_sampler": round(res["t3_head_sampler"], 5),
             "tokens_per_s": round(B / (res["t3_head_sampler"] / 1e3), 1),
             "algorithmic_bytes_per_step": int(bytes_step),
-            "hbm_frac_t3": round(bytes_step / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 5)}
+            "hbm_frac_t3": round(bytes_step / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 5),
+            "prefill": {"rows": B * P, "positions_per_stream": P,
+                        "ms": round(res["prefill"], 4),
+                        "positions_per_s": round(B * P / (res["prefill"] / 1e3), 1)}}
 
 
 def pkg_workloads():

@@ -262,6 +262,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.cbx_t3_step.restype = ctypes.c_int
     lib.cbx_t3_step.argtypes = [vp, ctypes.POINTER(T3Model), i32, vp, vp, vp, vp,
                                 ctypes.POINTER(T3Cache), vp, vp]
+    lib.cbx_t3_prefill.restype = ctypes.c_int
+    lib.cbx_t3_prefill.argtypes = [vp, ctypes.POINTER(T3Model), i32, vp, i32, vp, vp, vp,
+                                   ctypes.POINTER(T3Cache), vp, vp]
     lib.cbx_gguf_read_head.restype = ctypes.c_int
     lib.cbx_gguf_read_head.argtypes = [ctypes.c_char_p, ctypes.POINTER(HeadFile)]
     lib.cbx_gguf_load_head.restype = ctypes.c_int
@@ -547,6 +550,20 @@ class Sampler:
         _check(self.lib.cbx_t3_step(self.handle, ctypes.byref(model), positions.numel(),
                                     _ptr(tokens), _ptr(inputs), _ptr(positions), _ptr(state),
                                     ctypes.byref(c), _ptr(hidden), st))
+
+    def t3_prefill(self, model, slots, positions, k_cache, v_cache, hidden, *, tokens=None,
+                   inputs=None, stream=None):
+        """cbx_t3_prefill: rows of (slot, position) in one call (device int32
+        slots and positions [n_rows]); caches [n_slots, n_layer, n_head,
+        n_ctx, 64]; positions are only read."""
+        c = T3Cache()
+        c.k = k_cache.data_ptr()
+        c.v = v_cache.data_ptr()
+        c.n_ctx = k_cache.shape[-2]
+        st = _stream_ptr() if stream is None else ctypes.c_void_p(stream)
+        _check(self.lib.cbx_t3_prefill(self.handle, ctypes.byref(model), slots.numel(),
+                                       _ptr(slots), k_cache.shape[0], _ptr(tokens), _ptr(inputs),
+                                       _ptr(positions), ctypes.byref(c), _ptr(hidden), st))
 
     def decode_step(self, logits, params, tokens, decode, **kw):
         """cbx_decode_step (head=...: cbx_head_decode_step) of one step."""

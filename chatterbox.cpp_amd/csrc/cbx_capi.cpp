@@ -574,10 +574,14 @@ int cbx_head_decode_step(cbx_sampler* s, const cbx_head* h, const cbx_batch* b,
     return head_then_sample("cbx_head_decode_step", s, h, b, d, (hipStream_t)stream);
 }
 
-int cbx_t3_step(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows, const int32_t* tokens,
-                const float* inputs, int32_t* positions, const int32_t* state,
-                const cbx_t3_cache* cache, float* hidden, void* stream) {
-    const char* fn = "cbx_t3_step";
+}  // extern "C"
+
+namespace {
+// cbx_t3_step and cbx_t3_prefill (slots set): the checks and the launch.
+int t3_run(const char* fn, cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows,
+           const int32_t* tokens, const float* inputs, int32_t* positions, const int32_t* state,
+           const int32_t* slots, int32_t n_slots, const cbx_t3_cache* cache, float* hidden,
+           void* stream) {
     if (!s || !m || !cache) return fail(CBX_ERR_INVALID, "%s: NULL handle, model or cache", fn);
     if (n_rows < 1) return fail(CBX_ERR_INVALID, "%s: n_rows %d", fn, n_rows);
     if (m->n_layer < 1 || m->n_layer > 256 || !m->layers)
@@ -618,9 +622,31 @@ int cbx_t3_step(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows, const int
         CBX_HIP(hipMalloc(&s->d_t3, need));
         s->t3_bytes = need;
     }
-    CBX_HIP(cbx::launch_t3_step(*m, n_rows, tokens, inputs, positions, state, *cache, hidden,
-                                s->d_t3, (hipStream_t)stream));
+    CBX_HIP(cbx::launch_t3_step(*m, n_rows, tokens, inputs, positions, state, slots, n_slots,
+                                *cache, hidden, s->d_t3, (hipStream_t)stream));
     return CBX_OK;
 }
+}  // namespace
+
+extern "C" {
+
+int cbx_t3_step(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows, const int32_t* tokens,
+                const float* inputs, int32_t* positions, const int32_t* state,
+                const cbx_t3_cache* cache, float* hidden, void* stream) {
+    return t3_run("cbx_t3_step", s, m, n_rows, tokens, inputs, positions, state, nullptr, 0,
+                  cache, hidden, stream);
+}
+
+int cbx_t3_prefill(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows, const int32_t* slots,
+                   int32_t n_slots, const int32_t* tokens, const float* inputs,
+                   const int32_t* positions, const cbx_t3_cache* cache, float* hidden,
+                   void* stream) {
+    if (!slots || n_slots < 1)
+        return fail(CBX_ERR_INVALID, "cbx_t3_prefill: NULL slots or n_slots %d", n_slots);
+    // positions are read, not advanced, in the prefill form
+    return t3_run("cbx_t3_prefill", s, m, n_rows, tokens, inputs, const_cast<int32_t*>(positions),
+                  nullptr, slots, n_slots, cache, hidden, stream);
+}
+
 
 }  // extern "C"

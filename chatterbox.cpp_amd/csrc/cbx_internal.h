@@ -146,8 +146,10 @@ hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const fl
 bool t3_shape_ok(int32_t n_embd, int32_t n_head);
 size_t t3_attn_lds(int32_t n_ctx);
 size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd);
+// slots set: the prefill form (cbx_t3_prefill); positions are not advanced.
 hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* tokens,
                           const float* inputs, int32_t* positions, const int32_t* state,
-                          const cbx_t3_cache& c, float* hidden, void* ws, hipStream_t st);
+                          const int32_t* slots, int32_t n_slots, const cbx_t3_cache& c,
+                          float* hidden, void* ws, hipStream_t st);
 
 }  // namespace cbx

@@ -58,6 +58,8 @@ struct NormArgs {
     const int32_t* tokens;
     int32_t* positions;
     const int32_t* state;
+    const int32_t* slots;  // prefill: the cache slot of each row (NULL: the row)
+    int32_t n_slots;
     int32_t n_vocab, n_pos, n_ctx;
     int32_t* act;          // per row: 1 when the stream takes this step
     const float* g;
@@ -111,8 +113,10 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
     if (a.emb || a.inputs) {
         const int pos = a.positions[r];
         const int tok = a.tokens ? a.tokens[r] : 0;
+        const int slot = a.slots ? a.slots[r] : r;
         active = (!a.state || a.state[r] == CBX_DECODE_RUNNING) && pos >= 0 && pos < a.n_ctx &&
-                 pos < a.n_pos && (a.inputs || (tok >= 0 && tok < a.n_vocab));
+                 pos < a.n_pos && (a.inputs || (tok >= 0 && tok < a.n_vocab)) &&
+                 (!a.slots || (slot >= 0 && slot < a.n_slots));
         if (tid == 0) a.act[r] = active ? 1 : 0;
         if (!active) {
 #pragma unroll
@@ -219,9 +223,25 @@ struct AttnArgs {
     int32_t n_layer, layer, n_head, n_ctx;
     const int32_t* positions;
     const int32_t* act;
+    const int32_t* slots;  // prefill: the cache slot of each row (NULL: the row)
+    int32_t appended;      // the rows' k, v already stored (t3_kv_append)
     float* out;            // [n_rows][n_embd]
     float scale;           // 1 / sqrt(64)
 };
+
+// Prefill: every row's k and v stored at its slot and position before any
+// row attends, so rows of one stream in one call see each other causally.
+__global__ __launch_bounds__(kHeadDim) void t3_kv_append(AttnArgs a) {
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    if (!a.act[r]) return;
+    const int n = a.n_head * kHeadDim;
+    const int slot = a.slots ? a.slots[r] : r, pos = a.positions[r];
+    const float* qr = a.qkv + (int64_t)r * 3 * n + h * kHeadDim;
+    const int64_t base =
+        (((int64_t)slot * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim + (int64_t)pos * kHeadDim;
+    a.kc[base + lane] = qr[n + lane];
+    a.vc[base + lane] = qr[2 * n + lane];
+}
 
 // One workgroup of 4 waves per (stream, head).  Wave 0 stores the new k and
 // v at the stream's position (and keeps them in LDS: that position is never
@@ -250,14 +270,17 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
         return;
     }
     const int pos = a.positions[r];
+    const int slot = a.slots ? a.slots[r] : r;
     const float* qr = a.qkv + (int64_t)r * 3 * n + h * kHeadDim;
-    const int64_t base = (((int64_t)r * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim;
+    const int64_t base = (((int64_t)slot * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim;
     float* kc = a.kc + base;
     float* vc = a.vc + base;
     if (w == 0) {
         const float kn = qr[n + lane], vn = qr[2 * n + lane];
-        kc[(int64_t)pos * kHeadDim + lane] = kn;
-        vc[(int64_t)pos * kHeadDim + lane] = vn;
+        if (!a.appended) {
+            kc[(int64_t)pos * kHeadDim + lane] = kn;
+            vc[(int64_t)pos * kHeadDim + lane] = vn;
+        }
         kn_s[lane] = kn;
         vn_s[lane] = vn;
     }
@@ -404,7 +427,11 @@ size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd) {
 
 hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* tokens,
                           const float* inputs, int32_t* positions, const int32_t* state,
-                          const cbx_t3_cache& c, float* hidden, void* ws, hipStream_t st) {
+                          const int32_t* slots, int32_t n_slots, const cbx_t3_cache& c,
+                          float* hidden, void* ws, hipStream_t st) {
+    // slots set: a prefill (rows of one stream may share a call: their k and v
+    // are stored before the attention, and positions do not advance)
+    const bool prefill = slots != nullptr;
     const int n = m.n_embd;
     const size_t row = (size_t)n_rows * n;
     float* x = static_cast<float*>(ws);
@@ -426,6 +453,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     na.tokens = inputs ? nullptr : tokens;
     na.positions = positions;
     na.state = state;
+    na.slots = slots;
+    na.n_slots = n_slots;
     na.n_vocab = m.n_speech_vocab;
     na.n_pos = m.n_pos;
     na.n_ctx = c.n_ctx;
@@ -454,6 +483,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     aa.n_ctx = c.n_ctx;
     aa.positions = positions;
     aa.act = act;
+    aa.slots = slots;
+    aa.appended = prefill ? 1 : 0;
     aa.out = att;
     aa.scale = 0.125f;  // 1 / sqrt(64)
     const size_t lds = t3_attn_lds(c.n_ctx);
@@ -473,6 +504,11 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
                              n_rows, 3 * n, n, split, st);
         if (e != hipSuccess) return e;
         aa.layer = l;
+        if (prefill) {
+            hipLaunchKernelGGL(t3_kv_append, dim3((unsigned)n_rows, (unsigned)m.n_head),
+                               dim3(kHeadDim), 0, st, aa);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head),
                            dim3(kAttnWaves * kHeadDim), lds, st, aa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -519,7 +555,7 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         nc.out = last ? hidden : u;
         nc.parts = mc && !last ? sparts : nullptr;
         nc.positions = positions;
-        nc.advance = last ? 1 : 0;
+        nc.advance = last && !prefill ? 1 : 0;
         if ((e = launch_norm(nc, n_rows, st)) != hipSuccess) return e;
     }
     return hipSuccess;

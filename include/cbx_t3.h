@@ -87,6 +87,26 @@ int cbx_t3_step(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows,
                 const int32_t* state, const cbx_t3_cache* cache, float* hidden,
                 void* stream);
 
+/* The prompt pass for many streams: n_rows rows, row r the speech id
+ * tokens[r] (or the embedded row inputs[r][0, n_embd): the prompt's rows, as
+ * the reference builds them from the speaker projection, the conditioning
+ * and text embeddings and the start id, main.cpp:602-611) of the stream in
+ * cache slot slots[r] at position positions[r].  Every row's k and v are
+ * stored first, then each row attends over its stream's positions
+ * [0, positions[r]], so the rows of one stream in one call see each other
+ * as the reference's causal prompt graph does (main.cpp:490-497, :673-685);
+ * a stream's positions must be distinct within a call, and those below a
+ * row's position already in the cache or in the call.  ln_f's rows go to
+ * hidden[r]; positions are only read.  Rows whose slot is outside
+ * [0, n_slots), position outside [0, cache.n_ctx) or token outside
+ * [0, n_speech_vocab) are skipped.  The cache holds n_slots streams.
+ * Asynchronous on `stream`.  Replaces eval_prompt (main.cpp:643-689) up to
+ * ln_f, for any number of streams at once. */
+int cbx_t3_prefill(cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows,
+                   const int32_t* slots, int32_t n_slots, const int32_t* tokens,
+                   const float* inputs, const int32_t* positions,
+                   const cbx_t3_cache* cache, float* hidden, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

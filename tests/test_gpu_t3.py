@@ -277,3 +277,54 @@ def test_t3_from_gguf(cbx, torch_cuda, tmp_path, B):
         want = T3.step(rm, toks, pos_r, kr, vr)
         ok, err = close(hid.cpu().numpy(), want)
         assert ok, f"step {t}: max err {err:.3g}"
+
+
+@pytest.mark.parametrize("lens", [(5, 9, 7), (2, 3)])
+def test_t3_prefill_then_decode(cbx, torch_cuda, lens):
+    """Prompts of several streams in one cbx_t3_prefill call (rows in shuffled
+    order, embedded input rows), then two cbx_t3_step decode steps: every
+    prompt row's ln_f output matches the oracle stepping each stream through
+    its positions one at a time (the causal prompt pass), and the decode
+    steps continue from the caches the prefill wrote.  21 rows take the
+    matrix cores, 5 the mat-vec."""
+    torch = torch_cuda
+    mod, s = cbx
+    dm, rm = model(torch, mod, O.WTYPE_Q4_0)
+    S = len(lens)
+    rng = np.random.default_rng(0x7350 + sum(lens))
+    prompts = [(rng.standard_normal((L, N)) * 0.5).astype(np.float32) for L in lens]
+    rows = [(sl, p) for sl, L in enumerate(lens) for p in range(L)]
+    order = rng.permutation(len(rows))
+    slots = np.array([rows[i][0] for i in order], np.int32)
+    pos = np.array([rows[i][1] for i in order], np.int32)
+    inp = np.stack([prompts[rows[i][0]][rows[i][1]] for i in order])
+    kd = torch.zeros((S, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
+    vd = torch.zeros_like(kd)
+    hid = torch.zeros((len(rows), N), dtype=torch.float32, device="cuda")
+    say(f"t3 prefill lens={lens}")
+    s.t3_prefill(dm, torch.from_numpy(slots).cuda(), torch.from_numpy(pos).cuda(), kd, vd, hid,
+                 inputs=torch.from_numpy(inp).cuda())
+    torch.cuda.synchronize()
+    got = hid.cpu().numpy()
+    kr, vr = T3.new_cache(S, N_LAYER, H, N_POS)
+    pos_r = np.zeros(S, np.int64)
+    want = {}
+    for t in range(max(lens)):
+        act = np.array([t < L for L in lens])
+        x = np.stack([prompts[sl][min(t, L - 1)] for sl, L in enumerate(lens)])
+        out = T3.step(rm, None, pos_r, kr, vr, inputs=x, active=act)
+        for sl in np.nonzero(act)[0]:
+            want[(sl, t)] = out[sl]
+    ref = np.stack([want[(int(a), int(b))] for a, b in zip(slots, pos)])
+    ok, err = close(got, ref)
+    assert ok, f"prefill: max err {err:.3g}"
+    # decode from the prefilled caches
+    pos_d = torch.from_numpy(np.array(lens, np.int32)).cuda()
+    hd = torch.zeros((S, N), dtype=torch.float32, device="cuda")
+    for t in range(2):
+        toks = rng.integers(0, V, S).astype(np.int32)
+        s.t3_step(dm, pos_d, kd, vd, hd, tokens=torch.from_numpy(toks).cuda())
+        torch.cuda.synchronize()
+        w = T3.step(rm, toks, pos_r, kr, vr)
+        ok, err = close(hd.cpu().numpy(), w)
+        assert ok, f"decode {t}: max err {err:.3g}"
