@@ -227,7 +227,12 @@ struct AttnArgs {
     int32_t appended;      // the rows' k, v already stored (t3_kv_append)
     float* out;            // [n_rows][n_embd]
     float scale;           // 1 / sqrt(64)
+    float* part;           // gridDim.z > 1: per (row, head, z) max, sum, 64 sums
 };
+
+// Partial results per (row, head, split): the run's max, its sum of expf
+// terms and its 64 weighted sums.
+constexpr int kAttnPart = 2 + 64;
 
 // Prefill: every row's k and v stored at its slot and position before any
 // row attends, so rows of one stream in one call see each other causally.
@@ -271,13 +276,14 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     }
     const int pos = a.positions[r];
     const int slot = a.slots ? a.slots[r] : r;
+    const int z = blockIdx.z, S = gridDim.z;
     const float* qr = a.qkv + (int64_t)r * 3 * n + h * kHeadDim;
     const int64_t base = (((int64_t)slot * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim;
     float* kc = a.kc + base;
     float* vc = a.vc + base;
     if (w == 0) {
         const float kn = qr[n + lane], vn = qr[2 * n + lane];
-        if (!a.appended) {
+        if (!a.appended && z == 0) {
             kc[(int64_t)pos * kHeadDim + lane] = kn;
             vc[(int64_t)pos * kHeadDim + lane] = vn;
         }
@@ -288,8 +294,10 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     // dimensions 4e .. 4e + 3: a wave reads 4 rows of k per instruction
     const int sub = lane >> 4, e4 = 4 * (lane & 15);
     const float4 q4 = *reinterpret_cast<const float4*>(qr + e4);
-    const int L = pos + 1, run = (L + kAttnWaves - 1) / kAttnWaves;
-    const int c0 = min(w * run, L), c1 = min(c0 + run, L);
+    // split z of S takes positions [L z / S, L (z + 1) / S), in 4 runs
+    const int L = pos + 1, z0 = (int)((int64_t)L * z / S), z1 = (int)((int64_t)L * (z + 1) / S);
+    const int run = (z1 - z0 + kAttnWaves - 1) / kAttnWaves;
+    const int c0 = min(z0 + w * run, z1), c1 = min(c0 + run, z1);
     __syncthreads();
     // rows in batches of kAttnBatch per lane, every load issued before the
     // products (a row past the run reads the run's last row, unused); the
@@ -370,11 +378,45 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     }
     if (sub == 0) *reinterpret_cast<float4*>(&part[w][e4]) = acc;
     __syncthreads();
-    if (w == 0)
-        orow[lane] = __fdiv_rn(
+    if (w == 0) {
+        const float acc_all =
             __fadd_rn(__fadd_rn(__fadd_rn(part[0][lane], part[1][lane]), part[2][lane]),
-                      part[3][lane]),
-            sum);
+                      part[3][lane]);
+        if (S == 1) {
+            orow[lane] = __fdiv_rn(acc_all, sum);
+        } else {
+            float* pp = a.part + (((int64_t)r * a.n_head + h) * S + z) * kAttnPart;
+            if (lane == 0) {
+                pp[0] = mx;
+                pp[1] = sum;
+            }
+            pp[2 + lane] = acc_all;
+        }
+    }
+}
+
+// The S splits of each (row, head) merged in split order: with M the largest
+// split max, out = sum_z acc_z e^(m_z - M) / sum_z s_z e^(m_z - M) (a split
+// with no positions has m = -inf and adds nothing).
+__global__ __launch_bounds__(kHeadDim) void t3_attn_combine(AttnArgs a, int S) {
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int n = a.n_head * kHeadDim;
+    float* orow = a.out + (int64_t)r * n + h * kHeadDim;
+    if (!a.act[r]) {
+        orow[lane] = 0.0f;
+        return;
+    }
+    const float* pp = a.part + ((int64_t)r * a.n_head + h) * S * kAttnPart;
+    float M = -INFINITY;
+    for (int z = 0; z < S; ++z) M = fmaxf(M, pp[z * kAttnPart]);
+    float sum = 0.0f, acc = 0.0f;
+    for (int z = 0; z < S; ++z) {
+        const float m = pp[z * kAttnPart];
+        const float f = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, M));
+        sum = __fadd_rn(sum, __fmul_rn(pp[z * kAttnPart + 1], f));
+        acc = __fadd_rn(acc, __fmul_rn(pp[z * kAttnPart + 2 + lane], f));
+    }
+    orow[lane] = __fdiv_rn(acc, sum);
 }
 
 // gelu in place over n values (the fc output, bias included), for the
@@ -418,10 +460,20 @@ size_t t3_attn_lds(int32_t n_ctx) { return (size_t)n_ctx * 4; }
 // Workspace of a step: x, u, a [n_rows][n_embd], y [kMaxKSplit][n_rows][n_embd],
 // qkv [n_rows][3 n_embd], f [n_rows][4 n_embd], act [n_rows], then the matrix
 // products' split activations (the widest input, 4 n_embd).
+// Positions of a (row, head) split over this many workgroups when the grid
+// of rows x heads is small (the combine kernel merges them).
+int t3_attn_splits(int32_t n_rows, int32_t n_head) {
+    int S = 1;
+    while (S < 16 && (int64_t)n_rows * n_head * S < 256) S *= 2;
+    return S;
+}
+
 size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd) {
     const size_t row = (size_t)n_rows * n_embd * 4;
+    const int n_head = n_embd / kHeadDim, S = t3_attn_splits(n_rows, n_head);
+    const size_t parts = S > 1 ? ((size_t)n_rows * n_head * S * kAttnPart * 4 + 255) / 256 * 256 : 0;
     const size_t body = (3 + kMaxKSplit) * row + 3 * row + 4 * row +
-                        ((size_t)n_rows * 4 + 255) / 256 * 256;
+                        ((size_t)n_rows * 4 + 255) / 256 * 256 + parts;
     return body + head_scratch_bytes(n_rows, false, 4 * n_embd);
 }
 
@@ -441,7 +493,14 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     float* qkv = y + kMaxKSplit * row;
     float* f = qkv + 3 * row;
     int32_t* act = reinterpret_cast<int32_t*>(f + 4 * row);
-    void* split = reinterpret_cast<char*>(act) + ((size_t)n_rows * 4 + 255) / 256 * 256;
+    // attention splits (decode steps with few rows x heads)
+    const int S = prefill ? 1 : t3_attn_splits(n_rows, m.n_head);
+    float* apart = reinterpret_cast<float*>(reinterpret_cast<char*>(act) +
+                                            ((size_t)n_rows * 4 + 255) / 256 * 256);
+    const int S_ws = t3_attn_splits(n_rows, m.n_head);
+    const size_t parts =
+        S_ws > 1 ? ((size_t)n_rows * m.n_head * S_ws * kAttnPart * 4 + 255) / 256 * 256 : 0;
+    void* split = reinterpret_cast<char*>(apart) + parts;
 
     NormArgs na{};
     na.n_embd = n;
@@ -487,6 +546,7 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     aa.appended = prefill ? 1 : 0;
     aa.out = att;
     aa.scale = 0.125f;  // 1 / sqrt(64)
+    aa.part = apart;
     const size_t lds = t3_attn_lds(c.n_ctx);
     if (lds > 64 * 1024 - 2048) {  // beyond the default share (static LDS ~1.6 KB)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(&t3_attn),
@@ -509,9 +569,14 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
                                dim3(kHeadDim), 0, st, aa);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head),
+        hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head, (unsigned)S),
                            dim3(kAttnWaves * kHeadDim), lds, st, aa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (S > 1) {
+            hipLaunchKernelGGL(t3_attn_combine, dim3((unsigned)n_rows, (unsigned)m.n_head),
+                               dim3(kHeadDim), 0, st, aa, S);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         // the two products the residual adds take a K split when their grid
         // is narrow (the norm adds the slabs)
         e = launch_head_k(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
