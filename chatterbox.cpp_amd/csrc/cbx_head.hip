@@ -464,7 +464,7 @@ template <int WT, int RMAX, int LANES>
 __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const void* W, const float* bias, const float* hidden0, const float* hidden1,
     int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int n_rows, int n_vocab,
-    int n_embd) {
+    int n_embd, int gelu) {
     extern __shared__ float hs[];  // [R][gemv_row_words(n_embd)]
     const int R = hidden1 ? 2 * n_rows : n_rows;  // <= RMAX
     const int nball = n_embd / 32, rw_words = gemv_row_words(n_embd);
@@ -474,7 +474,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
         const int r = i / n_embd, k = i - r * n_embd;
         const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
                                       : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
-        hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
+        const float x = src[k];
+        hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = gelu ? t3_gelu_f(x) : x;
     }
     constexpr int64_t kBB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
     const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
@@ -540,14 +541,14 @@ template <int WT, int RMAX, int LANES>
 hipError_t launch_gemv_l(const void* W, const float* bias, const float* hidden0,
                          const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                          int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                         hipStream_t stream) {
+                         hipStream_t stream, int gelu) {
     const int R = hidden1 ? 2 * n_rows : n_rows;
     const size_t lds = (size_t)R * gemv_row_words(n_embd) * 4;
     constexpr int kRowsPerPass = 64 / LANES * kGemvWaves;
     const unsigned grid = (unsigned)((n_vocab + kRowsPerPass - 1) / kRowsPerPass);
     hipLaunchKernelGGL((head_gemv<WT, RMAX, LANES>), dim3(grid), dim3(64 * kGemvWaves), lds,
                        stream, W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
-                       n_vocab, n_embd);
+                       n_vocab, n_embd, gelu);
     return hipGetLastError();
 }
 
@@ -557,7 +558,7 @@ hipError_t launch_gemv_l(const void* W, const float* bias, const float* hidden0,
 template <int WT, int RMAX>
 hipError_t launch_gemv(const void* W, const float* bias, const float* hidden0, const float* hidden1,
                        int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int32_t n_rows,
-                       int32_t n_vocab, int32_t n_embd, hipStream_t stream) {
+                       int32_t n_vocab, int32_t n_embd, hipStream_t stream, int gelu) {
     const int nball = n_embd / 32;
     int lanes = 16;
     while (lanes < 64 && (n_vocab + 64 / lanes * kGemvWaves - 1) / (64 / lanes * kGemvWaves) < 256 &&
@@ -565,31 +566,31 @@ hipError_t launch_gemv(const void* W, const float* bias, const float* hidden0, c
         lanes *= 2;
     if (lanes == 64)
         return launch_gemv_l<WT, RMAX, 64>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
-                                           n_rows, n_vocab, n_embd, stream);
+                                           n_rows, n_vocab, n_embd, stream, gelu);
     if (lanes == 32)
         return launch_gemv_l<WT, RMAX, 32>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
-                                           n_rows, n_vocab, n_embd, stream);
+                                           n_rows, n_vocab, n_embd, stream, gelu);
     return launch_gemv_l<WT, RMAX, 16>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
-                                       n_rows, n_vocab, n_embd, stream);
+                                       n_rows, n_vocab, n_embd, stream, gelu);
 }
 
 template <int WT>
 hipError_t launch_gemv_r(const void* W, const float* bias, const float* hidden0,
                          const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                          int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                         hipStream_t stream) {
+                         hipStream_t stream, int gelu) {
     const int R = hidden1 ? 2 * n_rows : n_rows;
     if (R <= 2)
         return launch_gemv<WT, 2>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
-                                  n_vocab, n_embd, stream);
+                                  n_vocab, n_embd, stream, gelu);
     if (R <= 4)
         return launch_gemv<WT, 4>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
-                                  n_vocab, n_embd, stream);
+                                  n_vocab, n_embd, stream, gelu);
     if (R <= 8)
         return launch_gemv<WT, 8>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
-                                  n_vocab, n_embd, stream);
+                                  n_vocab, n_embd, stream, gelu);
     return launch_gemv<WT, 16>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
-                               n_vocab, n_embd, stream);
+                               n_vocab, n_embd, stream, gelu);
 }
 
 template <int WT, int NT>
@@ -683,19 +684,22 @@ hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const 
     // fewer than 16 projected rows: the mat-vec (activations staged in LDS,
     // at most 64 KiB of them), else the split and the 16-row matrix-core tiles
     const bool cfg = hidden1 != nullptr;
-    if (kz < 1 || ((kz > 1 || gelu_in) && (cfg || head_uses_gemv(n_rows, cfg, n_embd))))
-        return hipErrorInvalidValue;  // K split and gelu: one row set on the matrix cores
+    if (kz < 1 || (kz > 1 && (cfg || head_uses_gemv(n_rows, cfg, n_embd))))
+        return hipErrorInvalidValue;  // a K split: one row set on the matrix cores
     if (head_uses_gemv(n_rows, cfg, n_embd)) {
         switch (wtype) {
             case CBX_WTYPE_F16:
                 return launch_gemv_r<CBX_WTYPE_F16>(W, bias, hidden0, hidden1, ld_hidden, out0,
-                                                    out1, ld_out, n_rows, n_vocab, n_embd, stream);
+                                                    out1, ld_out, n_rows, n_vocab, n_embd, stream,
+                                                    gelu_in ? 1 : 0);
             case CBX_WTYPE_Q4_0:
                 return launch_gemv_r<CBX_WTYPE_Q4_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
-                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream,
+                                                    gelu_in ? 1 : 0);
             case CBX_WTYPE_Q8_0:
                 return launch_gemv_r<CBX_WTYPE_Q8_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
-                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream);
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream,
+                                                    gelu_in ? 1 : 0);
             default:
                 return hipErrorInvalidValue;
         }

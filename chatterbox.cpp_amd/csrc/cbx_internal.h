@@ -122,7 +122,7 @@ bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd);
 // (1 for the mat-vec, else doubled up to 8 while the grid holds fewer than
 // 512 workgroups and each wave keeps 4 blocks).
 // gelu_in: the T3 MLP's gelu (t3_gelu_f) applied to the hidden rows as they
-// are split (the matrix-core path only).
+// are read (split for the matrix cores, staged for the mat-vec).
 int head_k_split(int32_t n_rows, int32_t n_vocab, int32_t n_embd);
 hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                          const float* hidden1, int64_t ld_hidden, float* out0, float* out1,

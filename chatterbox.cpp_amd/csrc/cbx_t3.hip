@@ -22,12 +22,13 @@
 // n_in weights per output, F16 / Q4_0 / Q8_0): they run on the head's
 // kernels (fp16 matrix cores on split activations from 16 rows, a mat-vec
 // below).  From 16 rows the layer norms write the split activations of the
-// products they feed themselves, gelu is applied as the mlp output is split,
-// and the two products the residual adds take a K split over workgroups
-// when their grid is narrow, their slabs added by the norm that follows.
-// The kernels here are the row-wise rest: the embedding,
-// the residual add fused with the next layer norm, the attention with its
-// cache append (a workgroup of 4 waves per stream and head), and gelu.
+// products they feed themselves, and the two products the residual adds
+// take a K split over workgroups when their grid is narrow, their slabs
+// added by the norm that follows; gelu is applied as the mlp output is read
+// (split or staged).  The kernels here are the row-wise rest: the
+// embedding, the residual add fused with the next layer norm, and the
+// attention with its cache append (a workgroup of 4 waves per stream and
+// head, the positions split over more workgroups when there are few).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -419,14 +420,6 @@ __global__ __launch_bounds__(kHeadDim) void t3_attn_combine(AttnArgs a, int S) {
     orow[lane] = __fdiv_rn(acc, sum);
 }
 
-// gelu in place over n values (the fc output, bias included), for the
-// mat-vec path (the matrix-core path applies it in the split).
-__global__ __launch_bounds__(256) void t3_gelu(float* h, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    h[i] = t3_gelu_f(h[i]);
-}
-
 template <int EPT>
 hipError_t launch_norm_ept(const NormArgs& a, int n_rows, hipStream_t st) {
     hipLaunchKernelGGL(t3_norm<EPT>, dim3((unsigned)n_rows), dim3(kNormThreads), 0, st, a);
@@ -522,8 +515,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     na.b = m.layers[0].ln_1_b;
     na.out = u;
     // 16 streams and more (the matrix-core path): the norms write the next
-    // product's split activations themselves, and gelu is applied as the mlp
-    // output is split; below, plain rows for the mat-vec
+    // product's split activations themselves; below, plain rows for the
+    // mat-vec
     const bool mc = !head_uses_gemv(n_rows, false, n);
     uint32_t* const sparts = static_cast<uint32_t*>(split);
     float* const sinv = reinterpret_cast<float*>(static_cast<char*>(split) +
@@ -601,14 +594,9 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
                : launch_head(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows,
                              4 * n, n, split, st);
         if (e != hipSuccess) return e;
-        if (!mc) {
-            const int64_t nf = (int64_t)4 * row;
-            hipLaunchKernelGGL(t3_gelu, dim3((unsigned)((nf + 255) / 256)), dim3(256), 0, st, f,
-                               nf);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
+        // gelu applied as the mlp rows are read (split or staged)
         e = launch_head_k(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
-                          n_rows, n, 4 * n, split, st, kz_f, mc);
+                          n_rows, n, 4 * n, split, st, kz_f, true);
         if (e != hipSuccess) return e;
         // the residual, then the next layer's ln_1 or, after the last, ln_f
         // into `hidden` and the positions advanced
