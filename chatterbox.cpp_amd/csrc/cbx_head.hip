@@ -67,8 +67,6 @@ size_t split_bytes(int R, int n_embd) {
 // operand of block j / 4: dwords ((T nball + j/4) 512 + 4 lane) .. + 3 hold
 // its hi parts and the same + 256 its lo parts; inv[p] = 2^-s_p.
 constexpr int kSplitGroups = 16384 / 8 / kSplitThreads;
-// GELU: the T3 MLP's gelu (t3_gelu_f) applied to each value as it is read.
-template <bool GELU>
 __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0,
                                                             const float* hidden1, int64_t ld_hidden,
                                                             int n_rows, int n_embd,
@@ -92,8 +90,8 @@ __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0
             const f4 b = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16, 0, 0));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                x[q][i] = GELU ? t3_gelu_f(a[i]) : a[i];
-                x[q][4 + i] = GELU ? t3_gelu_f(b[i]) : b[i];
+                x[q][i] = a[i];
+                x[q][4 + i] = b[i];
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(x[q][i]));
@@ -203,7 +201,7 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
                                                      const uint32_t* parts, const float* inv,
                                                      int n_tiles, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
-                                                     int n_embd, int64_t zstride) {
+                                                     int n_embd, int64_t zstride, int gelu_out) {
     constexpr int BB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
     // Weights are staged per wave in chunks of CB blocks: for each of the 32
     // vocab rows the chunk's CB * BB bytes are contiguous, so whole-row dword
@@ -382,8 +380,10 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
             if (rr < n_rows) {
                 const float sinv = inv[T * 16 + 4 * g + i];
                 float* orow = o + (int64_t)rr * ld_out;
-                if (va < n_vocab) orow[va] = __fadd_rn(__fmul_rn(acc0[t][i], sinv), ba);
-                if (vb < n_vocab) orow[vb] = __fadd_rn(__fmul_rn(acc1[t][i], sinv), bb);
+                const float xa = __fadd_rn(__fmul_rn(acc0[t][i], sinv), ba);
+                const float xb = __fadd_rn(__fmul_rn(acc1[t][i], sinv), bb);
+                if (va < n_vocab) orow[va] = gelu_out ? t3_gelu_f(xa) : xa;
+                if (vb < n_vocab) orow[vb] = gelu_out ? t3_gelu_f(xb) : xb;
             }
         }
     }
@@ -474,8 +474,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
         const int r = i / n_embd, k = i - r * n_embd;
         const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
                                       : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
-        const float x = src[k];
-        hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = gelu ? t3_gelu_f(x) : x;
+        hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
     }
     constexpr int64_t kBB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
     const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
@@ -530,7 +529,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
                 if (r < R) {
                     float* o = r < n_rows ? out0 + (int64_t)r * ld_out
                                           : out1 + (int64_t)(r - n_rows) * ld_out;
-                    o[v] = __fadd_rn(acc[r], bv);
+                    const float x = __fadd_rn(acc[r], bv);
+                    o[v] = gelu ? t3_gelu_f(x) : x;
                 }
             }
         }
@@ -596,12 +596,13 @@ hipError_t launch_gemv_r(const void* W, const float* bias, const float* hidden0,
 template <int WT, int NT>
 hipError_t launch_mfma(const void* W, const float* bias, const uint32_t* parts, const float* inv,
                        int n_tiles, float* out0, float* out1, int64_t ld_out, int n_rows,
-                       int n_vocab, int n_embd, hipStream_t stream, int kz = 1) {
+                       int n_vocab, int n_embd, hipStream_t stream, int kz = 1,
+                       int gelu_out = 0) {
     const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT),
                     (unsigned)kz);
     hipLaunchKernelGGL((head_mfma<WT, NT>), grid, dim3(64 * KS), 0, stream, W, bias, parts, inv,
                        n_tiles, out0, out1, ld_out, n_rows, n_vocab, n_embd,
-                       (int64_t)n_rows * ld_out);
+                       (int64_t)n_rows * ld_out, gelu_out);
     return hipGetLastError();
 }
 
@@ -612,18 +613,21 @@ hipError_t launch_mfma(const void* W, const float* bias, const uint32_t* parts, 
 hipError_t mfma_dispatch(const void* W, int32_t wtype, const float* bias, const uint32_t* parts,
                          const float* inv, int n_tiles, float* out0, float* out1, int64_t ld_out,
                          int32_t n_rows, int32_t n_vocab, int32_t n_embd, hipStream_t stream,
-                         int kz) {
-    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512 || kz > 1) {
+                         int kz, int gelu_out) {
+    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512 || kz > 1 || gelu_out) {
         switch (wtype) {
             case CBX_WTYPE_F16:
                 return launch_mfma<CBX_WTYPE_F16, 1>(W, bias, parts, inv, n_tiles, out0, out1,
-                                                     ld_out, n_rows, n_vocab, n_embd, stream, kz);
+                                                     ld_out, n_rows, n_vocab, n_embd, stream, kz,
+                                                     gelu_out);
             case CBX_WTYPE_Q4_0:
                 return launch_mfma<CBX_WTYPE_Q4_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
-                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz);
+                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz,
+                                                     gelu_out);
             case CBX_WTYPE_Q8_0:
                 return launch_mfma<CBX_WTYPE_Q8_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
-                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz);
+                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz,
+                                                     gelu_out);
             default:
                 return hipErrorInvalidValue;
         }
@@ -680,26 +684,26 @@ int head_k_split(int32_t n_rows, int32_t n_vocab, int32_t n_embd) {
 hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                          const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                          int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                         void* scratch, hipStream_t stream, int kz, bool gelu_in) {
+                         void* scratch, hipStream_t stream, int kz, bool gelu_out) {
     // fewer than 16 projected rows: the mat-vec (activations staged in LDS,
     // at most 64 KiB of them), else the split and the 16-row matrix-core tiles
     const bool cfg = hidden1 != nullptr;
-    if (kz < 1 || (kz > 1 && (cfg || head_uses_gemv(n_rows, cfg, n_embd))))
-        return hipErrorInvalidValue;  // a K split: one row set on the matrix cores
+    if (kz < 1 || (kz > 1 && (cfg || gelu_out || head_uses_gemv(n_rows, cfg, n_embd))))
+        return hipErrorInvalidValue;  // a K split: one row set on the matrix cores, no gelu
     if (head_uses_gemv(n_rows, cfg, n_embd)) {
         switch (wtype) {
             case CBX_WTYPE_F16:
                 return launch_gemv_r<CBX_WTYPE_F16>(W, bias, hidden0, hidden1, ld_hidden, out0,
                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream,
-                                                    gelu_in ? 1 : 0);
+                                                    gelu_out ? 1 : 0);
             case CBX_WTYPE_Q4_0:
                 return launch_gemv_r<CBX_WTYPE_Q4_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
                                                      out1, ld_out, n_rows, n_vocab, n_embd, stream,
-                                                    gelu_in ? 1 : 0);
+                                                    gelu_out ? 1 : 0);
             case CBX_WTYPE_Q8_0:
                 return launch_gemv_r<CBX_WTYPE_Q8_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
                                                      out1, ld_out, n_rows, n_vocab, n_embd, stream,
-                                                    gelu_in ? 1 : 0);
+                                                    gelu_out ? 1 : 0);
             default:
                 return hipErrorInvalidValue;
         }
@@ -708,28 +712,25 @@ hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const 
     const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1), R = 16 * n_tiles;
     uint32_t* parts = static_cast<uint32_t*>(scratch);
     float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + split_inv_offset(R, n_embd));
-    if (gelu_in)
-        hipLaunchKernelGGL(head_split<true>, dim3((unsigned)R), dim3(kSplitThreads), 0, stream,
-                           hidden0, hidden1, ld_hidden, n_rows, n_embd, parts, inv);
-    else
-        hipLaunchKernelGGL(head_split<false>, dim3((unsigned)R), dim3(kSplitThreads), 0, stream,
-                           hidden0, hidden1, ld_hidden, n_rows, n_embd, parts, inv);
+    hipLaunchKernelGGL(head_split, dim3((unsigned)R), dim3(kSplitThreads), 0, stream, hidden0,
+                       hidden1, ld_hidden, n_rows, n_embd, parts, inv);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, out1, ld_out, n_rows, n_vocab,
-                         n_embd, stream, kz);
+                         n_embd, stream, kz, gelu_out ? 1 : 0);
 }
 
 hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias, float* out0,
                                 int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                                const void* scratch, hipStream_t stream, int kz) {
-    if (!scratch || kz < 1 || head_uses_gemv(n_rows, false, n_embd)) return hipErrorInvalidValue;
+                                const void* scratch, hipStream_t stream, int kz, bool gelu_out) {
+    if (!scratch || kz < 1 || head_uses_gemv(n_rows, false, n_embd) || (gelu_out && kz > 1))
+        return hipErrorInvalidValue;
     const int n_tiles = (n_rows + 15) / 16, R = 16 * n_tiles;
     const uint32_t* parts = static_cast<const uint32_t*>(scratch);
     const float* inv =
         reinterpret_cast<const float*>(static_cast<const char*>(scratch) + split_inv_offset(R, n_embd));
     return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, nullptr, ld_out, n_rows,
-                         n_vocab, n_embd, stream, kz);
+                         n_vocab, n_embd, stream, kz, gelu_out ? 1 : 0);
 }
 
 }  // namespace cbx

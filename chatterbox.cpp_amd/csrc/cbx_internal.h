@@ -121,19 +121,20 @@ bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd);
 // caller adds the kz slabs.  head_k_split: the kz that launch would use
 // (1 for the mat-vec, else doubled up to 8 while the grid holds fewer than
 // 512 workgroups and each wave keeps 4 blocks).
-// gelu_in: the T3 MLP's gelu (t3_gelu_f) applied to the hidden rows as they
-// are read (split for the matrix cores, staged for the mat-vec).
+// gelu_out: the T3 MLP's gelu (t3_gelu_f) applied to every output as it is
+// stored (no K split then).
 int head_k_split(int32_t n_rows, int32_t n_vocab, int32_t n_embd);
 hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                          const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                          int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                         void* scratch, hipStream_t stream, int kz, bool gelu_in);
+                         void* scratch, hipStream_t stream, int kz, bool gelu_out);
 // The matrix-core products of n_rows rows already split into `scratch` by
 // their producer (cbx_split.h's layout, n_rows padded to whole 16-row tiles):
 // launch_head_k without its split launch (one row set; 16 rows and more).
 hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias, float* out0,
                                 int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                                const void* scratch, hipStream_t stream, int kz);
+                                const void* scratch, hipStream_t stream, int kz,
+                                bool gelu_out);
 hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,

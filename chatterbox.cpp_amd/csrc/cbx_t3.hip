@@ -24,8 +24,8 @@
 // below).  From 16 rows the layer norms write the split activations of the
 // products they feed themselves, and the two products the residual adds
 // take a K split over workgroups when their grid is narrow, their slabs
-// added by the norm that follows; gelu is applied as the mlp output is read
-// (split or staged).  The kernels here are the row-wise rest: the
+// added by the norm that follows; gelu is applied as the mlp c_fc product
+// stores its outputs.  The kernels here are the row-wise rest: the
 // embedding, the residual add fused with the next layer norm, and the
 // attention with its cache append (a workgroup of 4 waves per stream and
 // head, the positions split over more workgroups when there are few).
@@ -552,7 +552,7 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     for (int l = 0; l < m.n_layer; ++l) {
         const cbx_t3_layer& L = m.layers[l];
         e = mc ? launch_head_presplit(L.attn_w, m.wtype, L.attn_b, qkv, 3 * n, n_rows, 3 * n, n,
-                                      split, st, 1)
+                                      split, st, 1, false)
                : launch_head(L.attn_w, m.wtype, L.attn_b, u, nullptr, n, qkv, nullptr, 3 * n,
                              n_rows, 3 * n, n, split, st);
         if (e != hipSuccess) return e;
@@ -589,14 +589,14 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         nb.parts = mc ? sparts : nullptr;
         nb.inv = sinv;
         if ((e = launch_norm(nb, n_rows, st)) != hipSuccess) return e;
+        // gelu applied as the mlp rows are stored
         e = mc ? launch_head_presplit(L.fc_w, m.wtype, L.fc_b, f, 4 * n, n_rows, 4 * n, n, split,
-                                      st, 1)
-               : launch_head(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows,
-                             4 * n, n, split, st);
+                                      st, 1, true)
+               : launch_head_k(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows,
+                               4 * n, n, split, st, 1, true);
         if (e != hipSuccess) return e;
-        // gelu applied as the mlp rows are read (split or staged)
         e = launch_head_k(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
-                          n_rows, n, 4 * n, split, st, kz_f, true);
+                          n_rows, n, 4 * n, split, st, kz_f, false);
         if (e != hipSuccess) return e;
         // the residual, then the next layer's ln_1 or, after the last, ln_f
         // into `hidden` and the positions advanced
