@@ -249,20 +249,18 @@ __global__ __launch_bounds__(kHeadDim) void t3_kv_append(AttnArgs a) {
     a.vc[base + lane] = qr[2 * n + lane];
 }
 
-// One workgroup of 4 waves per (stream, head).  Wave 0 stores the new k and
-// v at the stream's position (and keeps them in LDS: that position is never
-// read back from memory).  The positions [0, pos] are cut into 4 runs, one
-// per wave: its lanes score their run's positions (lane j takes positions
-// j, j + 64, ... of the run) into LDS, the maxima and then the sums of
-// expf(score - max) are combined over the 4 waves in a fixed order, and each
-// wave sums p_j v_j over its run (four interleaved partial sums, added in a
-// fixed order); the 4 waves' outputs are added in wave order and divided by
-// the sum.
+// One workgroup of 4 waves per (stream, head) (per (stream, head, split) when
+// the positions are split over several workgroups).  Wave 0 stores the new k
+// and v at the stream's position (and keeps them in LDS: that position is
+// never read back from memory).  The positions are cut into 4 runs, one per
+// wave; a wave's lanes take 16 per cache row, 4 rows per load instruction,
+// and go over the run once with a running softmax (max, sum, weighted v
+// sums, rescaled as the max grows); the runs of the 4 row groups of a wave
+// and of the 4 waves are merged by the same rescaling in a fixed order.
 constexpr int kAttnWaves = 4;
 constexpr int kAttnBatch = 8;  // cache rows per lane in flight
 
 __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
-    extern __shared__ float p[];  // [n_ctx] scores, then weights
     __shared__ __align__(16) float kn_s[kHeadDim];
     __shared__ __align__(16) float vn_s[kHeadDim];
     __shared__ float red[2 * kAttnWaves];
@@ -300,19 +298,26 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     const int run = (z1 - z0 + kAttnWaves - 1) / kAttnWaves;
     const int c0 = min(z0 + w * run, z1), c1 = min(c0 + run, z1);
     __syncthreads();
-    // rows in batches of kAttnBatch per lane, every load issued before the
-    // products (a row past the run reads the run's last row, unused); the
-    // new position's row is taken from LDS after its load (its store above
-    // need not be visible to this load)
+    // Each lane keeps, over the positions of its 16-lane group (position order),
+    // the running max m of the scores, the sum s of expf(score - m) and the
+    // sums acc of expf(score - m) v[4e .. 4e + 3], rescaled whenever m grows
+    // (one pass: k and v rows of a batch are loaded together, 8 per lane, a
+    // row past the run reading the run's last row, unused; the new position's
+    // k and v are taken from LDS, their stores above need not be visible).
     const float4 kn4 = *reinterpret_cast<const float4*>(kn_s + e4);
-    float mx = -INFINITY;
+    const float4 vn4 = *reinterpret_cast<const float4*>(vn_s + e4);
+    float m = -INFINITY, s = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int j0 = c0; j0 < c1; j0 += 4 * kAttnBatch) {
-        float4 kk[kAttnBatch];
+        float4 kk[kAttnBatch], vv[kAttnBatch];
 #pragma unroll
         for (int u = 0; u < kAttnBatch; ++u) {
-            const int jc = min(j0 + 4 * u + sub, c1 - 1);
-            kk[u] = *reinterpret_cast<const float4*>(kc + (int64_t)jc * kHeadDim + e4);
+            const int64_t jc = min(j0 + 4 * u + sub, c1 - 1);
+            kk[u] = *reinterpret_cast<const float4*>(kc + jc * kHeadDim + e4);
+            vv[u] = *reinterpret_cast<const float4*>(vc + jc * kHeadDim + e4);
         }
+        float sc[kAttnBatch];
+        float bm = -INFINITY;
 #pragma unroll
         for (int u = 0; u < kAttnBatch; ++u) {
             const int j = j0 + 4 * u + sub;
@@ -322,76 +327,75 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
             // the 16 lanes of a row: butterfly over e (the same sum in each)
 #pragma unroll
             for (int o = 1; o < 16; o <<= 1) dot = __fadd_rn(dot, __shfl_xor(dot, o));
-            if (j < c1) {
-                const float sc = __fmul_rn(dot, a.scale);
-                if ((lane & 15) == 0) p[j] = sc;
-                mx = fmaxf(mx, sc);
-            }
+            sc[u] = __fmul_rn(dot, a.scale);
+            if (j < c1) bm = fmaxf(bm, sc[u]);
         }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) red[w] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.0f;
-    for (int j = c0 + lane; j < c1; j += kHeadDim) {
-        const float e = expf(__fsub_rn(p[j], mx));
-        p[j] = e;
-        sum = __fadd_rn(sum, e);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o));
-    if (lane == 0) red[kAttnWaves + w] = __shfl(sum, 0);
-    __syncthreads();
-    sum = __fadd_rn(__fadd_rn(red[4], red[5]), __fadd_rn(red[6], red[7]));
-    // the same lanes for v: position c0 + sub + 4i, dimensions 4e .. 4e + 3;
-    // then the 4 subs' sums (sub 0 + sub 1) + (sub 2 + sub 3), the same in
-    // every lane
-    const float4 vn4 = *reinterpret_cast<const float4*>(vn_s + e4);
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int j0 = c0 + sub; j0 < c1; j0 += 4 * kAttnBatch) {
-        float4 vv[kAttnBatch];
-#pragma unroll
-        for (int u = 0; u < kAttnBatch; ++u) {
-            const int jc = min(j0 + 4 * u, c1 - 1);
-            vv[u] = *reinterpret_cast<const float4*>(vc + (int64_t)jc * kHeadDim + e4);
+        if (bm > m) {
+            const float f = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, bm));
+            s = __fmul_rn(s, f);
+            acc.x = __fmul_rn(acc.x, f);
+            acc.y = __fmul_rn(acc.y, f);
+            acc.z = __fmul_rn(acc.z, f);
+            acc.w = __fmul_rn(acc.w, f);
+            m = bm;
         }
 #pragma unroll
         for (int u = 0; u < kAttnBatch; ++u) {
-            const int j = j0 + 4 * u;
+            const int j = j0 + 4 * u + sub;
             if (j < c1) {
-                const float pj = p[j];
+                const float e = expf(__fsub_rn(sc[u], m));
                 const float4 v4 = j == pos ? vn4 : vv[u];
-                acc.x = __fadd_rn(acc.x, __fmul_rn(pj, v4.x));
-                acc.y = __fadd_rn(acc.y, __fmul_rn(pj, v4.y));
-                acc.z = __fadd_rn(acc.z, __fmul_rn(pj, v4.z));
-                acc.w = __fadd_rn(acc.w, __fmul_rn(pj, v4.w));
+                s = __fadd_rn(s, e);
+                acc.x = __fadd_rn(acc.x, __fmul_rn(e, v4.x));
+                acc.y = __fadd_rn(acc.y, __fmul_rn(e, v4.y));
+                acc.z = __fadd_rn(acc.z, __fmul_rn(e, v4.z));
+                acc.w = __fadd_rn(acc.w, __fmul_rn(e, v4.w));
             }
         }
     }
+    // the 4 groups of a wave, then the 4 waves, merged by the same rescaling:
+    // each pair's two products added in either lane give the same sum
 #pragma unroll
     for (int o = 16; o <= 32; o <<= 1) {
-        acc.x = __fadd_rn(acc.x, __shfl_xor(acc.x, o));
-        acc.y = __fadd_rn(acc.y, __shfl_xor(acc.y, o));
-        acc.z = __fadd_rn(acc.z, __shfl_xor(acc.z, o));
-        acc.w = __fadd_rn(acc.w, __shfl_xor(acc.w, o));
+        const float mo = __shfl_xor(m, o), so = __shfl_xor(s, o);
+        const float4 ao = make_float4(__shfl_xor(acc.x, o), __shfl_xor(acc.y, o),
+                                      __shfl_xor(acc.z, o), __shfl_xor(acc.w, o));
+        const float M = fmaxf(m, mo);
+        const float f = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, M));
+        const float fo = mo == -INFINITY ? 0.0f : expf(__fsub_rn(mo, M));
+        s = __fadd_rn(__fmul_rn(s, f), __fmul_rn(so, fo));
+        acc.x = __fadd_rn(__fmul_rn(acc.x, f), __fmul_rn(ao.x, fo));
+        acc.y = __fadd_rn(__fmul_rn(acc.y, f), __fmul_rn(ao.y, fo));
+        acc.z = __fadd_rn(__fmul_rn(acc.z, f), __fmul_rn(ao.z, fo));
+        acc.w = __fadd_rn(__fmul_rn(acc.w, f), __fmul_rn(ao.w, fo));
+        m = M;
+    }
+    if (lane == 0) {
+        red[w] = m;
+        red[kAttnWaves + w] = s;
     }
     if (sub == 0) *reinterpret_cast<float4*>(&part[w][e4]) = acc;
     __syncthreads();
     if (w == 0) {
-        const float acc_all =
-            __fadd_rn(__fadd_rn(__fadd_rn(part[0][lane], part[1][lane]), part[2][lane]),
-                      part[3][lane]);
+        float M = red[0];
+#pragma unroll
+        for (int q = 1; q < kAttnWaves; ++q) M = fmaxf(M, red[q]);
+        float st = 0.0f, at = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kAttnWaves; ++q) {
+            const float f = red[q] == -INFINITY ? 0.0f : expf(__fsub_rn(red[q], M));
+            st = __fadd_rn(st, __fmul_rn(red[kAttnWaves + q], f));
+            at = __fadd_rn(at, __fmul_rn(part[q][lane], f));
+        }
         if (S == 1) {
-            orow[lane] = __fdiv_rn(acc_all, sum);
+            orow[lane] = __fdiv_rn(at, st);
         } else {
             float* pp = a.part + (((int64_t)r * a.n_head + h) * S + z) * kAttnPart;
             if (lane == 0) {
-                pp[0] = mx;
-                pp[1] = sum;
+                pp[0] = M;
+                pp[1] = st;
             }
-            pp[2 + lane] = acc_all;
+            pp[2 + lane] = at;
         }
     }
 }
@@ -448,7 +452,7 @@ bool t3_shape_ok(int32_t n_embd, int32_t n_head) {
            (e == 1 || e == 2 || e == 3 || e == 4 || e == 6 || e == 8 || e == 12 || e == 16);
 }
 
-size_t t3_attn_lds(int32_t n_ctx) { return (size_t)n_ctx * 4; }
+size_t t3_attn_lds(int32_t) { return 0; }  // one pass: no per-position LDS
 
 // Workspace of a step: x, u, a [n_rows][n_embd], y [kMaxKSplit][n_rows][n_embd],
 // qkv [n_rows][3 n_embd], f [n_rows][4 n_embd], act [n_rows], then the matrix
@@ -541,11 +545,6 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     aa.scale = 0.125f;  // 1 / sqrt(64)
     aa.part = apart;
     const size_t lds = t3_attn_lds(c.n_ctx);
-    if (lds > 64 * 1024 - 2048) {  // beyond the default share (static LDS ~1.6 KB)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&t3_attn),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
 
     const int kz_a = min(head_k_split(n_rows, n, n), kMaxKSplit);
     const int kz_f = min(head_k_split(n_rows, n, 4 * n), kMaxKSplit);
