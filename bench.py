@@ -8,8 +8,9 @@ of every row, history length U[0,1000], temperature U[0.5,1.2], top_k in
 {50,250,1000}, top_p 0.9, repetition penalty 1.2, the draw's uniform from the
 device Philox keyed (seed, stream, step).  Inputs are synthetic and resident
 in HBM before timing.  Steps are issued `--steps-per-launch` at a time (one
-launch samples that many independent batches; 256 by default, so that the
-fill at a launch's start and the drain at its end stay small); `--steps` and
+launch samples that many independent batches; 1024 by default, so that the
+fill at a launch's start and the drain at its end stay small: 256 read 7%
+lower); `--steps` and
 `--warmup` are minimums, rounded up to whole launches (at least 64 timed and
 32 untimed), and the line reports the steps actually timed.  Logits rotate over slabs totalling > 2x the 256 MB
 Infinity Cache so every step reads its logits from HBM.
@@ -18,7 +19,7 @@ Prints one JSON line with the headline value, the roofline of the sampling
 kernel (algorithmic bytes / measured launch time vs 8 TB/s), the CPU baseline
 (the oracle, the reference's algorithm in C++, on host cores) and the other
 measured shapes:
-  launch_shapes           the same kernel at 16 and 64 steps per launch
+  launch_shapes           the same kernel at 16, 64 and 256 steps per launch
   single_launch_per_step  B=256, one launch per step (the decode-loop shape)
   decode_loop             B=256, cbx_decode_step per step with the streams'
                           state on the device, and with a per-token host sync
@@ -585,11 +586,11 @@ def config_masked_stress(torch, mod, sampler, stream, dev, steps=48, n_slabs=4):
 def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=16384,
+    ap.add_argument("--steps", type=int, default=65536,
                     help="timed steps (at least; rounded up to whole launches)")
     ap.add_argument("--warmup", type=int, default=1024,
                     help="untimed steps first (at least; rounded up to whole launches)")
-    ap.add_argument("--steps-per-launch", type=int, default=256)
+    ap.add_argument("--steps-per-launch", type=int, default=1024)
     ap.add_argument("--slabs", type=int, default=2)
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
@@ -607,7 +608,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other configurations (single stream, CFG pair, masked)")
-    ap.add_argument("--shape-steps", type=str, default="16,64",
+    ap.add_argument("--shape-steps", type=str, default="16,64,256",
                     help="also time launches of these many steps (comma list; entries that do "
                          "not divide --steps-per-launch are skipped; empty: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
