@@ -48,8 +48,6 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t hb) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
 }
 
-__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
-
 // ------------------------------------------------------------ activation split
 constexpr int kSplitThreads = 256;
 // Bytes of head_split's output for R rows (a multiple of 16) of n_embd: the

@@ -249,17 +249,20 @@ __global__ __launch_bounds__(kHeadDim) void t3_kv_append(AttnArgs a) {
     a.vc[base + lane] = qr[2 * n + lane];
 }
 
-// One workgroup of 4 waves per (stream, head) (per (stream, head, split) when
-// the positions are split over several workgroups).  Wave 0 stores the new k
-// and v at the stream's position (and keeps them in LDS: that position is
-// never read back from memory).  The positions are cut into 4 runs, one per
-// wave; a wave's lanes take 16 per cache row, 4 rows per load instruction,
-// and go over the run once with a running softmax (max, sum, weighted v
-// sums, rescaled as the max grows); the runs of the 4 row groups of a wave
-// and of the 4 waves are merged by the same rescaling in a fixed order.
-constexpr int kAttnWaves = 4;
-constexpr int kAttnBatch = 8;  // cache rows per lane in flight
-
+// One workgroup of kAttnWaves waves per (stream, head) (per (stream, head,
+// split) when the positions are split over several workgroups).  Wave 0
+// stores the new k and v at the stream's position (and keeps them in LDS:
+// that position is never read back from memory).  The positions are cut into
+// kAttnWaves runs, one per wave; a wave's lanes take 16 per cache row, 4 rows
+// per load instruction, kAttnBatch rows per lane in flight, and go over the
+// run once with a running softmax (max, sum, weighted v sums, rescaled as the
+// max grows); the runs of the 4 row groups of a wave and of the waves are
+// merged by the same rescaling in a fixed order.  Decode steps run 4 waves x
+// 6 rows (every workgroup resident at once), the prompt pass 2 waves x 8 rows
+// (many more workgroups: smaller ones keep more of them resident); measured
+// at 64 streams 1.89 -> 1.85 ms per step against 4 x 8, and the prompt of
+// 64 x 256 positions 93.8 -> 82.2 ms.
+template <int kAttnBatch, int kAttnWaves>
 __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     __shared__ __align__(16) float kn_s[kHeadDim];
     __shared__ __align__(16) float vn_s[kHeadDim];
@@ -301,9 +304,10 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     // Each lane keeps, over the positions of its 16-lane group (position order),
     // the running max m of the scores, the sum s of expf(score - m) and the
     // sums acc of expf(score - m) v[4e .. 4e + 3], rescaled whenever m grows
-    // (one pass: k and v rows of a batch are loaded together, 8 per lane, a
-    // row past the run reading the run's last row, unused; the new position's
-    // k and v are taken from LDS, their stores above need not be visible).
+    // (one pass: k and v rows of a batch are loaded together, kAttnBatch per
+    // lane, a row past the run reading the run's last row, unused; the new
+    // position's k and v are taken from LDS, their stores above need not be
+    // visible).
     const float4 kn4 = *reinterpret_cast<const float4*>(kn_s + e4);
     const float4 vn4 = *reinterpret_cast<const float4*>(vn_s + e4);
     float m = -INFINITY, s = 0.0f;
@@ -561,8 +565,13 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
                                dim3(kHeadDim), 0, st, aa);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(t3_attn, dim3((unsigned)n_rows, (unsigned)m.n_head, (unsigned)S),
-                           dim3(kAttnWaves * kHeadDim), lds, st, aa);
+        if (prefill)
+            hipLaunchKernelGGL((t3_attn<8, 2>), dim3((unsigned)n_rows, (unsigned)m.n_head),
+                               dim3(2 * kHeadDim), lds, st, aa);
+        else
+            hipLaunchKernelGGL((t3_attn<6, 4>),
+                               dim3((unsigned)n_rows, (unsigned)m.n_head, (unsigned)S),
+                               dim3(4 * kHeadDim), lds, st, aa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (S > 1) {
             hipLaunchKernelGGL(t3_attn_combine, dim3((unsigned)n_rows, (unsigned)m.n_head),
