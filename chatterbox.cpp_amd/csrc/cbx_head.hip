@@ -458,21 +458,88 @@ __device__ __forceinline__ void gemv_block(const __amdgpu_buffer_rsrc_t& rw, int
     }
 }
 
-template <int WT, int RMAX, int LANES>
+template <int WT, int RMAX, int LANES, bool NORM>
 __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const void* W, const float* bias, const float* hidden0, const float* hidden1,
     int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int n_rows, int n_vocab,
-    int n_embd, int gelu) {
+    int n_embd, int gelu, GemvNorm nm) {
     extern __shared__ float hs[];  // [R][gemv_row_words(n_embd)]
     const int R = hidden1 ? 2 * n_rows : n_rows;  // <= RMAX
     const int nball = n_embd / 32, rw_words = gemv_row_words(n_embd);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int s = lane & (LANES - 1), grp = lane / LANES;
-    for (int i = tid; i < R * n_embd; i += 64 * kGemvWaves) {
-        const int r = i / n_embd, k = i - r * n_embd;
-        const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
-                                      : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
-        hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
+    if constexpr (NORM) {
+        // the rows' residual add and layer norm (the T3 layer's, same
+        // operations in the same order as its norm kernel), into LDS;
+        // workgroup 0 stores the new residual rows
+        __shared__ float red[kGemvWaves];
+        static_assert(kGemvWaves == 4, "the four waves' sums are added in pairs");
+        const int ept = n_embd / (64 * kGemvWaves);  // <= 16
+        auto block_sum = [&](float v) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+            __syncthreads();
+            if (lane == 0) red[wave] = v;
+            __syncthreads();
+            return __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
+        };
+        for (int r = 0; r < R; ++r) {
+            const float* xr = nm.x_in + (int64_t)r * n_embd;
+            const float* yr = nm.y + (int64_t)r * n_embd;
+            float* xo = nm.x_out + (int64_t)r * n_embd;
+            float* hr = hs + r * rw_words;
+            float xv[16];
+            if (nm.act[r] == 0) {  // a stream that takes no step: zeros, x kept
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int k = j * 64 * kGemvWaves + tid;
+                    if (j < ept) {
+                        hr[(k >> 5) * 33 + (k & 31)] = 0.0f;
+                        if (blockIdx.x == 0) xo[k] = xr[k];
+                    }
+                }
+                continue;
+            }
+            float gv[16], bv[16];  // loaded with the rows: one wait for all
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (j < ept) {
+                    const int k = j * 64 * kGemvWaves + tid;
+                    gv[j] = nm.g[k];
+                    bv[j] = nm.b[k];
+                    xv[j] = __fadd_rn(yr[k], xr[k]);
+                    sum = __fadd_rn(sum, xv[j]);
+                }
+            }
+            const float mean = __fdiv_rn(block_sum(sum), (float)n_embd);
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (j < ept) {
+                    const float d = __fsub_rn(xv[j], mean);
+                    q = __fadd_rn(q, __fmul_rn(d, d));
+                }
+            }
+            const float var = __fdiv_rn(block_sum(q), (float)n_embd);
+            const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, nm.eps)));
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (j < ept) {
+                    const int k = j * 64 * kGemvWaves + tid;
+                    if (blockIdx.x == 0) xo[k] = xv[j];
+                    hr[(k >> 5) * 33 + (k & 31)] = __fadd_rn(
+                        __fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), gv[j]), bv[j]);
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < R * n_embd; i += 64 * kGemvWaves) {
+            const int r = i / n_embd, k = i - r * n_embd;
+            const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
+                                          : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
+            hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
+        }
     }
     constexpr int64_t kBB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
     const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
@@ -535,41 +602,42 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     }
 }
 
-template <int WT, int RMAX, int LANES>
+template <int WT, int RMAX, int LANES, bool NORM>
 hipError_t launch_gemv_l(const void* W, const float* bias, const float* hidden0,
                          const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                          int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                         hipStream_t stream, int gelu) {
+                         hipStream_t stream, int gelu, const GemvNorm& nm) {
     const int R = hidden1 ? 2 * n_rows : n_rows;
     const size_t lds = (size_t)R * gemv_row_words(n_embd) * 4;
     constexpr int kRowsPerPass = 64 / LANES * kGemvWaves;
     const unsigned grid = (unsigned)((n_vocab + kRowsPerPass - 1) / kRowsPerPass);
-    hipLaunchKernelGGL((head_gemv<WT, RMAX, LANES>), dim3(grid), dim3(64 * kGemvWaves), lds,
-                       stream, W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out, n_rows,
-                       n_vocab, n_embd, gelu);
+    hipLaunchKernelGGL((head_gemv<WT, RMAX, LANES, NORM>), dim3(grid), dim3(64 * kGemvWaves),
+                       lds, stream, W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
+                       n_rows, n_vocab, n_embd, gelu, nm);
     return hipGetLastError();
 }
 
 // Lanes per vocab row: 16, doubled (to 64 at most) while the grid would hold
 // fewer than 256 workgroups and every lane keeps a block (narrow outputs: the
 // T3 layers' products at one stream).
-template <int WT, int RMAX>
+template <int WT, int RMAX, bool NORM = false>
 hipError_t launch_gemv(const void* W, const float* bias, const float* hidden0, const float* hidden1,
                        int64_t ld_hidden, float* out0, float* out1, int64_t ld_out, int32_t n_rows,
-                       int32_t n_vocab, int32_t n_embd, hipStream_t stream, int gelu) {
+                       int32_t n_vocab, int32_t n_embd, hipStream_t stream, int gelu,
+                       const GemvNorm& nm = GemvNorm{}) {
     const int nball = n_embd / 32;
     int lanes = 16;
     while (lanes < 64 && (n_vocab + 64 / lanes * kGemvWaves - 1) / (64 / lanes * kGemvWaves) < 256 &&
            nball >= 2 * lanes)
         lanes *= 2;
     if (lanes == 64)
-        return launch_gemv_l<WT, RMAX, 64>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
-                                           n_rows, n_vocab, n_embd, stream, gelu);
+        return launch_gemv_l<WT, RMAX, 64, NORM>(W, bias, hidden0, hidden1, ld_hidden, out0, out1,
+                                                 ld_out, n_rows, n_vocab, n_embd, stream, gelu, nm);
     if (lanes == 32)
-        return launch_gemv_l<WT, RMAX, 32>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
-                                           n_rows, n_vocab, n_embd, stream, gelu);
-    return launch_gemv_l<WT, RMAX, 16>(W, bias, hidden0, hidden1, ld_hidden, out0, out1, ld_out,
-                                       n_rows, n_vocab, n_embd, stream, gelu);
+        return launch_gemv_l<WT, RMAX, 32, NORM>(W, bias, hidden0, hidden1, ld_hidden, out0, out1,
+                                                 ld_out, n_rows, n_vocab, n_embd, stream, gelu, nm);
+    return launch_gemv_l<WT, RMAX, 16, NORM>(W, bias, hidden0, hidden1, ld_hidden, out0, out1,
+                                             ld_out, n_rows, n_vocab, n_embd, stream, gelu, nm);
 }
 
 template <int WT>
@@ -729,6 +797,31 @@ hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias,
         reinterpret_cast<const float*>(static_cast<const char*>(scratch) + split_inv_offset(R, n_embd));
     return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, nullptr, ld_out, n_rows,
                          n_vocab, n_embd, stream, kz, gelu_out ? 1 : 0);
+}
+
+hipError_t launch_head_gemv_norm(const void* W, int32_t wtype, const float* bias,
+                                 const GemvNorm& nm, float* out, int64_t ld_out, int32_t n_rows,
+                                 int32_t n_vocab, int32_t n_embd, hipStream_t stream, bool gelu) {
+    if (n_rows < 1 || n_rows > 2 || n_embd % (64 * kGemvWaves) != 0 ||
+        n_embd > 16 * 64 * kGemvWaves || !head_uses_gemv(n_rows, false, n_embd))
+        return hipErrorInvalidValue;
+    const int g = gelu ? 1 : 0;
+    switch (wtype) {
+        case CBX_WTYPE_F16:
+            return launch_gemv<CBX_WTYPE_F16, 2, true>(W, bias, nullptr, nullptr, n_embd, out,
+                                                       nullptr, ld_out, n_rows, n_vocab, n_embd,
+                                                       stream, g, nm);
+        case CBX_WTYPE_Q4_0:
+            return launch_gemv<CBX_WTYPE_Q4_0, 2, true>(W, bias, nullptr, nullptr, n_embd, out,
+                                                        nullptr, ld_out, n_rows, n_vocab, n_embd,
+                                                        stream, g, nm);
+        case CBX_WTYPE_Q8_0:
+            return launch_gemv<CBX_WTYPE_Q8_0, 2, true>(W, bias, nullptr, nullptr, n_embd, out,
+                                                        nullptr, ld_out, n_rows, n_vocab, n_embd,
+                                                        stream, g, nm);
+        default:
+            return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace cbx

@@ -135,6 +135,26 @@ hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias,
                                 int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
                                 const void* scratch, hipStream_t stream, int kz,
                                 bool gelu_out);
+
+// The T3 layer's residual add and layer norm folded into the mat-vec product
+// that consumes them (1 or 2 rows of n_embd, a multiple of 256, at most
+// 4096): per row r, x_out[r] = x_in[r] + y[r], and the product's input row is
+// LN(x_out[r]) * g + b, with the same operations in the same order as the
+// separate norm kernel; a row with act[r] == 0 gets a zero input and
+// x_out[r] = x_in[r].  Workgroup 0 stores x_out (x_in is only read, so the
+// two must differ).
+struct GemvNorm {
+    const float* x_in;
+    float* x_out;
+    const float* y;
+    const float* g;
+    const float* b;
+    const int32_t* act;
+    float eps;
+};
+hipError_t launch_head_gemv_norm(const void* W, int32_t wtype, const float* bias,
+                                 const GemvNorm& nm, float* out, int64_t ld_out, int32_t n_rows,
+                                 int32_t n_vocab, int32_t n_embd, hipStream_t stream, bool gelu);
 hipError_t launch_head(const void* W, int32_t wtype, const float* bias, const float* hidden0,
                        const float* hidden1, int64_t ld_hidden, float* out0, float* out1,
                        int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,

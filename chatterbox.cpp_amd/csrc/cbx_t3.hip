@@ -552,12 +552,33 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
 
     const int kz_a = min(head_k_split(n_rows, n, n), kMaxKSplit);
     const int kz_f = min(head_k_split(n_rows, n, 4 * n), kMaxKSplit);
+    // one or two streams: the residual adds and norms between the layer's
+    // products run inside the mat-vec that consumes them (c_fc, and the next
+    // layer's c_attn), the residual rows alternating between x and y's
+    // second slab (the mat-vec products take no K split)
+    const bool fold = !mc && n_rows <= 2 && kz_a == 1 && kz_f == 1;
+    float* xcur = x;
+    float* const xalt = y + row;
+    GemvNorm gn{};
+    gn.y = y;
+    gn.act = act;
+    gn.eps = m.eps;
     for (int l = 0; l < m.n_layer; ++l) {
         const cbx_t3_layer& L = m.layers[l];
-        e = mc ? launch_head_presplit(L.attn_w, m.wtype, L.attn_b, qkv, 3 * n, n_rows, 3 * n, n,
-                                      split, st, 1, false)
-               : launch_head(L.attn_w, m.wtype, L.attn_b, u, nullptr, n, qkv, nullptr, 3 * n,
-                             n_rows, 3 * n, n, split, st);
+        if (mc) {
+            e = launch_head_presplit(L.attn_w, m.wtype, L.attn_b, qkv, 3 * n, n_rows, 3 * n, n,
+                                     split, st, 1, false);
+        } else if (fold && l > 0) {  // the previous layer's residual + this ln_1
+            gn.x_in = xcur;
+            gn.x_out = xcur = xcur == x ? xalt : x;
+            gn.g = L.ln_1_g;
+            gn.b = L.ln_1_b;
+            e = launch_head_gemv_norm(L.attn_w, m.wtype, L.attn_b, gn, qkv, 3 * n, n_rows, 3 * n,
+                                      n, st, false);
+        } else {
+            e = launch_head(L.attn_w, m.wtype, L.attn_b, u, nullptr, n, qkv, nullptr, 3 * n,
+                            n_rows, 3 * n, n, split, st);
+        }
         if (e != hipSuccess) return e;
         aa.layer = l;
         if (prefill) {
@@ -586,7 +607,7 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         NormArgs nb{};
         nb.n_embd = n;
         nb.eps = m.eps;
-        nb.x = x;
+        nb.x = xcur;
         nb.y = y;
         nb.ny = kz_a;
         nb.ystride = (int64_t)row;
@@ -596,21 +617,32 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         nb.out = u;
         nb.parts = mc ? sparts : nullptr;
         nb.inv = sinv;
-        if ((e = launch_norm(nb, n_rows, st)) != hipSuccess) return e;
         // gelu applied as the mlp rows are stored
-        e = mc ? launch_head_presplit(L.fc_w, m.wtype, L.fc_b, f, 4 * n, n_rows, 4 * n, n, split,
-                                      st, 1, true)
-               : launch_head_k(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n, n_rows,
-                               4 * n, n, split, st, 1, true);
+        if (fold) {  // the residual + ln_2 inside c_fc
+            gn.x_in = xcur;
+            gn.x_out = xcur = xcur == x ? xalt : x;
+            gn.g = L.ln_2_g;
+            gn.b = L.ln_2_b;
+            e = launch_head_gemv_norm(L.fc_w, m.wtype, L.fc_b, gn, f, 4 * n, n_rows, 4 * n, n, st,
+                                      true);
+        } else {
+            if ((e = launch_norm(nb, n_rows, st)) != hipSuccess) return e;
+            e = mc ? launch_head_presplit(L.fc_w, m.wtype, L.fc_b, f, 4 * n, n_rows, 4 * n, n,
+                                          split, st, 1, true)
+                   : launch_head_k(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n,
+                                   n_rows, 4 * n, n, split, st, 1, true);
+        }
         if (e != hipSuccess) return e;
         e = launch_head_k(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
                           n_rows, n, 4 * n, split, st, kz_f, false);
         if (e != hipSuccess) return e;
         // the residual, then the next layer's ln_1 or, after the last, ln_f
         // into `hidden` and the positions advanced
-        NormArgs nc = nb;
-        nc.ny = kz_f;
         const bool last = l + 1 == m.n_layer;
+        if (fold && !last) continue;  // inside the next layer's c_attn
+        NormArgs nc = nb;
+        nc.x = xcur;
+        nc.ny = kz_f;
         nc.g = last ? m.ln_f_g : m.layers[l + 1].ln_1_g;
         nc.b = last ? m.ln_f_b : m.layers[l + 1].ln_1_b;
         nc.out = last ? hidden : u;

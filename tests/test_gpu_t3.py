@@ -89,14 +89,15 @@ def close(got, want):
     return np.all(err <= TOL_ABS + TOL_REL * np.abs(want)), float(err.max())
 
 
-@pytest.mark.parametrize("B", [20, 5])
+@pytest.mark.parametrize("B", [20, 5, 2, 1])
 @pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
 def test_t3_step_matches_oracle(cbx, torch_cuda, wtype, B):
     """B streams, 4 steps with per-stream ids; in step 2 every third stream
     sits out (state not running), so positions differ afterwards.  Each step's
     ln_f rows, every stream's position and the skipped rows' zeros match the
     oracle.  B = 20 runs the products on the matrix cores, B = 5 on the
-    mat-vec (fc_proj's 4096-wide rows on the matrix cores)."""
+    mat-vec; B = 2 and 1 fold the residual adds and norms between a layer's
+    products into the mat-vec that consumes them."""
     torch = torch_cuda
     mod, s = cbx
     dm, rm = model(torch, mod, wtype)
@@ -125,6 +126,37 @@ def test_t3_step_matches_oracle(cbx, torch_cuda, wtype, B):
         assert np.all(got[state != 0] == 0.0)
         assert np.array_equal(pos_d.cpu().numpy(), pos_r)
     say(f"  max |err| {worst:.3g}")
+
+
+def test_t3_folded_norms_match_separate(cbx, torch_cuda):
+    """Two streams (norms folded into the mat-vec products) give bit for bit
+    the rows the same two streams give beside a third (separate norm
+    kernels): the folded norm repeats the norm kernel's operations in its
+    order, and every kernel's row results are independent of the other
+    rows.  Step 1 has stream 1 sitting out (its residual carried through)."""
+    torch = torch_cuda
+    mod, s = cbx
+    dm, _ = model(torch, mod, O.WTYPE_Q4_0)
+    rng = np.random.default_rng(0x7320)
+    outs = {}
+    toks = rng.integers(0, V, (3, 3)).astype(np.int32)
+    for B in (2, 3):
+        kd = torch.zeros((B, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
+        vd = torch.zeros_like(kd)
+        pos = torch.zeros(B, dtype=torch.int32, device="cuda")
+        hid = torch.zeros((B, N), dtype=torch.float32, device="cuda")
+        rows = []
+        for t in range(3):
+            state = np.zeros(B, np.int32)
+            if t == 1:
+                state[1] = 1
+            say(f"t3 folded B={B} t={t}")
+            s.t3_step(dm, pos, kd, vd, hid, tokens=torch.from_numpy(toks[t, :B].copy()).cuda(),
+                      state=torch.from_numpy(state).cuda())
+            torch.cuda.synchronize()
+            rows.append(hid.cpu().numpy()[:2].copy())
+        outs[B] = np.stack(rows)
+    assert np.array_equal(outs[2].view(np.uint32), outs[3].view(np.uint32))
 
 
 def test_t3_inputs_then_tokens(cbx, torch_cuda):
