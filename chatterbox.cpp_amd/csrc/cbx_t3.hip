@@ -28,7 +28,7 @@
 // stores its outputs.  The kernels here are the row-wise rest: the
 // embedding, the residual add fused with the next layer norm, and the
 // attention with its cache append (a workgroup of 4 waves per stream and
-// head, the positions split over more workgroups when there are few).
+// head, 16 when there are few).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -228,12 +228,7 @@ struct AttnArgs {
     int32_t appended;      // the rows' k, v already stored (t3_kv_append)
     float* out;            // [n_rows][n_embd]
     float scale;           // 1 / sqrt(64)
-    float* part;           // gridDim.z > 1: per (row, head, z) max, sum, 64 sums
 };
-
-// Partial results per (row, head, split): the run's max, its sum of expf
-// terms and its 64 weighted sums.
-constexpr int kAttnPart = 2 + 64;
 
 // Prefill: every row's k and v stored at its slot and position before any
 // row attends, so rows of one stream in one call see each other causally.
@@ -249,16 +244,16 @@ __global__ __launch_bounds__(kHeadDim) void t3_kv_append(AttnArgs a) {
     a.vc[base + lane] = qr[2 * n + lane];
 }
 
-// One workgroup of kAttnWaves waves per (stream, head) (per (stream, head,
-// split) when the positions are split over several workgroups).  Wave 0
-// stores the new k and v at the stream's position (and keeps them in LDS:
-// that position is never read back from memory).  The positions are cut into
+// One workgroup of kAttnWaves waves per (stream, head).  Wave 0 stores the
+// new k and v at the stream's position (and keeps them in LDS: that position
+// is never read back from memory).  The positions are cut into
 // kAttnWaves runs, one per wave; a wave's lanes take 16 per cache row, 4 rows
 // per load instruction, kAttnBatch rows per lane in flight, and go over the
 // run once with a running softmax (max, sum, weighted v sums, rescaled as the
 // max grows); the runs of the 4 row groups of a wave and of the waves are
 // merged by the same rescaling in a fixed order.  Decode steps run 4 waves x
-// 6 rows (every workgroup resident at once), the prompt pass 2 waves x 8 rows
+// 6 rows (every workgroup resident at once; 16 waves when rows x heads are
+// under 256, see t3_attn_wide), the prompt pass 2 waves x 8 rows
 // (many more workgroups: smaller ones keep more of them resident); measured
 // at 64 streams 1.89 -> 1.85 ms per step against 4 x 8, and the prompt of
 // 64 x 256 positions 93.8 -> 82.2 ms.
@@ -278,14 +273,13 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     }
     const int pos = a.positions[r];
     const int slot = a.slots ? a.slots[r] : r;
-    const int z = blockIdx.z, S = gridDim.z;
     const float* qr = a.qkv + (int64_t)r * 3 * n + h * kHeadDim;
     const int64_t base = (((int64_t)slot * a.n_layer + a.layer) * a.n_head + h) * a.n_ctx * kHeadDim;
     float* kc = a.kc + base;
     float* vc = a.vc + base;
     if (w == 0) {
         const float kn = qr[n + lane], vn = qr[2 * n + lane];
-        if (!a.appended && z == 0) {
+        if (!a.appended) {
             kc[(int64_t)pos * kHeadDim + lane] = kn;
             vc[(int64_t)pos * kHeadDim + lane] = vn;
         }
@@ -296,10 +290,10 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     // dimensions 4e .. 4e + 3: a wave reads 4 rows of k per instruction
     const int sub = lane >> 4, e4 = 4 * (lane & 15);
     const float4 q4 = *reinterpret_cast<const float4*>(qr + e4);
-    // split z of S takes positions [L z / S, L (z + 1) / S), in 4 runs
-    const int L = pos + 1, z0 = (int)((int64_t)L * z / S), z1 = (int)((int64_t)L * (z + 1) / S);
-    const int run = (z1 - z0 + kAttnWaves - 1) / kAttnWaves;
-    const int c0 = min(z0 + w * run, z1), c1 = min(c0 + run, z1);
+    // positions [0, L) in kAttnWaves runs
+    const int L = pos + 1;
+    const int run = (L + kAttnWaves - 1) / kAttnWaves;
+    const int c0 = min(w * run, L), c1 = min(c0 + run, L);
     __syncthreads();
     // Each lane keeps, over the positions of its 16-lane group (position order),
     // the running max m of the scores, the sum s of expf(score - m) and the
@@ -391,41 +385,8 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
             st = __fadd_rn(st, __fmul_rn(red[kAttnWaves + q], f));
             at = __fadd_rn(at, __fmul_rn(part[q][lane], f));
         }
-        if (S == 1) {
-            orow[lane] = __fdiv_rn(at, st);
-        } else {
-            float* pp = a.part + (((int64_t)r * a.n_head + h) * S + z) * kAttnPart;
-            if (lane == 0) {
-                pp[0] = M;
-                pp[1] = st;
-            }
-            pp[2 + lane] = at;
-        }
+        orow[lane] = __fdiv_rn(at, st);
     }
-}
-
-// The S splits of each (row, head) merged in split order: with M the largest
-// split max, out = sum_z acc_z e^(m_z - M) / sum_z s_z e^(m_z - M) (a split
-// with no positions has m = -inf and adds nothing).
-__global__ __launch_bounds__(kHeadDim) void t3_attn_combine(AttnArgs a, int S) {
-    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const int n = a.n_head * kHeadDim;
-    float* orow = a.out + (int64_t)r * n + h * kHeadDim;
-    if (!a.act[r]) {
-        orow[lane] = 0.0f;
-        return;
-    }
-    const float* pp = a.part + ((int64_t)r * a.n_head + h) * S * kAttnPart;
-    float M = -INFINITY;
-    for (int z = 0; z < S; ++z) M = fmaxf(M, pp[z * kAttnPart]);
-    float sum = 0.0f, acc = 0.0f;
-    for (int z = 0; z < S; ++z) {
-        const float m = pp[z * kAttnPart];
-        const float f = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, M));
-        sum = __fadd_rn(sum, __fmul_rn(pp[z * kAttnPart + 1], f));
-        acc = __fadd_rn(acc, __fmul_rn(pp[z * kAttnPart + 2 + lane], f));
-    }
-    orow[lane] = __fdiv_rn(acc, sum);
 }
 
 template <int EPT>
@@ -458,23 +419,21 @@ bool t3_shape_ok(int32_t n_embd, int32_t n_head) {
 
 size_t t3_attn_lds(int32_t) { return 0; }  // one pass: no per-position LDS
 
+// Decode steps whose grid of rows x heads is small run 16 waves per (row,
+// head) instead of 4, so the few workgroups still spread each stream's
+// positions over many waves (measured at one stream, 16 heads: 0.91 ->
+// 0.86 ms per step against 4 waves with the positions split over 16
+// workgroups and merged by a second kernel).
+bool t3_attn_wide(int32_t n_rows, int32_t n_head) { return (int64_t)n_rows * n_head < 256; }
+
 // Workspace of a step: x, u, a [n_rows][n_embd], y [kMaxKSplit][n_rows][n_embd],
 // qkv [n_rows][3 n_embd], f [n_rows][4 n_embd], act [n_rows], then the matrix
 // products' split activations (the widest input, 4 n_embd).
-// Positions of a (row, head) split over this many workgroups when the grid
-// of rows x heads is small (the combine kernel merges them).
-int t3_attn_splits(int32_t n_rows, int32_t n_head) {
-    int S = 1;
-    while (S < 16 && (int64_t)n_rows * n_head * S < 256) S *= 2;
-    return S;
-}
 
 size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd) {
     const size_t row = (size_t)n_rows * n_embd * 4;
-    const int n_head = n_embd / kHeadDim, S = t3_attn_splits(n_rows, n_head);
-    const size_t parts = S > 1 ? ((size_t)n_rows * n_head * S * kAttnPart * 4 + 255) / 256 * 256 : 0;
     const size_t body = (3 + kMaxKSplit) * row + 3 * row + 4 * row +
-                        ((size_t)n_rows * 4 + 255) / 256 * 256 + parts;
+                        ((size_t)n_rows * 4 + 255) / 256 * 256;
     return body + head_scratch_bytes(n_rows, false, 4 * n_embd);
 }
 
@@ -494,14 +453,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     float* qkv = y + kMaxKSplit * row;
     float* f = qkv + 3 * row;
     int32_t* act = reinterpret_cast<int32_t*>(f + 4 * row);
-    // attention splits (decode steps with few rows x heads)
-    const int S = prefill ? 1 : t3_attn_splits(n_rows, m.n_head);
-    float* apart = reinterpret_cast<float*>(reinterpret_cast<char*>(act) +
-                                            ((size_t)n_rows * 4 + 255) / 256 * 256);
-    const int S_ws = t3_attn_splits(n_rows, m.n_head);
-    const size_t parts =
-        S_ws > 1 ? ((size_t)n_rows * m.n_head * S_ws * kAttnPart * 4 + 255) / 256 * 256 : 0;
-    void* split = reinterpret_cast<char*>(apart) + parts;
+    const bool wide = !prefill && t3_attn_wide(n_rows, m.n_head);
+    void* split = reinterpret_cast<char*>(act) + ((size_t)n_rows * 4 + 255) / 256 * 256;
 
     NormArgs na{};
     na.n_embd = n;
@@ -547,7 +500,6 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     aa.appended = prefill ? 1 : 0;
     aa.out = att;
     aa.scale = 0.125f;  // 1 / sqrt(64)
-    aa.part = apart;
     const size_t lds = t3_attn_lds(c.n_ctx);
 
     const int kz_a = min(head_k_split(n_rows, n, n), kMaxKSplit);
@@ -589,16 +541,13 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         if (prefill)
             hipLaunchKernelGGL((t3_attn<8, 2>), dim3((unsigned)n_rows, (unsigned)m.n_head),
                                dim3(2 * kHeadDim), lds, st, aa);
+        else if (wide)
+            hipLaunchKernelGGL((t3_attn<6, 16>), dim3((unsigned)n_rows, (unsigned)m.n_head),
+                               dim3(16 * kHeadDim), lds, st, aa);
         else
-            hipLaunchKernelGGL((t3_attn<6, 4>),
-                               dim3((unsigned)n_rows, (unsigned)m.n_head, (unsigned)S),
+            hipLaunchKernelGGL((t3_attn<6, 4>), dim3((unsigned)n_rows, (unsigned)m.n_head),
                                dim3(4 * kHeadDim), lds, st, aa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        if (S > 1) {
-            hipLaunchKernelGGL(t3_attn_combine, dim3((unsigned)n_rows, (unsigned)m.n_head),
-                               dim3(kHeadDim), 0, st, aa, S);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
         // the two products the residual adds take a K split when their grid
         // is narrow (the norm adds the slabs)
         e = launch_head_k(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
