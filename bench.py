@@ -278,13 +278,55 @@ def q4_0_rows(torch, rows, n_in, dev, g):
     return b.reshape(-1)
 
 
-def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps):
+def t3_parity(torch, O, sampler, model, layers, wpe, emb, lnf, kc, vc, pos, hid, check, V):
+    """One more cbx_t3_step at the timed shape (every stream at the position
+    the timed steps left it) against the binary64 oracle for the streams in
+    `check`: their caches copied as the device holds them, the matrices
+    dequantized from the device's Q4_0 bytes.  Returns the largest error of
+    ln_f's rows and whether every row is within 5e-5 + 5e-5 |ref|."""
+    from oracle import cbx_t3_oracle as T3
+    n = T3_EMBD
+    B = pos.numel()
+    g = torch.Generator(device=kc.device)
+    g.manual_seed(0x7334)
+    toks = torch.randint(0, V, (B,), generator=g, device=kc.device, dtype=torch.int32)
+    p = pos.cpu().numpy().astype(np.int64)
+    assert np.all(p == p[0]) and p[0] + 1 < kc.shape[-2]
+    sampler.t3_step(model, pos, kc, vc, hid, tokens=toks)
+    torch.cuda.synchronize()
+    got = hid.cpu().numpy()[check]
+    deq = lambda w, o, i: O.dequantize(w.cpu().numpy().reshape(o, -1), O.WTYPE_Q4_0, i)
+    host = lambda t: t.cpu().numpy()
+    ref_layers = [dict(ln_1_g=host(L["ln_1_g"]), ln_1_b=host(L["ln_1_b"]),
+                       attn_w=deq(L["attn_w"], 3 * n, n), attn_b=host(L["attn_b"]),
+                       attn_proj_w=deq(L["attn_proj_w"], n, n),
+                       attn_proj_b=host(L["attn_proj_b"]), ln_2_g=host(L["ln_2_g"]),
+                       ln_2_b=host(L["ln_2_b"]), fc_w=deq(L["fc_w"], 4 * n, n),
+                       fc_b=host(L["fc_b"]), fc_proj_w=deq(L["fc_proj_w"], n, 4 * n),
+                       fc_proj_b=host(L["fc_proj_b"])) for L in layers]
+    rm = T3.Model(ref_layers, host(wpe), host(emb), host(lnf[0]), host(lnf[1]), 1e-5, T3_HEAD)
+    L = int(p[0]) + 1
+    # the device caches after the step: position p[0] holds the step's own k
+    # and v, which the oracle writes again from its own products
+    kr = T3.StreamCaches([host(kc[r, :, :, :L]) for r in check])
+    vr = T3.StreamCaches([host(vc[r, :, :, :L]) for r in check])
+    want = T3.step(rm, host(toks)[check], p[check].copy(), kr, vr)
+    err = np.abs(got.astype(np.float64) - want)
+    ok = bool(np.all(err <= 5e-5 + 5e-5 * np.abs(want)))
+    return {"streams_checked": [int(r) for r in check], "position": int(p[0]),
+            "max_abs_err": float(err.max()), "tol": "5e-5 + 5e-5 |ref| on ln_f rows",
+            "ok": ok}
+
+
+def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps, O=None):
     """The T3 decode step (cbx_t3_step) of B streams on the Turbo shape with
     random Q4_0 matrices, every stream at position pos0 (caches of n_ctx
     positions), alone and followed by the fused Q4_0 speech_head and the
     sampler (cbx_head_decode_step): the whole device decode step.  Bytes per
     step: the layer matrices once, every stream's K and V read over its
-    positions and the new row written."""
+    positions and the new row written.  With the oracle (O), one more step at
+    the timed shape is checked against it (t3_parity)."""
+    assert pos0 + steps + 1 < n_ctx, "every timed step and the checked one fit the caches"
     g = torch.Generator(device=dev)
     g.manual_seed(0x7333)
     n = T3_EMBD
@@ -329,6 +371,14 @@ def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps):
                 sampler.decode_step(logits, prm, tok_out, dec, head=head, seed=7, step0=i,
                                     stop_token=-1)
         res[name] = timed(torch, stream, one, steps, warm=1)
+        # every stream stepped at every timed call (none ran out of cache)
+        assert np.all(pos.cpu().numpy() == pos0 + steps)
+    parity = None
+    if O is not None:
+        check = [0, B - 1] if B > 1 else [0]
+        parity = t3_parity(torch, O, sampler, model, layers, wpe, emb, (model._keep[4],
+                                                                         model._keep[5]),
+                           kc, vc, pos, hid, check, V)
     # the prompt pass: every stream's first pos0 positions in one call
     P = min(pos0, n_ctx)
     slots = torch.arange(B, device=dev, dtype=torch.int32).repeat_interleave(P)
@@ -353,6 +403,7 @@ def t3_bench(torch, mod, sampler, dev, B, pos0, n_ctx, steps):
             "tokens_per_s": round(B / (res["t3_head_sampler"] / 1e3), 1),
             "algorithmic_bytes_per_step": int(bytes_step),
             "hbm_frac_t3": round(bytes_step / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 5),
+            "parity_vs_oracle": parity,
             "prefill": {"rows": B * P, "positions_per_stream": P,
                         "ms": round(res["prefill"], 4),
                         "positions_per_s": round(B * P / (res["prefill"] / 1e3), 1)}}
@@ -717,14 +768,16 @@ def main():
                                    args.decode_steps, philox_seed)
 
     # the T3 transformer's decode step feeding the head and the sampler
-    t3 = None
-    if args.t3_steps > 0:
-        t3 = {"b64": t3_bench(torch, mod, sampler, dev, 64, 256, 512, args.t3_steps),
-              "b1": t3_bench(torch, mod, sampler, dev, 1, 256, 512, args.t3_steps)}
-
     O = None
     if not args.no_cpu:
         import oracle_lib as O
+
+    t3 = None
+    if args.t3_steps > 0:
+        # caches hold every timed position and the checked step after them
+        n_ctx = max(512, 256 + args.t3_steps + 2)
+        t3 = {"b64": t3_bench(torch, mod, sampler, dev, 64, 256, n_ctx, args.t3_steps, O),
+              "b1": t3_bench(torch, mod, sampler, dev, 1, 256, n_ctx, args.t3_steps, O)}
 
     configs = None
     if not args.no_configs:

@@ -537,11 +537,40 @@ class Sampler:
         m._keep = (arr, layers, wpe, speech_emb, ln_f_g, ln_f_b)
         return m
 
+    @staticmethod
+    def _check_t3(fn, model, n_rows, n_slots, k_cache, v_cache, hidden, **rows):
+        """The C ABI takes the caches and rows as raw addresses: a cache built
+        for another layer or head count would be written past its end, so
+        the tensors' shapes, dtypes and layout are checked here first."""
+        import torch
+        want = (n_slots, model.n_layer, model.n_head, k_cache.shape[-2] if k_cache.dim() else 0, 64)
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != want:
+                raise ValueError("%s: %s must be contiguous float32 of shape %s, got %s %s%s" % (
+                    fn, name, want, t.dtype, tuple(t.shape),
+                    "" if t.is_contiguous() else " (not contiguous)"))
+        if hidden.dtype != torch.float32 or not hidden.is_contiguous() or \
+                tuple(hidden.shape) != (n_rows, model.n_embd):
+            raise ValueError("%s: hidden must be contiguous float32 [%d, %d], got %s %s" % (
+                fn, n_rows, model.n_embd, hidden.dtype, tuple(hidden.shape)))
+        for name, (t, dt, shape) in rows.items():
+            if t is None:
+                continue
+            if t.dtype != dt or not t.is_contiguous() or tuple(t.shape) != shape:
+                raise ValueError("%s: %s must be contiguous %s of shape %s, got %s %s" % (
+                    fn, name, dt, shape, t.dtype, tuple(t.shape)))
+
     def t3_step(self, model, positions, k_cache, v_cache, hidden, *, tokens=None, inputs=None,
                 state=None, stream=None):
         """cbx_t3_step: one decode step of positions.numel() streams; caches
         [n_rows, n_layer, n_head, n_ctx, 64] float32, hidden [n_rows, n_embd]
         out; positions (int32) advance by one for the streams that step."""
+        import torch
+        n = positions.numel()
+        self._check_t3("t3_step", model, n, n, k_cache, v_cache, hidden,
+                       positions=(positions, torch.int32, (n,)),
+                       tokens=(tokens, torch.int32, (n,)), state=(state, torch.int32, (n,)),
+                       inputs=(inputs, torch.float32, (n, model.n_embd)))
         c = T3Cache()
         c.k = k_cache.data_ptr()
         c.v = v_cache.data_ptr()
@@ -556,6 +585,13 @@ class Sampler:
         """cbx_t3_prefill: rows of (slot, position) in one call (device int32
         slots and positions [n_rows]); caches [n_slots, n_layer, n_head,
         n_ctx, 64]; positions are only read."""
+        import torch
+        n = slots.numel()
+        self._check_t3("t3_prefill", model, n, k_cache.shape[0] if k_cache.dim() else 0, k_cache,
+                       v_cache, hidden, slots=(slots, torch.int32, (n,)),
+                       positions=(positions, torch.int32, (n,)),
+                       tokens=(tokens, torch.int32, (n,)),
+                       inputs=(inputs, torch.float32, (n, model.n_embd)))
         c = T3Cache()
         c.k = k_cache.data_ptr()
         c.v = v_cache.data_ptr()

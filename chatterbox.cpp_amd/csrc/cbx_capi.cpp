@@ -465,7 +465,9 @@ int cbx_sample_batch_static(cbx_sampler* s, const cbx_batch* b, void* stream) {
     if (rc != CBX_OK) return rc;
     const int32_t full = pick_cap(s, b->n_vocab, 0);
     const int64_t rows = (int64_t)b->n_rows * b->n_steps;
-    if (a.cap < full && rows > cbx::kRedoMax)
+    // calls of at most latency_rows row-steps run at full capacity (no redo
+    // list is used), whatever their survivor bound
+    if (rows > s->latency_rows && a.cap < full && rows > cbx::kRedoMax)
         return fail(CBX_ERR_INVALID,
                     "cbx_sample_batch_static: %lld row-steps with max_survivors %d: its redo list "
                     "holds %d rows (at most %d row-steps per call, or max_survivors 0)",

@@ -13,7 +13,10 @@ Pinned (tests/test_t3_oracle.py) against torch's own routines on the CPU:
 layer_norm, gelu(approximate="tanh") and scaled_dot_product_attention, and the
 whole step, run position by position, against a full-sequence causal forward
 written with torch's functional ops (the prompt graph's form, main.cpp:
-490-497 mask).
+490-497 mask).  `prefill` (one stream's prompt rows in one pass) is pinned
+against that torch forward from position 0 and against the position-by-
+position decode when it continues a cache; `StreamCaches` (ragged fp32
+per-stream caches) against the dense binary64 cache.
 """
 import numpy as np
 
@@ -95,3 +98,54 @@ def step(m, tokens, positions, kc, vc, inputs=None, active=None):
     for r in np.nonzero(active)[0]:
         positions[r] += 1
     return out
+
+
+class StreamCaches:
+    """Per-stream caches of different lengths, indexed like new_cache's
+    arrays (c[r, layer, head, pos], c[r, layer, head, :p + 1]): stream r's
+    array is arrays[r] [n_layer][n_head][n_r][64], any float dtype (float32
+    stores what the reference's fp32 cache holds).  For long contexts where
+    one dense [n_rows][...][n_ctx][64] binary64 array would not fit."""
+
+    def __init__(self, arrays):
+        self.arrays = list(arrays)
+
+    def __getitem__(self, key):
+        return self.arrays[key[0]][tuple(key[1:])]
+
+    def __setitem__(self, key, value):
+        self.arrays[key[0]][tuple(key[1:])] = value
+
+
+def prefill(m, inputs, kc, vc, slot, p0):
+    """One stream's prompt rows at positions p0 .. p0 + T - 1 in one pass (the
+    prompt graph, main.cpp:643-689 up to ln_f, with n_past = p0): inputs
+    [T][n] embedded rows; every row's k and v stored in cache slot `slot`
+    before any row attends, row t attending over [0, p0 + t] (the causal mask
+    of main.cpp:490-497; positions below p0 are read from the cache as they
+    stand).  Returns the rows' ln_f outputs [T][n]."""
+    n, H = m.n_embd, m.n_head
+    x = np.asarray(inputs, np.float64).copy()
+    T = x.shape[0]
+    end = p0 + T
+    # row t may not see position j > p0 + t
+    mask = np.arange(end)[None, :] > (p0 + np.arange(T))[:, None]
+    for li, L in enumerate(m.layers):
+        u = layer_norm(x, L["ln_1_g"], L["ln_1_b"], m.eps)
+        qkv = u @ L["attn_w"].T + L["attn_b"]
+        att = np.zeros((T, n))
+        for h in range(H):
+            sl = slice(h * HEAD_DIM, (h + 1) * HEAD_DIM)
+            kc[slot, li, h, p0:end] = qkv[:, n:][:, sl]
+            vc[slot, li, h, p0:end] = qkv[:, 2 * n:][:, sl]
+            K = np.asarray(kc[slot, li, h, :end], np.float64)
+            V = np.asarray(vc[slot, li, h, :end], np.float64)
+            s = qkv[:, sl] @ K.T / np.sqrt(HEAD_DIM)
+            s[mask] = -np.inf
+            w = np.exp(s - s.max(axis=1, keepdims=True))
+            att[:, sl] = (w / w.sum(axis=1, keepdims=True)) @ V
+        x = x + att @ L["attn_proj_w"].T + L["attn_proj_b"]
+        u = layer_norm(x, L["ln_2_g"], L["ln_2_b"], m.eps)
+        f = gelu(u @ L["fc_w"].T + L["fc_b"])
+        x = x + f @ L["fc_proj_w"].T + L["fc_proj_b"]
+    return layer_norm(x, m.ln_f_g, m.ln_f_b, m.eps)

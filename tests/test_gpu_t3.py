@@ -23,6 +23,8 @@ from oracle import cbx_t3_oracle as T3
 
 pytestmark = pytest.mark.gpu
 
+N_CTX_LONG = 4096  # caches of the reference's context scale (n_ctx 8196, n_predict 1000)
+
 N_LAYER, N, H, N_POS, V = 24, 1024, 16, 64, 6563
 TOL_ABS, TOL_REL = 5e-5, 5e-5
 
@@ -49,9 +51,24 @@ def cbx(torch_cuda):
 _MODELS = {}
 
 
-def model(torch, mod, wtype):
+def model(torch, mod, wtype, n_pos=N_POS):
     """Random Turbo-shaped weights in `wtype` (matrices N(0, 0.02)): the
-    device model and the oracle's binary64 copy of the same values."""
+    device model and the oracle's binary64 copy of the same values.  A model
+    with more positions (n_pos) shares the layers of the N_POS one and takes
+    its own wpe rows."""
+    if n_pos != N_POS:
+        key = (wtype, n_pos)
+        if key not in _MODELS:
+            dm0, rm0 = model(torch, mod, wtype)
+            rng = np.random.default_rng(0x7301 + n_pos)
+            wpe = (rng.standard_normal((n_pos, N)) * 0.1).astype(np.float32)
+            t = lambda a: torch.from_numpy(a).cuda()
+            layers = dm0._keep[1]
+            _, _, _, emb, gf, bf = dm0._keep
+            dm = mod.Sampler.t3_model(layers, t(wpe), emb, gf, bf, wtype=wtype, n_head=H)
+            rm = T3.Model(rm0.layers, wpe, rm0.speech_emb, rm0.ln_f_g, rm0.ln_f_b, 1e-5, H)
+            _MODELS[key] = (dm, rm)
+        return _MODELS[key]
     if wtype in _MODELS:
         return _MODELS[wtype]
     rng = np.random.default_rng(0x7300 + wtype)
@@ -266,14 +283,17 @@ def test_t3_rejects_bad_arguments(cbx, torch_cuda):
     toks = torch.zeros(2, dtype=torch.int32, device="cuda")
     hid = torch.zeros((2, N), dtype=torch.float32, device="cuda")
     kd = torch.zeros((2, N_LAYER, H, N_POS, 64), dtype=torch.float32, device="cuda")
-    big = torch.zeros((1, 1, 1, N_POS + 1, 64), dtype=torch.float32, device="cuda")
+    big = torch.zeros((2, N_LAYER, H, N_POS + 1, 64), dtype=torch.float32, device="cuda")
     with pytest.raises(mod.CbxError):  # n_ctx above the model's positions
         s.t3_step(dm, pos, big, big, hid, tokens=toks)
     n_head = dm.n_head
     dm.n_head = 8  # 128-wide heads
+    k8 = torch.zeros((2, N_LAYER, 8, N_POS, 64), dtype=torch.float32, device="cuda")
     with pytest.raises(mod.CbxError):
-        s.t3_step(dm, pos, kd, kd, hid, tokens=toks)
+        s.t3_step(dm, pos, k8, k8, hid, tokens=toks)
     dm.n_head = n_head
+    with pytest.raises(ValueError):  # a cache built for another head count
+        s.t3_step(dm, pos, k8, k8, hid, tokens=toks)
     with pytest.raises(mod.CbxError):  # neither ids nor input rows
         s.t3_step(dm, pos, kd, kd, hid)
     torch.cuda.synchronize()
@@ -360,3 +380,130 @@ def test_t3_prefill_then_decode(cbx, torch_cuda, lens):
         w = T3.step(rm, toks, pos_r, kr, vr)
         ok, err = close(hd.cpu().numpy(), w)
         assert ok, f"decode {t}: max err {err:.3g}"
+
+
+def planted_caches(torch, B, n_layer, n_ctx, seed):
+    """Device caches [B][n_layer][H][n_ctx][64] of seeded N(0, 0.5) values, as
+    if earlier positions had been decoded; every 97th position's k rows are
+    8x larger, so scores far above or below the rest turn up late in a
+    run and the running softmax has to rescale what it has summed."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    kd = torch.randn((B, n_layer, H, n_ctx, 64), generator=g, device="cuda") * 0.5
+    vd = torch.randn((B, n_layer, H, n_ctx, 64), generator=g, device="cuda") * 0.5
+    kd[:, :, :, 13::97] *= 8.0
+    return kd, vd
+
+
+def host_caches(kd, vd, lengths):
+    """The oracle's copy of each stream's first lengths[r] positions (fp32,
+    as the device holds them)."""
+    kr = T3.StreamCaches([kd[r, :, :, :L].cpu().numpy() for r, L in enumerate(lengths)])
+    vr = T3.StreamCaches([vd[r, :, :, :L].cpu().numpy() for r, L in enumerate(lengths)])
+    return kr, vr
+
+
+# Positions past which each attention variant runs more than one batch per
+# wave (so the running softmax rescales across batches and the batch loop's
+# clamped tail loads are used): t3_attn<6,4> (16 streams and more: 4 waves, 24
+# positions per wave per batch) past 96, t3_attn<6,16> (rows x heads under
+# 256: 16 waves) past 384; n_ctx - 1 is the last slot of the cache.
+LONG_POSITIONS = {
+    16: [0, 1, 95, 96, 97, 98, 191, 200, 385, 500, 777, 1000, 1500, 2047, 3001, N_CTX_LONG - 1],
+    5: [384, 385, 1000, 2500, 4000],
+    1: [N_CTX_LONG - 2],
+}
+
+
+@pytest.mark.parametrize("B", sorted(LONG_POSITIONS))
+def test_t3_step_long_context(cbx, torch_cuda, B):
+    """One cbx_t3_step per stream at positions up to n_ctx - 1 in caches of
+    4096 positions (24 layers, Q4_0), the positions before each stream's
+    planted, several positions per call; then a second step, where a stream
+    at n_ctx - 1 has run out of cache and sits out (zero row, position
+    unchanged).  16 streams run the 4-wave attention and the matrix cores,
+    5 the 16-wave attention and the mat-vec, 1 the 16-wave attention and the
+    mat-vec with folded norms."""
+    torch = torch_cuda
+    mod, s = cbx
+    dm, rm = model(torch, mod, O.WTYPE_Q4_0, n_pos=N_CTX_LONG)
+    P = np.array(LONG_POSITIONS[B], np.int64)
+    say(f"t3 long context B={B} positions {P.min()}..{P.max()}")
+    kd, vd = planted_caches(torch, B, N_LAYER, N_CTX_LONG, 0x7360 + B)
+    kr, vr = host_caches(kd, vd, np.minimum(P + 2, N_CTX_LONG))
+    pos_d = torch.from_numpy(P.astype(np.int32)).cuda()
+    pos_r = P.copy()
+    hid = torch.zeros((B, N), dtype=torch.float32, device="cuda")
+    rng = np.random.default_rng(0x7361 + B)
+    worst = 0.0
+    for t in range(2):
+        toks = rng.integers(0, V, B).astype(np.int32)
+        act = pos_r < N_CTX_LONG
+        say(f"  step {t}")
+        s.t3_step(dm, pos_d, kd, vd, hid, tokens=torch.from_numpy(toks).cuda())
+        torch.cuda.synchronize()
+        want = T3.step(rm, toks, pos_r, kr, vr, active=act)
+        got = hid.cpu().numpy()
+        ok, err = close(got, want)
+        worst = max(worst, err)
+        assert ok, f"step {t}: max err {err:.3g}"
+        assert np.all(got[~act] == 0.0)
+        assert np.array_equal(pos_d.cpu().numpy(), pos_r)
+    if B == 16:
+        assert (pos_r == N_CTX_LONG).sum() == 1
+    say(f"  max |err| {worst:.3g}")
+    del kd, vd
+    torch.cuda.empty_cache()
+
+
+def test_t3_prefill_long_then_decode(cbx, torch_cuda):
+    """The prompt pass at lengths where the 2-wave prompt attention runs
+    several batches per wave: stream 0's 320-position prompt from position
+    0, and stream 1's 130 rows continuing a planted 150-position cache (a
+    prompt fed in two calls), 450 rows shuffled in one cbx_t3_prefill call
+    (matrix cores), against the oracle's one-pass prompt; then two decode
+    steps of both streams (mat-vec with folded norms, 16-wave attention)."""
+    torch = torch_cuda
+    mod, s = cbx
+    n_ctx = 1024
+    dm, rm = model(torch, mod, O.WTYPE_Q4_0, n_pos=N_CTX_LONG)
+    rng = np.random.default_rng(0x7370)
+    kd, vd = planted_caches(torch, 2, N_LAYER, n_ctx, 0x7371)
+    kd[0].zero_()
+    vd[0].zero_()
+    starts, lens = (0, 150), (320, 130)
+    kr, vr = T3.new_cache(2, N_LAYER, H, 330)
+    kr[1, :, :, :150] = kd[1, :, :, :150].cpu().numpy()
+    vr[1, :, :, :150] = vd[1, :, :, :150].cpu().numpy()
+    prompts = [(rng.standard_normal((L, N)) * 0.5).astype(np.float32) for L in lens]
+    rows = [(sl, starts[sl] + i) for sl in range(2) for i in range(lens[sl])]
+    order = rng.permutation(len(rows))
+    slots = np.array([rows[i][0] for i in order], np.int32)
+    pos = np.array([rows[i][1] for i in order], np.int32)
+    inp = np.stack([prompts[rows[i][0]][rows[i][1] - starts[rows[i][0]]] for i in order])
+    hid = torch.zeros((len(rows), N), dtype=torch.float32, device="cuda")
+    say(f"t3 long prefill rows={len(rows)}")
+    s.t3_prefill(dm, torch.from_numpy(slots).cuda(), torch.from_numpy(pos).cuda(), kd, vd, hid,
+                 inputs=torch.from_numpy(inp).cuda())
+    torch.cuda.synchronize()
+    want = {}
+    for sl in range(2):
+        out = T3.prefill(rm, prompts[sl], kr, vr, sl, starts[sl])
+        for i in range(lens[sl]):
+            want[(sl, starts[sl] + i)] = out[i]
+    ref = np.stack([want[(int(a), int(b))] for a, b in zip(slots, pos)])
+    ok, err = close(hid.cpu().numpy(), ref)
+    assert ok, f"prefill: max err {err:.3g}"
+    say(f"  prefill max |err| {err:.3g}")
+    pos_d = torch.tensor([320, 280], dtype=torch.int32, device="cuda")
+    pos_r = np.array([320, 280], np.int64)
+    hd = torch.zeros((2, N), dtype=torch.float32, device="cuda")
+    for t in range(2):
+        toks = rng.integers(0, V, 2).astype(np.int32)
+        s.t3_step(dm, pos_d, kd, vd, hd, tokens=torch.from_numpy(toks).cuda())
+        torch.cuda.synchronize()
+        w = T3.step(rm, toks, pos_r, kr, vr)
+        ok, err = close(hd.cpu().numpy(), w)
+        assert ok, f"decode {t}: max err {err:.3g}"
+    del kd, vd
+    torch.cuda.empty_cache()

@@ -112,3 +112,64 @@ def test_planted_kv_swap_fails():
             L[key][n:2 * n], L[key][2 * n:] = a[2 * n:], a[n:2 * n]
     got = np.array(run_streams(m, [seq])[0])
     assert not np.allclose(got[1:], want[1:], rtol=1e-6, atol=1e-6)
+
+
+def test_prefill_equals_causal_forward():
+    """The oracle's one-pass prompt (every row's k and v stored, then a causal
+    mask) of a whole sequence from position 0 equals torch's causal
+    forward."""
+    rng = np.random.default_rng(4)
+    m = rand_model(rng)
+    seq = list(rng.integers(0, 50, 9))
+    xs = m.speech_emb[seq] + m.wpe[:9]
+    kc, vc = T3.new_cache(2, len(m.layers), m.n_head, m.wpe.shape[0])
+    got = T3.prefill(m, xs, kc, vc, 1, 0)
+    assert np.allclose(got, torch_forward(m, xs), rtol=1e-10, atol=1e-10)
+    assert np.all(kc[0] == 0.0) and np.any(kc[1, :, :, 8] != 0.0)
+
+
+def test_prefill_continues_a_cache():
+    """A prompt continued from a cache the decode wrote (p0 = 6 positions
+    decoded one at a time, then 5 more rows in one prefill pass) gives the
+    rows the position-by-position decode gives, and leaves the same
+    caches."""
+    rng = np.random.default_rng(5)
+    m = rand_model(rng)
+    seq = list(rng.integers(0, 50, 11))
+    kc, vc = T3.new_cache(1, len(m.layers), m.n_head, m.wpe.shape[0])
+    kd, vd = T3.new_cache(1, len(m.layers), m.n_head, m.wpe.shape[0])
+    pos, pd = np.zeros(1, np.int64), np.zeros(1, np.int64)
+    want = []
+    for t in range(11):
+        out = T3.step(m, np.array([seq[t]]), pd, kd, vd)
+        if t < 6:
+            T3.step(m, np.array([seq[t]]), pos, kc, vc)
+        else:
+            want.append(out[0])
+    xs = m.speech_emb[seq[6:]] + m.wpe[6:11]
+    got = T3.prefill(m, xs, kc, vc, 0, 6)
+    assert np.allclose(got, np.array(want), rtol=1e-10, atol=1e-10)
+    assert np.allclose(kc[0, :, :, :11], kd[0, :, :, :11], rtol=0, atol=1e-12)
+    assert np.allclose(vc[0, :, :, :11], vd[0, :, :, :11], rtol=0, atol=1e-12)
+
+
+def test_stream_caches_index_like_dense():
+    """Ragged per-stream caches (float32, as the reference's fp32 cache)
+    give the step the dense binary64 cache gives, up to the fp32 rounding of
+    the stored k and v."""
+    rng = np.random.default_rng(7)
+    m = rand_model(rng)
+    nl, H = len(m.layers), m.n_head
+    kd, vd = T3.new_cache(2, nl, H, m.wpe.shape[0])
+    kr = T3.StreamCaches([np.zeros((nl, H, L, T3.HEAD_DIM), np.float32) for L in (5, 9)])
+    vr = T3.StreamCaches([np.zeros((nl, H, L, T3.HEAD_DIM), np.float32) for L in (5, 9)])
+    pd, pr = np.zeros(2, np.int64), np.zeros(2, np.int64)
+    for t in range(5):
+        toks = rng.integers(0, 50, 2)
+        a = T3.step(m, toks, pd, kd, vd)
+        b = T3.step(m, toks, pr, kr, vr)
+        assert np.allclose(a, b, rtol=1e-5, atol=1e-5)
+    # layer 0's first position: the same product, rounded once to fp32 (later
+    # layers read the rounded v of earlier ones)
+    assert np.array_equal(kr.arrays[1][0, :, 0], kd[1, 0, :, 0].astype(np.float32))
+    assert np.allclose(kr.arrays[1][:, :, :5], kd[1, :, :, :5], rtol=1e-5, atol=1e-6)

@@ -95,4 +95,21 @@ def test_static_scratch_matches_batch():
     tok = torch.zeros(4097, dtype=torch.int32, device="cuda")
     with pytest.raises(mod.CbxError):
         s.sample_batch(big, prm.repeat(4097), tok, max_survivors=5, static_scratch=True)
+    # ... unless the small-launch rule covers the call: then it runs at full
+    # capacity (no redo list) and gives the handle call's tokens
+    s.set_latency_rows(8192)
+    xb = rng.standard_normal((4200, 300)).astype(F32)
+    pb = torch.from_numpy(pkg.workloads().pack_params(
+        [dict(top_k=50, top_p=0.9, temp=0.9, repeat_penalty=1.0, min_p=0.0,
+              cfg_weight=0.0)])).cuda().repeat(4200)
+    ub = torch.from_numpy(rng.random(4200)).cuda()
+    outs = []
+    for static in (True, False):
+        say(f"4200 rows under the small-launch rule, static={static}")
+        t = torch.full((4200,), -7, dtype=torch.int32, device="cuda")
+        s.sample_batch(torch.from_numpy(xb).cuda(), pb, t, uniforms=ub, max_survivors=5,
+                       static_scratch=static)
+        torch.cuda.synchronize()
+        outs.append(t.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1]) and np.all(outs[0] >= 0)
     s.close()
