@@ -30,6 +30,7 @@ CBX_INFO_EMPTY = 0x04
 CBX_INFO_TOPP_TIE = 0x08
 CBX_INFO_NONFINITE = 0x10
 CBX_INFO_OVERFLOW = 0x20
+CBX_INFO_TOPP_SORTED = 0x80
 
 CBX_INFO_ENDED = 0x40
 

@@ -2218,12 +2218,25 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     }
 }
 
+// The row-step a workgroup samples.  Workgroups are handed to the 8 XCDs in
+// turn (workgroup b to XCD b % 8), and consecutive row-steps of a launch are
+// the streams of one step, each with its own knobs (and so its own cost: a
+// top_k of 1000 costs about twice a top_k of 50).  Taken in launch order, XCD
+// x would sample only the streams r = x mod 8, and the XCD holding the
+// costliest streams would set the launch's time; instead each XCD takes a
+// contiguous eighth of the launch's row-steps (every stream alike, and
+// neighbouring rows on one XCD's L2).
+__device__ __forceinline__ int64_t xcd_spread(int64_t b, int64_t n) {
+    return n % 8 == 0 ? (b % 8) * (n / 8) + b / 8 : b;
+}
+
 template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
 __global__ __launch_bounds__(BLOCK) void sample_rows_kernel(KernelArgs a) {
     __shared__ Shared sh;
     __shared__ uint64_t tab[32];
     extern __shared__ __align__(16) uint8_t smem[];
-    sample_row_wg<BLOCK, EPT, MAXNR, GENERAL>(a, blockIdx.x, sh, tab, smem);
+    sample_row_wg<BLOCK, EPT, MAXNR, GENERAL>(a, xcd_spread(blockIdx.x, gridDim.x), sh, tab,
+                                              smem);
 }
 
 // The rows a launch put on its redo list (more ids survived top-k than its

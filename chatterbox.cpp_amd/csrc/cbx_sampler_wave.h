@@ -457,6 +457,335 @@ __device__ __forceinline__ void tie_order_wave(WaveSmem<Q>& sm, const RowScores&
     wave_lds_sync();
 }
 
+// f(g, 4) for each group of four list rows g = 0, 4, .. N - 4 that holds
+// entries (g < n); rows of the last group past n are the callee's to skip.
+template <int G, int N, class F>
+__device__ __forceinline__ void for_row_groups4(int n, F&& f) {
+    if constexpr (G < N) {
+        if (G < n) f(std::integral_constant<int, G>{}, std::integral_constant<int, 4>{});
+        for_row_groups4<G + 4, N>(n, f);
+    }
+}
+// ------------------------------------------------ top-p by value bins
+//
+// The common case of top-p (main.cpp:750-772) without sorting the survivors.
+// Bins: the sort's monotone value map (descending scores -> ascending bins),
+// kLeanBins of them.  The exp terms e_i = expf(s_i - mx) are placed in bin
+// order by a counting sort with no order inside a bin, and the last position
+// of each bin is marked.  At a bin's last position the binary64 prefix P of
+// the terms is the prefix in sorted order whatever the order inside the bins
+// (equal scores share a bin).  The reference's float running sum cum_i of
+// q_j = fl(e_j / psum), psum its float sum in sorted order, differs from
+// Y_i = P_i / S (S the binary64 total) by at most: i half-ulps of cum_i (the
+// adds), 2^-24 Y_i (the divisions), and Y_i * gamma for psum itself, gamma =
+// (n - 1) 2^-24 / (1 - (n - 1) 2^-24) the classical bound of a recursive
+// float sum of n non-negative terms in any order.  When every bin's last
+// position lies certainly below or certainly at/above top_p, the crossing
+// lies in the bin between the last "below" and the first "above"; that bin's
+// few survivors are ranked (descending score, ascending id: std::sort's order
+// for distinct scores) and certified one by one the same way.  The kept
+// survivors are written to list[0, n_kept) as raw entries (score bits << 32 |
+// id), in any order.  Returns false (the list restored as it was) when a
+// bound straddles top_p, when equal scores straddle the cutoff, or when the
+// crossing bin holds more survivors than one row: the caller then sorts and
+// sums exactly.
+constexpr int kLeanBins = 768;
+constexpr int kLeanSpare = kLeanBins + 8;            // a spare counter per lane (past the list)
+constexpr int kLeanE = kLeanSpare + 64;              // word offset of the terms
+constexpr int kLeanEMax = 64 * (kWaveRows + 1) + 64; // terms read (64 lanes x C <= 17,
+                                                     // in groups of 4) and the zeros past them
+static_assert(kLeanE % 4 == 0, "16-byte aligned terms");
+static_assert(kLeanE + kLeanEMax <= 2 * (kWaveCap + 4), "terms fit the list area");
+static_assert(kLeanBins % 256 == 0, "whole uint4 groups of bins per lane");
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ int wave_max_i_dpp(int x) { return -wave_min_i_dpp(-x); }
+
+// Keeps a uniformly guarded block a branch: its instructions are not
+// speculated into straight-line code that every row would then execute.
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
+template <int Q>
+__device__ __forceinline__ bool lean_topp(WaveSmem<Q>& sm, int n_surv, float mx, float sxs,
+                                          float sxc, float top_p, int& n_kept) {
+    constexpr int R = kWaveRows;
+    constexpr int CM = R + 1;
+    constexpr int BPL = kLeanBins / 64;  // bins per lane in the scan
+    // the crossing bin's survivors, ranked in keptw (8 Q words): keys, then terms
+    constexpr int NBMAX = 3 * 64 <= 8 * Q ? 64 : 32;
+    static_assert(3 * NBMAX <= 8 * Q, "crossing bin fits keptw");
+    const int lane = threadIdx.x;
+    const int nr = uni((n_surv + 63) >> 6);
+    const int nv = fresh(n_surv);
+    uint32_t* const cnt = reinterpret_cast<uint32_t*>(sm.list);
+    uint32_t* const E = reinterpret_cast<uint32_t*>(sm.list) + kLeanE;  // term bits
+    uint64_t w[R];
+    // per entry: its bin (past the list: this lane's spare counter), then
+    // also its slot in the bin (bits 16..), then its position in bin order
+    int pos[R];
+    for_row_groups4<0, R>(nr, [&](auto gc, auto cc) {
+        constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+        for (int r = g; r < g + rows; ++r) {
+            const int i = r * 64 + lane;
+            w[r] = sm.list[i];
+            const float v = __builtin_bit_cast(float, (uint32_t)(w[r] >> 32));
+            const float xq = fmaxf(__fmaf_rn(v, -sxs, sxc), 0.0f);
+            const float y = __fmaf_rn(__fmul_rn(__fmul_rn(xq, xq), xq), (float)(kLeanBins - 4),
+                                      0x1p23f + 2.0f);
+            pos[r] = i < nv ? (int)(__builtin_bit_cast(uint32_t, y) - 0x4B000000u)
+                            : kLeanSpare + lane;
+        }
+    });
+    // the list as it was, for the exact path
+    auto restore = [&]() -> bool {
+        __syncthreads();
+        for_row_groups4<0, R>(nr, [&](auto gc, auto cc) {
+            constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+            for (int r = g; r < g + rows; ++r)
+                lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)(r * 64 + lane), w[r],
+                                    __ballot(r * 64 + lane < nv));
+        });
+        __syncthreads();
+        return false;
+    };
+    CBX_STAMP(40);
+    __syncthreads();  // entries read: the list area takes the counters and the terms
+    {
+        uint4* c4 = reinterpret_cast<uint4*>(cnt) + (BPL / 4) * lane;
+#pragma unroll
+        for (int i = 0; i < BPL / 4; ++i) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    CBX_STAMP(41);
+    for_row_groups4<0, R>(nr, [&](auto gc, auto cc) {
+        constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+        for (int r = g; r < g + rows; ++r)
+            pos[r] |= (int)atomicAdd(&cnt[pos[r]], 1u) << 16;
+    });
+    __syncthreads();
+    CBX_STAMP(42);
+    // bin counts -> exclusive offsets in place; cnt[kLeanBins] = n_surv
+    {
+        uint4* c4 = reinterpret_cast<uint4*>(cnt) + (BPL / 4) * lane;
+        uint4 w4[BPL / 4];
+        uint32_t loc = 0;
+#pragma unroll
+        for (int i = 0; i < BPL / 4; ++i) {
+            w4[i] = c4[i];
+            loc += (w4[i].x + w4[i].y) + (w4[i].z + w4[i].w);
+        }
+        int all;
+        uint32_t run = (uint32_t)wave_excl_scan_i((int)loc, all);
+#pragma unroll
+        for (int i = 0; i < BPL / 4; ++i) {
+            uint4 o;
+            o.x = run; run += w4[i].x;
+            o.y = run; run += w4[i].y;
+            o.z = run; run += w4[i].z;
+            o.w = run; run += w4[i].w;
+            c4[i] = o;
+        }
+        if (lane == 63) cnt[kLeanBins] = run;
+    }
+    __syncthreads();
+    // the terms in bin order, the last position of each bin with its sign bit
+    // set (a term is >= 0); zeros past the list
+    E[nv + lane] = 0u;
+    E[nv + 64 + lane] = 0u;
+    for_row_groups4<0, R>(nr, [&](auto gc, auto cc) {
+        constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+        for (int r = g; r < g + rows; ++r) {
+            if (r >= nr) {  // (last group: rows past the list)
+                pos[r] = 0x7fffffff;
+                continue;
+            }
+            keep_branch();
+            const bool in = r * 64 + lane < nv;
+            const int b = pos[r] & 0xffff;
+            const int o0 = (int)cnt[b], o1 = (int)cnt[b + 1];
+            const int p = o0 + (pos[r] >> 16);
+            const float v = __builtin_bit_cast(float, (uint32_t)(w[r] >> 32));
+            const uint32_t eb =
+                __builtin_bit_cast(uint32_t, expf_nonpos(__fsub_rn(v, mx), sm.tab));
+            lds_store_b32_lanes(lds_offset(E) + 4u * (uint32_t)(in ? p : 0),
+                                eb | (p + 1 == o1 ? 0x80000000u : 0u), __ballot(in));
+            pos[r] = in ? p : 0x7fffffff;
+        }
+    });
+    __syncthreads();
+    CBX_STAMP(43);
+    // lane l: positions [l*C, l*C + C), C odd (distinct banks), read in
+    // groups of 4 (positions past C are another lane's: zeroed here)
+    const int C = uni(((n_surv + 63) >> 6) | 1);
+    const int b0 = lane * C;
+    const uint32_t* El = E + b0;
+    float t[CM];
+    uint32_t mk = 0;  // bit q: position b0 + q ends a bin
+    double part = 0.0;
+#pragma unroll
+    for (int g = 0; g < CM; g += 4) {
+#pragma unroll
+        for (int q = g; q < g + 4 && q < CM; ++q) t[q] = 0.0f;
+        if (g < C) {
+            uint32_t raw[4];
+#pragma unroll
+            for (int q = 0; q < 4 && g + q < CM; ++q) raw[q] = El[g + q];
+#pragma unroll
+            for (int q = g; q < g + 4 && q < CM; ++q) {
+                const uint32_t rq = q < C ? raw[q - g] : 0u;
+                t[q] = __builtin_bit_cast(float, rq & 0x7fffffffu);
+                mk |= (rq >> 31) << q;
+                part = __dadd_rn(part, (double)t[q]);
+            }
+        }
+    }
+    const double incl = wave_incl_scan_f64_dpp(part);
+    const double S = readlane_f64(incl, 63);
+    const double x0 = __dsub_rn(incl, part);
+    CBX_STAMP(44);
+    const double p = (double)top_p;
+    const double gam = (double)n_surv * 0x1p-24 * (1.0 + 0x1p-10);
+    const double inv = __ddiv_rn(1.0, S);
+    // this lane's bound (its last index and the binade of its last Y); the
+    // thresholds scaled by S (their rounding is inside the 1e-12)
+    const double yl = __dmul_rn(__dadd_rn(x0, part), inv);
+    const int be = __builtin_amdgcn_frexp_exp(__dmul_rn(yl, 1.0 + 0x1p-12)) - 1;
+    const double err = __dadd_rn(
+        __dadd_rn(__dmul_rn((double)(b0 + C - 1), ldexp(1.0, max(be, -126) - 24)),
+                  __dmul_rn(yl, 0x1p-23 + gam)),
+        1e-12);
+    const double loP = __dmul_rn(__dsub_rn(p, err), S), hiP = __dmul_rn(__dadd_rn(p, err), S);
+    // prefixes increase with the position: positions q < nlo lie certainly
+    // below top_p, q >= nhi certainly at or above it (the zero terms past C
+    // only repeat the last prefix: their counts fall on unmarked positions)
+    int nlo = 0, nhi = 0;
+    double x = x0;
+#pragma unroll
+    for (int g = 0; g < CM; g += 4) {
+        if (g < C) {
+            keep_branch();
+#pragma unroll
+            for (int q = g; q < g + 4 && q < CM; ++q) {
+                x = __dadd_rn(x, (double)t[q]);
+                nlo += x < loP ? 1 : 0;
+                nhi += x < hiP ? 1 : 0;
+            }
+        }
+    }
+    const uint32_t below = mk & ((1u << nlo) - 1u);
+    const uint32_t above = mk & ~((1u << nhi) - 1u);
+    const bool unc = (mk & ~below & ~above) != 0u;
+    if (__ballot(unc) != 0) return restore();
+    const int jA = below ? b0 + 31 - (int)__builtin_clz(below) : -1;
+    const int jB = above ? b0 + (int)__builtin_ctz(above) : 0x7fffffff;
+    const int JA = wave_max_i_dpp(jA), JB = wave_min_i_dpp(jB);
+    // (the last bin ends at Y = 1 > top_p: some bin end is certainly at or
+    // above top_p unless top_p lies within the bound of 1)
+    if (JB == 0x7fffffff) return restore();
+    CBX_STAMP(45);
+    const int s0 = JA + 1, s1 = JB + 1;
+    const int nb = s1 - s0;
+    uint64_t kc = 0;  // kept in the crossing bin: keys <= kc
+    if (nb == 1) {
+        n_kept = s1;  // below at JA, at or above at JB
+    } else {
+        if (nb > NBMAX) return restore();
+        // the prefix at JA, summed again by its lane
+        double pa = x0;
+#pragma unroll
+        for (int g = 0; g < CM; g += 4) {
+            if (g < C) {
+                keep_branch();
+#pragma unroll
+                for (int q = g; q < g + 4 && q < CM; ++q)
+                    pa = __dadd_rn(pa, b0 + q <= JA ? (double)t[q] : 0.0);
+            }
+        }
+        const double PA = JA >= 0 ? readlane_f64(pa, JA / C) : 0.0;
+        // the bin's entries into one row (keptw: keys, then terms)
+        uint64_t* bk = reinterpret_cast<uint64_t*>(sm.keptw);
+        uint32_t* be4 = sm.keptw + 2 * NBMAX;
+        int nbin = 0;
+        for_row_groups4<0, R>(nr, [&](auto gc, auto cc) {
+            constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+            for (int r = g; r < g + rows; ++r) {
+                const bool inb = pos[r] >= s0 && pos[r] < s1;
+                const uint64_t m = __ballot(inb);
+                if (m != 0) {
+                    const int at = inb ? nbin + mbcnt64(m) : 0;
+                    const float v = __builtin_bit_cast(float, (uint32_t)(w[r] >> 32));
+                    lds_store_b64_lanes(lds_offset(bk) + 8u * (uint32_t)at,
+                                        desc_key(v, (uint32_t)w[r]), m);
+                    lds_store_b32_lanes(lds_offset(be4) + 4u * (uint32_t)at,
+                                        E[inb ? pos[r] : 0] & 0x7fffffffu, m);
+                    nbin += __popcll(m);
+                }
+            }
+        });
+        __syncthreads();
+        const bool mine = lane < nb;
+        const uint64_t key = mine ? bk[lane] : ~0ull;
+        const uint32_t em = mine ? be4[lane] : 0u;
+        int rank = 0;
+        for (int tt = 0; tt < nb; ++tt) rank += readlane_u64(key, tt) < key ? 1 : 0;
+        __syncthreads();  // read: the row takes rank order
+        lds_store_b64_lanes(lds_offset(bk) + 8u * (uint32_t)(mine ? rank : 0), key,
+                            __ballot(mine));
+        lds_store_b32_lanes(lds_offset(be4) + 4u * (uint32_t)(mine ? rank : 0), em,
+                            __ballot(mine));
+        __syncthreads();
+        const uint64_t kr = mine ? bk[lane] : ~0ull;
+        const double er = mine ? (double)__builtin_bit_cast(float, be4[lane]) : 0.0;
+        const double y = __dmul_rn(__dadd_rn(PA, wave_incl_scan_f64_dpp(er)), inv);
+        const int bi = __builtin_amdgcn_frexp_exp(__dmul_rn(y, 1.0 + 0x1p-12)) - 1;
+        const double erri = __dadd_rn(
+            __dadd_rn(__dmul_rn((double)(s0 + lane), ldexp(1.0, max(bi, -126) - 24)),
+                      __dmul_rn(y, 0x1p-23 + gam)),
+            1e-12);
+        const uint64_t mlo = __ballot(mine && y < __dsub_rn(p, erri));
+        const uint64_t mhi = __ballot(mine && y >= __dadd_rn(p, erri));
+        const int f = __builtin_ctzll(~mlo);  // first position not certainly below
+        if (f >= nb || !((mhi >> f) & 1ull)) return restore();
+        // equal scores straddling the cutoff: std::sort's order decides
+        if (f + 1 < nb && desc_key_value(readlane_u64(kr, f)) ==
+                              desc_key_value(readlane_u64(kr, f + 1)))
+            return restore();
+        kc = readlane_u64(kr, f);
+        n_kept = s0 + f + 1;
+    }
+    CBX_STAMP(46);
+    __syncthreads();  // terms and counters read: the list takes the kept entries
+    int nk = 0;
+    for_row_groups4<0, R>(nr, [&](auto gc, auto cc) {
+        constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+        for (int r = g; r < g + rows; ++r) {
+            // kept: positions before the crossing bin, and of that bin its
+            // one survivor or those up to the cutoff key
+            bool kp = pos[r] < (nb == 1 ? s1 : s0);
+            if (nb > 1 && pos[r] >= s0 && pos[r] < s1) {
+                const float v = __builtin_bit_cast(float, (uint32_t)(w[r] >> 32));
+                kp = desc_key(v, (uint32_t)w[r]) <= kc;
+            }
+            const uint64_t m = __ballot(kp);
+            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)(nk + mbcnt64(m)), w[r], m);
+            nk += __popcll(m);
+        }
+    });
+    __syncthreads();
+    return true;
+}
+
 // ------------------------------------------------------------------ kernel
 
 template <int Q, int JT>
@@ -466,7 +795,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     constexpr int EPL = 4 * Q;  // scores per lane
     constexpr int R = kWaveRows;
     const int lane = threadIdx.x;
-    const int64_t g = blockIdx.x;
+    const int64_t g = xcd_spread(blockIdx.x, gridDim.x);
     const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
     const int V = a.n_vocab;
     const int W = (V + 31) >> 5;
@@ -1037,12 +1366,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     const bool csort = use_topp && !bad && srange > 0.0f && sxs < kPosInf &&
                        sort_bin_y(hi) >= 0x1p23f &&
                        sort_bin_y(slo) <= 0x1p23f + (float)(kWaveBins - 1);
+    // The common top-p case without the sort (lean_topp); the rows it cannot
+    // certify take the sort and the exact sums below.
+    bool lean = use_topp && csort;
+    if (lean) {
+        int nk_l = 0;
+        lean = lean_topp<Q>(sm, n_surv, hi, sxs, sxc, P.top_p, nk_l);
+        if (lean) n_kept = nk_l;
+    }
     // raw entries -> composite keys (descending score, ascending id), in place;
     // positions [n_surv, 64*nr) become the maximum key (the counting sort
     // converts in registers instead).
     // Rows of the list are handled 4 at a time under one uniform branch, so
     // their LDS accesses overlap; rows past the list only touch unused slots.
-    if (!csort) {
+    if (!csort && use_topp) {
 #pragma unroll
         for (int g = 0; g < R; g += 4) {
             if (g < nr) {
@@ -1060,7 +1397,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     }
     CBX_STAMP(5);
 
-    if (use_topp) {
+    if (use_topp && !lean) {
+        rflags |= CBX_INFO_TOPP_SORTED;
         // ---- counting sort of the keys by value bin over [min survivor, max] ----
         // Every survivor is read into registers first, so the counters and
         // offsets can use the list's own storage until the keys go back to
@@ -1364,6 +1702,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
         }
         __syncthreads();
+        // the kept keys back to raw entries (score bits << 32 | id) for the
+        // stages below
+        const int nkr = (n_kept + 63) >> 6;
+        for_row_groups<0, R>(nkr, [&](auto gc, auto cc) {
+            constexpr int g = decltype(gc)::value, rows = decltype(cc)::value;
+#pragma unroll
+            for (int r = g; r < g + rows; ++r) {
+                const int i = r * 64 + lane;
+                const uint64_t key = sm.list[i];
+                sm.list[i] = ((uint64_t)__builtin_bit_cast(uint32_t, desc_key_value(key)) << 32) |
+                             (uint32_t)key;
+            }
+        });
+        __syncthreads();
     }
 
     // ---- min-p [extension], repetition penalty (main.cpp:774-781) ----
@@ -1387,9 +1739,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 #pragma unroll
             for (int r = g; r < g + rows; ++r) {
                 const int i = r * 64 + lane;
-                const uint64_t key = sm.list[i];
+                const uint64_t key = sm.list[i];  // raw: score bits << 32 | id
                 bool kp = i < nkv;
-                float v = desc_key_value(key);
+                float v = __builtin_bit_cast(float, (uint32_t)(key >> 32));
                 const int id = kp ? (int)(uint32_t)key : 0;
                 if (P.min_p > 0.0f) {
                     const float x = __fsub_rn(v, mx_kept);

@@ -66,6 +66,12 @@ typedef struct cbx_params {
                                     call's redo list (max_survivors set too low);
                                     at full capacity never on gfx950, whose LDS
                                     holds every id of a 32768 vocabulary           */
+#define CBX_INFO_TOPP_SORTED 0x80u /* diagnostic, one-wave kernel only: the top-p
+                                    cutoff was taken on the sorted survivor list
+                                    with exact float running sums, because value
+                                    bins could not certify it (the same token
+                                    either way; other kernels always sort and do
+                                    not set this bit)                              */
 
 #define CBX_DRAW_UNIFORM 0 /* uniforms[step][row] supplied by the caller            */
 #define CBX_DRAW_PHILOX  1 /* Philox4x32-10: counter {step lo, step hi, stream lo,

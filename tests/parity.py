@@ -16,6 +16,7 @@ import numpy as np
 
 INFO_DREW, INFO_GREEDY, INFO_EMPTY, INFO_TOPP_TIE, INFO_NONFINITE, INFO_OVERFLOW = (
     0x01, 0x02, 0x04, 0x08, 0x10, 0x20)
+INFO_TOPP_SORTED = 0x80  # diagnostic of the one-wave kernel (not compared with the oracle)
 DRAW_TIE_EPS = 1e-6
 
 
