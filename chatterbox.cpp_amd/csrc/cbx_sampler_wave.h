@@ -795,7 +795,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     constexpr int EPL = 4 * Q;  // scores per lane
     constexpr int R = kWaveRows;
     const int lane = threadIdx.x;
-    const int64_t g = xcd_spread(blockIdx.x, gridDim.x);
+    const int64_t g = xcd_spread(blockIdx.x, gridDim.x, a.n_rows);
     const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
     const int V = a.n_vocab;
     const int W = (V + 31) >> 5;
@@ -897,7 +897,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // this instantiation meets in vectors j >= JT alone (V > 256*JT); the
     // others need 4 operations per score and no predicate.
     const bool plain = !rsc.masked_ids && !rsc.fstop;
+    // lo, the smallest finite score, is taken only where a path needs it
+    // (have_lo): the common one bins from the mean of vector 0 and sorts
+    // from the top-k threshold
     float lo = kPosInf, hi = kNegInf;
+    bool have_lo = false;
     float msum = 0.0f;  // this lane's 4 scores of vector 0 (padding-free when JT >= 1)
     bool bad = false, neg_inf = false;  // NaN/+inf seen; -inf among unmasked scores
     if (!plain) {
@@ -939,9 +943,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                     if (j == 0) msum = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
                     acc = __fmaf_rn(w[0], w[1], acc);
                     acc = __fmaf_rn(w[2], w[3], acc);
-                    // running value first: one 3-input min / max per pair
-                    lo = fminf(fminf(lo, w[0]), w[1]);
-                    lo = fminf(fminf(lo, w[2]), w[3]);
+                    // running value first: one 3-input max per pair
                     hi = fmaxf(fmaxf(hi, w[0]), w[1]);
                     hi = fmaxf(fmaxf(hi, w[2]), w[3]);
                 } else {
@@ -950,7 +952,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         const bool pad = 256 * j + 4 * lane + c >= Vm;
                         acc = __fmaf_rn(pad ? 0.0f : w[c], 0.0f, acc);
                         w[c] = pad ? kNegInf : w[c];
-                        lo = fminf(lo, pad ? kPosInf : w[c]);
                         hi = fmaxf(hi, w[c]);
                     }
                 }
@@ -976,9 +977,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
             bad = wave_sum_dpp(nf) != 0;
             neg_inf = wave_sum_dpp(ni) != 0;
+            lo = wave_min_dpp(lo);
+            have_lo = true;
         }
     }
-    lo = wave_min_dpp(lo);
     hi = wave_max_dpp(hi);
     const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
     CBX_STAMP(2);
@@ -994,6 +996,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
     };
 
+    // lo from the scores in registers (every unmasked score finite here:
+    // rows holding -inf, NaN or +inf took it above) ...
+    auto lo_from_registers = [&]() {
+        if (have_lo) return;
+        float m = kPosInf;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) m = fminf(m, s[e] == kNegInf ? kPosInf : s[e]);  // padding
+        lo = wave_min_dpp(m);
+        have_lo = true;
+    };
+    // ... or reloaded, where the registers have been given up
+    auto lo_from_memory = [&]() {
+        if (have_lo) return;
+        float m = kPosInf;
+        each_score([&](float v, int) { m = fminf(m, v == kNegInf ? kPosInf : v); });
+        lo = wave_min_dpp(m);
+        have_lo = true;
+    };
+
     // ---- top-k (main.cpp:740-748) ----
     const int k = P.top_k;
     const bool use_topk = k > 0 && k < V;
@@ -1002,9 +1023,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     if (use_topk) {
         int above = 0;
         bool done = false;
-        const float range = __fsub_rn(hi, lo);
-        const float bscale = __fdiv_rn((float)kWaveBins, range);
-        const float nlo = -__fmul_rn(lo, bscale);
         // Plain rows: y(v) = fma(v, bs, c0) lands in [2^23, 2^23 + NB) for
         // every score in [lo, hi] (checked at both ends; y is monotone), where
         // a float is an integer: bin(v) = bits(y) - bits(2^23) is
@@ -1021,8 +1039,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         // below 2 (or holding fewer than k + 1 binned scores) takes the
         // full-range pass further down.
         const bool partial = JT >= 1 && 4 * k < V && !bad && !neg_inf;
-        const float hlo =
-            partial ? fmaxf(lo, __fmul_rn(wave_sum_f_dpp(msum), 1.0f / 256.0f)) : lo;
+        if (!partial) lo_from_registers();
+        const float hlo = partial ? __fmul_rn(wave_sum_f_dpp(msum), 1.0f / 256.0f) : lo;
         const float hrange = __fsub_rn(hi, hlo);
         const float bs = __fdiv_rn((float)(kWaveBins - 4), hrange);
         const float c0 = __fsub_rn(0x1p23f + 2.0f, __fmul_rn(hlo, bs));
@@ -1196,6 +1214,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                 }
             }
         }
+        if (!done) lo_from_memory();
+        const float range = __fsub_rn(hi, lo);
+        const float bscale = __fdiv_rn((float)kWaveBins, range);
+        const float nlo = -__fmul_rn(lo, bscale);
         if (!done && !bad && range > 0.0f && bscale < kPosInf) {
             // bins with -inf sent to the spare bin NB (masked rows, -inf logits)
             auto bin_of = [&](float v) -> int {
@@ -1350,7 +1372,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     int n_kept = n_surv;  // kept: list positions [0, n_kept)
     float mx_surv = hi;
     // top-p sorts by a counting sort over [min survivor, max] where it can
-    const float slo = use_topk ? fmaxf(thr, lo) : lo;
+    // (a threshold below lo only widens the range)
+    if (!(use_topk && thr > kNegInf)) lo_from_memory();
+    const float slo = use_topk && thr > kNegInf ? (have_lo ? fmaxf(thr, lo) : thr) : lo;
     const float srange = __fsub_rn(hi, slo);
     // descending sort bins, finer where survivors crowd (just above the
     // threshold): with x = max(0, (hi - v) / range) in [0, ~1], bin =
