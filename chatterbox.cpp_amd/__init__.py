@@ -90,7 +90,7 @@ class Batch(ctypes.Structure):
     ]
 
 
-CBX_WTYPE_F16, CBX_WTYPE_Q4_0, CBX_WTYPE_Q8_0 = 1, 2, 8
+CBX_WTYPE_F16, CBX_WTYPE_Q4_0, CBX_WTYPE_Q5_0, CBX_WTYPE_Q8_0 = 1, 2, 6, 8
 
 
 class Head(ctypes.Structure):

@@ -484,7 +484,7 @@ int check_head(const char* fn, const cbx_head* h, int32_t n_rows, int32_t n_voca
                int64_t ld_logits) {
     if (!h || !h->weights || !h->hidden || !h->logits)
         return fail(CBX_ERR_INVALID, "%s: NULL head, weights, hidden or logits", fn);
-    if (h->wtype != CBX_WTYPE_F16 && h->wtype != CBX_WTYPE_Q4_0 && h->wtype != CBX_WTYPE_Q8_0)
+    if (cbx::wtype_block_bytes(h->wtype) == 0)
         return fail(CBX_ERR_INVALID, "%s: unknown wtype %d", fn, h->wtype);
     if (h->n_embd < 32 || h->n_embd > 16384 || h->n_embd % 32)
         return fail(CBX_ERR_INVALID, "%s: n_embd %d not a multiple of 32 in [32, 16384]", fn,
@@ -498,7 +498,7 @@ int check_head(const char* fn, const cbx_head* h, int32_t n_rows, int32_t n_voca
         return fail(CBX_ERR_INVALID, "%s: n_rows %d, n_vocab %d, ld_logits %lld", fn, n_rows,
                     n_vocab, (long long)ld_logits);
     // the kernel's buffer descriptors address the weights and rows in 32 bits
-    const int64_t bpb = h->wtype == CBX_WTYPE_F16 ? 64 : (h->wtype == CBX_WTYPE_Q4_0 ? 18 : 34);
+    const int64_t bpb = cbx::wtype_block_bytes(h->wtype);
     if ((int64_t)n_vocab * (h->n_embd / 32) * bpb > 0x7fffffffLL ||
         ((int64_t)n_rows * h->ld_hidden + h->n_embd) * 4 > 0x7fffffffLL ||
         (int64_t)(h->hidden_uncond ? 2 : 1) * (n_rows + 15) * h->n_embd * 4 > 0x7fffffffLL)
@@ -592,7 +592,7 @@ int t3_run(const char* fn, cbx_sampler* s, const cbx_t3_model* m, int32_t n_rows
         return fail(CBX_ERR_UNSUPPORTED,
                     "%s: n_embd %d, n_head %d (heads of 64, n_embd in {256..1024 by 256, 1536, "
                     "2048, 3072, 4096})", fn, m->n_embd, m->n_head);
-    if (m->wtype != CBX_WTYPE_F16 && m->wtype != CBX_WTYPE_Q4_0 && m->wtype != CBX_WTYPE_Q8_0)
+    if (cbx::wtype_block_bytes(m->wtype) == 0)
         return fail(CBX_ERR_INVALID, "%s: unknown wtype %d", fn, m->wtype);
     if (!(m->eps >= 0.0f) || !m->wpe || !m->ln_f_g || !m->ln_f_b || m->n_pos < 1 ||
         (!inputs && (!tokens || !m->speech_emb || m->n_speech_vocab < 1)))

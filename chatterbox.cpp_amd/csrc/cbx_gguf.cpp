@@ -29,7 +29,7 @@ enum : uint32_t {
     kString = 8, kArray = 9, kU64 = 10, kI64 = 11, kF64 = 12
 };
 // ggml tensor types this reader sizes (the head's formats and the bias's)
-enum : uint32_t { kTF32 = 0, kTF16 = 1, kTQ4_0 = 2, kTQ8_0 = 8 };
+enum : uint32_t { kTF32 = 0, kTF16 = 1, kTQ4_0 = 2, kTQ5_0 = 6, kTQ8_0 = 8 };
 constexpr uint32_t kMagic = 0x46554747u;  // "GGUF" read as a little-endian u32
 constexpr int kMaxDims = 4;
 
@@ -86,6 +86,7 @@ uint64_t tensor_bytes(uint32_t t, uint64_t n0, uint64_t n_rows) {
         case kTF32: return 4 * n0 * n_rows;
         case kTF16: return 2 * n0 * n_rows;
         case kTQ4_0: return n0 % 32 ? 0 : 18 * (n0 / 32) * n_rows;
+        case kTQ5_0: return n0 % 32 ? 0 : 22 * (n0 / 32) * n_rows;
         case kTQ8_0: return n0 % 32 ? 0 : 34 * (n0 / 32) * n_rows;
         default: return 0;
     }
@@ -238,11 +239,12 @@ int parse(const char* path, cbx_head_file* out) {
     switch (head.type) {
         case kTF16: wtype = CBX_WTYPE_F16; break;
         case kTQ4_0: wtype = CBX_WTYPE_Q4_0; break;
+        case kTQ5_0: wtype = CBX_WTYPE_Q5_0; break;
         case kTQ8_0: wtype = CBX_WTYPE_Q8_0; break;
         default:
             return cbx::set_error(CBX_ERR_UNSUPPORTED,
                                   "cbx_gguf_read_head: %s: speech_head has ggml type %u "
-                                  "(F16, Q4_0 and Q8_0 are supported)",
+                                  "(F16, Q4_0, Q5_0 and Q8_0 are supported)",
                                   path, head.type);
     }
     if (head.n_dims != 2) return invalid("speech_head is not 2-D");
@@ -334,9 +336,9 @@ int plan_t3(const char* fn, const char* path, cbx_t3_file* out, std::vector<T3It
         const uint64_t rows = rows_out ? t->ne[1] : (ne1 ? ne1 : 1);
         T3Item it;
         if (matrix) {
-            if (t->type != kTF16 && t->type != kTQ4_0 && t->type != kTQ8_0)
-                return cbx::set_error(CBX_ERR_UNSUPPORTED, "%s: %s: %s has ggml type %u (F16, Q4_0 and "
-                                      "Q8_0 are supported)", fn, path, name.c_str(), t->type);
+            if (t->type != kTF16 && t->type != kTQ4_0 && t->type != kTQ5_0 && t->type != kTQ8_0)
+                return cbx::set_error(CBX_ERR_UNSUPPORTED, "%s: %s: %s has ggml type %u (F16, Q4_0, "
+                                      "Q5_0 and Q8_0 are supported)", fn, path, name.c_str(), t->type);
             if (*mtype == ~0u) *mtype = t->type;
             if (t->type != *mtype)
                 return cbx::set_error(CBX_ERR_UNSUPPORTED, "%s: %s: the layer matrices mix ggml types",
@@ -391,7 +393,10 @@ int plan_t3(const char* fn, const char* path, cbx_t3_file* out, std::vector<T3It
     o.n_head = (int32_t)s.kv_head;
     o.n_pos = (int32_t)n_pos;
     o.n_speech_vocab = (int32_t)n_vocab;
-    o.wtype = mtype == kTF16 ? CBX_WTYPE_F16 : (mtype == kTQ4_0 ? CBX_WTYPE_Q4_0 : CBX_WTYPE_Q8_0);
+    o.wtype = mtype == kTF16 ? CBX_WTYPE_F16
+            : mtype == kTQ4_0 ? CBX_WTYPE_Q4_0
+            : mtype == kTQ5_0 ? CBX_WTYPE_Q5_0
+                              : CBX_WTYPE_Q8_0;
     o.eps = s.eps;
     o.start_speech_token = (int32_t)s.kv_start;
     o.stop_speech_token = (int32_t)s.kv_stop;

@@ -1,10 +1,12 @@
 // cbx_head.hip -- the T3 speech_head projection:
 // logits[r][v] = sum_k W[v][k] * h[r][k] + b[v]   (src/main.cpp:577; the weights
-// and bias are chatterbox/speech_head(_bias), main.cpp:394-395), for F16, Q4_0
-// and Q8_0 weights in ggml's layout (ne = [n_embd, n_vocab]: row v holds the
-// n_embd weights of vocab id v; Q4_0 blocks are an fp16 scale d and 16 bytes
-// of nibbles, element j < 16 in the low nibble of byte j and element j + 16
-// in its high nibble, w = (q - 8) d; Q8_0 blocks are d and 32 int8, w = q d).
+// and bias are chatterbox/speech_head(_bias), main.cpp:394-395), for F16, Q4_0,
+// Q5_0 and Q8_0 weights in ggml's layout (ne = [n_embd, n_vocab]: row v holds
+// the n_embd weights of vocab id v; Q4_0 blocks are an fp16 scale d and 16
+// bytes of nibbles, element j < 16 in the low nibble of byte j and element
+// j + 16 in its high nibble, w = (q - 8) d; Q5_0 blocks are d, a 32-bit
+// little-endian word qh whose bit j is the fifth bit of element j, and the
+// nibbles as Q4_0's, w = (q - 16) d; Q8_0 blocks are d and 32 int8, w = q d).
 //
 // 16 rows and more run on the fp16 matrix cores in two launches:
 //  * head_split: each activation row r is scaled by a power of two 2^s_r (its
@@ -17,8 +19,8 @@
 //    contiguous (loads of 64-byte pieces of 16 rows were the kernel's limit).
 //  * head_mfma: a workgroup of KS waves computes 32 vocab ids x NT row tiles
 //    of 16 rows with v_mfma_f32_16x16x32_f16, A = the activation parts, B =
-//    the weights: F16 weights as they are, Q4_0 / Q8_0 as their integers
-//    (n - 8 or q, exact in fp16) with each block's product scaled by its d
+//    the weights: F16 weights as they are, Q4_0 / Q5_0 / Q8_0 as their
+//    integers (n - 8, q - 16 or q, exact in fp16) with each block's product scaled by its d
 //    in fp32.  Products of fp16 values are exact in fp32; sums are the
 //    matrix core's fp32.  Wave w takes the w-th of KS runs of 32-weight
 //    blocks along n_embd, and the KS partial tiles are added in wave order
@@ -46,6 +48,18 @@ constexpr int32_t kBufWord3 = 0x00020000;  // raw buffer: 32-bit data format
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t hb) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+}
+
+// Bytes of one block of 32 weights (F16: 32 halves).
+template <int WT>
+constexpr int block_bytes() {
+    return WT == CBX_WTYPE_F16 ? 64 : WT == CBX_WTYPE_Q4_0 ? 18 : WT == CBX_WTYPE_Q5_0 ? 22 : 34;
+}
+
+// Bits 0..3 of x to bit 4 of bytes 0..3 (the four products x << 7i land in
+// disjoint bit ranges: no carries).
+__device__ __forceinline__ uint32_t spread4(uint32_t x) {
+    return ((x * 0x00204081u) & 0x01010101u) << 4;
 }
 
 // ------------------------------------------------------------ activation split
@@ -113,10 +127,11 @@ __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0
 
 // --------------------------------------------------------------- matrix cores
 // Raw bytes of the 8 weights k = 8g .. 8g + 7 of one block of a vocab row,
-// from the row's chunk staged in LDS: F16 four dwords; Q4_0 / Q8_0 the fp16
-// scale in q[4] and the 8 bytes of nibbles or int8 in q[0..1].  Blocks are
-// 18 or 34 bytes, so only 2-byte alignment holds: `off` (the block's byte
-// offset in the staged row) is read as dwords shifted into place.
+// from the row's chunk staged in LDS: F16 four dwords; Q4_0 / Q5_0 / Q8_0 the
+// fp16 scale in q[4] and the 8 bytes of nibbles or int8 in q[0..1], Q5_0's
+// high-bit word qh in q[2].  Blocks are 18, 22 or 34 bytes, so only 2-byte
+// alignment holds: `off` (the block's byte offset in the staged row) is read
+// as dwords shifted into place.
 template <int WT>
 __device__ __forceinline__ void lds_w(const uint32_t* srow, int off, int g, uint32_t* q) {
     if constexpr (WT == CBX_WTYPE_F16) {
@@ -130,12 +145,18 @@ __device__ __forceinline__ void lds_w(const uint32_t* srow, int off, int g, uint
         q[3] = __builtin_amdgcn_alignbit(t4, t3, sh);
     } else {
         q[4] = (srow[off >> 2] >> (8 * (off & 3))) & 0xffffu;
-        const int qoff = off + 2 + (WT == CBX_WTYPE_Q4_0 ? 8 * (g & 1) : 8 * g);
+        const int qoff = off + (WT == CBX_WTYPE_Q5_0 ? 6 : 2) +
+                         (WT == CBX_WTYPE_Q8_0 ? 8 * g : 8 * (g & 1));
         const uint32_t* p = srow + (qoff >> 2);
         const uint32_t sh = 8u * (uint32_t)(qoff & 3);
         const uint32_t t0 = p[0], t1 = p[1], t2 = p[2];
         q[0] = __builtin_amdgcn_alignbit(t1, t0, sh);
         q[1] = __builtin_amdgcn_alignbit(t2, t1, sh);
+        if constexpr (WT == CBX_WTYPE_Q5_0) {
+            const int hoff = off + 2;
+            const uint32_t* ph = srow + (hoff >> 2);
+            q[2] = __builtin_amdgcn_alignbit(ph[1], ph[0], 8u * (uint32_t)(hoff & 3));
+        }
     }
 }
 
@@ -151,8 +172,8 @@ __device__ __forceinline__ uint32_t bytes_f16(uint32_t x, uint32_t sel, _Float16
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// The 8 integer weights of lds_w's bytes as fp16: Q4_0 n - 8, Q8_0 q; and the
-// block's scale d.
+// The 8 integer weights of lds_w's bytes as fp16: Q4_0 n - 8, Q5_0 q - 16
+// (q = n | the element's qh bit << 4), Q8_0 q; and the block's scale d.
 template <int WT>
 __device__ __forceinline__ u4v int_weights(const uint32_t* q, int g, float& d) {
     d = half_bits_to_float(q[4]);
@@ -163,6 +184,13 @@ __device__ __forceinline__ u4v int_weights(const uint32_t* q, int g, float& d) {
         x0 = (q[0] >> sh) & 0x0f0f0f0fu;
         x1 = (q[1] >> sh) & 0x0f0f0f0fu;
         off = (_Float16)1032.0f;
+    } else if constexpr (WT == CBX_WTYPE_Q5_0) {
+        // lane group g holds elements 8g .. 8g + 7: qh bits 8g .. 8g + 7
+        const int sh = g < 2 ? 0 : 4;
+        const uint32_t hb = q[2] >> (8 * g);
+        x0 = ((q[0] >> sh) & 0x0f0f0f0fu) | spread4(hb & 15u);
+        x1 = ((q[1] >> sh) & 0x0f0f0f0fu) | spread4((hb >> 4) & 15u);
+        off = (_Float16)1040.0f;
     } else {
         x0 = q[0] ^ 0x80808080u;
         x1 = q[1] ^ 0x80808080u;
@@ -200,7 +228,7 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
                                                      int n_tiles, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
                                                      int n_embd, int64_t zstride, int gelu_out) {
-    constexpr int BB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
+    constexpr int BB = block_bytes<WT>();
     // Weights are staged per wave in chunks of CB blocks: for each of the 32
     // vocab rows the chunk's CB * BB bytes are contiguous, so whole-row dword
     // loads touch two or three lines each (the per-block loads of the 18-byte
@@ -426,8 +454,8 @@ __device__ __forceinline__ void gemv_block(const __amdgpu_buffer_rsrc_t& rw, int
             w[2 * i + 1] = half_bits_to_float(t[i] >> 16);
         }
     } else {
-        constexpr int BB = WT == CBX_WTYPE_Q4_0 ? 18 : 34;
-        constexpr int ND = WT == CBX_WTYPE_Q4_0 ? 5 : 9;  // dwords covering the block
+        constexpr int BB = block_bytes<WT>();
+        constexpr int ND = (BB + 2 + 3) / 4;  // dwords covering the block (5, 6 or 9)
         const uint32_t off = (uint32_t)(((int64_t)v * nball + b) * BB);  // even
         const uint32_t a0 = off & ~3u, sh = 8u * (off & 3u);               // sh: 0 or 16
         uint32_t t[ND];
@@ -448,6 +476,18 @@ __device__ __forceinline__ void gemv_block(const __amdgpu_buffer_rsrc_t& rw, int
                 const uint32_t by = (q[j >> 2] >> (8 * (j & 3))) & 0xffu;
                 w[j] = __fmaf_rn((float)(by & 15u), d, o);
                 w[16 + j] = __fmaf_rn((float)(by >> 4), d, o);
+            }
+        } else if constexpr (WT == CBX_WTYPE_Q5_0) {
+            // q[0] = qh; element j < 16: low nibble of byte j of q[1..4] and
+            // qh bit j, element 16 + j: its high nibble and qh bit 16 + j;
+            // (q - 16) d is exact in fp32, and so is the fma
+            const uint32_t qh = q[0];
+            const float o = __fmul_rn(d, -16.0f);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t by = (q[1 + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+                w[j] = __fmaf_rn((float)((by & 15u) | (((qh >> j) & 1u) << 4)), d, o);
+                w[16 + j] = __fmaf_rn((float)((by >> 4) | (((qh >> (16 + j)) & 1u) << 4)), d, o);
             }
         } else {
             const float o = __fmul_rn(d, -128.0f);
@@ -541,7 +581,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
             hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
         }
     }
-    constexpr int64_t kBB = WT == CBX_WTYPE_F16 ? 64 : (WT == CBX_WTYPE_Q4_0 ? 18 : 34);
+    constexpr int64_t kBB = block_bytes<WT>();
     const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
@@ -690,6 +730,10 @@ hipError_t mfma_dispatch(const void* W, int32_t wtype, const float* bias, const 
                 return launch_mfma<CBX_WTYPE_Q4_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
                                                       ld_out, n_rows, n_vocab, n_embd, stream, kz,
                                                      gelu_out);
+            case CBX_WTYPE_Q5_0:
+                return launch_mfma<CBX_WTYPE_Q5_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
+                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz,
+                                                      gelu_out);
             case CBX_WTYPE_Q8_0:
                 return launch_mfma<CBX_WTYPE_Q8_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
                                                       ld_out, n_rows, n_vocab, n_embd, stream, kz,
@@ -698,7 +742,7 @@ hipError_t mfma_dispatch(const void* W, int32_t wtype, const float* bias, const 
                 return hipErrorInvalidValue;
         }
     }
-    const bool two = wtype == CBX_WTYPE_Q4_0 || n_tiles <= 2;
+    const bool two = wtype == CBX_WTYPE_Q4_0 || wtype == CBX_WTYPE_Q5_0 || n_tiles <= 2;
     switch (wtype) {
         case CBX_WTYPE_F16:
             return two ? launch_mfma<CBX_WTYPE_F16, 2>(W, bias, parts, inv, n_tiles, out0, out1,
@@ -707,6 +751,9 @@ hipError_t mfma_dispatch(const void* W, int32_t wtype, const float* bias, const 
                                                        ld_out, n_rows, n_vocab, n_embd, stream);
         case CBX_WTYPE_Q4_0:
             return launch_mfma<CBX_WTYPE_Q4_0, 2>(W, bias, parts, inv, n_tiles, out0, out1, ld_out,
+                                                  n_rows, n_vocab, n_embd, stream);
+        case CBX_WTYPE_Q5_0:
+            return launch_mfma<CBX_WTYPE_Q5_0, 2>(W, bias, parts, inv, n_tiles, out0, out1, ld_out,
                                                   n_rows, n_vocab, n_embd, stream);
         case CBX_WTYPE_Q8_0:
             return two ? launch_mfma<CBX_WTYPE_Q8_0, 2>(W, bias, parts, inv, n_tiles, out0, out1,
@@ -766,6 +813,10 @@ hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const 
                 return launch_gemv_r<CBX_WTYPE_Q4_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
                                                      out1, ld_out, n_rows, n_vocab, n_embd, stream,
                                                     gelu_out ? 1 : 0);
+            case CBX_WTYPE_Q5_0:
+                return launch_gemv_r<CBX_WTYPE_Q5_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
+                                                     out1, ld_out, n_rows, n_vocab, n_embd, stream,
+                                                     gelu_out ? 1 : 0);
             case CBX_WTYPE_Q8_0:
                 return launch_gemv_r<CBX_WTYPE_Q8_0>(W, bias, hidden0, hidden1, ld_hidden, out0,
                                                      out1, ld_out, n_rows, n_vocab, n_embd, stream,
@@ -813,6 +864,10 @@ hipError_t launch_head_gemv_norm(const void* W, int32_t wtype, const float* bias
                                                        stream, g, nm);
         case CBX_WTYPE_Q4_0:
             return launch_gemv<CBX_WTYPE_Q4_0, 2, true>(W, bias, nullptr, nullptr, n_embd, out,
+                                                        nullptr, ld_out, n_rows, n_vocab, n_embd,
+                                                        stream, g, nm);
+        case CBX_WTYPE_Q5_0:
+            return launch_gemv<CBX_WTYPE_Q5_0, 2, true>(W, bias, nullptr, nullptr, n_embd, out,
                                                         nullptr, ld_out, n_rows, n_vocab, n_embd,
                                                         stream, g, nm);
         case CBX_WTYPE_Q8_0:

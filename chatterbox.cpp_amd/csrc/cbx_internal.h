@@ -112,6 +112,16 @@ hipError_t launch_decode_v1024x32(const KernelArgs& a, hipStream_t stream);
 // head_scratch_bytes(n_rows, hidden1 != NULL, n_embd) bytes (the activations
 // split for the matrix cores; 0 bytes, and NULL allowed, below 16 rows).
 size_t head_scratch_bytes(int32_t n_rows, bool cfg, int32_t n_embd);
+// Bytes per block of 32 weights of a CBX_WTYPE_* (0 for an unknown type).
+inline int64_t wtype_block_bytes(int32_t wtype) {
+    switch (wtype) {
+        case CBX_WTYPE_F16: return 64;
+        case CBX_WTYPE_Q4_0: return 18;
+        case CBX_WTYPE_Q5_0: return 22;
+        case CBX_WTYPE_Q8_0: return 34;
+        default: return 0;
+    }
+}
 // Whether launch_head takes the mat-vec (fewer than 16 projected rows whose
 // activations fit its LDS) rather than the split and the matrix cores.
 bool head_uses_gemv(int32_t n_rows, bool cfg, int32_t n_embd);

@@ -19,7 +19,7 @@
 // 0.044715 x^2))) (Hendrycks and Gimpel's approximation, ggml_gelu's).
 //
 // The four matrix products of a layer have the speech_head's shape (rows of
-// n_in weights per output, F16 / Q4_0 / Q8_0): they run on the head's
+// n_in weights per output, F16 / Q4_0 / Q5_0 / Q8_0): they run on the head's
 // kernels (fp16 matrix cores on split activations from 16 rows, a mat-vec
 // below).  From 16 rows the layer norms write the split activations of the
 // products they feed themselves, and the two products the residual adds

@@ -5,7 +5,7 @@
  * (src/main.cpp:356-399): the speech vocabulary size and the stop token from
  * the keys of src/chatterbox_t3_internal.h:33-40, and the tensors
  * chatterbox/speech_head (ggml ne = [n_embd, n_vocab], F16 by default,
- * Q4_0 / Q8_0 when converted with --quant, scripts/convert-t3-turbo-to-gguf.py
+ * Q4_0 / Q5_0 / Q8_0 when converted with --quant, scripts/convert-t3-turbo-to-gguf.py
  * :65-104, :160-163) and chatterbox/speech_head_bias (F32 [n_vocab]).  These
  * entry points read the same items from the file for cbx_head: the parse
  * runs on the host only; the load copies the tensor bytes to device buffers
@@ -16,7 +16,7 @@
  * Return codes as in cbx_sampler.h; cbx_last_error() gives the reason.
  * Every size and offset read from the file is checked against the file size
  * before use: a damaged or truncated file is CBX_ERR_INVALID, a head in a
- * format cbx_head does not take (e.g. Q5_0) CBX_ERR_UNSUPPORTED. */
+ * format cbx_head does not take (e.g. Q4_1, K-quants) CBX_ERR_UNSUPPORTED. */
 #ifndef CBX_GGUF_H
 #define CBX_GGUF_H
 
@@ -32,7 +32,7 @@ extern "C" {
 typedef struct cbx_head_file {
     int32_t  n_vocab;            /* speech_head ne[1] (rows, one per vocab id)      */
     int32_t  n_embd;             /* speech_head ne[0]; chatterbox.n_embd if present */
-    int32_t  wtype;              /* CBX_WTYPE_F16 / _Q4_0 / _Q8_0                   */
+    int32_t  wtype;              /* CBX_WTYPE_F16 / _Q4_0 / _Q5_0 / _Q8_0           */
     int32_t  has_bias;           /* 1 if chatterbox/speech_head_bias is present     */
     int32_t  speech_vocab_size;  /* chatterbox.speech_vocab_size, -1 if absent      */
     int32_t  start_speech_token; /* chatterbox.start_speech_token, -1 if absent     */
@@ -67,7 +67,7 @@ int cbx_gguf_load_head(const char* path, const cbx_head_file* info, void* d_weig
  * gguf.py:150-189): model/wpe (F32 [n_embd, n_ctx]), chatterbox/speech_emb
  * (F16 or F32 [n_embd, n_speech_vocab]), model/ln_f/{g,b} and per layer i
  * model/h<i>/ln_1/{g,b}, ln_2/{g,b}, attn/c_attn/{w,b}, attn/c_proj/{w,b},
- * mlp/c_fc/{w,b}, mlp/c_proj/{w,b}: the four matrices F16, Q4_0 or Q8_0 (one
+ * mlp/c_fc/{w,b}, mlp/c_proj/{w,b}: the four matrices F16, Q4_0, Q5_0 or Q8_0 (one
  * type for all), the rest F32. */
 typedef struct cbx_t3_file {
     int32_t  n_layer;

@@ -185,6 +185,9 @@ int cbx_sample_batch_static(cbx_sampler* s, const cbx_batch* b, void* stream);
 #define CBX_WTYPE_Q4_0 2 /* 18-byte blocks of 32: fp16 d, 16 bytes of nibbles
                             (element j < 16 low nibble of byte j, j + 16 high);
                             w = (q - 8) * d                                       */
+#define CBX_WTYPE_Q5_0 6 /* 22-byte blocks of 32: fp16 d, 32-bit little-endian qh
+                            (bit j: fifth bit of element j), 16 bytes of nibbles
+                            as Q4_0; w = (q - 16) * d                             */
 #define CBX_WTYPE_Q8_0 8 /* 34-byte blocks of 32: fp16 d, 32 int8; w = q * d     */
 
 /* The T3 speech_head projection, logits = W h + b (src/main.cpp:577; weights

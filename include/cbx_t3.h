@@ -14,7 +14,7 @@
  * batched decode loop stays on the device.
  *
  * Device pointers throughout; fp32 except the four matrices of every layer,
- * which take the speech_head's formats (CBX_WTYPE_F16 / Q4_0 / Q8_0, rows of
+ * which take the speech_head's formats (CBX_WTYPE_F16 / Q4_0 / Q5_0 / Q8_0, rows of
  * n_in weights per output, ggml ne = [n_in, n_out]).
  */
 #ifndef CBX_T3_H

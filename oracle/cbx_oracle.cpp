@@ -434,49 +434,79 @@ static uint16_t float_to_half(float f) {
     return (uint16_t)out;
 }
 
+static size_t block_bytes(int32_t wtype) {
+    return wtype == 2 ? 18 : wtype == 6 ? 22 : 34;
+}
+
+// The formats' values (ggml's block layouts: ggml-common.h block_q4_0,
+// block_q5_0, block_q8_0 -- a third-party dependency the reference links and
+// does not vendor; the layouts are the GGUF format's).
 void cbx_oracle_dequant_row(const uint8_t* blocks, int32_t wtype, int32_t n_embd, float* out) {
     const int nb = n_embd / 32;
+    const size_t bsz = block_bytes(wtype);
     for (int b = 0; b < nb; ++b) {
-        if (wtype == 2) {  // Q4_0: 2-byte d + 16 bytes
-            const uint8_t* blk = blocks + (size_t)b * 18;
-            uint16_t dh;
-            std::memcpy(&dh, blk, 2);
-            const float d = half_to_float(dh);
+        const uint8_t* blk = blocks + (size_t)b * bsz;
+        uint16_t dh;
+        std::memcpy(&dh, blk, 2);
+        const float d = half_to_float(dh);
+        if (wtype == 2) {  // Q4_0: d, 16 bytes of nibbles
             for (int j = 0; j < 16; ++j) {
                 out[b * 32 + j] = (float)((int)(blk[2 + j] & 0x0f) - 8) * d;
                 out[b * 32 + j + 16] = (float)((int)(blk[2 + j] >> 4) - 8) * d;
             }
-        } else {  // Q8_0: 2-byte d + 32 int8
-            const uint8_t* blk = blocks + (size_t)b * 34;
-            uint16_t dh;
-            std::memcpy(&dh, blk, 2);
-            const float d = half_to_float(dh);
+        } else if (wtype == 6) {  // Q5_0: d, qh (little-endian u32), 16 bytes of nibbles
+            const uint32_t qh = (uint32_t)blk[2] | (uint32_t)blk[3] << 8 |
+                                (uint32_t)blk[4] << 16 | (uint32_t)blk[5] << 24;
+            for (int j = 0; j < 16; ++j) {
+                const int q0 = (blk[6 + j] & 0x0f) | (int)((qh >> j) & 1u) << 4;
+                const int q1 = (blk[6 + j] >> 4) | (int)((qh >> (16 + j)) & 1u) << 4;
+                out[b * 32 + j] = (float)(q0 - 16) * d;
+                out[b * 32 + j + 16] = (float)(q1 - 16) * d;
+            }
+        } else {  // Q8_0: d, 32 int8
             for (int j = 0; j < 32; ++j) out[b * 32 + j] = (float)(int8_t)blk[2 + j] * d;
         }
     }
 }
 
+// The quantizer of the reference's converter, gguf-py 0.18's
+// gguf.quants.quantize (scripts/convert-t3-turbo-to-gguf.py:78-104), per
+// block of 32: Q4_0 / Q5_0 take the signed value of largest magnitude mx,
+// d = mx / -8 (-16), id = 1 / d (0 for d = 0), q = trunc(float(double(x) *
+// double(id) + 8.5 (16.5))) clipped to [0, 15] ([0, 31]) -- the product
+// exact in binary64, one rounding to binary64 and one to binary32 before the
+// truncation; Q8_0 d = max|x| / 127, q = round half away from zero of x * id
+// in binary32.  d is stored as binary16 (round to nearest even).
 void cbx_oracle_quantize(const float* w, int32_t n_rows, int32_t n_embd, int32_t wtype,
                          uint8_t* blocks_out) {
     const int nb = n_embd / 32;
-    const size_t bsz = (wtype == 2) ? 18 : 34;
+    const size_t bsz = block_bytes(wtype);
     for (int32_t r = 0; r < n_rows; ++r) {
         for (int b = 0; b < nb; ++b) {
             const float* x = w + (size_t)r * n_embd + b * 32;
             uint8_t* blk = blocks_out + ((size_t)r * nb + b) * bsz;
-            if (wtype == 2) {
+            std::memset(blk, 0, bsz);
+            if (wtype == 2 || wtype == 6) {
+                const int qmax = wtype == 2 ? 15 : 31;
+                const float half = wtype == 2 ? 8.0f : 16.0f;
                 float amax = 0.0f, mx = 0.0f;
                 for (int j = 0; j < 32; ++j)
                     if (amax < std::fabs(x[j])) { amax = std::fabs(x[j]); mx = x[j]; }
-                const float d = mx / -8.0f;
+                const float d = mx / -half;
                 const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
                 const uint16_t dh = float_to_half(d);
                 std::memcpy(blk, &dh, 2);
-                for (int j = 0; j < 16; ++j) {
-                    const float x0 = x[j] * id, x1 = x[16 + j] * id;
-                    const int q0 = std::min(15, (int)(int8_t)(x0 + 8.5f));
-                    const int q1 = std::min(15, (int)(int8_t)(x1 + 8.5f));
-                    blk[2 + j] = (uint8_t)(q0 | (q1 << 4));
+                int q[32];
+                for (int j = 0; j < 32; ++j) {
+                    const double t = (double)x[j] * (double)id + ((double)half + 0.5);
+                    q[j] = std::min(qmax, std::max(0, (int)std::trunc((float)t)));
+                }
+                uint8_t* qs = blk + (wtype == 2 ? 2 : 6);
+                for (int j = 0; j < 16; ++j) qs[j] = (uint8_t)((q[j] & 15) | (q[16 + j] & 15) << 4);
+                if (wtype == 6) {
+                    uint32_t qh = 0;
+                    for (int j = 0; j < 32; ++j) qh |= (uint32_t)(q[j] >> 4) << j;
+                    for (int i = 0; i < 4; ++i) blk[2 + i] = (uint8_t)(qh >> (8 * i));
                 }
             } else {
                 float amax = 0.0f;
@@ -494,7 +524,7 @@ void cbx_oracle_quantize(const float* w, int32_t n_rows, int32_t n_embd, int32_t
 void cbx_oracle_head_f64(const uint8_t* W, int32_t wtype, const float* bias,
                          const float* hidden, int32_t n_rows, int32_t n_vocab,
                          int32_t n_embd, double* out) {
-    const size_t row_bytes = (size_t)(n_embd / 32) * ((wtype == 2) ? 18 : 34);
+    const size_t row_bytes = (size_t)(n_embd / 32) * block_bytes(wtype);
     std::vector<float> wrow(n_embd);
     for (int32_t v = 0; v < n_vocab; ++v) {
         cbx_oracle_dequant_row(W + (size_t)v * row_bytes, wtype, n_embd, wrow.data());

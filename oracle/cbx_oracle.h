@@ -111,14 +111,18 @@ double cbx_oracle_sample_batch(const float* logits, const float* logits_uncond,
                                const double* u, int32_t n_threads,
                                int32_t* tokens_out, uint32_t* info_out);
 
-/* Q4_0 / Q8_0 blocks of 32 weights (ggml layout: fp16 scale d, then 16 bytes
- * of nibbles -- low nibbles hold elements 0..15, high nibbles 16..31 -- or 32
- * int8 values).  Dequantise one row of n_embd weights to fp32. */
+/* Q4_0 / Q5_0 / Q8_0 blocks of 32 weights (ggml layout: fp16 scale d, then
+ * 16 bytes of nibbles -- low nibbles hold elements 0..15, high nibbles
+ * 16..31 --; Q5_0 puts a little-endian 32-bit word of fifth bits (bit j for
+ * element j) between d and the nibbles; Q8_0 32 int8 values).  Dequantise
+ * one row of n_embd weights to fp32: (q - 8) d, (q - 16) d, q d. */
 void cbx_oracle_dequant_row(const uint8_t* blocks, int32_t wtype, int32_t n_embd, float* out);
 
-/* Quantise fp32 rows to Q4_0 (wtype 2) or Q8_0 (wtype 8), round-to-nearest
- * with the ggml reference rule (d = max|x| signed / -8 for Q4_0, amax/127 for
- * Q8_0).  Output rows are n_embd/32 blocks. */
+/* Quantise fp32 rows to Q4_0 (wtype 2), Q5_0 (wtype 6) or Q8_0 (wtype 8)
+ * with the reference converter's quantizer, gguf-py's (d = the signed value of
+ * largest magnitude / -8 or / -16, q = trunc(x / d + 8.5 or 16.5) clipped;
+ * Q8_0 d = amax / 127, q rounded half away from zero).  Output rows are
+ * n_embd/32 blocks. */
 void cbx_oracle_quantize(const float* w, int32_t n_rows, int32_t n_embd, int32_t wtype,
                          uint8_t* blocks_out);
 

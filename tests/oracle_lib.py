@@ -186,8 +186,8 @@ def stdlib_draw(probs, x0, x1):
 
 
 # ---- speech_head formats (oracle/cbx_oracle.cpp) ----
-WTYPE_F16, WTYPE_Q4_0, WTYPE_Q8_0 = 1, 2, 8
-BLOCK_BYTES = {WTYPE_Q4_0: 18, WTYPE_Q8_0: 34}
+WTYPE_F16, WTYPE_Q4_0, WTYPE_Q5_0, WTYPE_Q8_0 = 1, 2, 6, 8
+BLOCK_BYTES = {WTYPE_Q4_0: 18, WTYPE_Q5_0: 22, WTYPE_Q8_0: 34}
 
 
 def quantize(w, wtype):

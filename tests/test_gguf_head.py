@@ -50,6 +50,7 @@ def _code(mod, path):
 @pytest.mark.parametrize("wtype,ggml_type,V,K", [
     (O.WTYPE_Q4_0, G.GGML_Q4_0, 6563, 1024),   # the Turbo head, --quant q4_0
     (O.WTYPE_Q8_0, G.GGML_Q8_0, 300, 64),
+    (O.WTYPE_Q5_0, G.GGML_Q5_0, 6563, 1024),   # --quant q5_0
     (O.WTYPE_F16, G.GGML_F16, 8194, 64),       # F16, the converter's default
 ])
 def test_reads_the_head(mod, tmp_path, wtype, ggml_type, V, K):
@@ -112,8 +113,8 @@ def test_rejects_damaged_and_mismatched_files(mod, tmp_path):
         "version 1": (G.build([], [], version=1)[0], CBX_ERR_UNSUPPORTED),
         "version 4": (G.build([], [], version=4)[0], CBX_ERR_UNSUPPORTED),
         "no head": (G.build([("a", G.U32, 1)], [])[0], CBX_ERR_INVALID),
-        "Q5_0 head": (G.build([], [("chatterbox/speech_head", (64, 8), G.GGML_Q5_0,
-                                    b"\0" * 22 * 2 * 8)])[0], CBX_ERR_UNSUPPORTED),
+        "Q4_1 head": (G.build([], [("chatterbox/speech_head", (64, 8), 3,
+                                    b"\0" * 20 * 2 * 8)])[0], CBX_ERR_UNSUPPORTED),
         "F32 head": (G.build([], [("chatterbox/speech_head", (64, 8), G.GGML_F32,
                                    b"\0" * 4 * 64 * 8)])[0], CBX_ERR_UNSUPPORTED),
         "3-D head": (G.build([], [("chatterbox/speech_head", (64, 8, 1), G.GGML_Q4_0,

@@ -12,7 +12,8 @@ import gguf_writer as G
 import oracle_lib as O
 import pkg
 
-GGML = {O.WTYPE_F16: G.GGML_F16, O.WTYPE_Q4_0: G.GGML_Q4_0, O.WTYPE_Q8_0: G.GGML_Q8_0}
+GGML = {O.WTYPE_F16: G.GGML_F16, O.WTYPE_Q4_0: G.GGML_Q4_0, O.WTYPE_Q5_0: G.GGML_Q5_0,
+        O.WTYPE_Q8_0: G.GGML_Q8_0}
 
 
 @pytest.fixture(scope="module")
@@ -88,7 +89,7 @@ def _code(mod, path):
     return 0
 
 
-@pytest.mark.parametrize("wtype", [O.WTYPE_F16, O.WTYPE_Q4_0, O.WTYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [O.WTYPE_F16, O.WTYPE_Q4_0, O.WTYPE_Q5_0, O.WTYPE_Q8_0])
 def test_reads_the_t3_model(mod, tmp_path, wtype):
     rng = np.random.default_rng(31 + wtype)
     data, _ = make_t3(rng, wtype=wtype, emb_f16=wtype != O.WTYPE_F16)
@@ -97,7 +98,7 @@ def test_reads_the_t3_model(mod, tmp_path, wtype):
     assert (info.n_layer, info.n_embd, info.n_head, info.n_pos, info.n_speech_vocab) == (L, n, 4, 32, 300)
     assert info.wtype == wtype and info.eps == np.float32(1e-5)
     assert (info.start_speech_token, info.stop_speech_token, info.gguf_version) == (298, 299, 3)
-    bb = {O.WTYPE_F16: 64, O.WTYPE_Q4_0: 18, O.WTYPE_Q8_0: 34}[wtype]
+    bb = {O.WTYPE_F16: 64, O.WTYPE_Q4_0: 18, O.WTYPE_Q5_0: 22, O.WTYPE_Q8_0: 34}[wtype]
     r = lambda x: (x + 255) // 256 * 256
     want = r(4 * n * 32) + r(4 * n * 300) + 2 * r(4 * n)
     want += L * (4 * r(4 * n) + r(4 * 3 * n) + 2 * r(4 * n) + r(4 * 4 * n)
@@ -127,13 +128,13 @@ def test_rejects_damaged_and_mismatched_files(mod, tmp_path):
     for kw, code in cases:
         data, _ = make_t3(rng, **kw)
         assert _code(mod, _write(tmp_path, data)) == code, kw
-    # every matrix in a format the kernels do not take (Q5_0: 22-byte blocks)
-    q5 = {}
+    # every matrix in a format the kernels do not take (Q4_1: 20-byte blocks)
+    q41 = {}
     for l in range(2):
         for nm, (i, o) in (("attn/c_attn/w", (256, 768)), ("attn/c_proj/w", (256, 256)),
                            ("mlp/c_fc/w", (256, 1024)), ("mlp/c_proj/w", (1024, 256))):
-            q5[f"model/h{l}/{nm}"] = ((i, o), G.GGML_Q5_0, bytes(o * i // 32 * 22))
-    data, _ = make_t3(rng, override=q5)
+            q41[f"model/h{l}/{nm}"] = ((i, o), 3, bytes(o * i // 32 * 20))
+    data, _ = make_t3(rng, override=q41)
     assert _code(mod, _write(tmp_path, data)) == UNS
 
 

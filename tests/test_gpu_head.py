@@ -89,6 +89,10 @@ CASES = [
     (O.WTYPE_Q4_0, 300, 64, 5, 301),
     (O.WTYPE_F16, 500, 8192, 1, 500),
     (O.WTYPE_Q4_0, 700, 512, 16, 700),       # 16 rows: the matrix-core tiles again
+    (O.WTYPE_Q5_0, 6563, 1024, 128, 6563),   # Q5_0 (--quant q5_0): the matrix cores
+    (O.WTYPE_Q5_0, 300, 64, 17, 301),        #   ragged tiles on both axes
+    (O.WTYPE_Q5_0, 6563, 1024, 2, 6563),     #   the mat-vec, one CFG pair
+    (O.WTYPE_Q5_0, 1000, 4096, 3, 1000),     #   the mat-vec, long rows
 ]
 
 
@@ -107,7 +111,7 @@ def test_head_logits_against_f64(cbx, torch_cuda, case):
         assert np.all(got[:, V:] == -7.0), "stores past n_vocab"
 
 
-@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q5_0, O.WTYPE_Q8_0, O.WTYPE_F16])
 def test_head_from_gguf(cbx, torch_cuda, tmp_path, wtype):
     """cbx_gguf_read_head + cbx_gguf_load_head (csrc/cbx_gguf.cpp) put the
     file's speech_head and bias in device memory byte for byte, and the
@@ -118,7 +122,8 @@ def test_head_from_gguf(cbx, torch_cuda, tmp_path, wtype):
     V, K, R = 700, 256, 24
     rng = np.random.default_rng(40 + wtype)
     blocks, bias, h = _problem(rng, V, K, R, wtype)
-    gt = {O.WTYPE_Q4_0: G.GGML_Q4_0, O.WTYPE_Q8_0: G.GGML_Q8_0, O.WTYPE_F16: G.GGML_F16}[wtype]
+    gt = {O.WTYPE_Q4_0: G.GGML_Q4_0, O.WTYPE_Q5_0: G.GGML_Q5_0, O.WTYPE_Q8_0: G.GGML_Q8_0,
+          O.WTYPE_F16: G.GGML_F16}[wtype]
     data, _, _ = G.t3_head_file(blocks, gt, K, bias, stop=V - 1, start=V - 2)
     path = tmp_path / "head.gguf"
     path.write_bytes(data)
@@ -138,7 +143,7 @@ def test_head_from_gguf(cbx, torch_cuda, tmp_path, wtype):
     assert np.all(np.abs(got.astype(np.float64) - ref) <= tol)
 
 
-@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q5_0, O.WTYPE_Q8_0, O.WTYPE_F16])
 def test_head_row_magnitudes(cbx, torch_cuda, wtype):
     """The matrix-core path scales each activation row by its own power of two
     before splitting it into two fp16 parts: rows of magnitude 1e6 (past the
@@ -174,7 +179,7 @@ def test_head_without_bias(cbx, torch_cuda):
 
 
 @pytest.mark.parametrize("B,S", [(64, 2), (1, 1), (7, 1)])
-@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q5_0, O.WTYPE_Q8_0, O.WTYPE_F16])
 def test_fused_head_sample_cfg(cbx, torch_cuda, wtype, B, S):
     """B CFG streams, S steps: projection of cond and uncond hidden rows
     (weights from N(0, 0.02), hidden rows N(0, 1)), then the sampler (k 1000,

@@ -107,7 +107,7 @@ def close(got, want):
 
 
 @pytest.mark.parametrize("B", [20, 5, 2, 1])
-@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16])
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q4_0, O.WTYPE_Q5_0, O.WTYPE_Q8_0, O.WTYPE_F16])
 def test_t3_step_matches_oracle(cbx, torch_cuda, wtype, B):
     """B streams, 4 steps with per-stream ids; in step 2 every third stream
     sits out (state not running), so positions differ afterwards.  Each step's
@@ -299,21 +299,23 @@ def test_t3_rejects_bad_arguments(cbx, torch_cuda):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("wtype", [O.WTYPE_Q8_0, O.WTYPE_Q5_0])
 @pytest.mark.parametrize("B", [18, 3])
-def test_t3_from_gguf(cbx, torch_cuda, tmp_path, B):
-    """A T3 GGUF (2 layers, n_embd 256, Q8_0 matrices, speech_emb F16 as the
-    converter writes it) loaded by cbx_gguf_load_t3 into one device buffer:
-    3 steps of cbx_t3_step match the oracle built from the file's values."""
+def test_t3_from_gguf(cbx, torch_cuda, tmp_path, B, wtype):
+    """A T3 GGUF (2 layers, n_embd 256, Q8_0 or Q5_0 matrices -- the
+    converter's --quant q8_0 / q5_0 -- speech_emb F16 as the converter writes
+    it) loaded by cbx_gguf_load_t3 into one device buffer: 3 steps of
+    cbx_t3_step match the oracle built from the file's values."""
     import test_gguf_t3 as GT
     torch = torch_cuda
     mod, s = cbx
-    rng = np.random.default_rng(0x7340 + B)
-    data, vals = GT.make_t3(rng)
+    rng = np.random.default_rng(0x7340 + B + wtype)
+    data, vals = GT.make_t3(rng, wtype=wtype)
     path = tmp_path / "t3.gguf"
     path.write_bytes(data)
-    say(f"t3 from gguf B={B}")
+    say(f"t3 from gguf B={B} wtype={wtype}")
     info, dm = mod.load_t3_gguf(str(path))
-    assert (info.n_layer, info.n_embd, info.wtype) == (2, 256, O.WTYPE_Q8_0)
+    assert (info.n_layer, info.n_embd, info.wtype) == (2, 256, wtype)
     rm = T3.Model(vals["layers"], vals["wpe"], vals["speech_emb"], vals["ln_f_g"],
                   vals["ln_f_b"], 1e-5, 4)
     kd = torch.zeros((B, 2, 4, 32, 64), dtype=torch.float32, device="cuda")

@@ -1,12 +1,17 @@
 """Pins of the oracle's speech_head weight formats (oracle/cbx_oracle.cpp):
-ggml's Q4_0 / Q8_0 blocks of 32 (fp16 scale d first; Q4_0 element j < 16 in
-the low nibble of byte j, element j + 16 in its high nibble, w = (q - 8) d;
-Q8_0 w = q d), quantized with ggml's reference rules (Q4_0: d = the signed
-largest-magnitude value / -8, q = min(15, trunc(x / d + 8.5)); Q8_0:
-d = max|x| / 127, q = round half away from zero), the rules the reference's
-converter gets from gguf.quants.quantize (scripts/convert-t3-turbo-to-gguf.py:
-86-104).  Known-answer blocks worked by hand, the error bounds the rules
-imply on random rows, and the binary64 head against a direct product.
+ggml's Q4_0 / Q5_0 / Q8_0 blocks of 32 (fp16 scale d first; Q4_0 element
+j < 16 in the low nibble of byte j, element j + 16 in its high nibble,
+w = (q - 8) d; Q5_0 a little-endian 32-bit word qh after d whose bit j is the
+fifth bit of element j, then nibbles as Q4_0, w = (q - 16) d; Q8_0 w = q d),
+quantized with the rules the reference's converter gets from
+gguf.quants.quantize (scripts/convert-t3-turbo-to-gguf.py:78-104; Q4_0 / Q5_0:
+d = the signed largest-magnitude value / -8 or / -16, q = trunc(x / d + 8.5
+or 16.5) clipped to [0, 15] or [0, 31]; Q8_0: d = max|x| / 127, q = round
+half away from zero).  Known-answer blocks worked by hand, the error bounds
+the rules imply on random rows, and the binary64 head against a direct
+product.  gguf-py itself is not installed here: the quantizer (which only
+makes test weights; the kernels read whatever blocks a file holds) is pinned
+by the hand-worked blocks alone.
 """
 import numpy as np
 
@@ -43,6 +48,58 @@ def test_q8_0_known_blocks():
     assert np.array_equal(deq, rows)
 
 
+def test_q5_0_known_block():
+    # x_j = (p_j - 16) / 2 for a permutation p of 0..31 (p_1 = 0: the largest
+    # magnitude is x_1 = -8, so d = 0.5 and q_j = trunc(p_j + 0.5) = p_j).
+    # qs byte j = (p_j & 15) | (p_{j+16} & 15) << 4; qh bit j = p_j >> 4.
+    p = [25, 0, 17, 8, 30, 3, 12, 21, 6, 29, 14, 1, 19, 10, 27, 4,
+         11, 22, 2, 31, 16, 7, 24, 13, 9, 28, 5, 18, 15, 26, 20, 23]
+    x = ((np.array(p) - 16) / 2.0).astype(np.float32)[None, :]
+    b = O.quantize(x, O.WTYPE_Q5_0)[0]
+    want = bytes([0x00, 0x38,              # d = 0.5 in binary16
+                  0x95, 0x52, 0x5A, 0xEA,  # qh, little-endian
+                  0xB9, 0x60, 0x21, 0xF8, 0x0E, 0x73, 0x8C, 0xD5,
+                  0x96, 0xCD, 0x5E, 0x21, 0xF3, 0xAA, 0x4B, 0x74])
+    assert bytes(b) == want
+    deq = O.dequantize(b[None, :], O.WTYPE_Q5_0, 32)[0]
+    assert np.array_equal(deq, x[0])  # every step of 0.5 in [-8, 7.5] is exact
+
+
+def test_q5_0_clipped_block():
+    # the largest magnitude positive (x_0 = 8): d = -0.5; -8 maps to
+    # trunc(32.5) = 32, clipped to 31 (-7.5); 0.25 -> 16, -0.25 -> 17,
+    # 0.3 -> trunc(15.9) = 15, -0.3 -> 17, 7.7 -> 1, -7.74 -> 31, 0 -> 16
+    x = np.zeros(32, np.float32)
+    x[:8] = [8, -8, 0.25, -0.25, 0.3, -0.3, 7.7, -7.74]
+    b = O.quantize(x[None, :], O.WTYPE_Q5_0)[0]
+    want = bytes([0x00, 0xB8,              # d = -0.5
+                  0xAE, 0xFF, 0xFF, 0xFF,  # fifth bits: q = 0,31,16,17,15,17,1,31, then 16s
+                  0x00, 0x0F, 0x00, 0x01, 0x0F, 0x01, 0x01, 0x0F] + [0x00] * 8)
+    assert bytes(b) == want
+    deq = O.dequantize(b[None, :], O.WTYPE_Q5_0, 32)[0]
+    assert list(deq[:8]) == [8.0, -7.5, 0.0, -0.5, 0.5, -0.5, 7.5, -7.5]
+    assert np.all(deq[8:] == 0.0)
+
+
+def test_q5_0_dequant_of_planted_bits():
+    # each of the 32 elements in turn: q = 16 + 15 (only its fifth bit and
+    # all four nibble bits set) against q = 16 elsewhere, d = 1 -- a wrong
+    # qh bit order, nibble half or offset moves the value off its element
+    for j in range(32):
+        blk = np.zeros(22, np.uint8)
+        blk[0:2] = [0x00, 0x3C]            # d = 1.0
+        qh = 0xFFFFFFFF                    # every element's fifth bit: q >= 16
+        blk[2:6] = np.frombuffer(qh.to_bytes(4, "little"), np.uint8)
+        blk[6 + (j % 16)] = 0x0F if j < 16 else 0xF0
+        deq = O.dequantize(blk[None, :], O.WTYPE_Q5_0, 32)[0]
+        want = np.zeros(32, np.float32)
+        want[j] = 15.0
+        assert np.array_equal(deq, want), j
+    blk = np.zeros(22, np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    assert np.all(O.dequantize(blk[None, :], O.WTYPE_Q5_0, 32)[0] == -16.0)  # q = 0
+
+
 def _scales(blocks, wtype, n_embd):
     bb = O.BLOCK_BYTES[wtype]
     nb = n_embd // 32
@@ -54,19 +111,20 @@ def test_quantize_error_bounds():
     rng = np.random.default_rng(11)
     w = (rng.standard_normal((64, 256)) * 0.05).astype(np.float32)
     w[3, :32] = 0.0  # an all-zero block: d = 0, every weight 0
-    for wtype, frac, qmax in ((O.WTYPE_Q4_0, 1.0, 8), (O.WTYPE_Q8_0, 0.5, 127)):
+    for wtype, frac, qmax in ((O.WTYPE_Q4_0, 1.0, 8), (O.WTYPE_Q5_0, 1.0, 16),
+                              (O.WTYPE_Q8_0, 0.5, 127)):
         b = O.quantize(w, wtype)
         assert b.shape == (64, 256 // 32 * O.BLOCK_BYTES[wtype])
         d = np.abs(_scales(b, wtype, 256))
         deq = O.dequantize(b, wtype, 256)
         err = np.abs(deq - w).reshape(64, 8, 32).max(axis=-1)
-        # Q4_0 rounds to the nearest step except the clipped +8 step (one d);
+        # Q4_0 / Q5_0 round to the nearest step except the clipped top step (one d);
         # Q8_0 to the nearest step; the binary16 scale (quantization divides
         # by the binary32 one) moves a weight q d by up to |q| d 2^-11
         assert np.all(err <= d * (frac + (qmax + 1) * 2.0 ** -11) + 1e-12)
         assert np.all(deq[3, :32] == 0.0)
-        # the largest-magnitude weight of each Q4_0 block is exact (q = 0)
-        if wtype == O.WTYPE_Q4_0:
+        # the largest-magnitude weight of each Q4_0 / Q5_0 block is exact (q = 0)
+        if wtype in (O.WTYPE_Q4_0, O.WTYPE_Q5_0):
             blk = w.reshape(64, 8, 32)
             i = np.abs(blk).argmax(axis=-1)
             mx = np.take_along_axis(blk, i[..., None], -1)[..., 0]
@@ -80,7 +138,7 @@ def test_head_f64_matches_direct_product():
     w = (rng.standard_normal((V, K)) * 0.1).astype(np.float32)
     h = rng.standard_normal((R, K)).astype(np.float32)
     bias = rng.standard_normal(V).astype(np.float32)
-    for wtype in (O.WTYPE_Q4_0, O.WTYPE_Q8_0, O.WTYPE_F16):
+    for wtype in (O.WTYPE_Q4_0, O.WTYPE_Q5_0, O.WTYPE_Q8_0, O.WTYPE_F16):
         b = O.quantize(w, wtype)
         got = O.head_f64(b, wtype, bias, h, V, K)
         deq = O.dequantize(b, wtype, K).astype(np.float64)
