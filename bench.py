@@ -643,6 +643,9 @@ def parse_args(argv=None):
                     help="untimed steps first (at least; rounded up to whole launches)")
     ap.add_argument("--steps-per-launch", type=int, default=1024)
     ap.add_argument("--slabs", type=int, default=2)
+    ap.add_argument("--latency-rows", type=int, default=None,
+                    help="the sampler's small-launch rule: calls of at most this many row-steps "
+                         "run the workgroup kernel (library default 512; 0: never)")
     ap.add_argument("--single-launch-steps", type=int, default=200,
                     help="also time this many steps issued one launch per step (0: skip)")
     ap.add_argument("--t3-steps", type=int, default=20,
@@ -691,6 +694,8 @@ def main():
     d_hlen = torch.from_numpy(hist_len).to(dev)
     d_par = torch.from_numpy(w.pack_params(params)).to(dev)
     sampler = mod.Sampler(device=0, max_vocab=32768, max_history=HIST_MAX)
+    if args.latency_rows is not None:
+        sampler.set_latency_rows(args.latency_rows)
     tokens = torch.empty(S * B, dtype=torch.int32, device=dev)
     philox_seed = 0xC0FFEE
 
@@ -759,7 +764,8 @@ def main():
                                  draw_mode=mod.CBX_DRAW_PHILOX, seed=philox_seed, step0=i,
                                  max_survivors=1000)
         ms = timed(torch, stream, one, args.single_launch_steps, warm=10)
-        single = {"ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1)}
+        single = {"ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1),
+                  "latency_rows": 512 if args.latency_rows is None else args.latency_rows}
 
     # the decode loop with its state on the device, beside a per-token host sync
     decode = None

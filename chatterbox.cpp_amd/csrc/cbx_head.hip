@@ -64,65 +64,43 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) {
 
 // ------------------------------------------------------------ activation split
 constexpr int kSplitThreads = 256;
-// Bytes of head_split's output for R rows (a multiple of 16) of n_embd: the
-// parts (4 bytes per activation), then R scales from the next 256-byte
-// boundary.
-size_t split_bytes(int R, int n_embd) {
-    return ((size_t)R * n_embd * 4 + 255) / 256 * 256 + (size_t)R * 4;
-}
 
-// One workgroup per padded row p = 16 T + m of the row tiles T (the tiles of
-// hidden0's n_rows rows, then those of hidden1's); rows past a set's n_rows
-// are written as zeros.  The row is read once into registers (thread t holds
-// the groups t, t + 256, ...: at most kSplitGroups of them, n_embd <= 16384).
-// Group j (activations 8j .. 8j + 7) of the row is lane 16 (j % 4) + m's
-// operand of block j / 4: dwords ((T nball + j/4) 512 + 4 lane) .. + 3 hold
-// its hi parts and the same + 256 its lo parts; inv[p] = 2^-s_p.
-constexpr int kSplitGroups = 16384 / 8 / kSplitThreads;
+// One thread per group of 8 activations of the padded rows p = 16 T + m of
+// the row tiles T (the tiles of hidden0's n_rows rows, then those of
+// hidden1's), in row order: thread i takes group j = i mod ng of row
+// p = i / ng.  The 4 groups of a block are 4 consecutive lanes, which share
+// the block's scale (cbx_split.h); rows past a set's n_rows are zeros.
 __global__ __launch_bounds__(kSplitThreads) void head_split(const float* hidden0,
                                                             const float* hidden1, int64_t ld_hidden,
-                                                            int n_rows, int n_embd,
+                                                            int n_rows, int n_embd, int R,
                                                             uint32_t* parts, float* inv) {
-    __shared__ float wmax[kSplitThreads / 64];
-    const int p = blockIdx.x, tid = threadIdx.x;
+    const int ng = n_embd / 8, nball = n_embd / 32;
+    const int64_t i = (int64_t)blockIdx.x * kSplitThreads + threadIdx.x;
+    const bool in = i < (int64_t)R * ng;  // a whole wave's blocks are in or out together
+    const int p = in ? (int)(i / ng) : 0, j = in ? (int)(i % ng) : 0;
     const int tps = (n_rows + 15) / 16, T = p / 16, m = p % 16;
     const int rr = (T % tps) * 16 + m;
-    const bool real = rr < n_rows;
+    const bool real = in && rr < n_rows;
     const float* src = (T < tps ? hidden0 : hidden1) + (int64_t)(real ? rr : 0) * ld_hidden;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(src), (short)0, real ? n_embd * 4 : 0, kBufWord3);
-    const int ng = n_embd / 8, nball = n_embd / 32;
-    float x[kSplitGroups][8];
+    const f4 a = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j, 0, 0));
+    const f4 c = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16, 0, 0));
+    float x[8];
     float mx = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kSplitGroups; ++q) {
-        const int j = tid + q * kSplitThreads;
-        if (q == 0 || j < ng) {  // past the row (or a padding row): zeros
-            const f4 a = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j, 0, 0));
-            const f4 b = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 32 * j + 16, 0, 0));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x[q][i] = a[i];
-                x[q][4 + i] = b[i];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(x[q][i]));
-        }
+    for (int e = 0; e < 4; ++e) {
+        x[e] = a[e];
+        x[4 + e] = c[e];
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < kSplitThreads / 64; ++w) mx = fmaxf(mx, wmax[w]);
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[e]));
+    mx = split_block_max4(mx);
+    if (!in) return;
     float sc, sinv;
     split_scale(mx, sc, sinv);
-    if (tid == 0) inv[p] = sinv;
-#pragma unroll
-    for (int q = 0; q < kSplitGroups; ++q) {
-        const int j = tid + q * kSplitThreads;
-        if (j < ng) split_store(parts, T, m, nball, j, x[q], sc);
-    }
+    split_store(parts, T, m, nball, j, x, sc);
+    if ((j & 3) == 0) inv[split_inv_index(T, m, nball, j >> 2)] = sinv;
 }
 
 // --------------------------------------------------------------- matrix cores
@@ -217,17 +195,23 @@ constexpr int KS = 4;  // waves per workgroup (runs of blocks along n_embd)
 // sets measured no faster than 2).
 constexpr int RING = 2;
 
-// parts, inv: head_split's output for the n_tiles row tiles (those of
-// hidden0, then those of hidden1).
+// parts, inv: the split activations of the n_tiles row tiles (those of
+// hidden0, then those of hidden1), cbx_split.h's layout; each block's
+// products are scaled back by its rows' 2^-s (exact) as they are added.
 // K split over workgroups (gridDim.z > 1): workgroup z takes blocks
 // [nball z / Z, nball (z + 1) / Z) and writes its partial products to
 // out0 + z * zstride (the bias in slab 0 only); the caller adds the slabs.
+// Split output (out_parts set, one row set, no K split): the outputs, gelu
+// applied when gelu_out, are written as the next product's split activations
+// (rows of n_vocab values: this workgroup's 32 outputs are block blockIdx.x
+// of each of its rows) instead of fp32 rows.
 template <int WT, int NT>
 __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float* bias,
                                                      const uint32_t* parts, const float* inv,
                                                      int n_tiles, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
-                                                     int n_embd, int64_t zstride, int gelu_out) {
+                                                     int n_embd, int64_t zstride, int gelu_out,
+                                                     uint32_t* out_parts, float* out_inv) {
     constexpr int BB = block_bytes<WT>();
     // Weights are staged per wave in chunks of CB blocks: for each of the 32
     // vocab rows the chunk's CB * BB bytes are contiguous, so whole-row dword
@@ -249,6 +233,9 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     const int pbytes = n_tiles * 16 * n_embd * 4;
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(parts), (short)0, pbytes, kBufWord3);
+    const int sbytes = n_tiles * 16 * (n_embd / 32) * 4;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(inv), (short)0, sbytes, kBufWord3);
     const int va = v0 + m, vb = v0 + 16 + m;
     // rows past the table read zeros (byte offsets past the range)
     const int va_c = va < n_vocab ? va : n_vocab, vb_c = vb < n_vocab ? vb : n_vocab;
@@ -256,11 +243,13 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     // of hidden0, then those of hidden1): set T / tps, rows 16 (T % tps) ...
     const int tps = (n_rows + 15) / 16;
     const int nball = n_embd / 32;
-    uint32_t hoff[NT];
+    uint32_t hoff[NT], soff[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int T = blockIdx.y * NT + t;
         hoff[t] = T < n_tiles ? (uint32_t)(T * nball * 512 + 4 * lane) * 4u : (uint32_t)pbytes;
+        // the scales of rows 4g .. 4g + 3 (the rows of this lane's outputs)
+        soff[t] = T < n_tiles ? (uint32_t)split_inv_index(T, 4 * g, nball, 0) * 4u : (uint32_t)sbytes;
     }
     f4 acc0[NT], acc1[NT];
 #pragma unroll
@@ -277,12 +266,14 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     // zeros past the buffer) and the block loop is unrolled by RING, so no
     // register copies (and no waits for the loads just issued) join the sets.
     u4v ph[RING][NT], pl[RING][NT];
+    f4 sv[RING][NT];
     auto load = [&](int kb, int r) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint32_t o = hoff[t] + (uint32_t)kb * 2048u;
             ph[r][t] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 0));
             pl[r][t] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(rp, o + 1024, 0, 0));
+            sv[r][t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, soff[t] + (uint32_t)kb * 64u, 0, 0));
         }
     };
 #pragma unroll
@@ -293,18 +284,29 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
     auto block = [&](int kb, int kbc, int sha, int shb, int r) {
         const u4v* const ch = ph[r];
         const u4v* const cl = pl[r];
+        const f4* const sc = sv[r];
         uint32_t qa[5], qb[5];
         lds_w<WT>(sw + m * RSW, sha + (kb - kbc) * BB, g, qa);
         lds_w<WT>(sw + (16 + m) * RSW, shb + (kb - kbc) * BB, g, qb);
         load(kb + RING - 1, (r + RING - 1) % RING);
         if constexpr (WT == CBX_WTYPE_F16) {
             const u4v wa = u4v{qa[0], qa[1], qa[2], qa[3]}, wb = u4v{qb[0], qb[1], qb[2], qb[3]};
+            f4 pa[NT], pb[NT];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                acc0[t] = mfma_f16(cl[t], wa, acc0[t]);
-                acc1[t] = mfma_f16(cl[t], wb, acc1[t]);
-                acc0[t] = mfma_f16(ch[t], wa, acc0[t]);
-                acc1[t] = mfma_f16(ch[t], wb, acc1[t]);
+                const f4 z = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                pa[t] = mfma_f16(cl[t], wa, z);
+                pb[t] = mfma_f16(cl[t], wb, z);
+                pa[t] = mfma_f16(ch[t], wa, pa[t]);
+                pb[t] = mfma_f16(ch[t], wb, pb[t]);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc0[t][i] = __fmaf_rn(pa[t][i], sc[t][i], acc0[t][i]);
+                    acc1[t][i] = __fmaf_rn(pb[t][i], sc[t][i], acc1[t][i]);
+                }
             }
         } else {
             float da, db;
@@ -318,12 +320,13 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
                 pa[t] = mfma_f16(ch[t], ia, pa[t]);
                 pb[t] = mfma_f16(ch[t], ib, pb[t]);
             }
+            // d 2^-s: exact (a power of two times a binary16 value)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    acc0[t][i] = __fmaf_rn(pa[t][i], da, acc0[t][i]);
-                    acc1[t][i] = __fmaf_rn(pb[t][i], db, acc1[t][i]);
+                    acc0[t][i] = __fmaf_rn(pa[t][i], __fmul_rn(da, sc[t][i]), acc0[t][i]);
+                    acc1[t][i] = __fmaf_rn(pb[t][i], __fmul_rn(db, sc[t][i]), acc1[t][i]);
                 }
             }
         }
@@ -390,11 +393,60 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
             }
         }
     }
-    // D[4g + i][m]: hidden row 4g + i of the tile, vocab ids va and vb; the
-    // scale 2^-s is exact
+    // D[4g + i][m]: hidden row 4g + i of the tile, vocab ids va and vb
     const bool with_bias = bias && blockIdx.z == 0;
     const float ba = with_bias && va < n_vocab ? bias[va] : 0.0f;
     const float bb = with_bias && vb < n_vocab ? bias[vb] : 0.0f;
+    if (out_parts) {
+        // the 32 outputs of each row as block blockIdx.x of the next
+        // product's split row: its largest magnitude over the 16 lanes of
+        // the row (ids m and 16 + m), then lane (g, m) holds the values of
+        // group m / 8 (id m) and group 2 + m / 8 (id 16 + m) at place m % 8;
+        // pairs of lanes join their halves into dwords
+        const int nb_out = n_vocab / 32;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int T = blockIdx.y * NT + t;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float xa = __fadd_rn(acc0[t][i], ba), xb = __fadd_rn(acc1[t][i], bb);
+                if (gelu_out) {
+                    xa = t3_gelu_f(xa);
+                    xb = t3_gelu_f(xb);
+                }
+                float mx = fmaxf(fabsf(xa), fabsf(xb));
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+                float scl, sinv;
+                split_scale(mx, scl, sinv);
+                const float ya = __fmul_rn(xa, scl), yb = __fmul_rn(xb, scl);
+                const _Float16 ha = (_Float16)ya, hb = (_Float16)yb;
+                const _Float16 la = (_Float16)__fsub_rn(ya, (float)ha);
+                const _Float16 lb = (_Float16)__fsub_rn(yb, (float)hb);
+                // the odd lane's halves join the even lane's dword
+                const uint32_t hab = (uint32_t)__builtin_bit_cast(uint16_t, ha) |
+                                     (uint32_t)__builtin_bit_cast(uint16_t, hb) << 16;
+                const uint32_t lab = (uint32_t)__builtin_bit_cast(uint16_t, la) |
+                                     (uint32_t)__builtin_bit_cast(uint16_t, lb) << 16;
+                const uint32_t hab_o = (uint32_t)__shfl_xor((int)hab, 1);
+                const uint32_t lab_o = (uint32_t)__shfl_xor((int)lab, 1);
+                const int mrow = 4 * g + i;  // the row's place in its tile
+                if (T < n_tiles && (m & 1) == 0) {
+                    // dword (m % 8) / 2 of lane 16 gq + mrow's hi (lo) 16 bytes
+                    uint32_t* const base = out_parts + ((int64_t)T * nb_out + blockIdx.x) * 512 +
+                                           (m & 7) / 2;
+                    const int ga = m >> 3, gb = 2 + (m >> 3);
+                    base[4 * (16 * ga + mrow)] = (hab & 0xffffu) | (hab_o << 16);
+                    base[4 * (16 * ga + mrow) + 256] = (lab & 0xffffu) | (lab_o << 16);
+                    base[4 * (16 * gb + mrow)] = (hab >> 16) | (hab_o & 0xffff0000u);
+                    base[4 * (16 * gb + mrow) + 256] = (lab >> 16) | (lab_o & 0xffff0000u);
+                }
+                if (T < n_tiles && m == 0)
+                    out_inv[split_inv_index(T, mrow, nb_out, blockIdx.x)] = sinv;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int T = blockIdx.y * NT + t;
@@ -404,10 +456,9 @@ __global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float*
         for (int i = 0; i < 4; ++i) {
             const int rr = (T % tps) * 16 + 4 * g + i;
             if (rr < n_rows) {
-                const float sinv = inv[T * 16 + 4 * g + i];
                 float* orow = o + (int64_t)rr * ld_out;
-                const float xa = __fadd_rn(__fmul_rn(acc0[t][i], sinv), ba);
-                const float xb = __fadd_rn(__fmul_rn(acc1[t][i], sinv), bb);
+                const float xa = __fadd_rn(acc0[t][i], ba);
+                const float xb = __fadd_rn(acc1[t][i], bb);
                 if (va < n_vocab) orow[va] = gelu_out ? t3_gelu_f(xa) : xa;
                 if (vb < n_vocab) orow[vb] = gelu_out ? t3_gelu_f(xb) : xb;
             }
@@ -433,41 +484,58 @@ constexpr int kGemvWaves = 4;
 // Words of one staged activation row: 33 per 32-element block.
 __host__ __device__ inline int gemv_row_words(int n_embd) { return n_embd / 32 * 33; }
 
-// The 32 weights of block b of vocab row v (zeros past the table).
+// The raw words of block b of vocab row v (zeros past the table): F16 its
+// 16 dwords; the quantized formats the dwords covering the block from the one
+// holding its first byte, and that byte's bit offset sh in it (0 or 16: rows
+// and blocks start at even bytes).
 template <int WT>
-__device__ __forceinline__ void gemv_block(const __amdgpu_buffer_rsrc_t& rw, int v, int nball, int b,
-                                           float* w) {
+struct GemvRaw {
+    static constexpr int N = WT == CBX_WTYPE_F16 ? 16 : (block_bytes<WT>() + 2 + 3) / 4;
+    uint32_t t[N];
+    uint32_t sh;
+};
+
+template <int WT>
+__device__ __forceinline__ void gemv_load(const __amdgpu_buffer_rsrc_t& rw, int v, int nball, int b,
+                                          GemvRaw<WT>& r) {
     if constexpr (WT == CBX_WTYPE_F16) {
         const uint32_t off = (uint32_t)(((int64_t)v * nball + b) * 64);
-        uint32_t t[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const auto x = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 16u * i, 0, 0);
-            uint32_t y[4];
-            __builtin_memcpy(y, &x, 16);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) t[4 * i + c] = y[c];
+            __builtin_memcpy(&r.t[4 * i], &x, 16);
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            w[2 * i] = half_bits_to_float(t[i] & 0xffffu);
-            w[2 * i + 1] = half_bits_to_float(t[i] >> 16);
-        }
+        r.sh = 0;
     } else {
         constexpr int BB = block_bytes<WT>();
-        constexpr int ND = (BB + 2 + 3) / 4;  // dwords covering the block (5, 6 or 9)
         const uint32_t off = (uint32_t)(((int64_t)v * nball + b) * BB);  // even
-        const uint32_t a0 = off & ~3u, sh = 8u * (off & 3u);               // sh: 0 or 16
-        uint32_t t[ND];
+        const uint32_t a0 = off & ~3u;
+        r.sh = 8u * (off & 3u);
 #pragma unroll
-        for (int i = 0; i < ND; ++i)
-            t[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, a0 + 4u * i, 0, 0);
-        const float d = half_bits_to_float((t[0] >> sh) & 0xffffu);
+        for (int i = 0; i < GemvRaw<WT>::N; ++i)
+            r.t[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, a0 + 4u * i, 0, 0);
+    }
+}
+
+// The 32 weights of a block from its raw words, exactly as the format defines
+// them.
+template <int WT>
+__device__ __forceinline__ void gemv_decode(const GemvRaw<WT>& r, float* w) {
+    if constexpr (WT == CBX_WTYPE_F16) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            w[2 * i] = half_bits_to_float(r.t[i] & 0xffffu);
+            w[2 * i + 1] = half_bits_to_float(r.t[i] >> 16);
+        }
+    } else {
+        constexpr int ND = GemvRaw<WT>::N;
+        const uint32_t sh = r.sh;
+        const float d = half_bits_to_float((r.t[0] >> sh) & 0xffffu);
         // the block's bytes after the scale, as dwords: byte 2 of the block first
         uint32_t q[ND - 1];
 #pragma unroll
         for (int i = 0; i < ND - 1; ++i)
-            q[i] = sh ? t[i + 1] : __builtin_amdgcn_alignbit(t[i + 1], t[i], 16);
+            q[i] = sh ? r.t[i + 1] : __builtin_amdgcn_alignbit(r.t[i + 1], r.t[i], 16);
         if constexpr (WT == CBX_WTYPE_Q4_0) {
             // element j < 16: low nibble of byte j; element 16 + j: its high nibble
             const float o = __fmul_rn(d, -8.0f);
@@ -508,6 +576,26 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const int nball = n_embd / 32, rw_words = gemv_row_words(n_embd);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int s = lane & (LANES - 1), grp = lane / LANES;
+    constexpr int kRowsPerWave = 64 / LANES;
+    constexpr int kRowsPerPass = kRowsPerWave * kGemvWaves;
+    // with the norm folded in, the first pass's first PF blocks per lane are
+    // requested before the activations are staged, so their latency overlaps
+    // the norm instead of following it (measured at one T3 stream: c_fc 7.9
+    // -> 7.1 us, c_attn 6.8 -> 6.5 us; the plain products, whose staging is a
+    // copy, measured no faster with it and hold twice the registers)
+    constexpr int PF = NORM ? 2 : 0;
+    constexpr int64_t kBB = block_bytes<WT>();
+    const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
+    GemvRaw<WT> pre[PF > 0 ? PF : 1];
+    {
+        const int v = blockIdx.x * kRowsPerPass + wave * kRowsPerWave + grp;
+        const int vc = v < n_vocab ? v : n_vocab;
+#pragma unroll
+        for (int p = 0; p < PF; ++p)
+            if (s + p * LANES < nball) gemv_load<WT>(rw, vc, nball, s + p * LANES, pre[p]);
+    }
     if constexpr (NORM) {
         // the rows' residual add and layer norm (the T3 layer's, same
         // operations in the same order as its norm kernel), into LDS;
@@ -581,22 +669,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
             hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
         }
     }
-    constexpr int64_t kBB = block_bytes<WT>();
-    const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
     __syncthreads();
-    constexpr int kRowsPerWave = 64 / LANES;
-    constexpr int kRowsPerPass = kRowsPerWave * kGemvWaves;
+    bool first = true;
     for (int vb = blockIdx.x * kRowsPerPass; vb < n_vocab; vb += gridDim.x * kRowsPerPass) {
         const int v = vb + wave * kRowsPerWave + grp;
         const int vc = v < n_vocab ? v : n_vocab;  // past the table: zeros
         float acc[RMAX];
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) acc[r] = 0.0f;
-        for (int b = s; b < nball; b += LANES) {
+        // block b's products, in block order
+        auto block = [&](const GemvRaw<WT>& raw, int b) {
             float w[32];
-            gemv_block<WT>(rw, vc, nball, b, w);
+            gemv_decode<WT>(raw, w);
             const float* hb = hs + b * 33;
 #pragma unroll
             for (int r = 0; r < RMAX; ++r) {
@@ -608,6 +692,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
                     acc[r] = a;
                 }
             }
+        };
+        int b = s;
+        if (first) {  // the prefetched blocks of this pass's row
+#pragma unroll
+            for (int p = 0; p < PF; ++p, b += LANES)
+                if (b < nball) block(pre[p], b);
+            first = false;
+        }
+        for (; b < nball; b += LANES) {
+            GemvRaw<WT> raw;
+            gemv_load<WT>(rw, vc, nball, b, raw);
+            block(raw, b);
         }
         // the lanes' sums: lane 15 of each 16-lane row ends with its total,
         // then lanes 16 and 32 apart add theirs, so lane LANES - 1 of each
@@ -703,41 +799,45 @@ template <int WT, int NT>
 hipError_t launch_mfma(const void* W, const float* bias, const uint32_t* parts, const float* inv,
                        int n_tiles, float* out0, float* out1, int64_t ld_out, int n_rows,
                        int n_vocab, int n_embd, hipStream_t stream, int kz = 1,
-                       int gelu_out = 0) {
+                       int gelu_out = 0, uint32_t* out_parts = nullptr,
+                       float* out_inv = nullptr) {
     const dim3 grid((unsigned)((n_vocab + 31) / 32), (unsigned)((n_tiles + NT - 1) / NT),
                     (unsigned)kz);
     hipLaunchKernelGGL((head_mfma<WT, NT>), grid, dim3(64 * KS), 0, stream, W, bias, parts, inv,
                        n_tiles, out0, out1, ld_out, n_rows, n_vocab, n_embd,
-                       (int64_t)n_rows * ld_out, gelu_out);
+                       (int64_t)n_rows * ld_out, gelu_out, out_parts, out_inv);
     return hipGetLastError();
 }
 
 // The matrix-core products on split activations: one row tile per workgroup
 // where two would leave fewer than 512 workgroups (narrow outputs, few rows:
-// the T3 layer products) or the K is split; else two row tiles per
-// workgroup for Q4_0 and for at most two tiles.
+// the T3 layer products), the K is split or the outputs are split for the
+// next product; else two row tiles per workgroup for Q4_0 and for at most
+// two tiles.
 hipError_t mfma_dispatch(const void* W, int32_t wtype, const float* bias, const uint32_t* parts,
                          const float* inv, int n_tiles, float* out0, float* out1, int64_t ld_out,
                          int32_t n_rows, int32_t n_vocab, int32_t n_embd, hipStream_t stream,
-                         int kz, int gelu_out) {
-    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512 || kz > 1 || gelu_out) {
+                         int kz, int gelu_out, uint32_t* out_parts = nullptr,
+                         float* out_inv = nullptr) {
+    if ((int64_t)((n_vocab + 31) / 32) * ((n_tiles + 1) / 2) < 512 || kz > 1 || gelu_out ||
+        out_parts) {
         switch (wtype) {
             case CBX_WTYPE_F16:
                 return launch_mfma<CBX_WTYPE_F16, 1>(W, bias, parts, inv, n_tiles, out0, out1,
                                                      ld_out, n_rows, n_vocab, n_embd, stream, kz,
-                                                     gelu_out);
+                                                     gelu_out, out_parts, out_inv);
             case CBX_WTYPE_Q4_0:
                 return launch_mfma<CBX_WTYPE_Q4_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
                                                       ld_out, n_rows, n_vocab, n_embd, stream, kz,
-                                                     gelu_out);
+                                                     gelu_out, out_parts, out_inv);
             case CBX_WTYPE_Q5_0:
                 return launch_mfma<CBX_WTYPE_Q5_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
                                                       ld_out, n_rows, n_vocab, n_embd, stream, kz,
-                                                      gelu_out);
+                                                      gelu_out, out_parts, out_inv);
             case CBX_WTYPE_Q8_0:
                 return launch_mfma<CBX_WTYPE_Q8_0, 1>(W, bias, parts, inv, n_tiles, out0, out1,
                                                       ld_out, n_rows, n_vocab, n_embd, stream, kz,
-                                                     gelu_out);
+                                                     gelu_out, out_parts, out_inv);
             default:
                 return hipErrorInvalidValue;
         }
@@ -829,8 +929,10 @@ hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const 
     const int n_tiles = ((n_rows + 15) / 16) * (cfg ? 2 : 1), R = 16 * n_tiles;
     uint32_t* parts = static_cast<uint32_t*>(scratch);
     float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + split_inv_offset(R, n_embd));
-    hipLaunchKernelGGL(head_split, dim3((unsigned)R), dim3(kSplitThreads), 0, stream, hidden0,
-                       hidden1, ld_hidden, n_rows, n_embd, parts, inv);
+    const int64_t groups = (int64_t)R * (n_embd / 8);
+    hipLaunchKernelGGL(head_split, dim3((unsigned)((groups + kSplitThreads - 1) / kSplitThreads)),
+                       dim3(kSplitThreads), 0, stream, hidden0, hidden1, ld_hidden, n_rows, n_embd,
+                       R, parts, inv);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, out1, ld_out, n_rows, n_vocab,
@@ -839,15 +941,21 @@ hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const 
 
 hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias, float* out0,
                                 int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
-                                const void* scratch, hipStream_t stream, int kz, bool gelu_out) {
-    if (!scratch || kz < 1 || head_uses_gemv(n_rows, false, n_embd) || (gelu_out && kz > 1))
+                                const void* scratch, hipStream_t stream, int kz, bool gelu_out,
+                                void* out_split) {
+    if (!scratch || kz < 1 || head_uses_gemv(n_rows, false, n_embd) || (gelu_out && kz > 1) ||
+        (out_split && (kz > 1 || n_vocab % 32 != 0)))
         return hipErrorInvalidValue;
     const int n_tiles = (n_rows + 15) / 16, R = 16 * n_tiles;
     const uint32_t* parts = static_cast<const uint32_t*>(scratch);
     const float* inv =
         reinterpret_cast<const float*>(static_cast<const char*>(scratch) + split_inv_offset(R, n_embd));
+    uint32_t* out_parts = static_cast<uint32_t*>(out_split);
+    float* out_inv = out_split ? reinterpret_cast<float*>(static_cast<char*>(out_split) +
+                                                          split_inv_offset(R, n_vocab))
+                               : nullptr;
     return mfma_dispatch(W, wtype, bias, parts, inv, n_tiles, out0, nullptr, ld_out, n_rows,
-                         n_vocab, n_embd, stream, kz, gelu_out ? 1 : 0);
+                         n_vocab, n_embd, stream, kz, gelu_out ? 1 : 0, out_parts, out_inv);
 }
 
 hipError_t launch_head_gemv_norm(const void* W, int32_t wtype, const float* bias,

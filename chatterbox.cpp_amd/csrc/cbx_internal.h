@@ -141,10 +141,12 @@ hipError_t launch_head_k(const void* W, int32_t wtype, const float* bias, const 
 // The matrix-core products of n_rows rows already split into `scratch` by
 // their producer (cbx_split.h's layout, n_rows padded to whole 16-row tiles):
 // launch_head_k without its split launch (one row set; 16 rows and more).
+// out_split set (no K split, n_vocab a multiple of 32): the outputs go there
+// split for the next product (rows of n_vocab) instead of to out0.
 hipError_t launch_head_presplit(const void* W, int32_t wtype, const float* bias, float* out0,
                                 int64_t ld_out, int32_t n_rows, int32_t n_vocab, int32_t n_embd,
                                 const void* scratch, hipStream_t stream, int kz,
-                                bool gelu_out);
+                                bool gelu_out, void* out_split = nullptr);
 
 // The T3 layer's residual add and layer norm folded into the mat-vec product
 // that consumes them (1 or 2 rows of n_embd, a multiple of 256, at most

@@ -1,13 +1,19 @@
 // cbx_split.h -- the matrix-core products' activation split, shared by its
 // producers (head_split in cbx_head.hip, the T3 layer norm in cbx_t3.hip).
 //
-// A row is scaled by 2^s (its largest magnitude to [2^14, 2^15)) and each
-// value written as two fp16 parts, y = x 2^s = hi + lo + e with
-// |e| <= 2^-23 |y| + 2^-25 (hi and lo rounded to nearest), next to 2^-s.
+// Each block of 32 values of a row is scaled by 2^s (the block's largest
+// magnitude to [2^14, 2^15)) and each value written as two fp16 parts,
+// y = x 2^s = hi + lo + e with |e| <= 2^-23 |y| + 2^-25 (hi and lo rounded to
+// nearest), next to 2^-s.  A scale per block (not per row) lets any producer
+// that holds whole blocks of a row write its split itself (the attention's
+// heads hold two blocks each, a product's 32-output tile one).
 // Layout for padded row p = 16 T + m (row tile T): group j (values 8j ..
 // 8j + 7) is lane 16 (j % 4) + m's operand of block j / 4, its hi parts in
 // dwords ((T nball + j/4) 512 + 4 lane) .. + 3 and its lo parts 256 dwords on;
-// the scales follow the parts from the next 256-byte boundary.
+// the scales follow the parts from the next 256-byte boundary, block kb of
+// row p at float (T nball + kb) 16 + m (the 16 rows of a tile's block
+// together: the lanes holding rows 4g .. 4g + 3 of a product tile read
+// theirs as one 16-byte load).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -60,6 +66,23 @@ __device__ __forceinline__ float t3_gelu_f(float x) {
 // Byte offset of the scales in a split buffer of R padded rows of n_embd.
 __host__ __device__ inline size_t split_inv_offset(int R, int n_embd) {
     return ((size_t)R * n_embd * 4 + 255) / 256 * 256;
+}
+
+// Bytes of a split buffer of R padded rows (a multiple of 16) of n_embd.
+__host__ __device__ inline size_t split_bytes(int R, int n_embd) {
+    return split_inv_offset(R, n_embd) + (size_t)R * (n_embd / 32) * 4;
+}
+
+// Index of block kb's scale of row (T, m) among the scales.
+__host__ __device__ inline int64_t split_inv_index(int T, int m, int nball, int kb) {
+    return ((int64_t)T * nball + kb) * 16 + m;
+}
+
+// The largest magnitude over the 4 consecutive lanes (lane & ~3 .. + 3) that
+// hold one block's 4 groups.
+__device__ __forceinline__ float split_block_max4(float mx) {
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    return fmaxf(mx, __shfl_xor(mx, 2));
 }
 
 }  // namespace cbx

@@ -67,7 +67,7 @@ struct NormArgs {
     const float* b;
     float* out;            // LN(x) * g + b
     uint32_t* parts;       // when set, LN(x) * g + b goes there instead, split
-    float* inv;            //   for the next product (cbx_split.h), and 2^-s here
+    float* inv;            //   for the next product (cbx_split.h), the scales here
     int32_t advance;       // last norm of the step: positions[r] += 1
 };
 
@@ -85,19 +85,27 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 // One row per workgroup: the embedding or the residual add, then the layer
 // norm.  Inactive rows (streams that take no step) keep x and write zeros.
-// The next product's split activations for row r from its values in LDS:
-// the row's scale from its largest magnitude mx, then 8 consecutive values
-// per group, groups tid, tid + 256, ...
-__device__ __forceinline__ void norm_split(const NormArgs& a, int r, const float* row_s, float mx) {
-    const int n = a.n_embd, tid = threadIdx.x;
-    float sc, sinv;
-    split_scale(mx, sc, sinv);
-    if (tid == 0) a.inv[r] = sinv;
-    for (int j = tid; j < n / 8; j += kNormThreads) {
+// The next product's split activations for row r from its values in LDS: 8
+// consecutive values per group, groups tid, tid + 256, ..., each block's
+// scale from the largest magnitude of its 4 groups (4 consecutive threads).
+__device__ __forceinline__ void norm_split(const NormArgs& a, int r, const float* row_s) {
+    const int n = a.n_embd, tid = threadIdx.x, nball = n / 32;
+    for (int j0 = 0; j0 < n / 8; j0 += kNormThreads) {  // whole waves in or out
+        const int j = j0 + tid;
+        if (j0 + (tid & ~63) >= n / 8) break;
         float v[8];
+        float mx = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = row_s[8 * j + i];
-        split_store(a.parts, r >> 4, r & 15, n / 32, j, v, sc);
+        for (int i = 0; i < 8; ++i) {
+            v[i] = j < n / 8 ? row_s[8 * j + i] : 0.0f;
+            mx = fmaxf(mx, fabsf(v[i]));
+        }
+        mx = split_block_max4(mx);
+        if (j >= n / 8) continue;
+        float sc, sinv;
+        split_scale(mx, sc, sinv);
+        split_store(a.parts, r >> 4, r & 15, nball, j, v, sc);
+        if ((j & 3) == 0) a.inv[split_inv_index(r >> 4, r & 15, nball, j >> 2)] = sinv;
     }
 }
 
@@ -128,7 +136,7 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
             }
             if (a.parts) {
                 __syncthreads();
-                norm_split(a, r, row_s, 0.0f);
+                norm_split(a, r, row_s);
             }
             return;
         }
@@ -153,7 +161,7 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
             }
             if (a.parts) {
                 __syncthreads();
-                norm_split(a, r, row_s, 0.0f);
+                norm_split(a, r, row_s);
             }
             return;
         }
@@ -191,28 +199,20 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
     }
     const float var = __fdiv_rn(block_sum(q, red), (float)n);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, a.eps)));
-    float mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const int i = j * kNormThreads + tid;
         xr[i] = xv[j];
         const float o =
             __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), a.g[i]), a.b[i]);
-        if (a.parts) {
+        if (a.parts)
             row_s[i] = o;
-            mx = fmaxf(mx, fabsf(o));
-        } else {
+        else
             orow[i] = o;
-        }
     }
     if (a.parts) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        __syncthreads();  // red[] was read by the sums; row_s complete
-        if ((tid & 63) == 0) red[tid >> 6] = mx;
-        __syncthreads();
-        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        norm_split(a, r, row_s, mx);
+        __syncthreads();  // row_s complete
+        norm_split(a, r, row_s);
     }
     if (a.advance && tid == 0) a.positions[r] += 1;
 }
@@ -227,8 +227,42 @@ struct AttnArgs {
     const int32_t* slots;  // prefill: the cache slot of each row (NULL: the row)
     int32_t appended;      // the rows' k, v already stored (t3_kv_append)
     float* out;            // [n_rows][n_embd]
+    uint32_t* parts;       // when set, the rows go there instead, split for the
+    float* inv;            //   next product (cbx_split.h), the scales here
     float scale;           // 1 / sqrt(64)
 };
+
+// Element `lane` (0..63) of head h of row r's attention output, o, from wave
+// 0: to out, or split (the head's 64 values are blocks 2h and 2h + 1 of the
+// row: lanes 0-31 and 32-63, each block scaled by its own largest magnitude,
+// pairs of lanes joining their fp16 halves into dwords).
+__device__ __forceinline__ void attn_store(const AttnArgs& a, int r, int h, int lane, float o) {
+    const int n = a.n_head * kHeadDim;
+    if (!a.parts) {
+        a.out[(int64_t)r * n + h * kHeadDim + lane] = o;
+        return;
+    }
+    float mx = fabsf(o);
+#pragma unroll
+    for (int q = 1; q < 32; q <<= 1) mx = fmaxf(mx, __shfl_xor(mx, q));
+    float sc, sinv;
+    split_scale(mx, sc, sinv);
+    const float y = __fmul_rn(o, sc);
+    const _Float16 hh = (_Float16)y;
+    const _Float16 ll = (_Float16)__fsub_rn(y, (float)hh);
+    const uint32_t hv = __builtin_bit_cast(uint16_t, hh), lv = __builtin_bit_cast(uint16_t, ll);
+    const uint32_t ho = (uint32_t)__shfl_xor((int)hv, 1), lo = (uint32_t)__shfl_xor((int)lv, 1);
+    const int nball = n / 32, kb = 2 * h + (lane >> 5), k = lane & 31;
+    const int T = r >> 4, m = r & 15;
+    if ((lane & 1) == 0) {
+        // dword (k % 8) / 2 of lane 16 (k / 8) + m's hi (lo) 16 bytes
+        uint32_t* const base =
+            a.parts + ((int64_t)T * nball + kb) * 512 + 4 * (16 * (k >> 3) + m) + (k & 7) / 2;
+        base[0] = hv | (ho << 16);
+        base[256] = lv | (lo << 16);
+    }
+    if (k == 0) a.inv[split_inv_index(T, m, nball, kb)] = sinv;
+}
 
 // Prefill: every row's k and v stored at its slot and position before any
 // row attends, so rows of one stream in one call see each other causally.
@@ -266,9 +300,8 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
     const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int n = a.n_head * kHeadDim;
-    float* orow = a.out + (int64_t)r * n + h * kHeadDim;
     if (!a.act[r]) {
-        if (tid < kHeadDim) orow[tid] = 0.0f;
+        if (tid < kHeadDim) attn_store(a, r, h, tid, 0.0f);
         return;
     }
     const int pos = a.positions[r];
@@ -385,7 +418,7 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
             st = __fadd_rn(st, __fmul_rn(red[kAttnWaves + q], f));
             at = __fadd_rn(at, __fmul_rn(part[q][lane], f));
         }
-        orow[lane] = __fdiv_rn(at, st);
+        attn_store(a, r, h, lane, __fdiv_rn(at, st));
     }
 }
 
@@ -427,14 +460,17 @@ size_t t3_attn_lds(int32_t) { return 0; }  // one pass: no per-position LDS
 bool t3_attn_wide(int32_t n_rows, int32_t n_head) { return (int64_t)n_rows * n_head < 256; }
 
 // Workspace of a step: x, u, a [n_rows][n_embd], y [kMaxKSplit][n_rows][n_embd],
-// qkv [n_rows][3 n_embd], f [n_rows][4 n_embd], act [n_rows], then the matrix
-// products' split activations (the widest input, 4 n_embd).
+// qkv [n_rows][3 n_embd], f [n_rows][4 n_embd], act [n_rows], then two
+// buffers of split activations for the matrix products (each for the widest
+// input, 4 n_embd): the norms and the attention write the first, the mlp's
+// c_fc the second (c_fc reads the first as it writes).
 
 size_t t3_workspace_bytes(int32_t n_rows, int32_t n_embd) {
     const size_t row = (size_t)n_rows * n_embd * 4;
     const size_t body = (3 + kMaxKSplit) * row + 3 * row + 4 * row +
                         ((size_t)n_rows * 4 + 255) / 256 * 256;
-    return body + head_scratch_bytes(n_rows, false, 4 * n_embd);
+    const size_t sp = (head_scratch_bytes(n_rows, false, 4 * n_embd) + 255) / 256 * 256;
+    return body + 2 * sp;
 }
 
 hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* tokens,
@@ -455,6 +491,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     int32_t* act = reinterpret_cast<int32_t*>(f + 4 * row);
     const bool wide = !prefill && t3_attn_wide(n_rows, m.n_head);
     void* split = reinterpret_cast<char*>(act) + ((size_t)n_rows * 4 + 255) / 256 * 256;
+    void* split2 = static_cast<char*>(split) +
+                   (head_scratch_bytes(n_rows, false, 4 * n) + 255) / 256 * 256;
 
     NormArgs na{};
     na.n_embd = n;
@@ -475,9 +513,9 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     na.g = m.layers[0].ln_1_g;
     na.b = m.layers[0].ln_1_b;
     na.out = u;
-    // 16 streams and more (the matrix-core path): the norms write the next
-    // product's split activations themselves; below, plain rows for the
-    // mat-vec
+    // 16 streams and more (the matrix-core path): every product's input is
+    // written split by its producer (the norms, the attention, c_fc); below,
+    // plain rows for the mat-vec
     const bool mc = !head_uses_gemv(n_rows, false, n);
     uint32_t* const sparts = static_cast<uint32_t*>(split);
     float* const sinv = reinterpret_cast<float*>(static_cast<char*>(split) +
@@ -499,6 +537,8 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
     aa.slots = slots;
     aa.appended = prefill ? 1 : 0;
     aa.out = att;
+    aa.parts = mc ? sparts : nullptr;  // c_attn has read them by then
+    aa.inv = sinv;
     aa.scale = 0.125f;  // 1 / sqrt(64)
     const size_t lds = t3_attn_lds(c.n_ctx);
 
@@ -550,8 +590,10 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // the two products the residual adds take a K split when their grid
         // is narrow (the norm adds the slabs)
-        e = launch_head_k(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr, n,
-                          n_rows, n, n, split, st, kz_a, false);
+        e = mc ? launch_head_presplit(L.attn_proj_w, m.wtype, L.attn_proj_b, y, n, n_rows, n, n,
+                                      split, st, kz_a, false)
+               : launch_head_k(L.attn_proj_w, m.wtype, L.attn_proj_b, att, nullptr, n, y, nullptr,
+                               n, n_rows, n, n, split, st, kz_a, false);
         if (e != hipSuccess) return e;
         NormArgs nb{};
         nb.n_embd = n;
@@ -577,13 +619,15 @@ hipError_t launch_t3_step(const cbx_t3_model& m, int32_t n_rows, const int32_t* 
         } else {
             if ((e = launch_norm(nb, n_rows, st)) != hipSuccess) return e;
             e = mc ? launch_head_presplit(L.fc_w, m.wtype, L.fc_b, f, 4 * n, n_rows, 4 * n, n,
-                                          split, st, 1, true)
+                                          split, st, 1, true, split2)
                    : launch_head_k(L.fc_w, m.wtype, L.fc_b, u, nullptr, n, f, nullptr, 4 * n,
                                    n_rows, 4 * n, n, split, st, 1, true);
         }
         if (e != hipSuccess) return e;
-        e = launch_head_k(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
-                          n_rows, n, 4 * n, split, st, kz_f, false);
+        e = mc ? launch_head_presplit(L.fc_proj_w, m.wtype, L.fc_proj_b, y, n, n_rows, n, 4 * n,
+                                      split2, st, kz_f, false)
+               : launch_head_k(L.fc_proj_w, m.wtype, L.fc_proj_b, f, nullptr, 4 * n, y, nullptr, n,
+                               n_rows, n, 4 * n, split, st, kz_f, false);
         if (e != hipSuccess) return e;
         // the residual, then the next layer's ln_1 or, after the last, ln_f
         // into `hidden` and the positions advanced
