@@ -58,7 +58,8 @@ constexpr int32_t kRedoWords = 2 + kRedoMax;
 
 constexpr int32_t kMaxVocab = 32768;
 // Survivors after top-k that the one-wave kernel holds; launches whose
-// capacity is at most this (and V <= kWaveMaxVocab) use it.
+// capacity is at most this (and V <= kWaveMaxVocab, or V <= kMaxVocab without
+// CFG rows: the chunked form) use it.
 constexpr int32_t kWaveCap = 1024;
 // Launches of at most this many rows (two per CU) run the workgroup kernel at
 // full survivor capacity: one row's latency, not throughput, sets their time.
@@ -83,6 +84,8 @@ hipError_t launch_w33(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w16t(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w26t(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w33t(const KernelArgs& a, hipStream_t stream);
+// V <= 32768 without CFG rows: the one-wave kernel reading the row in chunks.
+hipError_t launch_w128c(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v512x8(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v512x13(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v512x16(const KernelArgs& a, hipStream_t stream);

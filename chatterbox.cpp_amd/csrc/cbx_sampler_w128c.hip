@@ -1,0 +1,9 @@
+// One-wave sampler for vocabularies up to 32768 ids (no CFG rows), the row
+// read once in chunks of 2048 ids.
+#include "cbx_sampler_wave.h"
+
+namespace cbx {
+hipError_t launch_w128c(const KernelArgs& a, hipStream_t stream) {
+    return launch_wave<128, 0, true>(a, stream);
+}
+}  // namespace cbx

@@ -225,6 +225,11 @@ struct RowScores {
         if (masked_ids)
             word = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ra, (8 * j + (lane >> 3)) * 4,
                                                                   0, 0);
+        finish4w(j, lane, v, Vm, word);
+    }
+    // The same with the allowed word of this lane's 4 ids given (all ones for
+    // rows without a mask).
+    __device__ __forceinline__ void finish4w(int j, int lane, float* v, int Vm, uint32_t word) const {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float x = v[c];
@@ -786,9 +791,265 @@ __device__ __forceinline__ bool lean_topp(WaveSmem<Q>& sm, int n_surv, float mx,
     return true;
 }
 
+// ------------------------------------------------- chunked rows (V > 8448)
+//
+// Rows too long to hold in registers (V <= 256 Q with Q = 128: 32768 ids) are
+// read once, in chunks of kChunkV vectors (256 kChunkV ids) streamed through
+// registers, the next chunk's loads in flight while one is scanned.  A lower
+// bound tau of the top-k threshold rises as the row is read: every finite
+// score >= tau goes on the list (raw entries, in the scan order the one-pass
+// kernel lists its survivors in), and when the list has no room for the next
+// vector's candidates, tau rises to the smallest entry of the bin holding the
+// list's (k+1)-th largest, less 1e-10 (so it stays at or below the row's
+// (k+1)-th largest, and below that threshold's nudge), and the entries below
+// it leave the list.  At the end the list holds every score >= tau, hence
+// the row's (k+1)-th largest: the threshold is taken on it as the reference
+// takes it (nth_element, keep s > thr, the -1e-10 nudge when fewer than k are
+// above; main.cpp:741-748), and the entries above it are the survivors.
+// Rows holding NaN or +inf, and rows whose candidates do not fit the list,
+// are marked to overflow (the redo pass samples them at full capacity).
+constexpr int kChunkV = 8;
+constexpr int kChunkBins = 256;
+
+template <int Q>
+__device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rsc, int lane,
+                                            int k, bool use_topk, float (&cur)[4 * kChunkV],
+                                            float& hi, float& lo, bool& have_lo, bool& bad,
+                                            float& thr, int& n_surv) {
+    static_assert(kChunkBins == 4 * 64, "four bins per lane");
+    static_assert(8 * Q >= kWaveCap, "the list's values fit the kept-bitmap words");
+    const int V = rsc.V;
+    const int nch = (V + 256 * kChunkV - 1) / (256 * kChunkV);
+    const uint32_t list0 = lds_offset(&sm.list[0]);
+    uint32_t* const hist = sm.keptw;  // free until the filters: bins, then candidates
+    auto val = [](uint64_t w) { return __builtin_bit_cast(float, (uint32_t)(w >> 32)); };
+    float tau = kNegInf;
+    int cnt = 0;
+    bool over = false;
+    float nf = 0.0f;  // NaN once a NaN or +inf score is seen
+    hi = kNegInf;
+    // bins of the list's values over [lmn, lmx]: bin(v) = floor(fma(v, bs, nb)),
+    // monotone in v; the bin holding rank k from the top, and the entries above it
+    auto rank_bin = [&](float bs, float nb, int& bsel, int& above_bins) {
+        auto bin = [&](float v) {
+            return (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bs, nb), 0.0f, (float)(kChunkBins - 1));
+        };
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hist[4 * lane + q] = 0u;
+        __syncthreads();
+        for (int i = lane; i < cnt; i += 64) atomicAdd(&hist[bin(val(sm.list[i]))], 1u);
+        __syncthreads();
+        uint32_t c4[4];
+        int tot = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            c4[q] = hist[kChunkBins - 1 - (4 * lane + q)];  // descending bins
+            tot += (int)c4[q];
+        }
+        int all;
+        const int excl = wave_excl_scan_i(tot, all);
+        const bool mine = excl <= k && k < excl + tot;
+        int b = 0, ab = 0, run = excl;
+        bool found = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (mine && !found && run + (int)c4[q] > k) {
+                b = kChunkBins - 1 - (4 * lane + q);
+                ab = run;
+                found = true;
+            }
+            run += (int)c4[q];
+        }
+        const int L = __builtin_ctzll(__ballot(mine));
+        bsel = __builtin_amdgcn_readlane(b, L);
+        above_bins = __builtin_amdgcn_readlane(ab, L);
+        __syncthreads();  // bin counts read
+    };
+    auto list_range = [&](float& lmn, float& lmx) {
+        float a0 = kPosInf, a1 = kNegInf;
+        for (int i = lane; i < cnt; i += 64) {
+            const float v = val(sm.list[i]);
+            a0 = fminf(a0, v);
+            a1 = fmaxf(a1, v);
+        }
+        lmn = wave_min_dpp(a0);
+        lmx = wave_max_dpp(a1);
+    };
+    // entries v with keep(v) moved down in place, in order
+    auto compact = [&](auto&& keep) {
+        int nn = 0;
+        for (int base = 0; base < cnt; base += 64) {
+            const int i = base + lane;
+            const uint64_t w = i < cnt ? sm.list[i] : 0ull;
+            const uint64_t m = __ballot(i < cnt && keep(val(w)));
+            lds_store_b64_lanes(list0 + 8u * (uint32_t)(nn + ballot_rank(m)), w, m);
+            nn += __popcll(m);
+        }
+        cnt = nn;
+        __syncthreads();
+    };
+    // tau raised as far as the list's bins allow; false when it cannot rise
+    auto prune = [&]() -> bool {
+        if (!use_topk || cnt <= k) return false;
+        float lmn, lmx;
+        list_range(lmn, lmx);
+        const float bs = __fdiv_rn((float)kChunkBins, __fsub_rn(lmx, lmn));
+        if (!(lmx > lmn) || !(bs < kPosInf)) return false;
+        const float nb = -__fmul_rn(lmn, bs);
+        int bsel, above_bins;
+        rank_bin(bs, nb, bsel, above_bins);
+        float mn = kPosInf;
+        for (int i = lane; i < cnt; i += 64) {
+            const float v = val(sm.list[i]);
+            const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bs, nb), 0.0f,
+                                                       (float)(kChunkBins - 1));
+            if (b >= bsel) mn = fminf(mn, v);
+        }
+        const float tn = __fsub_rn(wave_min_dpp(mn), 1e-10f);
+        if (!(tn > tau)) return false;
+        tau = tn;
+        compact([&](float v) { return v >= tn; });
+        return true;
+    };
+    // a ring of kRing chunks: kRing - 1 in flight (scores and mask words)
+    // while one is scanned, the slot refilled as soon as it is scanned
+    constexpr int kRing = 3;
+    float buf[kRing][4 * kChunkV];
+    uint32_t mw[kRing][kChunkV];
+    auto issue = [&](int c, float (&bv)[4 * kChunkV], uint32_t (&wv)[kChunkV]) {
+        if (c >= nch) return;
+#pragma unroll
+        for (int j = 0; j < kChunkV; ++j) load4(rsc.rl, lane * 16, (c * kChunkV + j) * 1024, &bv[4 * j]);
+        if (rsc.masked_ids) {
+#pragma unroll
+            for (int j = 0; j < kChunkV; ++j)
+                wv[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    rsc.ra, (8 * (c * kChunkV + j) + (lane >> 3)) * 4, 0, 0);
+        }
+    };
+    auto scan = [&](int c, float (&bv)[4 * kChunkV], const uint32_t (&wv)[kChunkV]) {
+#pragma unroll
+        for (int j = 0; j < kChunkV; ++j) {
+            // masks, padding, temperature
+            rsc.finish4w(c * kChunkV + j, lane, &bv[4 * j], V, rsc.masked_ids ? wv[j] : 0xffffffffu);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float v = bv[4 * j + q];
+                nf = __fmaf_rn(v == kNegInf ? 0.0f : v, 0.0f, nf);
+                hi = fmaxf(hi, v);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kChunkV; ++j) {
+            if (cnt + 256 > kWaveCap && (!prune() || cnt + 256 > kWaveCap)) {
+                over = true;
+                break;
+            }
+            // finite scores >= tau (-inf and NaN never pass)
+            const float t2 = tau == kNegInf ? -3.40282347e38f : tau;
+            const int id0 = 256 * (c * kChunkV + j) + 4 * lane;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float v = bv[4 * j + q];
+                const uint64_t m = __ballot(v >= t2);
+                if (m) {
+                    lds_store_b64_lanes(
+                        list0 + 8u * (uint32_t)(cnt + ballot_rank(m)),
+                        ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)(id0 + q), m);
+                    cnt += __popcll(m);
+                }
+            }
+        }
+    };
+#pragma unroll
+    for (int e = 0; e < 4 * kChunkV; ++e) buf[0][e] = cur[e];  // chunk 0, loaded by the caller
+    if (rsc.masked_ids) {
+#pragma unroll
+        for (int j = 0; j < kChunkV; ++j)
+            mw[0][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, (8 * j + (lane >> 3)) * 4,
+                                                                      0, 0);
+    }
+#pragma unroll
+    for (int r = 1; r < kRing; ++r) issue(r, buf[r], mw[r]);
+#pragma unroll 1
+    for (int c0 = 0; c0 < nch && !over; c0 += kRing) {
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) {
+            if (c0 + r < nch && !over) {
+                scan(c0 + r, buf[r], mw[r]);
+                issue(c0 + r + kRing, buf[r], mw[r]);
+            }
+        }
+    }
+    __syncthreads();
+    bad = __ballot(!(__builtin_fabsf(nf) < kPosInf)) != 0;
+    hi = wave_max_dpp(hi);
+    if (bad || over) {
+        n_surv = kWaveCap + 1;  // more than any capacity: the redo pass takes the row
+        return;
+    }
+    thr = kNegInf;
+    if (use_topk && cnt > k) {
+        // the (k+1)-th largest: its bin, then that bin's entries ranked
+        float lmn, lmx;
+        list_range(lmn, lmx);
+        const float bs = __fdiv_rn((float)kChunkBins, __fsub_rn(lmx, lmn));
+        const bool binned = lmx > lmn && bs < kPosInf;
+        const float nb = binned ? -__fmul_rn(lmn, bs) : 0.0f;
+        int bsel = 0, above_bins = 0;
+        if (binned) rank_bin(bs, nb, bsel, above_bins);
+        float* const cand = reinterpret_cast<float*>(hist);
+        int nc = 0;
+        for (int base = 0; base < cnt; base += 64) {
+            const int i = base + lane;
+            const float v = i < cnt ? val(sm.list[i]) : 0.0f;
+            const int b = binned ? (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bs, nb), 0.0f,
+                                                                (float)(kChunkBins - 1))
+                                 : 0;
+            const bool in = i < cnt && b == bsel;
+            const uint64_t m = __ballot(in);
+            if (in) cand[nc + ballot_rank(m)] = v;
+            nc += __popcll(m);
+        }
+        __syncthreads();
+        const int rem = k - above_bins;  // 0 <= rem < nc
+        float tv = kNegInf;
+        int tgt = 0;
+        bool hit = false;
+        for (int c0 = lane; c0 < nc; c0 += 64) {
+            const float v = cand[c0];
+            int gt = 0, ge = 0;
+            for (int t = 0; t < nc; ++t) {
+                const float w = cand[t];
+                gt += (w > v) ? 1 : 0;
+                ge += (w >= v) ? 1 : 0;
+            }
+            if (gt <= rem && rem < ge) {
+                tv = v;
+                tgt = gt;
+                hit = true;
+            }
+        }
+        const int L2 = __builtin_ctzll(__ballot(hit));
+        thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tv), L2));
+        const int above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
+        if (above < k) thr = __fsub_rn(thr, 1e-10f);
+        __syncthreads();  // candidates read
+        const float th = thr;
+        compact([&](float v) { return v > th; });
+    } else {
+        // every finite score of the row is on the list (tau never rose):
+        // all of them survive (at most k, or no top-k), and the smallest is lo
+        float lmx;
+        list_range(lo, lmx);
+        have_lo = true;
+    }
+    n_surv = cnt;
+}
+
 // ------------------------------------------------------------------ kernel
 
-template <int Q, int JT>
+template <int Q, int JT, bool CH = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) void sample_rows_wave(
     KernelArgs a) {
     __shared__ WaveSmem<Q> sm;
@@ -834,21 +1095,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // exp table's words, the row, then the history's first 1024 ids, so no
     // wait comes between them and one wait covers the row and the ids.
     const uint64_t tabv = kExp2TabDev.t[lane & 31];
-    float s[EPL];
+    float s[CH ? 1 : EPL];
+    float cur[CH ? 4 * kChunkV : 1];  // chunked rows: the chunk being read
+    if constexpr (!CH) {
 #pragma unroll
-    for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
-    if (rsc.uncond) {
-        // CFG rows: the uncond vectors stream through a ring of UD register
-        // quads, UD - 1 loads ahead of the combine (the waits are in order)
-        constexpr int UD = 3;
-        float un[UD][4];
+        for (int j = 0; j < Q; ++j) load4(rsc.rl, lane * 16, j * 1024, &s[4 * j]);
+        if (rsc.uncond) {
+            // CFG rows: the uncond vectors stream through a ring of UD register
+            // quads, UD - 1 loads ahead of the combine (the waits are in order)
+            constexpr int UD = 3;
+            float un[UD][4];
 #pragma unroll
-        for (int j = 0; j < UD - 1; ++j) load4(rsc.ru, lane * 16, j * 1024, un[j]);
+            for (int j = 0; j < UD - 1; ++j) load4(rsc.ru, lane * 16, j * 1024, un[j]);
 #pragma unroll
-        for (int j = 0; j < Q; ++j) {
-            if (j + UD - 1 < Q) load4(rsc.ru, lane * 16, (j + UD - 1) * 1024, un[(j + UD - 1) % UD]);
-            rsc.combine4(&s[4 * j], un[j % UD]);
+            for (int j = 0; j < Q; ++j) {
+                if (j + UD - 1 < Q) load4(rsc.ru, lane * 16, (j + UD - 1) * 1024, un[(j + UD - 1) % UD]);
+                rsc.combine4(&s[4 * j], un[j % UD]);
+            }
         }
+    } else {
+        // chunk 0 (ids 0 .. 256 kChunkV - 1); the rest stream in as it is scanned
+#pragma unroll
+        for (int j = 0; j < kChunkV; ++j) load4(rsc.rl, lane * 16, j * 1024, &cur[4 * j]);
     }
     // ---- history ids -> seen bitmap (main.cpp:775) ----
     // Loads past the history read 0 and are masked out.
@@ -896,94 +1164,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     // Then every row takes the same pass: only ids >= V are padding, which
     // this instantiation meets in vectors j >= JT alone (V > 256*JT); the
     // others need 4 operations per score and no predicate.
-    const bool plain = !rsc.masked_ids && !rsc.fstop;
+    [[maybe_unused]] const bool plain = !rsc.masked_ids && !rsc.fstop;
     // lo, the smallest finite score, is taken only where a path needs it
     // (have_lo): the common one bins from the mean of vector 0 and sorts
     // from the top-k threshold
     float lo = kPosInf, hi = kNegInf;
     bool have_lo = false;
-    float msum = 0.0f;  // this lane's 4 scores of vector 0 (padding-free when JT >= 1)
-    bool bad = false, neg_inf = false;  // NaN/+inf seen; -inf among unmasked scores
-    if (!plain) {
-        if (rsc.masked_ids)
-            for (int w = lane; w < W; w += 64)
-                sm.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < Q; ++j) {
-            const uint32_t word = rsc.masked_ids ? sm.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int id = 256 * j + 4 * lane + c;
-                const bool m = !((word >> (4 * (lane & 7) + c)) & 1u) |
-                               (rsc.fstop & (id != rsc.stop));
-                s[4 * j + c] = m ? kNegInf : s[4 * j + c];
-            }
-        }
-        __syncthreads();
-    }
-    {
-        // acc = sum of the products of score pairs: finite while every
-        // unmasked score is finite, NaN or infinite once one is NaN or
-        // infinite (or, for huge scores, when the sum overflows: the check
-        // below then finds no such score).  Vectors j >= JT may hold padding.
-        float acc = 0.0f;
-        const int Vm = fresh(V);
-        auto pass = [&](auto scaled) {
-            msum = 0.0f;
-#pragma unroll
-            for (int j = 0; j < Q; ++j) {
-                float w[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    w[c] = s[4 * j + c];
-                    if (decltype(scaled)::value) w[c] = __fmul_rn(w[c], rsc.inv_t);
-                }
-                if (j < JT) {
-                    if (j == 0) msum = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
-                    acc = __fmaf_rn(w[0], w[1], acc);
-                    acc = __fmaf_rn(w[2], w[3], acc);
-                    // running value first: one 3-input max per pair
-                    hi = fmaxf(fmaxf(hi, w[0]), w[1]);
-                    hi = fmaxf(fmaxf(hi, w[2]), w[3]);
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const bool pad = 256 * j + 4 * lane + c >= Vm;
-                        acc = __fmaf_rn(pad ? 0.0f : w[c], 0.0f, acc);
-                        w[c] = pad ? kNegInf : w[c];
-                        hi = fmaxf(hi, w[c]);
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < 4; ++c) s[4 * j + c] = w[c];
-            }
-        };
-        if (rsc.scale) pass(std::true_type{});
-        else pass(std::false_type{});
-        const bool spec = __ballot(!(__builtin_fabsf(acc) < kPosInf)) != 0;
-        if (spec) {
-            // rare: tell NaN/+inf (reported) from -inf logits, and take the
-            // minimum over finite scores only
-            int nf = 0, ni = 0;
-            lo = kPosInf;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float v = s[e];
-                const bool pad = (e >> 2) >= JT && 256 * (e >> 2) + 4 * lane + (e & 3) >= Vm;
-                nf |= (!pad && (v != v || v == kPosInf)) ? 1 : 0;
-                ni |= (!pad && v == kNegInf) ? 1 : 0;
-                lo = fminf(lo, v == kNegInf ? kPosInf : v);
-            }
-            bad = wave_sum_dpp(nf) != 0;
-            neg_inf = wave_sum_dpp(ni) != 0;
-            lo = wave_min_dpp(lo);
-            have_lo = true;
-        }
-    }
-    hi = wave_max_dpp(hi);
-    const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
-    CBX_STAMP(2);
+    [[maybe_unused]] float msum = 0.0f;  // this lane's 4 scores of vector 0 (padding-free when JT >= 1)
+    bool bad = false;                     // NaN/+inf seen
+    [[maybe_unused]] bool neg_inf = false;  // -inf among unmasked scores
+    uint32_t flags = 0u;
     // The scores again, reloaded four at a time, for the passes after the
     // fast top-k path (so the register copy of the row need not stay live).
     auto each_score = [&](auto&& f) {
@@ -996,17 +1186,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
         }
     };
 
-    // lo from the scores in registers (every unmasked score finite here:
-    // rows holding -inf, NaN or +inf took it above) ...
-    auto lo_from_registers = [&]() {
-        if (have_lo) return;
-        float m = kPosInf;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) m = fminf(m, s[e] == kNegInf ? kPosInf : s[e]);  // padding
-        lo = wave_min_dpp(m);
-        have_lo = true;
-    };
-    // ... or reloaded, where the registers have been given up
+    // lo from scores reloaded (where the registers have been given up, and
+    // for chunked rows)
     auto lo_from_memory = [&]() {
         if (have_lo) return;
         float m = kPosInf;
@@ -1020,167 +1201,364 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     const bool use_topk = k > 0 && k < V;
     float thr = kNegInf;  // survivors: s > thr
     int n_surv = -1;      // >= 0 once the survivor list is built
-    if (use_topk) {
-        int above = 0;
-        bool done = false;
-        // Plain rows: y(v) = fma(v, bs, c0) lands in [2^23, 2^23 + NB) for
-        // every score in [lo, hi] (checked at both ends; y is monotone), where
-        // a float is an integer: bin(v) = bits(y) - bits(2^23) is
-        // non-decreasing in v and costs two operations per score.  The
-        // V..256Q padding (-inf) is raised to bin 0 and taken off its count.
-        // The bins cover [hlo, hi]: for k < V/4 the (k+1)-th largest score
-        // lies, for any ordinary row, above the mean of the 256 scores of
-        // vector 0, so the bins start there (half the atomics, bins twice as
-        // fine).  Scores below hlo land in bins 0..1 (some, within two bins
-        // of hlo) or in a dump word of their own lane below the histogram
-        // (y below 2^23, where floats step by 1/2: y = 2^23 - (l + 1)/2 has
-        // bits(y) - bits(2^23) = -(l + 1)), as does the padding (-inf).  So
-        // the counts of bins >= 2 are exact, and a row whose rank-k bin is
-        // below 2 (or holding fewer than k + 1 binned scores) takes the
-        // full-range pass further down.
-        const bool partial = JT >= 1 && 4 * k < V && !bad && !neg_inf;
-        if (!partial) lo_from_registers();
-        const float hlo = partial ? __fmul_rn(wave_sum_f_dpp(msum), 1.0f / 256.0f) : lo;
-        const float hrange = __fsub_rn(hi, hlo);
-        const float bs = __fdiv_rn((float)(kWaveBins - 4), hrange);
-        const float c0 = __fsub_rn(0x1p23f + 2.0f, __fmul_rn(hlo, bs));
-        const bool bins_fit = __fmaf_rn(hlo, bs, c0) >= 0x1p23f &&
-                              __fmaf_rn(hi, bs, c0) <= 0x1p23f + (float)(kWaveBins - 1);
-        if (!bad && !neg_inf && hrange > 0.0f && bs < kPosInf && bins_fit) {
-            uint32_t* hist = sm.khist() + 64;  // words -64..-1: the lanes' dump words
-            const float dump_y = 0x1p23f - 0.5f * (float)(lane + 1);
-#pragma unroll
-            for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
+    if constexpr (!CH) {
+        if (!plain) {
+            if (rsc.masked_ids)
+                for (int w = lane; w < W; w += 64)
+                    sm.keptw[w] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, w * 4, 0, 0);
             __syncthreads();
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float y = fmaxf(__fmaf_rn(s[e], bs, c0), dump_y);
-                atomicAdd(&hist[(int)(__builtin_bit_cast(uint32_t, y) - 0x4B000000u)], 1u);
-            }
-            __syncthreads();
-            CBX_STAMP(16);
-            // Lane l owns the 16 bins kWaveBins-1-16l .. kWaveBins-16-16l
-            // (descending scores), contiguous in LDS: their total from four
-            // 16-byte reads.
-            static_assert(kWaveBins == 1024, "16 bins per lane");
-            int tot;
-            {
-                const uint4* h4 = reinterpret_cast<const uint4*>(hist) + (kWaveBins / 4 - 4 - 4 * lane);
-                uint32_t sum = 0;
+            for (int j = 0; j < Q; ++j) {
+                const uint32_t word = rsc.masked_ids ? sm.keptw[8 * j + (lane >> 3)] : 0xffffffffu;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint4 w = h4[i];
-                    sum += (w.x + w.y) + (w.z + w.w);
+                for (int c = 0; c < 4; ++c) {
+                    const int id = 256 * j + 4 * lane + c;
+                    const bool m = !((word >> (4 * (lane & 7) + c)) & 1u) |
+                                   (rsc.fstop & (id != rsc.stop));
+                    s[4 * j + c] = m ? kNegInf : s[4 * j + c];
                 }
-                tot = (int)sum;
             }
-            int n_fin;
-            const int excl = wave_excl_scan_i(tot, n_fin);
-            if (n_fin <= k) {
-                if (!partial) {
+            __syncthreads();
+        }
+        {
+            // acc = sum of the products of score pairs: finite while every
+            // unmasked score is finite, NaN or infinite once one is NaN or
+            // infinite (or, for huge scores, when the sum overflows: the check
+            // below then finds no such score).  Vectors j >= JT may hold padding.
+            float acc = 0.0f;
+            const int Vm = fresh(V);
+            auto pass = [&](auto scaled) {
+                msum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < Q; ++j) {
+                    float w[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        w[c] = s[4 * j + c];
+                        if (decltype(scaled)::value) w[c] = __fmul_rn(w[c], rsc.inv_t);
+                    }
+                    if (j < JT) {
+                        if (j == 0) msum = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
+                        acc = __fmaf_rn(w[0], w[1], acc);
+                        acc = __fmaf_rn(w[2], w[3], acc);
+                        // running value first: one 3-input max per pair
+                        hi = fmaxf(fmaxf(hi, w[0]), w[1]);
+                        hi = fmaxf(fmaxf(hi, w[2]), w[3]);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const bool pad = 256 * j + 4 * lane + c >= Vm;
+                            acc = __fmaf_rn(pad ? 0.0f : w[c], 0.0f, acc);
+                            w[c] = pad ? kNegInf : w[c];
+                            hi = fmaxf(hi, w[c]);
+                        }
+                    }
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) s[4 * j + c] = w[c];
+                }
+            };
+            if (rsc.scale) pass(std::true_type{});
+            else pass(std::false_type{});
+            const bool spec = __ballot(!(__builtin_fabsf(acc) < kPosInf)) != 0;
+            if (spec) {
+                // rare: tell NaN/+inf (reported) from -inf logits, and take the
+                // minimum over finite scores only
+                int nf = 0, ni = 0;
+                lo = kPosInf;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const float v = s[e];
+                    const bool pad = (e >> 2) >= JT && 256 * (e >> 2) + 4 * lane + (e & 3) >= Vm;
+                    nf |= (!pad && (v != v || v == kPosInf)) ? 1 : 0;
+                    ni |= (!pad && v == kNegInf) ? 1 : 0;
+                    lo = fminf(lo, v == kNegInf ? kPosInf : v);
+                }
+                bad = wave_sum_dpp(nf) != 0;
+                neg_inf = wave_sum_dpp(ni) != 0;
+                lo = wave_min_dpp(lo);
+                have_lo = true;
+            }
+        }
+        hi = wave_max_dpp(hi);
+        flags = bad ? CBX_INFO_NONFINITE : 0u;
+        CBX_STAMP(2);
+        // lo from the scores in registers (every unmasked score finite here:
+        // rows holding -inf, NaN or +inf took it above) ...
+        auto lo_from_registers = [&]() {
+            if (have_lo) return;
+            float m = kPosInf;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) m = fminf(m, s[e] == kNegInf ? kPosInf : s[e]);  // padding
+            lo = wave_min_dpp(m);
+            have_lo = true;
+        };
+        if (use_topk) {
+            int above = 0;
+            bool done = false;
+            // Plain rows: y(v) = fma(v, bs, c0) lands in [2^23, 2^23 + NB) for
+            // every score in [lo, hi] (checked at both ends; y is monotone), where
+            // a float is an integer: bin(v) = bits(y) - bits(2^23) is
+            // non-decreasing in v and costs two operations per score.  The
+            // V..256Q padding (-inf) is raised to bin 0 and taken off its count.
+            // The bins cover [hlo, hi]: for k < V/4 the (k+1)-th largest score
+            // lies, for any ordinary row, above the mean of the 256 scores of
+            // vector 0, so the bins start there (half the atomics, bins twice as
+            // fine).  Scores below hlo land in bins 0..1 (some, within two bins
+            // of hlo) or in a dump word of their own lane below the histogram
+            // (y below 2^23, where floats step by 1/2: y = 2^23 - (l + 1)/2 has
+            // bits(y) - bits(2^23) = -(l + 1)), as does the padding (-inf).  So
+            // the counts of bins >= 2 are exact, and a row whose rank-k bin is
+            // below 2 (or holding fewer than k + 1 binned scores) takes the
+            // full-range pass further down.
+            const bool partial = JT >= 1 && 4 * k < V && !bad && !neg_inf;
+            if (!partial) lo_from_registers();
+            const float hlo = partial ? __fmul_rn(wave_sum_f_dpp(msum), 1.0f / 256.0f) : lo;
+            const float hrange = __fsub_rn(hi, hlo);
+            const float bs = __fdiv_rn((float)(kWaveBins - 4), hrange);
+            const float c0 = __fsub_rn(0x1p23f + 2.0f, __fmul_rn(hlo, bs));
+            const bool bins_fit = __fmaf_rn(hlo, bs, c0) >= 0x1p23f &&
+                                  __fmaf_rn(hi, bs, c0) <= 0x1p23f + (float)(kWaveBins - 1);
+            if (!bad && !neg_inf && hrange > 0.0f && bs < kPosInf && bins_fit) {
+                uint32_t* hist = sm.khist() + 64;  // words -64..-1: the lanes' dump words
+                const float dump_y = 0x1p23f - 0.5f * (float)(lane + 1);
+#pragma unroll
+                for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
+                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const float y = fmaxf(__fmaf_rn(s[e], bs, c0), dump_y);
+                    atomicAdd(&hist[(int)(__builtin_bit_cast(uint32_t, y) - 0x4B000000u)], 1u);
+                }
+                __syncthreads();
+                CBX_STAMP(16);
+                // Lane l owns the 16 bins kWaveBins-1-16l .. kWaveBins-16-16l
+                // (descending scores), contiguous in LDS: their total from four
+                // 16-byte reads.
+                static_assert(kWaveBins == 1024, "16 bins per lane");
+                int tot;
+                {
+                    const uint4* h4 = reinterpret_cast<const uint4*>(hist) + (kWaveBins / 4 - 4 - 4 * lane);
+                    uint32_t sum = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint4 w = h4[i];
+                        sum += (w.x + w.y) + (w.z + w.w);
+                    }
+                    tot = (int)sum;
+                }
+                int n_fin;
+                const int excl = wave_excl_scan_i(tot, n_fin);
+                if (n_fin <= k) {
+                    if (!partial) {
+                        thr = kNegInf;  // at most k finite scores: nothing is removed
+                        above = n_fin;
+                        done = true;
+                    }  // else fewer than k + 1 scores above hlo: the full-range pass
+                } else {
+                    // the lane whose bins hold rank k; lanes 0..15 take its bins
+                    // (q-th largest first) and scan their counts
+                    const int L = __builtin_ctzll(__ballot(excl <= k && k < excl + tot));
+                    const int exclL = __builtin_amdgcn_readlane(excl, L);
+                    const int bq = kWaveBins - 1 - (16 * L + (lane & 15));
+                    const int cq = (int)hist[bq];
+                    int inc = cq;  // inclusive scan inside lanes 0..15 (row 0)
+                    inc += dpp_i<0x111, 0xf>(0, inc);
+                    inc += dpp_i<0x112, 0xf>(0, inc);
+                    inc += dpp_i<0x114, 0xf>(0, inc);
+                    inc += dpp_i<0x118, 0xf>(0, inc);
+                    const int Qh = __builtin_ctzll(__ballot(lane < 16 && exclL + inc > k));
+                    const int bsel = kWaveBins - 1 - (16 * L + Qh);
+                    const int nsel = __builtin_amdgcn_readlane(cq, Qh);
+                    const int above_bins = exclL + __builtin_amdgcn_readlane(inc, Qh) - nsel;
+                    // Score boundaries of the selected bin: B0 = least float with
+                    // bin >= bsel, B1 = least float with bin >= bsel + 1 (+inf past
+                    // the top bin).  bin(v) >= b  <=>  fma(v, bs, c0) >= 2^23 + b,
+                    // which (the fma rounding to integers) holds from about
+                    // v*bs + c0 = 2^23 + b - 1/2 on; probed over 64 consecutive
+                    // floats around that root.
+                    auto boundary = [&](int b, float& B) -> bool {
+                        const float tb = 0x1p23f + (float)b;
+                        const float v0 = (float)(((double)tb - 0.5 - (double)c0) / (double)bs);
+                        const float v = okey_inv(okey(v0) + (uint32_t)(lane - 32));
+                        const uint64_t m = __ballot(__fmaf_rn(v, bs, c0) >= tb);
+                        if (m == 0 || m == ~0ull) return false;
+                        const int L0 = __builtin_ctzll(m);
+                        if (m != (~0ull << L0)) return false;
+                        B = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                          __builtin_bit_cast(int, v), L0));
+                        return true;
+                    };
+                    CBX_STAMP(17);
+                    float B0 = kNegInf, B1 = kPosInf;
+                    const bool have_b = bsel >= (partial ? 2 : 1) && nsel <= kWaveCand &&
+                                        boundary(bsel, B0) &&
+                                        (bsel == kWaveBins - 1 || boundary(bsel + 1, B1));
+                    __syncthreads();  // histogram reads done: the candidates reuse it
+                    CBX_STAMP(18);
+                    if (have_b && above_bins + nsel <= kWaveCap) {
+                        // One pass: every score >= B0 (the survivors >= B1 and the
+                        // selected bin's candidates) joins the list, in (vector,
+                        // element, lane) order.
+                        auto val_of = [](uint64_t pk) {
+                            return __builtin_bit_cast(float, (uint32_t)(pk >> 32));
+                        };
+                        // sb: byte offset of the next free slot (a running scalar)
+                        const uint32_t lbase = lds_offset(&sm.list[0]);
+                        uint32_t sb = lbase;
+#pragma unroll
+                        for (int j = 0; j < Q; ++j) {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c)
+                                sb = append_ge(sb, B0, s[4 * j + c], (uint32_t)(256 * j + 4 * lane + c));
+                        }
+                        const int n = (int)((sb - lbase) >> 3);
+                        __syncthreads();
+                        CBX_STAMP(19);
+                        const int nr0 = (n + 63) >> 6;
+                        int nc = 0;
+                        uint64_t x[kWaveRows];  // the list, read once
+#pragma unroll
+                        for (int g = 0; g < kWaveRows; g += 4) {
+                            if (g < nr0) {
+#pragma unroll
+                                for (int r = g; r < g + 4; ++r) x[r] = sm.list[r * 64 + lane];
+                            }
+                        }
+                        if (n == above_bins + nsel) {
+                            // the candidates: list entries below B1
+#pragma unroll
+                            for (int r = 0; r < kWaveRows; ++r) {
+                                if (r < nr0) {
+                                    const int i = r * 64 + lane;
+                                    const bool inb = i < n && val_of(x[r]) < B1;
+                                    const uint64_t m = __ballot(inb);
+                                    const int at = ballot_rank(m) + nc;
+                                    // (more than the array holds: the count check below fails)
+                                    if (nc + __popcll(m) <= kWaveCand)
+                                        lds_store_b64_lanes(lds_offset(sm.candk()) + 8u * (uint32_t)at,
+                                                            x[r], m);
+                                    nc += __popcll(m);
+                                }
+                            }
+                        }
+                        __syncthreads();
+                        CBX_STAMP(20);
+                        if (n == above_bins + nsel && nc == nsel) {
+                            const int rem = k - above_bins;  // 0 <= rem < nc
+                            float tv = kNegInf;
+                            int tgt = 0;
+                            bool hitc = false;
+                            for (int c0 = lane; c0 < nc; c0 += 64) {
+                                const float v = val_of(sm.candk()[c0]);
+                                int gt = 0, ge = 0;
+                                for (int t = 0; t < nc; ++t) {
+                                    const float w = val_of(sm.candk()[t]);
+                                    gt += (w > v) ? 1 : 0;
+                                    ge += (w >= v) ? 1 : 0;
+                                }
+                                if (gt <= rem && rem < ge) { tv = v; tgt = gt; hitc = true; }
+                            }
+                            const int L2 = __builtin_ctzll(__ballot(hitc));
+                            thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                 __builtin_bit_cast(int, tv), L2));
+                            above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
+                            if (above < k) thr = __fsub_rn(thr, 1e-10f);
+                            CBX_STAMP(21);
+                            if (!(thr < B0)) {
+                                // survivors: entries > thr, compacted in place
+                                int n2 = 0;
+#pragma unroll
+                                for (int r = 0; r < kWaveRows; ++r) {
+                                    if (r < nr0) {
+                                        const bool keep = r * 64 + lane < n && val_of(x[r]) > thr;
+                                        const uint64_t m = __ballot(keep);
+                                        const int at = ballot_rank(m) + n2;
+                                        lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)at,
+                                                            x[r], m);
+                                        n2 += __popcll(m);
+                                    }
+                                }
+                                n_surv = n2;
+                            }
+                            done = true;  // thr < B0 (nudge past the bin): the full pass below
+                        }
+                        __syncthreads();
+                    }
+                }
+            }
+            if (!done) lo_from_memory();
+            const float range = __fsub_rn(hi, lo);
+            const float bscale = __fdiv_rn((float)kWaveBins, range);
+            const float nlo = -__fmul_rn(lo, bscale);
+            if (!done && !bad && range > 0.0f && bscale < kPosInf) {
+                // bins with -inf sent to the spare bin NB (masked rows, -inf logits)
+                auto bin_of = [&](float v) -> int {
+                    const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bscale, nlo), 0.0f,
+                                                               (float)(kWaveBins - 1));
+                    return v == kNegInf ? kWaveBins : b;
+                };
+                uint32_t* hist = sm.khist();
+#pragma unroll
+                for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
+                if (lane == 0) hist[kWaveBins] = 0u;
+                __syncthreads();
+                each_score([&](float v, int) { atomicAdd(&hist[bin_of(v)], 1u); });
+                __syncthreads();
+                constexpr int BPL = kWaveBins / 64;
+                uint32_t cnt[BPL];
+                int tot = 0;
+#pragma unroll
+                for (int q = 0; q < BPL; ++q) {
+                    cnt[q] = hist[kWaveBins - 1 - (lane * BPL + q)];  // descending bins
+                    tot += (int)cnt[q];
+                }
+                int n_fin;
+                const int excl = wave_excl_scan_i(tot, n_fin);
+                if (n_fin <= k) {
                     thr = kNegInf;  // at most k finite scores: nothing is removed
                     above = n_fin;
                     done = true;
-                }  // else fewer than k + 1 scores above hlo: the full-range pass
-            } else {
-                // the lane whose bins hold rank k; lanes 0..15 take its bins
-                // (q-th largest first) and scan their counts
-                const int L = __builtin_ctzll(__ballot(excl <= k && k < excl + tot));
-                const int exclL = __builtin_amdgcn_readlane(excl, L);
-                const int bq = kWaveBins - 1 - (16 * L + (lane & 15));
-                const int cq = (int)hist[bq];
-                int inc = cq;  // inclusive scan inside lanes 0..15 (row 0)
-                inc += dpp_i<0x111, 0xf>(0, inc);
-                inc += dpp_i<0x112, 0xf>(0, inc);
-                inc += dpp_i<0x114, 0xf>(0, inc);
-                inc += dpp_i<0x118, 0xf>(0, inc);
-                const int Qh = __builtin_ctzll(__ballot(lane < 16 && exclL + inc > k));
-                const int bsel = kWaveBins - 1 - (16 * L + Qh);
-                const int nsel = __builtin_amdgcn_readlane(cq, Qh);
-                const int above_bins = exclL + __builtin_amdgcn_readlane(inc, Qh) - nsel;
-                // Score boundaries of the selected bin: B0 = least float with
-                // bin >= bsel, B1 = least float with bin >= bsel + 1 (+inf past
-                // the top bin).  bin(v) >= b  <=>  fma(v, bs, c0) >= 2^23 + b,
-                // which (the fma rounding to integers) holds from about
-                // v*bs + c0 = 2^23 + b - 1/2 on; probed over 64 consecutive
-                // floats around that root.
-                auto boundary = [&](int b, float& B) -> bool {
-                    const float tb = 0x1p23f + (float)b;
-                    const float v0 = (float)(((double)tb - 0.5 - (double)c0) / (double)bs);
-                    const float v = okey_inv(okey(v0) + (uint32_t)(lane - 32));
-                    const uint64_t m = __ballot(__fmaf_rn(v, bs, c0) >= tb);
-                    if (m == 0 || m == ~0ull) return false;
-                    const int L0 = __builtin_ctzll(m);
-                    if (m != (~0ull << L0)) return false;
-                    B = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                      __builtin_bit_cast(int, v), L0));
-                    return true;
-                };
-                CBX_STAMP(17);
-                float B0 = kNegInf, B1 = kPosInf;
-                const bool have_b = bsel >= (partial ? 2 : 1) && nsel <= kWaveCand &&
-                                    boundary(bsel, B0) &&
-                                    (bsel == kWaveBins - 1 || boundary(bsel + 1, B1));
-                __syncthreads();  // histogram reads done: the candidates reuse it
-                CBX_STAMP(18);
-                if (have_b && above_bins + nsel <= kWaveCap) {
-                    // One pass: every score >= B0 (the survivors >= B1 and the
-                    // selected bin's candidates) joins the list, in (vector,
-                    // element, lane) order.
-                    auto val_of = [](uint64_t pk) {
-                        return __builtin_bit_cast(float, (uint32_t)(pk >> 32));
-                    };
-                    // sb: byte offset of the next free slot (a running scalar)
-                    const uint32_t lbase = lds_offset(&sm.list[0]);
-                    uint32_t sb = lbase;
+                } else {
+                    const bool mine = excl <= k && k < excl + tot;
+                    int bsel = 0, above_bins = 0;
+                    if (mine) {
+                        int run = excl;
+                        bool found = false;
 #pragma unroll
-                    for (int j = 0; j < Q; ++j) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            sb = append_ge(sb, B0, s[4 * j + c], (uint32_t)(256 * j + 4 * lane + c));
-                    }
-                    const int n = (int)((sb - lbase) >> 3);
-                    __syncthreads();
-                    CBX_STAMP(19);
-                    const int nr0 = (n + 63) >> 6;
-                    int nc = 0;
-                    uint64_t x[kWaveRows];  // the list, read once
-#pragma unroll
-                    for (int g = 0; g < kWaveRows; g += 4) {
-                        if (g < nr0) {
-#pragma unroll
-                            for (int r = g; r < g + 4; ++r) x[r] = sm.list[r * 64 + lane];
-                        }
-                    }
-                    if (n == above_bins + nsel) {
-                        // the candidates: list entries below B1
-#pragma unroll
-                        for (int r = 0; r < kWaveRows; ++r) {
-                            if (r < nr0) {
-                                const int i = r * 64 + lane;
-                                const bool inb = i < n && val_of(x[r]) < B1;
-                                const uint64_t m = __ballot(inb);
-                                const int at = ballot_rank(m) + nc;
-                                // (more than the array holds: the count check below fails)
-                                if (nc + __popcll(m) <= kWaveCand)
-                                    lds_store_b64_lanes(lds_offset(sm.candk()) + 8u * (uint32_t)at,
-                                                        x[r], m);
-                                nc += __popcll(m);
+                        for (int q = 0; q < BPL; ++q) {
+                            if (!found && run + (int)cnt[q] > k) {
+                                bsel = kWaveBins - 1 - (lane * BPL + q);
+                                above_bins = run;
+                                found = true;
                             }
+                            run += (int)cnt[q];
                         }
                     }
+                    const int L = __builtin_ctzll(__ballot(mine));
+                    bsel = __builtin_amdgcn_readlane(bsel, L);
+                    above_bins = __builtin_amdgcn_readlane(above_bins, L);
+                    __syncthreads();  // histogram reads done: the candidates reuse it
+                    int nc = 0;
+                    each_score([&](float v, int) {
+                        const bool in = bin_of(v) == bsel;
+                        const uint64_t m = __ballot(in);
+                        const int at = nc + ballot_rank(m);
+                        if (nc + __popcll(m) <= kWaveCand)  // else nc > kWaveCand: not used
+                            lds_store_b32_lanes(lds_offset(sm.cand()) + 4u * (uint32_t)at,
+                                                __builtin_bit_cast(uint32_t, v), m);
+                        nc += __popcll(m);
+                    });
                     __syncthreads();
-                    CBX_STAMP(20);
-                    if (n == above_bins + nsel && nc == nsel) {
+                    if (nc <= kWaveCand) {
                         const int rem = k - above_bins;  // 0 <= rem < nc
                         float tv = kNegInf;
                         int tgt = 0;
                         bool hitc = false;
                         for (int c0 = lane; c0 < nc; c0 += 64) {
-                            const float v = val_of(sm.candk()[c0]);
+                            const float v = sm.cand()[c0];
                             int gt = 0, ge = 0;
                             for (int t = 0; t < nc; ++t) {
-                                const float w = val_of(sm.candk()[t]);
+                                const float w = sm.cand()[t];
                                 gt += (w > v) ? 1 : 0;
                                 ge += (w >= v) ? 1 : 0;
                             }
@@ -1190,164 +1568,62 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
                         thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                              __builtin_bit_cast(int, tv), L2));
                         above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
-                        if (above < k) thr = __fsub_rn(thr, 1e-10f);
-                        CBX_STAMP(21);
-                        if (!(thr < B0)) {
-                            // survivors: entries > thr, compacted in place
-                            int n2 = 0;
-#pragma unroll
-                            for (int r = 0; r < kWaveRows; ++r) {
-                                if (r < nr0) {
-                                    const bool keep = r * 64 + lane < n && val_of(x[r]) > thr;
-                                    const uint64_t m = __ballot(keep);
-                                    const int at = ballot_rank(m) + n2;
-                                    lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)at,
-                                                        x[r], m);
-                                    n2 += __popcll(m);
-                                }
-                            }
-                            n_surv = n2;
-                        }
-                        done = true;  // thr < B0 (nudge past the bin): the full pass below
+                        done = true;
                     }
-                    __syncthreads();
+                }
+                if (done) {
+                    if (above < k) thr = __fsub_rn(thr, 1e-10f);
                 }
             }
-        }
-        if (!done) lo_from_memory();
-        const float range = __fsub_rn(hi, lo);
-        const float bscale = __fdiv_rn((float)kWaveBins, range);
-        const float nlo = -__fmul_rn(lo, bscale);
-        if (!done && !bad && range > 0.0f && bscale < kPosInf) {
-            // bins with -inf sent to the spare bin NB (masked rows, -inf logits)
-            auto bin_of = [&](float v) -> int {
-                const int b = (int)__builtin_amdgcn_fmed3f(__fmaf_rn(v, bscale, nlo), 0.0f,
-                                                           (float)(kWaveBins - 1));
-                return v == kNegInf ? kWaveBins : b;
-            };
-            uint32_t* hist = sm.khist();
-#pragma unroll
-            for (int q = 0; q < kWaveBins / 64; ++q) hist[lane * (kWaveBins / 64) + q] = 0u;
-            if (lane == 0) hist[kWaveBins] = 0u;
-            __syncthreads();
-            each_score([&](float v, int) { atomicAdd(&hist[bin_of(v)], 1u); });
-            __syncthreads();
-            constexpr int BPL = kWaveBins / 64;
-            uint32_t cnt[BPL];
-            int tot = 0;
-#pragma unroll
-            for (int q = 0; q < BPL; ++q) {
-                cnt[q] = hist[kWaveBins - 1 - (lane * BPL + q)];  // descending bins
-                tot += (int)cnt[q];
-            }
-            int n_fin;
-            const int excl = wave_excl_scan_i(tot, n_fin);
-            if (n_fin <= k) {
-                thr = kNegInf;  // at most k finite scores: nothing is removed
-                above = n_fin;
+            if (!done && !bad && !(range > 0.0f)) {
+                // every finite score equal (or none; forced-stop rows): the
+                // (k+1)-th largest is that score when more than k are finite,
+                // else -inf, and no score is above it
+                int nf = 0;
+                each_score([&](float v, int) { nf += (v != kNegInf) ? 1 : 0; });
+                const int n_fin = wave_sum_dpp(nf);
+                thr = n_fin > k ? lo : kNegInf;
+                above = n_fin > k ? 0 : n_fin;
+                if (above < k) thr = __fsub_rn(thr, 1e-10f);
                 done = true;
-            } else {
-                const bool mine = excl <= k && k < excl + tot;
-                int bsel = 0, above_bins = 0;
-                if (mine) {
-                    int run = excl;
-                    bool found = false;
-#pragma unroll
-                    for (int q = 0; q < BPL; ++q) {
-                        if (!found && run + (int)cnt[q] > k) {
-                            bsel = kWaveBins - 1 - (lane * BPL + q);
-                            above_bins = run;
-                            found = true;
-                        }
-                        run += (int)cnt[q];
-                    }
-                }
-                const int L = __builtin_ctzll(__ballot(mine));
-                bsel = __builtin_amdgcn_readlane(bsel, L);
-                above_bins = __builtin_amdgcn_readlane(above_bins, L);
-                __syncthreads();  // histogram reads done: the candidates reuse it
-                int nc = 0;
-                each_score([&](float v, int) {
-                    const bool in = bin_of(v) == bsel;
-                    const uint64_t m = __ballot(in);
-                    const int at = nc + ballot_rank(m);
-                    if (nc + __popcll(m) <= kWaveCand)  // else nc > kWaveCand: not used
-                        lds_store_b32_lanes(lds_offset(sm.cand()) + 4u * (uint32_t)at,
-                                            __builtin_bit_cast(uint32_t, v), m);
-                    nc += __popcll(m);
-                });
-                __syncthreads();
-                if (nc <= kWaveCand) {
-                    const int rem = k - above_bins;  // 0 <= rem < nc
-                    float tv = kNegInf;
-                    int tgt = 0;
-                    bool hitc = false;
-                    for (int c0 = lane; c0 < nc; c0 += 64) {
-                        const float v = sm.cand()[c0];
-                        int gt = 0, ge = 0;
-                        for (int t = 0; t < nc; ++t) {
-                            const float w = sm.cand()[t];
-                            gt += (w > v) ? 1 : 0;
-                            ge += (w >= v) ? 1 : 0;
-                        }
-                        if (gt <= rem && rem < ge) { tv = v; tgt = gt; hitc = true; }
-                    }
-                    const int L2 = __builtin_ctzll(__ballot(hitc));
-                    thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                         __builtin_bit_cast(int, tv), L2));
-                    above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
-                    done = true;
-                }
             }
-            if (done) {
+            if (!done) {
+                // 8-bit radix select over all ids (NaN / inf rows)
+                uint32_t prefix = 0, pmask = 0, rem = (uint32_t)k;
+                wave_radix_pass<Q>(rsc, 24, prefix, pmask, rem, sm.khist());
+                wave_radix_pass<Q>(rsc, 16, prefix, pmask, rem, sm.khist());
+                wave_radix_pass<Q>(rsc, 8, prefix, pmask, rem, sm.khist());
+                wave_radix_pass<Q>(rsc, 0, prefix, pmask, rem, sm.khist());
+                thr = okey_inv(prefix);
+                int n_above = 0;
+                each_score([&](float v, int) { n_above += (v > thr) ? 1 : 0; });
+                above = wave_sum_dpp(n_above);
                 if (above < k) thr = __fsub_rn(thr, 1e-10f);
             }
         }
-        if (!done && !bad && !(range > 0.0f)) {
-            // every finite score equal (or none; forced-stop rows): the
-            // (k+1)-th largest is that score when more than k are finite,
-            // else -inf, and no score is above it
-            int nf = 0;
-            each_score([&](float v, int) { nf += (v != kNegInf) ? 1 : 0; });
-            const int n_fin = wave_sum_dpp(nf);
-            thr = n_fin > k ? lo : kNegInf;
-            above = n_fin > k ? 0 : n_fin;
-            if (above < k) thr = __fsub_rn(thr, 1e-10f);
-            done = true;
-        }
-        if (!done) {
-            // 8-bit radix select over all ids (NaN / inf rows)
-            uint32_t prefix = 0, pmask = 0, rem = (uint32_t)k;
-            wave_radix_pass<Q>(rsc, 24, prefix, pmask, rem, sm.khist());
-            wave_radix_pass<Q>(rsc, 16, prefix, pmask, rem, sm.khist());
-            wave_radix_pass<Q>(rsc, 8, prefix, pmask, rem, sm.khist());
-            wave_radix_pass<Q>(rsc, 0, prefix, pmask, rem, sm.khist());
-            thr = okey_inv(prefix);
-            int n_above = 0;
-            each_score([&](float v, int) { n_above += (v > thr) ? 1 : 0; });
-            above = wave_sum_dpp(n_above);
-            if (above < k) thr = __fsub_rn(thr, 1e-10f);
-        }
-    }
-    CBX_STAMP(3);
+        CBX_STAMP(3);
 
-    // ---- survivors -> LDS list of (score bits << 32 | id) ----
-    // keep = score != -inf and not (top-k and score <= thr); without NaN that
-    // is score > thr (thr = -inf when nothing is cut).  Only kept items that
-    // fit the list are stored.
-    if (n_surv < 0) {
-        int n = 0;
-        each_score([&](float v, int id) {
-            const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
-            const uint64_t m = __ballot(keep);
-            const int at = n + ballot_rank(m);
-            // past the list: the row overflows and its list is not used
-            lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)at,
-                                ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)id,
-                                __ballot(keep && at < kWaveCap));
-            n += __popcll(m);
-        });
-        n_surv = n;
+        // ---- survivors -> LDS list of (score bits << 32 | id) ----
+        // keep = score != -inf and not (top-k and score <= thr); without NaN that
+        // is score > thr (thr = -inf when nothing is cut).  Only kept items that
+        // fit the list are stored.
+        if (n_surv < 0) {
+            int n = 0;
+            each_score([&](float v, int id) {
+                const bool keep = bad ? (v != kNegInf && !(v <= thr)) : (v > thr);
+                const uint64_t m = __ballot(keep);
+                const int at = n + ballot_rank(m);
+                // past the list: the row overflows and its list is not used
+                lds_store_b64_lanes(lds_offset(&sm.list[0]) + 8u * (uint32_t)at,
+                                    ((uint64_t)__builtin_bit_cast(uint32_t, v) << 32) | (uint32_t)id,
+                                    __ballot(keep && at < kWaveCap));
+                n += __popcll(m);
+            });
+            n_surv = n;
+        }
+    } else {
+        chunk_front<Q>(sm, rsc, lane, k, use_topk, cur, hi, lo, have_lo, bad, thr, n_surv);
+        flags = bad ? CBX_INFO_NONFINITE : 0u;
     }
     CBX_STAMP(4);
     if (n_surv > cap) {
@@ -1978,11 +2254,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     }
 }
 
-// Q: scores per lane / 4 (V <= 256*Q); JT: V > 256*JT for every launch.
-template <int Q, int JT>
+// Q: scores per lane / 4 (V <= 256*Q); JT: V > 256*JT for every launch; CH:
+// the row read in chunks (no CFG rows).
+template <int Q, int JT, bool CH = false>
 hipError_t launch_wave(const KernelArgs& a, hipStream_t stream) {
     const int64_t rows = (int64_t)a.n_steps * a.n_rows;
-    hipLaunchKernelGGL((sample_rows_wave<Q, JT>), dim3((unsigned)rows), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((sample_rows_wave<Q, JT, CH>), dim3((unsigned)rows), dim3(64), 0, stream, a);
     return hipGetLastError();
 }
 

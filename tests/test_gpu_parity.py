@@ -365,6 +365,48 @@ def test_masked_stress(cbx, torch_cuda):
     assert np.all(tg[d["force_stop"] == 1] == d["stop"])
 
 
+@pytest.mark.parametrize("V", [8449, 12000, 20000, 32768])
+def test_chunked_one_wave(cbx, torch_cuda, V):
+    """Vocabularies past the register-resident one-wave kernel (V > 8448),
+    launches of more than 512 rows and a survivor bound of at most 1024: the
+    one-wave kernel reading each row once in chunks, its top-k threshold
+    raised as it reads.  Masked rows (allowed bitmask, forced stop), min-p and
+    penalty; then batched streams with top_k 50 / 250 / 1000 (the 1000 rows
+    overflow its list and take the redo pass), planted rows of tied scores
+    at and above the threshold, an all-masked row, and a NaN row (redo; NaN
+    is outside the reference's contract: the row is flagged and returns an id
+    in range, and the other rows keep parity)."""
+    w = pkg.workloads()
+    d = w.masked_stress(B=768, V=V, seed=0x5EED9 + V)
+    u = O.mt_canonical(23 + V, d["B"])
+    say(f"chunked one-wave: masked B=768 V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, d["logits"], d["params"], u, d["history"],
+                           d["hist_len"], allowed=d["allowed"], force_stop=d["force_stop"],
+                           stop=d["stop"], max_survivors=50)
+    tr, ir, pr = oracle_rows(d["logits"], d["params"], u, d["history"], d["hist_len"],
+                             allowed=d["allowed"], force_stop=d["force_stop"], stop=d["stop"])
+    parity.compare(f"chunked_masked_{V}", tg, ig, tr, ir, u, pg, pr)
+    d = w.batched_streams(B=256, steps=3, seed=0x5EEDA + V, V=V)
+    x = d["logits"]
+    rng = np.random.default_rng(V)
+    for r in range(0, x.shape[0], 37):  # 70 equal scores above the rest
+        x[r, rng.choice(V, size=70, replace=False)] = 13.0
+    for r in range(5, x.shape[0], 41):  # 40 equal scores at the threshold's rank
+        x[r, rng.choice(V, size=40, replace=False)] = 9.0
+        x[r, rng.choice(V, size=30, replace=False)] = 10.0
+    x[7, :] = -np.inf  # nothing to sample
+    x[9, 100] = np.nan
+    n = x.shape[0]
+    u = O.mt_canonical(29 + V, n)
+    say(f"chunked one-wave: batched streams 256 x 3, V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, d["params"], u, d["history"], d["hist_len"],
+                           n_steps=3, max_survivors=1000)
+    tr, ir, pr = oracle_rows(x, d["params"], u, d["history"], d["hist_len"])
+    assert ig[9] & parity.INFO_NONFINITE and 0 <= tg[9] < V, (ig[9], tg[9])
+    ok = np.arange(n) != 9
+    parity.compare(f"chunked_batched_{V}", tg[ok], ig[ok], tr[ok], ir[ok], u[ok], pg[ok], pr[ok])
+
+
 @pytest.mark.parametrize("V", [6563, 8194, 3000])
 def test_masked_one_wave(cbx, torch_cuda, V):
     """Allowed bitmask, forced stop, min-p and penalty at vocabularies the
