@@ -459,10 +459,10 @@ def fused_head_bench(torch, mod, sampler, stream, steps, dev):
     for name, fn in (("head", head_only), ("fused", fused_step), ("pair", head_pair)):
         res[name] = timed(torch, stream, fn, steps, warm=20)
     flops = 2.0 * 2 * HEAD_B * V * HEAD_EMBD  # cond and uncond rows
-    # the fp16 matrix cores take each activation as two parts (hi, lo): twice
-    # the products of the projection itself; the split pre-pass and launch
-    # gaps are inside the timed call
-    tf = 2 * flops / (res["head"] / 1e3) / 1e12
+    # the fraction on the projection's own FLOPs; the fp16 matrix cores take
+    # each activation as two parts (hi, lo), so they execute twice as many;
+    # the split pre-pass and launch gaps are inside the timed call
+    tf = flops / (res["head"] / 1e3) / 1e12
     return {"workload": "fused Q4_0 speech_head (V=6563 x 1024) + sampler, B=64 CFG pairs "
                         "(128 projected rows), k 1000, p 0.95, T 0.8, pen 1.2, min_p 0.05",
             "steps": steps, "ms_per_step": round(res["fused"], 5),
@@ -630,7 +630,7 @@ def config_masked_stress(torch, mod, sampler, stream, dev, steps=48, n_slabs=4):
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 5),
                          "algorithmic_bytes_per_step": bytes_step,
-                         "kernel": "sample_rows_kernel<1024,32>"},
+                         "kernel": "sample_rows_wave<128,0,true> (the row read in chunks)"},
             "overflow_rows": int(np.sum((flags & 0x20) != 0))}
 
 

@@ -826,8 +826,38 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
     float tau = kNegInf;
     int cnt = 0;
     bool over = false;
-    float nf = 0.0f;  // NaN once a NaN or +inf score is seen
+    bool nfb = false;  // a NaN or +inf score seen by this lane
     hi = kNegInf;
+    thr = kNegInf;
+    if (rsc.fstop) {
+        // forced stop: every id but the stop token is -inf (as the one-pass
+        // kernel's masks make it), so that token's score alone decides; the
+        // chunks already requested are not read
+        float x = kNegInf;
+        if (rsc.stop >= 0 && rsc.stop < V) {
+            x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc.rl, rsc.stop * 4, 0, 0));
+            const uint32_t w = rsc.masked_ids
+                                   ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, (rsc.stop >> 5) * 4, 0, 0)
+                                   : 0xffffffffu;
+            x = ((w >> (rsc.stop & 31)) & 1u) ? x : kNegInf;
+            if (rsc.scale) x = __fmul_rn(x, rsc.inv_t);
+        }
+        hi = x;
+        bad = x != x || x == kPosInf;
+        if (bad) {
+            n_surv = kWaveCap + 1;
+            return;
+        }
+        const bool fin = x != kNegInf;
+        if (lane == 0 && fin)
+            sm.list[0] = ((uint64_t)__builtin_bit_cast(uint32_t, x) << 32) | (uint32_t)rsc.stop;
+        lo = fin ? x : kPosInf;
+        have_lo = true;
+        n_surv = fin ? 1 : 0;
+        __syncthreads();
+        return;
+    }
+    const uint32_t shl = 4u * (uint32_t)(lane & 7);  // this lane's 4 ids in its mask word
     // bins of the list's values over [lmn, lmx]: bin(v) = floor(fma(v, bs, nb)),
     // monotone in v; the bin holding rank k from the top, and the entries above it
     auto rank_bin = [&](float bs, float nb, int& bsel, int& above_bins) {
@@ -930,13 +960,25 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
     auto scan = [&](int c, float (&bv)[4 * kChunkV], const uint32_t (&wv)[kChunkV]) {
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j) {
-            // masks, padding, temperature
-            rsc.finish4w(c * kChunkV + j, lane, &bv[4 * j], V, rsc.masked_ids ? wv[j] : 0xffffffffu);
+            // masks, padding (the last vectors only), temperature: finish4's
+            // operations with the lane's mask bits shifted once per vector
+            const int jj = c * kChunkV + j;
+            uint32_t bits = rsc.masked_ids ? (wv[j] >> shl) : 0xfu;
+            // ids past V: the low min(4, max(0, V - id0)) bits stay (one
+            // mask per vector, not a compare per score)
+            const int nin = min(max(V - (256 * jj + 4 * lane), 0), 4);
+            bits &= (1u << nin) - 1u;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float v = bv[4 * j + q];
-                nf = __fmaf_rn(v == kNegInf ? 0.0f : v, 0.0f, nf);
-                hi = fmaxf(hi, v);
+                // bit q of `bits` as an all-ones or zero word, then a bitwise
+                // select with -inf (no per-score condition register)
+                const uint32_t m = (uint32_t)((int32_t)(bits << (31 - q)) >> 31);
+                float x = __builtin_bit_cast(
+                    float, (__builtin_bit_cast(uint32_t, bv[4 * j + q]) & m) | (0xff800000u & ~m));
+                if (rsc.scale) x = __fmul_rn(x, rsc.inv_t);
+                bv[4 * j + q] = x;
+                nfb = nfb || __builtin_amdgcn_classf(x, 0x203);  // NaN or +inf
+                hi = fmaxf(hi, x);
             }
         }
 #pragma unroll
@@ -982,13 +1024,12 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
         }
     }
     __syncthreads();
-    bad = __ballot(!(__builtin_fabsf(nf) < kPosInf)) != 0;
+    bad = __ballot(nfb) != 0;
     hi = wave_max_dpp(hi);
     if (bad || over) {
         n_surv = kWaveCap + 1;  // more than any capacity: the redo pass takes the row
         return;
     }
-    thr = kNegInf;
     if (use_topk && cnt > k) {
         // the (k+1)-th largest: its bin, then that bin's entries ranked
         float lmn, lmx;
