@@ -264,6 +264,27 @@ __device__ __forceinline__ void attn_store(const AttnArgs& a, int r, int h, int 
     if (k == 0) a.inv[split_inv_index(T, m, nball, kb)] = sinv;
 }
 
+// A DPP lane exchange within each 16-lane row (ctrl a compile-time DPP code).
+template <int CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                  0xf, 0xf, false));
+}
+
+// Sum of v over each 16-lane row, the same in every lane of the row: the
+// pairs of lanes 1 apart, then 2 (quad_perm), then the two quads of each 8
+// (row_half_mirror: every lane of a quad already holds the quad's sum, so
+// the mirror's partner adds what lane i ^ 4 would), then the two 8-lane
+// halves (row_mirror): the operations of an xor butterfly over 1, 2, 4, 8,
+// each add of a pair the same in either lane, without the LDS-routed
+// permutes a general shuffle takes.
+__device__ __forceinline__ float sum16_dpp(float v) {
+    v = __fadd_rn(v, dpp16<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = __fadd_rn(v, dpp16<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = __fadd_rn(v, dpp16<0x141>(v));  // row_half_mirror
+    return __fadd_rn(v, dpp16<0x140>(v));  // row_mirror
+}
+
 // Prefill: every row's k and v stored at its slot and position before any
 // row attends, so rows of one stream in one call see each other causally.
 __global__ __launch_bounds__(kHeadDim) void t3_kv_append(AttnArgs a) {
@@ -356,8 +377,7 @@ __global__ __launch_bounds__(kAttnWaves * kHeadDim) void t3_attn(AttnArgs a) {
             float dot = __fadd_rn(__fadd_rn(__fmul_rn(q4.x, k4.x), __fmul_rn(q4.y, k4.y)),
                                   __fadd_rn(__fmul_rn(q4.z, k4.z), __fmul_rn(q4.w, k4.w)));
             // the 16 lanes of a row: butterfly over e (the same sum in each)
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) dot = __fadd_rn(dot, __shfl_xor(dot, o));
+            dot = sum16_dpp(dot);
             sc[u] = __fmul_rn(dot, a.scale);
             if (j < c1) bm = fmaxf(bm, sc[u]);
         }
