@@ -47,13 +47,15 @@
 
 // Stage timestamps for a profiling build (CBX_STAGE_CLOCKS defined, one
 // translation unit): wave 0 of each of the first 16384 workgroups records the
-// shader clock at each marker.  Compiled out otherwise.
+// shader clock at each marker (0 .. 63, 64 slots per workgroup).  Compiled
+// out otherwise.
 #if defined(CBX_STAGE_CLOCKS)
-__device__ unsigned long long cbx_stage_clock[16384 * 32];
+__device__ unsigned long long cbx_stage_clock[16384 * 64];
 #define CBX_STAMP(n)                                                      \
     do {                                                                  \
+        static_assert((n) >= 0 && (n) < 64, "stage marker out of range"); \
         if (threadIdx.x == 0 && blockIdx.x < 16384)                       \
-            cbx_stage_clock[blockIdx.x * 32 + (n)] = clock64();           \
+            cbx_stage_clock[blockIdx.x * 64 + (n)] = clock64();           \
     } while (0)
 #else
 #define CBX_STAMP(n) ((void)0)
@@ -100,44 +102,30 @@ __device__ __forceinline__ float desc_key_value(uint64_t k) { return okey_inv(~(
 // Values that are the same in every lane, kept in scalar registers so that
 // the branches they control are scalar branches.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// An opaque copy of a wave-uniform double in scalar registers: its
+// computation stays where it is written (not sunk to its use).
+__device__ __forceinline__ double fresh_d(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    int lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    int hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 __device__ __forceinline__ float unif(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
-
-__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(x, o, 64);
-        if (lane >= o) x += t;
-    }
-    return x;
-}
-__device__ __forceinline__ double wave_incl_scan_f64(double x, int lane) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double t = __shfl_up(x, o, 64);
-        if (lane >= o) x = __dadd_rn(x, t);
-    }
-    return x;
-}
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
-}
-__device__ __forceinline__ float wave_min(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o, 64));
-    return x;
 }
 __device__ __forceinline__ int wave_min_i(int x) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o, 64));
     return x;
 }
-__device__ __forceinline__ int wave_or_i(int x) {
+
+__device__ __forceinline__ double wave_incl_scan_f64(double x, int lane) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x |= __shfl_xor(x, o, 64);
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(x, o, 64);
+        if (lane >= o) x = __dadd_rn(x, t);
+    }
     return x;
 }
 
@@ -172,12 +160,20 @@ struct Shared {
     uint32_t mxk;      // okey of the largest kept score (an LDS maximum)
 };
 
+__device__ __forceinline__ int wave_incl_scan_dpp(int x);
+__device__ __forceinline__ int wave_sum_dpp(int x);
+__device__ __forceinline__ float wave_max_dpp(float x);
+__device__ __forceinline__ float wave_min_dpp(float x);
+__device__ __forceinline__ int wave_min_i_dpp(int x);
+
 // Exclusive block scan of one int per lane; `total` receives the block sum.
+// The wave steps are DPP operations (no LDS round trip per step), as in every
+// block reduction below.
 template <int BLOCK>
 __device__ __forceinline__ int block_excl_scan(int v, Shared& sh, int& total) {
     constexpr int NW = BLOCK / 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int incl = wave_incl_scan(v, lane);
+    const int incl = wave_incl_scan_dpp(v);
     if (lane == 63) sh.red_i[wid] = incl;
     __syncthreads();
     int before = 0, tot = 0;
@@ -203,7 +199,7 @@ template <int BLOCK>
 __device__ __forceinline__ float block_max(float v, Shared& sh) {
     constexpr int NW = BLOCK / 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    v = wave_max(v);
+    v = wave_max_dpp(v);
     if (lane == 0) sh.red_f[wid] = v;
     __syncthreads();
     float m = sh.red_f[0];
@@ -220,9 +216,9 @@ __device__ __forceinline__ void block_minmax(float lo, float hi, int bad, Shared
                                              float& bhi, int& bbad) {
     constexpr int NW = BLOCK / 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    lo = wave_min(lo);
-    hi = wave_max(hi);
-    bad = wave_or_i(bad);
+    lo = wave_min_dpp(lo);
+    hi = wave_max_dpp(hi);
+    bad = wave_sum_dpp(bad != 0 ? 1 : 0);
     if (lane == 0) { sh.red_f[wid] = lo; sh.red_f2[wid] = hi; sh.red_i[wid] = bad; }
     __syncthreads();
     float l = sh.red_f[0], h = sh.red_f2[0];
@@ -367,17 +363,34 @@ __device__ __forceinline__ bool topk_value_bins(const float (&s)[EPT], int k, fl
     if (n_c > kCandMax) return false;
     const int rem = k - above_bins;  // 0 <= rem < n_c
     if (wid == 0) {
-        for (int c0 = lane; c0 < n_c; c0 += 64) {
-            const float v = cand[c0];
+        if (n_c <= 64) {
+            // one candidate per lane, ranked against the others by readlane
+            // (no LDS round trip per comparison)
+            const float v = lane < n_c ? cand[lane] : kNegInf;
             int gt = 0, ge = 0;
             for (int t = 0; t < n_c; ++t) {
-                const float w = cand[t];
+                const float w = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), t));
                 gt += (w > v) ? 1 : 0;
                 ge += (w >= v) ? 1 : 0;
             }
-            if (gt <= rem && rem < ge) {  // equal candidates all write the same
+            if (lane < n_c && gt <= rem && rem < ge) {  // equal candidates all write the same
                 sh.thr = v;
                 sh.above = above_bins + gt;
+            }
+        } else {
+            for (int c0 = lane; c0 < n_c; c0 += 64) {
+                const float v = cand[c0];
+                int gt = 0, ge = 0;
+                for (int t = 0; t < n_c; ++t) {
+                    const float w = cand[t];
+                    gt += (w > v) ? 1 : 0;
+                    ge += (w >= v) ? 1 : 0;
+                }
+                if (gt <= rem && rem < ge) {  // equal candidates all write the same
+                    sh.thr = v;
+                    sh.above = above_bins + gt;
+                }
             }
         }
     }
@@ -977,8 +990,10 @@ __device__ __forceinline__ float chain_segments_x(const float (&t)[CM], int nl, 
 // one wave, in chunks of 64*C terms (lane l: terms l*C .. l*C + C - 1 of a
 // chunk; odd C reads distinct LDS banks), and with THR the first index whose
 // running sum is >= thr (`hit`, else -1).  finite: every term finite and >= 0
-// and acc finite -- binade segments for C >= 5, sweeps otherwise (and for
-// non-finite terms, exact for NaN and infinities too).  DESC: the terms do
+// and acc finite -- binade segments for C >= 5 or more than 8 lanes of terms
+// (a sweep chain is one dependent add and lane shift per lane, the segments a
+// few scans whatever the length), sweeps otherwise (and for non-finite
+// terms, exact for NaN and infinities too).  DESC: the terms do
 // not increase, so once fl(acc + term(base)) == acc at a chunk's start every
 // later add leaves acc unchanged (rounding is monotone) and the rest of the
 // sum is skipped; no threshold is crossed after that point either.  The test
@@ -1003,7 +1018,7 @@ __device__ __forceinline__ float wave_run(Term&& term, int n, float acc, float t
         const int nl = min(64, (n - base + C - 1) / C);
         int h = -1;
         float end;
-        if (C >= 5 && finite) end = chain_segments_x<C, THR>(t, nl, acc, thr, h);
+        if ((C >= 5 || nl > 8) && finite) end = chain_segments_x<C, THR>(t, nl, acc, thr, h);
         else end = chain_sweeps<C, THR, C, true>(t, nl, thr, h, acc);
         if (THR && h >= 0) {
             hit = base + h;
@@ -1448,14 +1463,19 @@ __device__ __forceinline__ int draw_rank_c(const float* F, int n, double u, bool
     return -1;
 }
 
-// draw_rank_c with C picked from n (at most NMAX).
+// draw_rank_c with C picked from n (at most NMAX): the smallest of the odd
+// run lengths 1, 3, 5, 9, 17, 33 whose one chunk holds n (each lane's run is
+// a serial chain of binary64 adds, so a row drawing among few ids should not
+// walk a long run of zeros).
 template <int NMAX>
 __device__ __forceinline__ int draw_rank(const float* F, int n, double u, bool last_kept) {
     n = uni(n);
     if (NMAX <= 64 || n <= 64) return draw_rank_c<1>(F, n, u, last_kept);
     if constexpr (NMAX > 64) {
+        if (n <= 192) return draw_rank_c<3>(F, n, u, last_kept);
         if (NMAX <= 320 || n <= 320) return draw_rank_c<5>(F, n, u, last_kept);
         if constexpr (NMAX > 320) {
+            if (n <= 576) return draw_rank_c<9>(F, n, u, last_kept);
             if (NMAX <= 1088 || n <= 1088) return draw_rank_c<17>(F, n, u, last_kept);
             if constexpr (NMAX > 1088) return draw_rank_c<33>(F, n, u, last_kept);
         }
@@ -1464,7 +1484,8 @@ __device__ __forceinline__ int draw_rank(const float* F, int n, double u, bool l
 }
 
 // Softmax over the kept entries (val[q], id[q] for bit q of `kept`), then
-// greedy or draw; writes token, info and, if asked, the probability row.
+// greedy or draw with the row's uniform u_draw; writes token, info and, if
+// asked, the probability row, and returns the token (in thread 0).
 // Shared by both paths.  Every wave takes part in three steps -- the kept
 // bitmap and the maximum kept score (each wave's maximum into an LDS
 // maximum), then (wave 0) the bitmap's word offsets, then the exp terms F in
@@ -1472,8 +1493,8 @@ __device__ __forceinline__ int draw_rank(const float* F, int n, double u, bool l
 // (main.cpp:786-790) and the token, with no workgroup barrier; the other
 // waves are done, or wait once for the sum when probabilities are written.
 template <int BLOCK, int EPT, int N>
-__device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], uint64_t kept,
-                           const KernelArgs& a, const cbx_params& P, int64_t rs, int row, int step,
+__device__ __forceinline__ int finish_row(float (&val)[N], const int (&id)[N], uint64_t kept,
+                           const KernelArgs& a, const cbx_params& P, int64_t rs, double u_draw,
                            uint32_t flags, uint32_t* keptw, uint32_t* woff, float* F,
                            const uint64_t* tab, Shared& sh) {
     constexpr int WMAX = (BLOCK * EPT + 31) / 32;  // bitmap words of the largest vocabulary
@@ -1497,6 +1518,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
     // wave 0: word offsets; each lane keeps its words' counts for id lookups
     int cw[WPL];
     int loc = 0, wbase = 0, n_final = 0;
+    int token = 0;
     if (wid == 0) {
 #pragma unroll
         for (int q = 0; q < WPL; ++q) {
@@ -1563,7 +1585,6 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
             return psum2;
         };
         CBX_STAMP(10);
-        int token = 0;
         if (empty) {
             flags |= CBX_INFO_EMPTY;
         } else if (P.temp <= 0.0f) {
@@ -1582,13 +1603,7 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
             flags |= CBX_INFO_GREEDY;
         } else if (V >= 2) {
             flags |= CBX_INFO_DREW;
-            double u;
-            if (a.draw_mode == CBX_DRAW_PHILOX) {
-                const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
-                u = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
-            } else {
-                u = a.uniforms[rs];
-            }
+            const double u = u_draw;
             const bool last_kept = bit_of(keptw, V - 1);
             int rank = -1;
             if (!(u > 0.0)) {
@@ -1638,15 +1653,17 @@ __device__ __forceinline__ void finish_row(float (&val)[N], const int (&id)[N], 
                                                           : 0.0f;
         }
     }
+    return token;
 }
 
 // ------------------------------------------------------------------ kernel
 
 // The rest of a row whose n_surv <= NR*BLOCK survivors sit in the LDS list
 // xbuf[0, n_surv) as composite keys: each lane holds positions r*BLOCK + tid.
+// Returns the token (in thread 0).
 template <int BLOCK, int EPT, int NR>
-__device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params& P, int64_t rs,
-                                          int row, int step, uint32_t flags, int n_surv,
+__device__ __forceinline__ int fast_path(const KernelArgs& a, const cbx_params& P, int64_t rs,
+                                          double u_draw, uint32_t flags, int n_surv,
                                           float blo, float bhi,
                                           bool use_topp, bool use_pen, const uint32_t* seen,
                                           uint32_t* keptw, uint32_t* woff, uint8_t* region,
@@ -1682,8 +1699,8 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
         __syncthreads();
         CBX_STAMP(5);
         if (wid == 0) {
-            // psum = 0 + e_0 + e_1 + ... (e_0 = 1), then q_i = e_i / psum in place,
-            // then the first i with q_0 + ... + q_i >= top_p.  Rows holding NaN or
+            // psum = 0 + e_0 + e_1 + ... (e_0 = 1), then with q_i = e_i / psum
+            // the first i with q_0 + ... + q_i >= top_p.  Rows holding NaN or
             // +inf take the term-by-term chains (the segment scan needs finite
             // terms).  The sorted terms do not increase: the sums stop once
             // the adds are no-ops.
@@ -1695,11 +1712,10 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
             CBX_STAMP(6);
             int last;
             if (!(fin && certified_cut<run_bound<BLOCK>(NR * BLOCK)>(e_at, n_surv, psum, P.top_p, last))) {
-                for (int i = lane; i < n_surv; i += 64) E[i] = __fdiv_rn(E[i], psum);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                (void)wave_run_sum<run_bound<BLOCK>(NR * BLOCK), true, true>(e_at, n_surv, 0.0f, P.top_p, hit, fin);
+                // q_i = e_i / psum formed as the sum reads them: a run's
+                // loads and divisions are in flight together
+                auto q_at = [&](int i) { return __fdiv_rn(E[i], psum); };
+                (void)wave_run_sum<run_bound<BLOCK>(NR * BLOCK), true, true>(q_at, n_surv, 0.0f, P.top_p, hit, fin);
                 last = hit < 0 ? n_surv - 1 : hit;
             }
             if (lane == 0) sh.n_kept = last + 1;
@@ -1817,16 +1833,21 @@ __device__ __forceinline__ void fast_path(const KernelArgs& a, const cbx_params&
     }
     __syncthreads();  // E and xbuf are done with; F takes the region
     CBX_STAMP(8);
-    finish_row<BLOCK, EPT, NR>(val, id, kept, a, P, rs, row, step, flags, keptw, woff, F, tab, sh);
+    return finish_row<BLOCK, EPT, NR>(val, id, kept, a, P, rs, u_draw, flags, keptw, woff, F, tab,
+                                      sh);
 }
 
 // MAXNR: the largest register list (rows per lane) compiled in; GENERAL: the
 // per-element path for more survivors is compiled in (the launch picks the
 // variant from the survivor capacity, so lean variants carry no unused code).
-// One workgroup samples row-step g of the launch.
-template <int BLOCK, int EPT, int MAXNR, bool GENERAL>
-__device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Shared& sh,
-                                              uint64_t* tab, uint8_t* smem) {
+// One workgroup samples row-step g of the launch and returns its token (in
+// thread 0; -1 for a row put on the redo list).  DEC: a decode step, whose
+// stream state `dec_state` (read by the caller) is checked once the row's
+// loads are in flight; an ended stream returns kEndedRow from every thread.
+constexpr int kEndedRow = -2;
+template <int BLOCK, int EPT, int MAXNR, bool GENERAL, bool DEC = false>
+__device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Shared& sh,
+                                             uint64_t* tab, uint8_t* smem, int32_t dec_state = 0) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
     const int V = a.n_vocab;
@@ -1863,8 +1884,6 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     // j*BLOCK stride in a scalar offset, ids >= V read 0 (masked below);
     // non-temporal (cache policy nt): each row's logits are read once.
     const float* lrow = a.logits + rs * a.ld_logits;
-    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
-    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
     const int32_t* hrow = a.history ? a.history + (int64_t)row * a.ld_history : nullptr;
     float s[EPT];
     {
@@ -1876,16 +1895,43 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
                                                  rl, tid * 4, j * BLOCK * 4, 2));
     }
     // the history's first kHistPre*BLOCK ids, issued right behind the row so
-    // that one wait covers both (loads past the history read 0; masked below)
+    // that one wait covers both.  They are bounded by the history's row
+    // stride, not its length: the length is a load of its own, and waiting
+    // for it would put a second memory round trip before these.  Ids past the
+    // length are masked below; loads past the stride read 0.
     constexpr int kHistPre = 4;
     int32_t hid[kHistPre];
+    const int hpre = a.history ? (int)min(a.ld_history, (int64_t)(kHistPre * BLOCK)) : 0;
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
-    if (use_pen) {
+        const_cast<int32_t*>(hrow), (short)0, hpre * 4, kBufferWord3);
+    if (a.history) {
 #pragma unroll
         for (int q = 0; q < kHistPre; ++q)
             hid[q] = __builtin_amdgcn_raw_buffer_load_b32(rh, tid * 4, q * BLOCK * 4, 0);
     }
+    if constexpr (DEC) {
+        // an ended stream is not sampled (its row's loads are simply dropped)
+        if (dec_state != CBX_DECODE_RUNNING) {
+            if (tid == 0) {
+                a.tokens[row] = a.stop_token;
+                if (a.info) a.info[row] = CBX_INFO_ENDED;
+            }
+            return kEndedRow;
+        }
+    }
+    // the draw's uniform and the force-stop flag, while the loads are in
+    // flight (scalar work and loads: the draw at the row's end need not wait)
+    double u_draw = 0.0;
+    if (a.draw_mode == CBX_DRAW_PHILOX) {
+        const uint64_t sid = a.stream_ids ? a.stream_ids[row] : (uint64_t)row;
+        u_draw = philox_uniform(a.seed, sid, a.step0 + (uint64_t)step);
+    } else if (a.uniforms) {
+        u_draw = a.uniforms[rs];
+    }
+    u_draw = fresh_d(u_draw);
+    const bool fstop = a.force_stop && a.force_stop[rs];
+    const int hlen = a.history ? (int)min((int64_t)a.history_len[row], a.ld_history) : 0;
+    const bool use_pen = P.repeat_penalty != 1.0f && hlen > 0;
     if (a.uncond) {
         const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(a.uncond + rs * a.ld_logits), (short)0, V * 4, kBufferWord3);
@@ -1919,7 +1965,6 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
             if (t >= 0 && t < V) atomicOr(&seen[t >> 5], 1u << (t & 31));
         }
     }
-    const bool fstop = a.force_stop && a.force_stop[rs];
     const bool scale = P.temp > 0.0f && P.temp != 1.0f;
     const float inv_t = __fdiv_rn(1.0f, P.temp);
     int nonfinite = 0;
@@ -1999,7 +2044,7 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
             float* prow = a.probs + rs * a.ld_probs;
             for (int i = tid; i < V; i += BLOCK) prow[i] = 0.0f;
         }
-        return;
+        return -1;
     }
     const bool use_topp = P.top_p < 1.0f && n_surv > 0;
 
@@ -2012,26 +2057,28 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
         CBX_STAMP(3);
         const int rows_needed = uni((max(64, pow2ceil(n_surv)) + BLOCK - 1) / BLOCK);
         if (rows_needed <= 1) {
-            fast_path<BLOCK, EPT, 1>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp, use_pen,
-                                     seen, keptw, woff, region, tab, sh);
+            return fast_path<BLOCK, EPT, 1>(a, P, rs, u_draw, flags, n_surv, sblo, hi, use_topp,
+                                            use_pen, seen, keptw, woff, region, tab, sh);
         } else if constexpr (MAXNR >= 2) {
             if (rows_needed == 2) {
-                fast_path<BLOCK, EPT, 2>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp, use_pen,
-                                         seen, keptw, woff, region, tab, sh);
+                return fast_path<BLOCK, EPT, 2>(a, P, rs, u_draw, flags, n_surv, sblo, hi, use_topp,
+                                                use_pen, seen, keptw, woff, region, tab, sh);
             } else if constexpr (MAXNR >= 4) {
                 if (rows_needed <= 4) {
-                    fast_path<BLOCK, EPT, 4>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp,
-                                             use_pen, seen, keptw, woff, region, tab, sh);
+                    return fast_path<BLOCK, EPT, 4>(a, P, rs, u_draw, flags, n_surv, sblo, hi,
+                                                    use_topp, use_pen, seen, keptw, woff, region,
+                                                    tab, sh);
                 } else if constexpr (MAXNR >= 8) {
-                    fast_path<BLOCK, EPT, 8>(a, P, rs, row, step, flags, n_surv, sblo, hi, use_topp,
-                                             use_pen, seen, keptw, woff, region, tab, sh);
+                    return fast_path<BLOCK, EPT, 8>(a, P, rs, u_draw, flags, n_surv, sblo, hi,
+                                                    use_topp, use_pen, seen, keptw, woff, region,
+                                                    tab, sh);
                 }
             }
         }
-        return;
+        return -1;  // not reached: rows_needed <= MAXNR
     }
     if constexpr (!GENERAL) {
-        return;  // unreachable: the launch capacity never exceeds MAXNR*BLOCK here
+        return -1;  // not reached: the launch capacity never exceeds MAXNR*BLOCK here
     } else {
     // ================= general path: scores per element =================
     // ---- top-p (main.cpp:750-772) ----
@@ -2214,7 +2261,7 @@ __device__ __forceinline__ void sample_row_wg(const KernelArgs& a, int64_t g, Sh
     int id[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) id[j] = j * BLOCK + tid;
-    finish_row<BLOCK, EPT, EPT>(s, id, kept, a, P, rs, row, step, flags, keptw, woff, F, tab, sh);
+    return finish_row<BLOCK, EPT, EPT>(s, id, kept, a, P, rs, u_draw, flags, keptw, woff, F, tab, sh);
     }
 }
 
@@ -2288,7 +2335,7 @@ __global__ __launch_bounds__(BLOCK) void redo_rows_kernel(KernelArgs a) {
 // the row-step is the row) at full capacity, where no row overflows.  A
 // stream that has ended is not sampled; a running one is sampled by the
 // plain row code, after which thread 0 -- the thread that stored the row's
-// token -- reads its own store back and applies the engine loop's update
+// token, which the row code returns to it -- applies the engine loop's update
 // (chatterbox_engine.cpp:345-353): the stop token ends the stream, any other
 // id is pushed onto its history (which the row read, [0, len), for its
 // penalty), written as the next step's input, and ends the stream at its
@@ -2299,23 +2346,20 @@ __global__ __launch_bounds__(BLOCK) void decode_rows_kernel(KernelArgs a) {
     __shared__ uint64_t tab[32];
     extern __shared__ __align__(16) uint8_t smem[];
     const int row = blockIdx.x;
-    if (a.dec_state[row] != CBX_DECODE_RUNNING) {
-        if (threadIdx.x == 0) {
-            a.tokens[row] = a.stop_token;
-            if (a.info) a.info[row] = CBX_INFO_ENDED;
-        }
-        return;
-    }
-    sample_row_wg<BLOCK, EPT, MAXNR, true>(a, row, sh, tab, smem);
-    if (threadIdx.x == 0) {
-        const int32_t token = a.tokens[row];
+    // the stream's state, length and limit, read while the row loads (no
+    // memory round trip of their own before or after the row)
+    const int32_t state = a.dec_state[row];
+    const int32_t len0 = a.dec_len[row];
+    const int32_t max0 = a.dec_max ? a.dec_max[row] : 0;
+    const int32_t token = sample_row_wg<BLOCK, EPT, MAXNR, true, true>(a, row, sh, tab, smem, state);
+    if (token == kEndedRow) return;
+    if (threadIdx.x == 0) {  // the thread that stored the token
         if (token == a.stop_token) {
             a.dec_state[row] = CBX_DECODE_STOP;
             return;
         }
-        const int64_t lim =
-            a.dec_max ? min((int64_t)a.dec_max[row], a.ld_history) : a.ld_history;
-        int32_t len = max(a.dec_len[row], 0);
+        const int64_t lim = a.dec_max ? min((int64_t)max0, a.ld_history) : a.ld_history;
+        int32_t len = max(len0, 0);
         if (len < lim) {
             a.dec_history[(int64_t)row * a.ld_history + len] = token;
             a.dec_len[row] = ++len;

@@ -196,15 +196,6 @@ __device__ __forceinline__ float fresh_v(float v) {
     return v;
 }
 
-// The same for a wave-uniform double, moved to scalar registers (also keeps
-// its computation where it is written).
-__device__ __forceinline__ double fresh_d(double v) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    int lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-    int hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-    asm volatile("" : "+s"(lo), "+s"(hi));
-    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
 
 // What turns a row's logits into its scores (main.cpp:733-738 and the
 // extensions): CFG combine, allowed mask, forced stop, temperature.
