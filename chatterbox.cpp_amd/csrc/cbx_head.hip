@@ -578,16 +578,23 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     const int s = lane & (LANES - 1), grp = lane / LANES;
     constexpr int kRowsPerWave = 64 / LANES;
     constexpr int kRowsPerPass = kRowsPerWave * kGemvWaves;
-    // with the norm folded in, the first pass's first PF blocks per lane are
-    // requested before the activations are staged, so their latency overlaps
-    // the norm instead of following it (measured at one T3 stream: c_fc 7.9
-    // -> 7.1 us, c_attn 6.8 -> 6.5 us; the plain products, whose staging is a
-    // copy, measured no faster with it and hold twice the registers)
-    constexpr int PF = NORM ? 2 : 0;
+    // the first pass's first PF blocks per lane are requested before the
+    // activations are staged, so their latency overlaps the staging instead
+    // of following it (measured at one T3 stream with the norm folded in:
+    // c_fc 7.9 -> 7.1 us, c_attn 6.8 -> 6.5 us); the kernels for more rows
+    // keep their registers for the rows' sums instead
+    constexpr int PF = (NORM || RMAX <= 2) ? 2 : 0;
     constexpr int64_t kBB = block_bytes<WT>();
     const int64_t wbytes = (int64_t)n_vocab * nball * kBB;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(W), (short)0, (int)wbytes, kBufWord3);
+    // the rows' step flags, requested before the weights: waiting for them
+    // then does not wait for the weights too (loads return in order)
+    int act_r[RMAX];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) act_r[r] = r < R ? nm.act[r] : 0;
+    }
     GemvRaw<WT> pre[PF > 0 ? PF : 1];
     {
         const int v = blockIdx.x * kRowsPerPass + wave * kRowsPerWave + grp;
@@ -598,26 +605,22 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
     }
     if constexpr (NORM) {
         // the rows' residual add and layer norm (the T3 layer's, same
-        // operations in the same order as its norm kernel), into LDS;
-        // workgroup 0 stores the new residual rows
-        __shared__ float red[kGemvWaves];
-        static_assert(kGemvWaves == 4, "the four waves' sums are added in pairs");
+        // operations in the same order as its norm kernel, block_sum256
+        // included), into LDS; workgroup 0 stores the new residual rows
+        __shared__ float red[2 * kGemvWaves];
+        static_assert(kGemvWaves == 4, "block_sum256 takes 256 threads");
+        int ph = 0;
         const int ept = n_embd / (64 * kGemvWaves);  // <= 16
-        auto block_sum = [&](float v) {
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
-            __syncthreads();
-            if (lane == 0) red[wave] = v;
-            __syncthreads();
-            return __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
-        };
         for (int r = 0; r < R; ++r) {
             const float* xr = nm.x_in + (int64_t)r * n_embd;
             const float* yr = nm.y + (int64_t)r * n_embd;
             float* xo = nm.x_out + (int64_t)r * n_embd;
             float* hr = hs + r * rw_words;
             float xv[16];
-            if (nm.act[r] == 0) {  // a stream that takes no step: zeros, x kept
+            int act = act_r[0];
+#pragma unroll
+            for (int q = 1; q < RMAX; ++q) act = r == q ? act_r[q] : act;
+            if (act == 0) {  // a stream that takes no step: zeros, x kept
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const int k = j * 64 * kGemvWaves + tid;
@@ -628,45 +631,84 @@ __global__ __launch_bounds__(64 * kGemvWaves) void head_gemv(
                 }
                 continue;
             }
-            float gv[16], bv[16];  // loaded with the rows: one wait for all
+            // x + y in chunks of 4 values per thread, each chunk's loads
+            // first, then its adds (one wait per chunk: one for n_embd 1024)
             float sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                if (j < ept) {
-                    const int k = j * 64 * kGemvWaves + tid;
-                    gv[j] = nm.g[k];
-                    bv[j] = nm.b[k];
-                    xv[j] = __fadd_rn(yr[k], xr[k]);
-                    sum = __fadd_rn(sum, xv[j]);
+            for (int j0 = 0; j0 < 16; j0 += 4) {
+                if (j0 < ept) {
+                    // unconditional loads (indices clamped to the row), so
+                    // the four are issued before the first add waits
+                    float xa[4], ya[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int k = min(j0 + q, ept - 1) * 64 * kGemvWaves + tid;
+                        xa[q] = xr[k];
+                        ya[q] = yr[k];
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int j = j0 + q;
+                        if (j < ept) {
+                            xv[j] = __fadd_rn(ya[q], xa[q]);
+                            sum = __fadd_rn(sum, xv[j]);
+                        }
+                    }
                 }
             }
-            const float mean = __fdiv_rn(block_sum(sum), (float)n_embd);
-            float q = 0.0f;
+            // the first chunk's g and b, requested now: they arrive during
+            // the reductions (later chunks' with their stores)
+            float g0[4], b0[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int k = min(q, ept - 1) * 64 * kGemvWaves + tid;
+                g0[q] = nm.g[k];
+                b0[q] = nm.b[k];
+            }
+            const float mean = __fdiv_rn(block_sum256(sum, red, ph), (float)n_embd);
+            float q2 = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 if (j < ept) {
                     const float d = __fsub_rn(xv[j], mean);
-                    q = __fadd_rn(q, __fmul_rn(d, d));
+                    q2 = __fadd_rn(q2, __fmul_rn(d, d));
                 }
             }
-            const float var = __fdiv_rn(block_sum(q), (float)n_embd);
+            const float var = __fdiv_rn(block_sum256(q2, red, ph), (float)n_embd);
             const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, nm.eps)));
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 if (j < ept) {
                     const int k = j * 64 * kGemvWaves + tid;
+                    const float gj = j < 4 ? g0[j & 3] : nm.g[k];
+                    const float bj = j < 4 ? b0[j & 3] : nm.b[k];
                     if (blockIdx.x == 0) xo[k] = xv[j];
                     hr[(k >> 5) * 33 + (k & 31)] = __fadd_rn(
-                        __fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), gv[j]), bv[j]);
+                        __fmul_rn(__fmul_rn(__fsub_rn(xv[j], mean), scale), gj), bj);
                 }
             }
         }
     } else {
-        for (int i = tid; i < R * n_embd; i += 64 * kGemvWaves) {
-            const int r = i / n_embd, k = i - r * n_embd;
-            const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
-                                          : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
-            hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = src[k];
+        // the rows into LDS, kStage values per thread requested together and
+        // then written: one memory round trip per batch, not one per value
+        constexpr int kStage = 16;
+        const int total = R * n_embd;
+        for (int i0 = 0; i0 < total; i0 += 64 * kGemvWaves * kStage) {
+            float v[kStage];
+#pragma unroll
+            for (int q = 0; q < kStage; ++q) {
+                const int i = i0 + q * 64 * kGemvWaves + tid;
+                const int r = i / n_embd, k = i - r * n_embd;
+                const float* src = r < n_rows ? hidden0 + (int64_t)r * ld_hidden
+                                              : hidden1 + (int64_t)(r - n_rows) * ld_hidden;
+                v[q] = i < total ? src[k] : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < kStage; ++q) {
+                const int i = i0 + q * 64 * kGemvWaves + tid;
+                const int r = i / n_embd, k = i - r * n_embd;
+                if (i < total) hs[r * rw_words + (k >> 5) * 33 + (k & 31)] = v[q];
+            }
         }
     }
     __syncthreads();

@@ -63,6 +63,49 @@ __device__ __forceinline__ float t3_gelu_f(float x) {
     return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
 }
 
+// A DPP lane exchange within each 16-lane row (ctrl a compile-time DPP code).
+template <int CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                  0xf, 0xf, false));
+}
+
+// Sum of v over each 16-lane row, the same in every lane of the row: the
+// pairs of lanes 1 apart, then 2 (quad_perm), then the two quads of each 8
+// (row_half_mirror: every lane of a quad already holds the quad's sum, so
+// the mirror's partner adds what lane i ^ 4 would), then the two 8-lane
+// halves (row_mirror): the operations of an xor butterfly over 1, 2, 4, 8,
+// each add of a pair the same in either lane, without the LDS-routed
+// permutes a general shuffle takes.
+__device__ __forceinline__ float sum16_dpp(float v) {
+    v = __fadd_rn(v, dpp16<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = __fadd_rn(v, dpp16<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = __fadd_rn(v, dpp16<0x141>(v));  // row_half_mirror
+    return __fadd_rn(v, dpp16<0x140>(v));  // row_mirror
+}
+
+// Sum of one value per thread over a workgroup of 256 threads, the same
+// value in every thread (the T3 layer norm's mean and variance, in the norm
+// kernel and where a product stages the norm itself: both use this, so
+// their results agree bit for bit).  Each wave: its 16-lane rows by
+// sum16_dpp, then the rows' sums as (r0 + r1) + (r2 + r3); the waves' sums
+// the same way through red.  red holds 8 floats and consecutive calls use its
+// halves in turn (ph, starting at 0 in every thread): one barrier per call
+// suffices, since a wave that writes a half again has passed the barrier of
+// the call in between, which no wave reaches before it has read that half.
+__device__ __forceinline__ float block_sum256(float v, float* red, int& ph) {
+    v = sum16_dpp(v);
+    auto lane_v = [&](int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+    };
+    const float w = __fadd_rn(__fadd_rn(lane_v(0), lane_v(16)), __fadd_rn(lane_v(32), lane_v(48)));
+    float* const h = red + 4 * ph;
+    ph ^= 1;
+    if ((threadIdx.x & 63) == 0) h[threadIdx.x >> 6] = w;
+    __syncthreads();
+    return __fadd_rn(__fadd_rn(h[0], h[1]), __fadd_rn(h[2], h[3]));
+}
+
 // Byte offset of the scales in a split buffer of R padded rows of n_embd.
 __host__ __device__ inline size_t split_inv_offset(int R, int n_embd) {
     return ((size_t)R * n_embd * 4 + 255) / 256 * 256;

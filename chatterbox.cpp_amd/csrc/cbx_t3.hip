@@ -71,18 +71,6 @@ struct NormArgs {
     int32_t advance;       // last norm of the step: positions[r] += 1
 };
 
-// Sum of one value per thread over the workgroup (256 threads): butterfly in
-// each wave, then the four waves' sums in a fixed order, so every thread
-// returns the same value.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
-    __syncthreads();  // red[] is reused by consecutive calls
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
-}
-
 // One row per workgroup: the embedding or the residual add, then the layer
 // norm.  Inactive rows (streams that take no step) keep x and write zeros.
 // The next product's split activations for row r from its values in LDS: 8
@@ -111,8 +99,9 @@ __device__ __forceinline__ void norm_split(const NormArgs& a, int r, const float
 
 template <int EPT>
 __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
-    __shared__ float red[4];
+    __shared__ float red[8];
     __shared__ float row_s[EPT * kNormThreads];
+    int ph = 0;
     const int r = blockIdx.x, tid = threadIdx.x;
     const int n = a.n_embd;
     float* xr = a.x + (int64_t)r * n;
@@ -190,14 +179,14 @@ __global__ __launch_bounds__(kNormThreads) void t3_norm(NormArgs a) {
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) s = __fadd_rn(s, xv[j]);
-    const float mean = __fdiv_rn(block_sum(s, red), (float)n);
+    const float mean = __fdiv_rn(block_sum256(s, red, ph), (float)n);
     float q = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const float d = __fsub_rn(xv[j], mean);
         q = __fadd_rn(q, __fmul_rn(d, d));
     }
-    const float var = __fdiv_rn(block_sum(q, red), (float)n);
+    const float var = __fdiv_rn(block_sum256(q, red, ph), (float)n);
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, a.eps)));
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
@@ -262,27 +251,6 @@ __device__ __forceinline__ void attn_store(const AttnArgs& a, int r, int h, int 
         base[256] = lv | (lo << 16);
     }
     if (k == 0) a.inv[split_inv_index(T, m, nball, kb)] = sinv;
-}
-
-// A DPP lane exchange within each 16-lane row (ctrl a compile-time DPP code).
-template <int CTRL>
-__device__ __forceinline__ float dpp16(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                                                  0xf, 0xf, false));
-}
-
-// Sum of v over each 16-lane row, the same in every lane of the row: the
-// pairs of lanes 1 apart, then 2 (quad_perm), then the two quads of each 8
-// (row_half_mirror: every lane of a quad already holds the quad's sum, so
-// the mirror's partner adds what lane i ^ 4 would), then the two 8-lane
-// halves (row_mirror): the operations of an xor butterfly over 1, 2, 4, 8,
-// each add of a pair the same in either lane, without the LDS-routed
-// permutes a general shuffle takes.
-__device__ __forceinline__ float sum16_dpp(float v) {
-    v = __fadd_rn(v, dpp16<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-    v = __fadd_rn(v, dpp16<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-    v = __fadd_rn(v, dpp16<0x141>(v));  // row_half_mirror
-    return __fadd_rn(v, dpp16<0x140>(v));  // row_mirror
 }
 
 // Prefill: every row's k and v stored at its slot and position before any
