@@ -146,9 +146,11 @@ __host__ __device__ inline size_t region_bytes(int32_t cap) {
 }
 
 struct Shared {
-    int red_i[16];
-    float red_f[16];
-    float red_f2[16];
+    // the block reductions' per-wave slots, two sets used in turn (the
+    // row's phase ph): one barrier per reduction (see block_excl_scan)
+    int red_i[2][16];
+    float red_f[2][16];
+    float red_f2[2][16];
     uint32_t sel_digit, sel_above;
     int bin, above_bins, n_cand, above;
     float thr;
@@ -168,44 +170,50 @@ __device__ __forceinline__ int wave_min_i_dpp(int x);
 
 // Exclusive block scan of one int per lane; `total` receives the block sum.
 // The wave steps are DPP operations (no LDS round trip per step), as in every
-// block reduction below.
+// block reduction below.  Each reduction takes one barrier: its waves' slots
+// are set ph of the reduction slots, and consecutive reductions of a row use
+// the two sets in turn (ph, 0 at the row's start in every thread, flips per
+// reduction).  A wave that writes set ph again has passed the barrier of the
+// reduction in between, which no wave reaches before it has read set ph.
 template <int BLOCK>
-__device__ __forceinline__ int block_excl_scan(int v, Shared& sh, int& total) {
+__device__ __forceinline__ int block_excl_scan(int v, Shared& sh, int& total, int& ph) {
     constexpr int NW = BLOCK / 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int incl = wave_incl_scan_dpp(v);
-    if (lane == 63) sh.red_i[wid] = incl;
+    int* const slot = sh.red_i[ph];
+    ph ^= 1;
+    if (lane == 63) slot[wid] = incl;
     __syncthreads();
     int before = 0, tot = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        const int t = sh.red_i[w];
+        const int t = slot[w];
         before += (w < wid) ? t : 0;
         tot += t;
     }
-    __syncthreads();
     total = uni(tot);
     return before + incl - v;
 }
 
 template <int BLOCK>
-__device__ __forceinline__ int block_sum(int v, Shared& sh) {
+__device__ __forceinline__ int block_sum(int v, Shared& sh, int& ph) {
     int total;
-    (void)block_excl_scan<BLOCK>(v, sh, total);
+    (void)block_excl_scan<BLOCK>(v, sh, total, ph);
     return total;
 }
 
 template <int BLOCK>
-__device__ __forceinline__ float block_max(float v, Shared& sh) {
+__device__ __forceinline__ float block_max(float v, Shared& sh, int& ph) {
     constexpr int NW = BLOCK / 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     v = wave_max_dpp(v);
-    if (lane == 0) sh.red_f[wid] = v;
+    float* const slot = sh.red_f[ph];
+    ph ^= 1;
+    if (lane == 0) slot[wid] = v;
     __syncthreads();
-    float m = sh.red_f[0];
+    float m = slot[0];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) m = fmaxf(m, sh.red_f[w]);
-    __syncthreads();
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, slot[w]);
     return unif(m);
 }
 
@@ -213,23 +221,26 @@ __device__ __forceinline__ float block_max(float v, Shared& sh) {
 // min and max of the finite scores and whether any score is NaN / +inf.
 template <int BLOCK>
 __device__ __forceinline__ void block_minmax(float lo, float hi, int bad, Shared& sh, float& blo,
-                                             float& bhi, int& bbad) {
+                                             float& bhi, int& bbad, int& ph) {
     constexpr int NW = BLOCK / 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     lo = wave_min_dpp(lo);
     hi = wave_max_dpp(hi);
     bad = wave_sum_dpp(bad != 0 ? 1 : 0);
-    if (lane == 0) { sh.red_f[wid] = lo; sh.red_f2[wid] = hi; sh.red_i[wid] = bad; }
+    float* const sl = sh.red_f[ph];
+    float* const sh2 = sh.red_f2[ph];
+    int* const sb = sh.red_i[ph];
+    ph ^= 1;
+    if (lane == 0) { sl[wid] = lo; sh2[wid] = hi; sb[wid] = bad; }
     __syncthreads();
-    float l = sh.red_f[0], h = sh.red_f2[0];
-    int b = sh.red_i[0];
+    float l = sl[0], h = sh2[0];
+    int b = sb[0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) {
-        l = fminf(l, sh.red_f[w]);
-        h = fmaxf(h, sh.red_f2[w]);
-        b |= sh.red_i[w];
+        l = fminf(l, sl[w]);
+        h = fmaxf(h, sh2[w]);
+        b |= sb[w];
     }
-    __syncthreads();
     blo = unif(l);
     bhi = unif(h);
     bbad = uni(b);
@@ -243,7 +254,7 @@ __device__ __forceinline__ void block_minmax(float lo, float hi, int bad, Shared
 template <int BLOCK, int EPT, int SHIFT, int BITS>
 __device__ __forceinline__ void radix_pass(const float (&s)[EPT], int n_valid, uint32_t& prefix,
                                            uint32_t& pmask, uint32_t& rem, uint32_t* hist,
-                                           Shared& sh) {
+                                           Shared& sh, int& ph) {
     constexpr int NB = 1 << BITS;
     constexpr int BPT = NB >= BLOCK ? NB / BLOCK : 1;  // bins per lane
     constexpr int NT = NB / BPT;                        // lanes holding bins
@@ -265,7 +276,7 @@ __device__ __forceinline__ void radix_pass(const float (&s)[EPT], int n_valid, u
         tot += (int)c[q];
     }
     int all;
-    uint32_t excl = (uint32_t)block_excl_scan<BLOCK>(tot, sh, all);
+    uint32_t excl = (uint32_t)block_excl_scan<BLOCK>(tot, sh, all, ph);
     if (tid < NT && excl <= rem && rem < excl + (uint32_t)tot) {
 #pragma unroll
         for (int q = 0; q < BPT; ++q) {
@@ -287,11 +298,11 @@ __device__ __forceinline__ void radix_pass(const float (&s)[EPT], int n_valid, u
 // The (rank+1)-th largest key among the first n_valid elements (rank 0-based).
 template <int BLOCK, int EPT>
 __device__ __forceinline__ uint32_t radix_select_desc(const float (&s)[EPT], int n_valid, int rank,
-                                      uint32_t* hist, Shared& sh) {
+                                      uint32_t* hist, Shared& sh, int& ph) {
     uint32_t prefix = 0, pmask = 0, rem = (uint32_t)rank;
-    radix_pass<BLOCK, EPT, 20, 12>(s, n_valid, prefix, pmask, rem, hist, sh);
-    radix_pass<BLOCK, EPT, 8, 12>(s, n_valid, prefix, pmask, rem, hist, sh);
-    radix_pass<BLOCK, EPT, 0, 8>(s, n_valid, prefix, pmask, rem, hist, sh);
+    radix_pass<BLOCK, EPT, 20, 12>(s, n_valid, prefix, pmask, rem, hist, sh, ph);
+    radix_pass<BLOCK, EPT, 8, 12>(s, n_valid, prefix, pmask, rem, hist, sh, ph);
+    radix_pass<BLOCK, EPT, 0, 8>(s, n_valid, prefix, pmask, rem, hist, sh, ph);
     return prefix;
 }
 
@@ -306,7 +317,7 @@ __device__ __forceinline__ uint32_t radix_select_desc(const float (&s)[EPT], int
 // `above` the number of scores strictly larger.
 template <int BLOCK, int EPT>
 __device__ __forceinline__ bool topk_value_bins(const float (&s)[EPT], int k, float lo, float hi, uint32_t* hist,
-                                float* cand, Shared& sh, float& thr, int& above) {
+                                float* cand, Shared& sh, float& thr, int& above, int& ph) {
     constexpr int NB = kValueBins;
     constexpr int BPT = NB / BLOCK >= 1 ? NB / BLOCK : 1;
     constexpr int NT = NB / BPT;
@@ -331,7 +342,7 @@ __device__ __forceinline__ bool topk_value_bins(const float (&s)[EPT], int k, fl
         tot += (int)c[q];
     }
     int n_fin;
-    int excl = block_excl_scan<BLOCK>(tot, sh, n_fin);
+    int excl = block_excl_scan<BLOCK>(tot, sh, n_fin, ph);
     if (n_fin <= k) {  // the (k+1)-th largest is -inf: nothing is removed
         thr = kNegInf;
         above = n_fin;
@@ -517,7 +528,7 @@ __device__ __forceinline__ void sort_list(uint64_t (&x)[NR], int n2, uint64_t* x
 // LDS: start offsets u32[NB + 4], then the keys u64[n].
 template <int BLOCK, int NR>
 __device__ __forceinline__ bool bin_sort(uint64_t (&x)[NR], int n, float blo, float hi,
-                                         uint8_t* region, Shared& sh) {
+                                         uint8_t* region, Shared& sh, int& ph) {
     constexpr int NB = kSortBins;
     constexpr int BPT = NB / BLOCK;  // bins per lane in the scan
     const int tid = threadIdx.x;
@@ -549,7 +560,7 @@ __device__ __forceinline__ bool bin_sort(uint64_t (&x)[NR], int n, float blo, fl
         big = max(big, c[q]);
     }
     int total;
-    int base = block_excl_scan<BLOCK>(local, sh, total);
+    int base = block_excl_scan<BLOCK>(local, sh, total, ph);
 #pragma unroll
     for (int q = 0; q < BPT; ++q) {
         start[tid * BPT + q] = (uint32_t)base;
@@ -597,7 +608,8 @@ __device__ __forceinline__ bool bin_sort(uint64_t (&x)[NR], int n, float blo, fl
 // bitonic network.  LDS: key32[n], start u32[kKeyBins + 4].
 template <int BLOCK, int EPT>
 __device__ __forceinline__ bool bin_sort_keys(const float (&s)[EPT], int n, float lo, float hi,
-                                              uint32_t* key32, uint32_t* start, Shared& sh) {
+                                              uint32_t* key32, uint32_t* start, Shared& sh,
+                                              int& ph) {
     constexpr int NB = kKeyBins;
     constexpr int BPT = NB / BLOCK;  // bins per lane in the scan
     const int tid = threadIdx.x;
@@ -629,7 +641,7 @@ __device__ __forceinline__ bool bin_sort_keys(const float (&s)[EPT], int n, floa
         big = max(big, c[q]);
     }
     int total;
-    int base = block_excl_scan<BLOCK>(local, sh, total);
+    int base = block_excl_scan<BLOCK>(local, sh, total, ph);
 #pragma unroll
     for (int q = 0; q < BPT; ++q) {
         start[tid * BPT + q] = (uint32_t)base;
@@ -1224,7 +1236,8 @@ __device__ __forceinline__ int rank_of(const uint32_t* keptw, const uint32_t* wo
 
 // Exclusive prefix counts of the kept bitmap's words; returns the count.
 template <int BLOCK>
-__device__ __forceinline__ int bitmap_offsets(const uint32_t* keptw, uint32_t* woff, int W, Shared& sh) {
+__device__ __forceinline__ int bitmap_offsets(const uint32_t* keptw, uint32_t* woff, int W, Shared& sh,
+                                              int& ph) {
     constexpr int WPT = (kMaxVocab / 32 + BLOCK - 1) / BLOCK;  // words per lane
     const int tid = threadIdx.x;
     int cnt[WPT];
@@ -1236,7 +1249,7 @@ __device__ __forceinline__ int bitmap_offsets(const uint32_t* keptw, uint32_t* w
         local += cnt[q];
     }
     int n;
-    int base = block_excl_scan<BLOCK>(local, sh, n);
+    int base = block_excl_scan<BLOCK>(local, sh, n, ph);
 #pragma unroll
     for (int q = 0; q < WPT; ++q) {
         const int w = tid * WPT + q;
@@ -1667,7 +1680,7 @@ __device__ __forceinline__ int fast_path(const KernelArgs& a, const cbx_params& 
                                           float blo, float bhi,
                                           bool use_topp, bool use_pen, const uint32_t* seen,
                                           uint32_t* keptw, uint32_t* woff, uint8_t* region,
-                                          const uint64_t* tab, Shared& sh) {
+                                          const uint64_t* tab, Shared& sh, int& ph) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     uint64_t* xbuf = reinterpret_cast<uint64_t*>(region);
     float* E = reinterpret_cast<float*>(region);
@@ -1684,7 +1697,7 @@ __device__ __forceinline__ int fast_path(const KernelArgs& a, const cbx_params& 
     float mx_surv = kNegInf;
     // ---- top-p (main.cpp:750-772) ----
     if (use_topp) {
-        if (!bin_sort<BLOCK, NR>(x, n_surv, blo, bhi, region, sh)) sort_list<BLOCK, NR>(x, n2, xbuf);
+        if (!bin_sort<BLOCK, NR>(x, n_surv, blo, bhi, region, sh, ph)) sort_list<BLOCK, NR>(x, n2, xbuf);
         CBX_STAMP(4);
         if (tid == 0) sh.mx = desc_key_value(x[0]);
         __syncthreads();
@@ -1751,7 +1764,7 @@ __device__ __forceinline__ int fast_path(const KernelArgs& a, const cbx_params& 
                     atomicOr(&keptw[i >> 5], 1u << (i & 31));
                 }
             __syncthreads();
-            (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+            (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh, ph);
             // first sorted position of v: the count of scores above it
             auto above = [&](float v) {
                 int lo = 0, hi = n_surv;
@@ -1816,7 +1829,7 @@ __device__ __forceinline__ int fast_path(const KernelArgs& a, const cbx_params& 
         float m = kNegInf;
 #pragma unroll
         for (int r = 0; r < NR; ++r) m = ((kept >> r) & 1u) ? fmaxf(m, val[r]) : m;
-        const float mx_kept = use_topp ? mx_surv : block_max<BLOCK>(m, sh);
+        const float mx_kept = use_topp ? mx_surv : block_max<BLOCK>(m, sh, ph);
 #pragma unroll
         for (int r = 0; r < NR; ++r)
             if (((kept >> r) & 1u) &&
@@ -1877,6 +1890,7 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
 
     const cbx_params P = a.params[row];
     const int64_t rs = (int64_t)step * a.n_rows + row;  // row-step linear id
+    int ph = 0;  // the block reductions' slot set (block_excl_scan)
     CBX_STAMP(0);
 
     // ---- load (all loads first), combine, mask, temperature (main.cpp:733-738) ----
@@ -1991,7 +2005,7 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
         s[j] = v;
     }
     int bad;
-    block_minmax<BLOCK>(lo, hi, nonfinite, sh, lo, hi, bad);
+    block_minmax<BLOCK>(lo, hi, nonfinite, sh, lo, hi, bad, ph);
     CBX_STAMP(1);
     const uint32_t flags = bad ? CBX_INFO_NONFINITE : 0u;
 
@@ -2007,16 +2021,16 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
             int mine_f = 0;
 #pragma unroll
             for (int j = 0; j < EPT; ++j) mine_f += (s[j] != kNegInf) ? 1 : 0;
-            const int n_fin = block_sum<BLOCK>(mine_f, sh);
+            const int n_fin = block_sum<BLOCK>(mine_f, sh, ph);
             thr = n_fin > P.top_k ? lo : kNegInf;
             above = n_fin > P.top_k ? 0 : n_fin;
         } else if (bad ||
-                   !topk_value_bins<BLOCK, EPT>(s, P.top_k, lo, hi, hist, cand, sh, thr, above)) {
-            thr = okey_inv(radix_select_desc<BLOCK, EPT>(s, V, P.top_k, hist, sh));
+                   !topk_value_bins<BLOCK, EPT>(s, P.top_k, lo, hi, hist, cand, sh, thr, above, ph)) {
+            thr = okey_inv(radix_select_desc<BLOCK, EPT>(s, V, P.top_k, hist, sh, ph));
             int n_above = 0;
 #pragma unroll
             for (int j = 0; j < EPT; ++j) n_above += (s[j] > thr) ? 1 : 0;
-            above = block_sum<BLOCK>(n_above, sh);
+            above = block_sum<BLOCK>(n_above, sh, ph);
         }
         if (above < P.top_k) thr = __fsub_rn(thr, 1e-10f);
         sblo = fmaxf(thr, lo);
@@ -2030,7 +2044,7 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
 #pragma unroll
     for (int j = 0; j < EPT; ++j) mine += (s[j] != kNegInf) ? 1 : 0;
     int n_surv;
-    int off = block_excl_scan<BLOCK>(mine, sh, n_surv);
+    int off = block_excl_scan<BLOCK>(mine, sh, n_surv, ph);
     if (n_surv > cap) {
         if (tid == 0) {
             a.tokens[rs] = -1;
@@ -2058,20 +2072,20 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
         const int rows_needed = uni((max(64, pow2ceil(n_surv)) + BLOCK - 1) / BLOCK);
         if (rows_needed <= 1) {
             return fast_path<BLOCK, EPT, 1>(a, P, rs, u_draw, flags, n_surv, sblo, hi, use_topp,
-                                            use_pen, seen, keptw, woff, region, tab, sh);
+                                            use_pen, seen, keptw, woff, region, tab, sh, ph);
         } else if constexpr (MAXNR >= 2) {
             if (rows_needed == 2) {
                 return fast_path<BLOCK, EPT, 2>(a, P, rs, u_draw, flags, n_surv, sblo, hi, use_topp,
-                                                use_pen, seen, keptw, woff, region, tab, sh);
+                                                use_pen, seen, keptw, woff, region, tab, sh, ph);
             } else if constexpr (MAXNR >= 4) {
                 if (rows_needed <= 4) {
                     return fast_path<BLOCK, EPT, 4>(a, P, rs, u_draw, flags, n_surv, sblo, hi,
                                                     use_topp, use_pen, seen, keptw, woff, region,
-                                                    tab, sh);
+                                                    tab, sh, ph);
                 } else if constexpr (MAXNR >= 8) {
                     return fast_path<BLOCK, EPT, 8>(a, P, rs, u_draw, flags, n_surv, sblo, hi,
                                                     use_topp, use_pen, seen, keptw, woff, region,
-                                                    tab, sh);
+                                                    tab, sh, ph);
                 }
             }
         }
@@ -2090,7 +2104,7 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
     bool tie = false;
     if (use_topp) {
         // counting sort by value bins (finite rows), else the bitonic network
-        if (bad || !bin_sort_keys<BLOCK, EPT>(s, n_surv, sblo, hi, key32, key32 + cap, sh)) {
+        if (bad || !bin_sort_keys<BLOCK, EPT>(s, n_surv, sblo, hi, key32, key32 + cap, sh, ph)) {
 #pragma unroll
             for (int j = 0; j < EPT; ++j)
                 if (s[j] != kNegInf) key32[off++] = ~okey(s[j]);
@@ -2195,7 +2209,7 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
                     atomicOr(&keptw[i >> 5], 1u << (i & 31));
                 }
             __syncthreads();
-            (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh);
+            (void)bitmap_offsets<BLOCK>(keptw, woff, W, sh, ph);
 #pragma unroll
             for (int j = 0; j < EPT; ++j)
                 if (s[j] != kNegInf) {
@@ -2240,7 +2254,7 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
         float m = kNegInf;
 #pragma unroll
         for (int j = 0; j < EPT; ++j) m = ((kept >> j) & 1u) ? fmaxf(m, s[j]) : m;
-        const float mx_kept = use_topp ? unif(sh.mx) : block_max<BLOCK>(m, sh);
+        const float mx_kept = use_topp ? unif(sh.mx) : block_max<BLOCK>(m, sh, ph);
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
             if (((kept >> j) & 1u) && expf_libm_branchless(__fsub_rn(s[j], mx_kept), tab) < P.min_p)
