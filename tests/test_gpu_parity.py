@@ -161,6 +161,31 @@ def test_device_running_sum_scan(cbx, torch_cuda):
     assert (n <= 64).sum() > 10 and ((n > 1088) & (desc == 1)).sum() > 100
 
 
+def test_device_running_sum_short_lists(cbx, torch_cuda):
+    # The workgroup kernel's running sums over 1 to 64 terms (one term per
+    # lane): sweep chains for at most 8 lanes, binade segments (with the
+    # threshold search in the same pass) above that, against numpy's
+    # left-to-right float32 accumulation, bit for bit.
+    import seqsum_cases
+    torch = torch_cuda
+    mod, s = cbx
+    t, off, thr, want_sum, want_hit, desc = seqsum_cases.make_cases(3000, 29, max_n=64,
+                                                                    with_order=True)
+    sums = torch.zeros(len(off) - 1, dtype=torch.float32, device="cuda")
+    hits = torch.full((len(off) - 1,), -9, dtype=torch.int32, device="cuda")
+    D.runsum(torch.from_numpy(t).cuda(), torch.from_numpy(off).cuda(),
+             torch.from_numpy(thr).cuda(), torch.from_numpy(desc).cuda(), sums, hits)
+    torch.cuda.synchronize()
+    got_sum = sums.cpu().numpy()
+    got_hit = hits.cpu().numpy()
+    bad = np.nonzero(got_sum.view(np.uint32) != want_sum.view(np.uint32))[0]
+    assert bad.size == 0, (bad[:5], got_sum[bad[:5]], want_sum[bad[:5]])
+    has_thr = thr > 0
+    assert np.array_equal(got_hit[has_thr], want_hit[has_thr])
+    n = np.diff(off)
+    assert (n <= 8).sum() > 100 and ((n > 8) & has_thr).sum() > 300 and ((n > 8) & (desc == 1)).sum() > 1000
+
+
 def test_device_chain_sums(cbx, torch_cuda):
     # The one-wave kernel's running sums (sweep chains, binade segments for
     # long per-lane runs) against numpy's left-to-right float32 accumulation,
