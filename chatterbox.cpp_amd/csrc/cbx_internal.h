@@ -86,6 +86,11 @@ hipError_t launch_w26t(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_w33t(const KernelArgs& a, hipStream_t stream);
 // V <= 32768 without CFG rows: the one-wave kernel reading the row in chunks.
 hipError_t launch_w128c(const KernelArgs& a, hipStream_t stream);
+hipError_t launch_w128c2(const KernelArgs& a, hipStream_t stream);
+// Launches of chunked rows (V > 8448) with at most this many row-steps split
+// each row over two waves (two per SIMD at this size): a row's time is its
+// wave's serial scan, halved; above it, one wave per row.
+constexpr int64_t kChunkTwoWaveRows = 2048;
 hipError_t launch_v512x8(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v512x13(const KernelArgs& a, hipStream_t stream);
 hipError_t launch_v512x16(const KernelArgs& a, hipStream_t stream);

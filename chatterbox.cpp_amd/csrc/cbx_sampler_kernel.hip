@@ -29,7 +29,8 @@ hipError_t launch_sample(const KernelArgs& a, hipStream_t stream) {
         if (a.n_vocab <= 256 * 26) return a.n_vocab > 256 * 25 ? launch_w26t(a, stream) : launch_w26(a, stream);
         if (a.n_vocab <= kWaveMaxVocab)
             return a.n_vocab > 256 * 32 ? launch_w33t(a, stream) : launch_w33(a, stream);
-        return launch_w128c(a, stream);
+        return (int64_t)a.n_steps * a.n_rows <= kChunkTwoWaveRows ? launch_w128c2(a, stream)
+                                                                  : launch_w128c(a, stream);
     }
     // registers per lane sized to the vocabulary (6563 -> 13 per lane)
     if (a.n_vocab <= 512 * 8) return launch_v512x8(a, stream);

@@ -6,4 +6,9 @@ namespace cbx {
 hipError_t launch_w128c(const KernelArgs& a, hipStream_t stream) {
     return launch_wave<128, 0, true>(a, stream);
 }
+// the same with each row's chunks split over two waves (launches of at most
+// kChunkTwoWaveRows row-steps)
+hipError_t launch_w128c2(const KernelArgs& a, hipStream_t stream) {
+    return launch_wave<128, 0, true, true>(a, stream);
+}
 }  // namespace cbx

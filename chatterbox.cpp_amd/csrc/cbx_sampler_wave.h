@@ -802,15 +802,35 @@ __device__ __forceinline__ bool lean_topp(WaveSmem<Q>& sm, int n_surv, float mx,
 constexpr int kChunkV = 8;
 constexpr int kChunkBins = 256;
 
-template <int Q>
+// W2: the row's chunks split over two waves of one workgroup (smv: their two
+// WaveSmem, wv: this wave).  Wave 1 scans the second half into its own list
+// with wave-local synchronisation, publishes its count, maximum and flags and
+// meets wave 0 at the row's one workgroup barrier, then leaves (n_surv = -1:
+// the caller returns); wave 0 scans the first half, merges wave 1's entries
+// at or above its running bound tau (the global top k + 1 scores are among
+// them: each half's tau is at most that half's (k+1)-th largest score, so at
+// most the row's), and goes on alone.  Every early return of either wave
+// comes after that barrier.
+template <int Q, bool W2 = false>
 __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rsc, int lane,
                                             int k, bool use_topk, float (&cur)[4 * kChunkV],
                                             float& hi, float& lo, bool& have_lo, bool& bad,
-                                            float& thr, int& n_surv) {
+                                            float& thr, int& n_surv, WaveSmem<Q>* smv = nullptr,
+                                            int wv = 0) {
     static_assert(kChunkBins == 4 * 64, "four bins per lane");
     static_assert(8 * Q >= kWaveCap, "the list's values fit the kept-bitmap words");
     const int V = rsc.V;
     const int nch = (V + 256 * kChunkV - 1) / (256 * kChunkV);
+    // this wave's chunks [cb, ce)
+    const int cb = W2 && wv == 1 ? (nch + 1) / 2 : 0;
+    const int ce = W2 && wv == 0 ? (nch + 1) / 2 : nch;
+    // LDS ordering among this wave's lanes (one wave per workgroup: the
+    // workgroup barrier; two: a wave-local fence, the other wave's storage
+    // being its own)
+    auto sync = [&]() {
+        if constexpr (W2) wave_lds_sync();
+        else __syncthreads();
+    };
     const uint32_t list0 = lds_offset(&sm.list[0]);
     uint32_t* const hist = sm.keptw;  // free until the filters: bins, then candidates
     auto val = [](uint64_t w) { return __builtin_bit_cast(float, (uint32_t)(w >> 32)); };
@@ -823,7 +843,13 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
     if (rsc.fstop) {
         // forced stop: every id but the stop token is -inf (as the one-pass
         // kernel's masks make it), so that token's score alone decides; the
-        // chunks already requested are not read
+        // chunks already requested are not read (and wave 1 has nothing to do)
+        if constexpr (W2) {
+            if (wv == 1) {
+                n_surv = -1;
+                return;
+            }
+        }
         float x = kNegInf;
         if (rsc.stop >= 0 && rsc.stop < V) {
             x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc.rl, rsc.stop * 4, 0, 0));
@@ -845,7 +871,7 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
         lo = fin ? x : kPosInf;
         have_lo = true;
         n_surv = fin ? 1 : 0;
-        __syncthreads();
+        sync();
         return;
     }
     const uint32_t shl = 4u * (uint32_t)(lane & 7);  // this lane's 4 ids in its mask word
@@ -857,9 +883,9 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
         };
 #pragma unroll
         for (int q = 0; q < 4; ++q) hist[4 * lane + q] = 0u;
-        __syncthreads();
+        sync();
         for (int i = lane; i < cnt; i += 64) atomicAdd(&hist[bin(val(sm.list[i]))], 1u);
-        __syncthreads();
+        sync();
         uint32_t c4[4];
         int tot = 0;
 #pragma unroll
@@ -884,7 +910,7 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
         const int L = __builtin_ctzll(__ballot(mine));
         bsel = __builtin_amdgcn_readlane(b, L);
         above_bins = __builtin_amdgcn_readlane(ab, L);
-        __syncthreads();  // bin counts read
+        sync();  // bin counts read
     };
     auto list_range = [&](float& lmn, float& lmx) {
         float a0 = kPosInf, a1 = kNegInf;
@@ -907,7 +933,7 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
             nn += __popcll(m);
         }
         cnt = nn;
-        __syncthreads();
+        sync();
     };
     // tau raised as far as the list's bins allow; false when it cannot rise
     auto prune = [&]() -> bool {
@@ -938,7 +964,7 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
     float buf[kRing][4 * kChunkV];
     uint32_t mw[kRing][kChunkV];
     auto issue = [&](int c, float (&bv)[4 * kChunkV], uint32_t (&wv)[kChunkV]) {
-        if (c >= nch) return;
+        if (c >= ce) return;
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j) load4(rsc.rl, lane * 16, (c * kChunkV + j) * 1024, &bv[4 * j]);
         if (rsc.masked_ids) {
@@ -995,28 +1021,64 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
         }
     };
 #pragma unroll
-    for (int e = 0; e < 4 * kChunkV; ++e) buf[0][e] = cur[e];  // chunk 0, loaded by the caller
+    for (int e = 0; e < 4 * kChunkV; ++e) buf[0][e] = cur[e];  // chunk cb, loaded by the caller
     if (rsc.masked_ids) {
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j)
-            mw[0][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc.ra, (8 * j + (lane >> 3)) * 4,
-                                                                      0, 0);
+            mw[0][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                rsc.ra, (8 * (cb * kChunkV + j) + (lane >> 3)) * 4, 0, 0);
     }
 #pragma unroll
-    for (int r = 1; r < kRing; ++r) issue(r, buf[r], mw[r]);
+    for (int r = 1; r < kRing; ++r) issue(cb + r, buf[r], mw[r]);
 #pragma unroll 1
-    for (int c0 = 0; c0 < nch && !over; c0 += kRing) {
+    for (int c0 = cb; c0 < ce && !over; c0 += kRing) {
 #pragma unroll
         for (int r = 0; r < kRing; ++r) {
-            if (c0 + r < nch && !over) {
+            if (c0 + r < ce && !over) {
                 scan(c0 + r, buf[r], mw[r]);
                 issue(c0 + r + kRing, buf[r], mw[r]);
             }
         }
     }
-    __syncthreads();
+    sync();
     bad = __ballot(nfb) != 0;
     hi = wave_max_dpp(hi);
+    if constexpr (W2) {
+        // wave 1 publishes (its list stays in its own storage), both waves
+        // meet once, wave 1 leaves; wave 0 takes the second half's entries
+        // at or above its tau into its list, pruning as it fills
+        WaveSmem<Q>& s1 = smv[1];
+        if (wv == 1 && lane == 0) {
+            s1.h.seen[0] = over ? 0xffffffffu : (uint32_t)cnt;
+            s1.h.seen[1] = __builtin_bit_cast(uint32_t, hi);
+            s1.h.seen[2] = bad ? 1u : 0u;
+        }
+        __syncthreads();
+        if (wv == 1) {
+            n_surv = -1;
+            return;
+        }
+        const uint32_t c1w = s1.h.seen[0];
+        hi = fmaxf(hi, __builtin_bit_cast(float, s1.h.seen[1]));
+        bad = bad || s1.h.seen[2] != 0u;
+        over = over || c1w == 0xffffffffu;
+        if (!bad && !over) {
+            const int c1 = (int)c1w;
+            for (int base = 0; base < c1; base += 64) {
+                if (cnt + 64 > kWaveCap && (!prune() || cnt + 64 > kWaveCap)) {
+                    over = true;
+                    break;
+                }
+                const int i = base + lane;
+                const uint64_t w = i < c1 ? s1.list[i] : 0ull;
+                const float t2 = tau == kNegInf ? -3.40282347e38f : tau;
+                const uint64_t m = __ballot(i < c1 && val(w) >= t2);
+                lds_store_b64_lanes(list0 + 8u * (uint32_t)(cnt + ballot_rank(m)), w, m);
+                cnt += __popcll(m);
+            }
+            sync();
+        }
+    }
     if (bad || over) {
         n_surv = kWaveCap + 1;  // more than any capacity: the redo pass takes the row
         return;
@@ -1043,7 +1105,7 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
             if (in) cand[nc + ballot_rank(m)] = v;
             nc += __popcll(m);
         }
-        __syncthreads();
+        sync();
         const int rem = k - above_bins;  // 0 <= rem < nc
         float tv = kNegInf;
         int tgt = 0;
@@ -1066,7 +1128,7 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
         thr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tv), L2));
         const int above = above_bins + __builtin_amdgcn_readlane(tgt, L2);
         if (above < k) thr = __fsub_rn(thr, 1e-10f);
-        __syncthreads();  // candidates read
+        sync();  // candidates read
         const float th = thr;
         compact([&](float v) { return v > th; });
     } else {
@@ -1081,13 +1143,19 @@ __device__ __forceinline__ void chunk_front(WaveSmem<Q>& sm, const RowScores& rs
 
 // ------------------------------------------------------------------ kernel
 
-template <int Q, int JT, bool CH = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) void sample_rows_wave(
+template <int Q, int JT, bool CH = false, bool W2 = false>
+__global__ __launch_bounds__(W2 ? 128 : 64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) void sample_rows_wave(
     KernelArgs a) {
-    __shared__ WaveSmem<Q> sm;
+    static_assert(!W2 || CH, "two waves per row: chunked rows only");
+    // W2: two waves per row, each with its own storage (chunk_front)
+    __shared__ WaveSmem<Q> smv[W2 ? 2 : 1];
+    // (readfirstlane: the compiler then knows it is the same across the wave,
+    // so branches on it are uniform)
+    const int wv = W2 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
+    WaveSmem<Q>& sm = smv[wv];
     constexpr int EPL = 4 * Q;  // scores per lane
     constexpr int R = kWaveRows;
-    const int lane = threadIdx.x;
+    const int lane = W2 ? (int)(threadIdx.x & 63u) : (int)threadIdx.x;
     const int64_t g = xcd_spread(blockIdx.x, gridDim.x, a.n_rows);
     const int step = (int)(g / a.n_rows), row = (int)(g % a.n_rows);
     const int V = a.n_vocab;
@@ -1146,9 +1214,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             }
         }
     } else {
-        // chunk 0 (ids 0 .. 256 kChunkV - 1); the rest stream in as it is scanned
+        // the wave's first chunk (chunk 0: ids 0 .. 256 kChunkV - 1; wave 1 of
+        // two: the second half's first); the rest stream in as it is scanned
+        const int nch = (V + 256 * kChunkV - 1) / (256 * kChunkV);
+        const int cb = W2 && wv == 1 ? (nch + 1) / 2 : 0;
 #pragma unroll
-        for (int j = 0; j < kChunkV; ++j) load4(rsc.rl, lane * 16, j * 1024, &cur[4 * j]);
+        for (int j = 0; j < kChunkV; ++j) load4(rsc.rl, lane * 16, (cb * kChunkV + j) * 1024, &cur[4 * j]);
     }
     // ---- history ids -> seen bitmap (main.cpp:775) ----
     // Loads past the history read 0 and are masked out.
@@ -1156,7 +1227,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(hrow), (short)0, hlen * 4, kBufferWord3);
     int hid[HB];
-    if (use_pen) {
+    const bool build_seen = use_pen && wv == 0;  // (wave 1 of two only scans)
+    if (build_seen) {
 #pragma unroll
         for (int u = 0; u < HB; ++u)
             hid[u] = __builtin_amdgcn_raw_buffer_load_b32(rh, (u * 64 + lane) * 4, 0, 0);
@@ -1172,7 +1244,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
     u_draw = fresh_d(u_draw);
     if (lane < 32) sm.tab[lane] = tabv;
     for (int w = lane; w < 8 * Q; w += 64) sm.h.seen[w] = 0u;
-    if (use_pen) {
+    if (build_seen) {
         for (int b0 = 0; b0 < hlen; b0 += HB * 64) {
             if (b0 > 0) {
 #pragma unroll
@@ -1654,7 +1726,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
             n_surv = n;
         }
     } else {
-        chunk_front<Q>(sm, rsc, lane, k, use_topk, cur, hi, lo, have_lo, bad, thr, n_surv);
+        chunk_front<Q, W2>(sm, rsc, lane, k, use_topk, cur, hi, lo, have_lo, bad, thr, n_surv, smv,
+                           wv);
+        if constexpr (W2) {
+            if (wv == 1) return;  // its half is merged into wave 0's list
+        }
         flags = bad ? CBX_INFO_NONFINITE : 0u;
     }
     CBX_STAMP(4);
@@ -2288,10 +2364,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WAVE_WPE))) 
 
 // Q: scores per lane / 4 (V <= 256*Q); JT: V > 256*JT for every launch; CH:
 // the row read in chunks (no CFG rows).
-template <int Q, int JT, bool CH = false>
+template <int Q, int JT, bool CH = false, bool W2 = false>
 hipError_t launch_wave(const KernelArgs& a, hipStream_t stream) {
     const int64_t rows = (int64_t)a.n_steps * a.n_rows;
-    hipLaunchKernelGGL((sample_rows_wave<Q, JT, CH>), dim3((unsigned)rows), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((sample_rows_wave<Q, JT, CH, W2>), dim3((unsigned)rows), dim3(W2 ? 128 : 64), 0,
+                       stream, a);
     return hipGetLastError();
 }
 

@@ -432,6 +432,32 @@ def test_chunked_one_wave(cbx, torch_cuda, V):
     parity.compare(f"chunked_batched_{V}", tg[ok], ig[ok], tr[ok], ir[ok], u[ok], pg[ok], pr[ok])
 
 
+@pytest.mark.parametrize("V", [12000, 32768])
+def test_chunked_one_wave_large_launch(cbx, torch_cuda, V):
+    """Chunked rows in a launch of more than 2048 row-steps (256 streams x 9
+    steps): one wave per row, where the smaller launches above split each
+    row's chunks over two waves.  top_k 50 / 250 / 1000, planted ties above
+    and at the threshold, an all-masked row."""
+    w = pkg.workloads()
+    d = w.batched_streams(B=256, steps=9, seed=0x5EEDB + V, V=V)
+    x = d["logits"]
+    rng = np.random.default_rng(V + 1)
+    for r in range(0, x.shape[0], 53):
+        x[r, rng.choice(V, size=70, replace=False)] = 13.0
+    for r in range(11, x.shape[0], 59):
+        x[r, rng.choice(V, size=40, replace=False)] = 9.0
+        x[r, rng.choice(V, size=30, replace=False)] = 10.0
+    x[3, :] = -np.inf
+    n = x.shape[0]
+    assert n > 2048
+    u = O.mt_canonical(31 + V, n)
+    say(f"chunked one-wave, large launch: 256 x 9, V={V}")
+    tg, ig, pg = gpu_batch(cbx, torch_cuda, x, d["params"], u, d["history"], d["hist_len"],
+                           n_steps=9, max_survivors=1000)
+    tr, ir, pr = oracle_rows(x, d["params"], u, d["history"], d["hist_len"])
+    parity.compare(f"chunked_large_{V}", tg, ig, tr, ir, u, pg, pr)
+
+
 @pytest.mark.parametrize("V", [6563, 8194, 3000])
 def test_masked_one_wave(cbx, torch_cuda, V):
     """Allowed bitmask, forced stop, min-p and penalty at vocabularies the
