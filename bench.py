@@ -630,7 +630,7 @@ def config_masked_stress(torch, mod, sampler, stream, dev, steps=48, n_slabs=4):
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 5),
                          "algorithmic_bytes_per_step": bytes_step,
-                         "kernel": "sample_rows_wave<128,0,true> (the row read in chunks)"},
+                         "kernel": "sample_rows_wave<128,0,true,true> (the row read in chunks by two waves)"},
             "overflow_rows": int(np.sum((flags & 0x20) != 0))}
 
 
