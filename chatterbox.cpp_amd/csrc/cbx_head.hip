@@ -206,7 +206,7 @@ constexpr int RING = 2;
 // (rows of n_vocab values: this workgroup's 32 outputs are block blockIdx.x
 // of each of its rows) instead of fp32 rows.
 template <int WT, int NT>
-__global__ __launch_bounds__(64 * KS) void head_mfma(const void* W, const float* bias,
+__global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(WT == CBX_WTYPE_Q4_0 ? 4 : 1))) void head_mfma(const void* W, const float* bias,
                                                      const uint32_t* parts, const float* inv,
                                                      int n_tiles, float* out0, float* out1,
                                                      int64_t ld_out, int n_rows, int n_vocab,
