@@ -96,10 +96,12 @@ def make_inputs(torch, steps_per_launch, n_slabs, dev):
     rows = steps_per_launch * B
     for _ in range(n_slabs):
         x = torch.randn((rows, V), generator=g, device=dev) * 3.0
-        # 5 spikes per row at random ids (a repeated id keeps one spike)
+        # 5 spikes per row at random ids; a repeated id keeps the higher spike
+        # (a plain scatter of duplicate ids keeps either one, differently from
+        # one process to the next)
         pos = torch.randint(0, V, (rows, 5), generator=g, device=dev)
         heights = torch.rand((rows, 5), generator=g, device=dev) * 6.0 + 6.0
-        x.scatter_(1, pos, heights)
+        x.scatter_reduce_(1, pos, heights, reduce="amax", include_self=False)
         slabs.append(x.contiguous())
     rng = np.random.default_rng(SEED)
     hist = rng.integers(0, V, size=(B, HIST_MAX)).astype(np.int32)

@@ -473,9 +473,10 @@ __device__ __forceinline__ void for_row_groups4(int n, F&& f) {
 // (equal scores share a bin).  The reference's float running sum cum_i of
 // q_j = fl(e_j / psum), psum its float sum in sorted order, differs from
 // Y_i = P_i / S (S the binary64 total) by at most: i half-ulps of cum_i (the
-// adds), 2^-24 Y_i (the divisions), and Y_i * gamma for psum itself, gamma =
-// (n - 1) 2^-24 / (1 - (n - 1) 2^-24) the classical bound of a recursive
-// float sum of n non-negative terms in any order.  When every bin's last
+// adds), 2^-24 Y_i (the divisions), and Y_i * gamma for psum itself: the
+// classical bound of a recursive float sum of n non-negative terms in any
+// order, (n - 1) 2^-24 / (1 - (n - 1) 2^-24), or where smaller (n - 1) half
+// ulps of the binade that bound puts the float sum in, over S.  When every bin's last
 // position lies certainly below or certainly at/above top_p, the crossing
 // lies in the bin between the last "below" and the first "above"; that bin's
 // few survivors are ranked (descending score, ascending id: std::sort's order
@@ -649,8 +650,16 @@ __device__ __forceinline__ bool lean_topp(WaveSmem<Q>& sm, int n_surv, float mx,
     const double x0 = __dsub_rn(incl, part);
     CBX_STAMP(44);
     const double p = (double)top_p;
-    const double gam = (double)n_surv * 0x1p-24 * (1.0 + 0x1p-10);
+    // psum's relative rounding: each of its n - 1 adds of non-negative terms
+    // is off by at most half an ulp of its result, whose binade is at most
+    // that of the float sum, itself at most S (1 + n 2^-24 (1 + 2^-10)) (the
+    // textbook bound of a recursive sum, Higham §4.2): (n - 1) 2^(E - 24) / S
+    // with 2^E <= that bound's binade, at most the textbook n 2^-24
     const double inv = __ddiv_rn(1.0, S);
+    const double gam_t = (double)n_surv * 0x1p-24 * (1.0 + 0x1p-10);
+    const int es = __builtin_amdgcn_frexp_exp(__dmul_rn(S, 1.0 + gam_t)) - 1;
+    const double gam = fmin(gam_t, __dmul_rn(__dmul_rn((double)(n_surv - 1), ldexp(1.0, es - 24)),
+                                             __dmul_rn(inv, 1.0 + 0x1p-10)));
     // this lane's bound (its last index and the binade of its last Y); the
     // thresholds scaled by S (their rounding is inside the 1e-12)
     const double yl = __dmul_rn(__dadd_rn(x0, part), inv);
