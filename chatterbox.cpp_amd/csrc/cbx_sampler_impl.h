@@ -1076,10 +1076,12 @@ constexpr int run_bound(int n) {
 // the second term, plus 1e-12 for the binary64 arithmetic.  Where Y -/+ that
 // bound puts the first crossing at one index the answer is certain (`last`,
 // n - 1 when the sum never reaches top_p); otherwise returns false and the
-// caller sums the q's.  One wave, chunks of 64*C terms.
+// caller sums the q's, of which the first `upto` hold the crossing (the sum
+// of the first upto q's is certainly >= top_p; n when no index is certain).
+// One wave, chunks of 64*C terms.
 template <int C, class Term>
 __device__ __forceinline__ bool certified_cut_c(Term&& term, int n, float psum, float top_p,
-                                                int& last) {
+                                                int& last, int& upto) {
     const int lane = threadIdx.x & 63;
     const double p = (double)top_p;
     const double inv = __ddiv_rn(1.0, (double)psum);
@@ -1118,7 +1120,10 @@ __device__ __forceinline__ bool certified_cut_c(Term&& term, int n, float psum, 
         const int c_hi = min(wave_min_i_dpp(n_hi < C ? base + lane * C + n_hi : 0x7fffffff), n);
         const int c_lo = min(wave_min_i_dpp(n_lo < C ? base + lane * C + n_lo : 0x7fffffff), n);
         if (c_hi < n) {  // the earliest possible crossing is here
-            if (c_lo != c_hi) return false;
+            if (c_lo != c_hi) {
+                upto = c_lo < n ? c_lo + 1 : n;
+                return false;
+            }
             last = c_hi;
             return true;
         }
@@ -1131,14 +1136,15 @@ __device__ __forceinline__ bool certified_cut_c(Term&& term, int n, float psum, 
 // certified_cut_c with C picked from n (at most NMAX): 1, 5, 17 or 33.
 template <int NMAX, class Term>
 __device__ __forceinline__ bool certified_cut(Term&& term, int n, float psum, float top_p,
-                                              int& last) {
+                                              int& last, int& upto) {
     n = uni(n);
-    if (NMAX <= 64 || n <= 64) return certified_cut_c<1>(term, n, psum, top_p, last);
+    upto = n;
+    if (NMAX <= 64 || n <= 64) return certified_cut_c<1>(term, n, psum, top_p, last, upto);
     if constexpr (NMAX > 64) {
-        if (NMAX <= 320 || n <= 320) return certified_cut_c<5>(term, n, psum, top_p, last);
+        if (NMAX <= 320 || n <= 320) return certified_cut_c<5>(term, n, psum, top_p, last, upto);
         if constexpr (NMAX > 320) {
-            if (NMAX <= 1088 || n <= 1088) return certified_cut_c<17>(term, n, psum, top_p, last);
-            if constexpr (NMAX > 1088) return certified_cut_c<33>(term, n, psum, top_p, last);
+            if (NMAX <= 1088 || n <= 1088) return certified_cut_c<17>(term, n, psum, top_p, last, upto);
+            if constexpr (NMAX > 1088) return certified_cut_c<33>(term, n, psum, top_p, last, upto);
         }
     }
     return false;  // not reached
@@ -1723,12 +1729,16 @@ __device__ __forceinline__ int fast_path(const KernelArgs& a, const cbx_params& 
             const float psum =
                 wave_run_sum<run_bound<BLOCK>(NR * BLOCK), false, true>(e_at, n_surv, 0.0f, 0.0f, hit, fin);
             CBX_STAMP(6);
-            int last;
-            if (!(fin && certified_cut<run_bound<BLOCK>(NR * BLOCK)>(e_at, n_surv, psum, P.top_p, last))) {
+            int last, upto = n_surv;
+            if (!(fin && certified_cut<run_bound<BLOCK>(NR * BLOCK)>(e_at, n_surv, psum, P.top_p, last, upto))) {
                 // q_i = e_i / psum formed as the sum reads them: a run's
-                // loads and divisions are in flight together
+                // loads and divisions are in flight together.  Only the
+                // first upto q's can hold the crossing; the whole list is
+                // summed if they do not reach top_p after all.
                 auto q_at = [&](int i) { return __fdiv_rn(E[i], psum); };
-                (void)wave_run_sum<run_bound<BLOCK>(NR * BLOCK), true, true>(q_at, n_surv, 0.0f, P.top_p, hit, fin);
+                (void)wave_run_sum<run_bound<BLOCK>(NR * BLOCK), true, true>(q_at, upto, 0.0f, P.top_p, hit, fin);
+                if (hit < 0 && upto < n_surv)
+                    (void)wave_run_sum<run_bound<BLOCK>(NR * BLOCK), true, true>(q_at, n_surv, 0.0f, P.top_p, hit, fin);
                 last = hit < 0 ? n_surv - 1 : hit;
             }
             if (lane == 0) sh.n_kept = last + 1;
@@ -2139,9 +2149,12 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
         CBX_STAMP(15);
         const float psum = unif(sh.psum);
         // the cutoff: certified in binary64 where it can be, else the q's summed
-        int last = -1;
-        if (wid == 0 && !bad && !certified_cut<NG>(e_of, n_surv, psum, P.top_p, last)) last = -1;
-        if (wid == 0 && lane == 0) sh.n_kept = last + 1;
+        int last = -1, upto = n_surv;
+        if (wid == 0 && !bad && !certified_cut<NG>(e_of, n_surv, psum, P.top_p, last, upto)) last = -1;
+        if (wid == 0 && lane == 0) {
+            sh.n_kept = last + 1;
+            sh.n_cand = upto;  // the q's that hold the crossing
+        }
         __syncthreads();
         if (uni(sh.n_kept) == 0) {  // not certain (or NaN / +inf rows)
             if (e_lds) {
@@ -2150,9 +2163,11 @@ __device__ __forceinline__ int sample_row_wg(const KernelArgs& a, int64_t g, Sha
             }
             if (wid == 0) {
                 int hit;
-                (void)wave_run_sum<NG, true, true>(
-                    [&](int i) { return e_lds ? eg[i] : __fdiv_rn(e_form(i), psum); }, n_surv,
-                    0.0f, P.top_p, hit, !bad);
+                auto q_of = [&](int i) { return e_lds ? eg[i] : __fdiv_rn(e_form(i), psum); };
+                const int nq = bad ? n_surv : uni(sh.n_cand);
+                (void)wave_run_sum<NG, true, true>(q_of, nq, 0.0f, P.top_p, hit, !bad);
+                if (hit < 0 && nq < n_surv)
+                    (void)wave_run_sum<NG, true, true>(q_of, n_surv, 0.0f, P.top_p, hit, !bad);
                 if (lane == 0) sh.n_kept = (hit < 0 ? n_surv - 1 : hit) + 1;
             }
             __syncthreads();
