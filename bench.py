@@ -478,11 +478,6 @@ def fused_head_bench(torch, mod, sampler, stream, steps, dev):
                          "flops_per_launch": flops, "fp16_flops_per_launch": 2 * flops}}
 
 
-def pkg_workloads():
-    import pkg
-    return pkg.workloads()
-
-
 def config_single_stream(torch, mod, sampler, stream, dev, O):
     """B=1, V=6563, 500 steps, fixed history of 256 ids; k 1000, p 0.95,
     T 0.8, pen 1.2, min_p 0.05.  Philox draws keyed (seed, stream 0, step)."""
