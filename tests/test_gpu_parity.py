@@ -886,6 +886,49 @@ def test_topp_value_bin_paths(cbx, torch_cuda):
     assert np.all((ir[kind == "tie"] & parity.INFO_TOPP_TIE) != 0)
 
 
+def test_topp_open_cut_workgroup_kernel(cbx_default, torch_cuda):
+    """The workgroup kernel's top-p cut where its certificate cannot decide:
+    top_p equal to a cumulative value, or one float step either side of it,
+    so the exact sum of the q's runs over the prefix the bound leaves open
+    (and over the whole list should that prefix fall short).  A launch of
+    96 rows takes the workgroup kernel under the small-launch rule; the same
+    rows with the rule off take the one-wave kernel; both against the
+    oracle and against each other."""
+    mod, s = cbx_default
+    rng = np.random.default_rng(0x0C07)
+    V = 6563
+    rows, plist = [], []
+    for r in range(96):
+        k = [250, 1000, 1000][r % 3]
+        x = (rng.standard_normal(V) * [3.0, 1.0, 0.5][r % 3]).astype(F32)
+        surv, y = _sorted_prefix(x, k, 1.0)
+        m = int(rng.integers(5, max(6, int(np.searchsorted(y, 0.999)))))  # top_p < 1 in float
+        p = F32(y[m])
+        p = [p, np.nextafter(p, F32(1)), np.nextafter(p, F32(0))][(r // 3) % 3]
+        rows.append(x)
+        plist.append(dict(top_k=k, top_p=float(p), temp=1.0, repeat_penalty=1.2, min_p=0.0,
+                          cfg_weight=0.0))
+    x = np.stack(rows)
+    n = x.shape[0]
+    hist = rng.integers(0, V, size=(n, 300)).astype(np.int32)
+    hl = rng.integers(0, 301, size=n).astype(np.int32)
+    u = rng.random(n)
+    say(f"top-p open cuts: {n} rows, workgroup kernel (small-launch rule on)")
+    on = gpu_batch(cbx_default, torch_cuda, x, plist, u, hist, hl)
+    say("top-p open cuts: same rows, one-wave kernel (rule off)")
+    s.set_latency_rows(0)
+    try:
+        off = gpu_batch(cbx_default, torch_cuda, x, plist, u, hist, hl, max_survivors=1024)
+    finally:
+        s.set_latency_rows(512)
+    tr, ir, pr = oracle_rows(x, plist, u, hist, hl)
+    parity.compare("topp_open_cut_wg", on[0], on[1], tr, ir, u, on[2], pr)
+    parity.compare("topp_open_cut_wave", off[0], off[1], tr, ir, u, off[2], pr)
+    diag = np.uint32(parity.INFO_TOPP_SORTED)  # the one-wave kernel's diagnostic bit
+    assert np.array_equal(on[0], off[0]) and np.array_equal(on[1] & ~diag, off[1] & ~diag)
+    assert np.count_nonzero(off[1] & diag) > n // 2  # the bound straddles top_p
+
+
 def test_topp_tie_full_vocab_32768(cbx, torch_cuda):
     """Equal scores across the top-p cutoff with every id of V = 32768
     surviving: the replay of std::sort runs on 16-bit score ranks."""
